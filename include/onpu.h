@@ -1,0 +1,136 @@
+/*
+ * libonpu_hip: the int4 weight-only matmul operator surface of OpenNPU, implemented for one AMD
+ * Instinct MI355X (gfx950) with HIP kernels. It is a drop-in for the reference's libonpu C ABI
+ * (llama/ggml-opennpu/onpu_api.cpp, onpu_cpu.cpp), which opennpu/native/npu4/model.py binds with
+ * ctypes in clib() (model.py:281-335): set OPENNPU_LIBONPU to this library.
+ *
+ * Conventions (as in the reference):
+ *   - x and y of the host-pointer calls are row-major fp32; x is rounded to bf16 (nearest even)
+ *     before the product, y is overwritten and the call is synchronous.
+ *   - weights: a handle owns a host staging buffer (*_buf) that the caller fills with the staging
+ *     layout below, then *_sync uploads it to HBM and repacks it into the GPU layout.
+ *   - construction returns NULL for an unsupported shape or format; a HIP failure inside a void
+ *     call prints the error and aborts the process (the reference throws across extern "C").
+ *     onpu_last_error() reports the last failure of an int-returning call on this thread.
+ *   - every call is thread-safe (one library mutex for the host-pointer calls; the *_dev calls
+ *     run on the caller's stream).
+ *
+ * Weight formats (the `sym` argument of the reference calls; 0 and 1 are the reference's):
+ *   ONPU_FMT_Q4NX  0  asymmetric, w = u*s + m, 32-wide groups along K, bf16 s and m   (q4nx)
+ *   ONPU_FMT_Q4S   1  symmetric,  w = (u-8)*s, 32-wide groups, bf16 s                 (q4s)
+ *   ONPU_FMT_G128S 2  symmetric,  w = (u-8)*s, 128-wide groups, bf16 s
+ *   ONPU_FMT_Q4_0  3  GGUF Q4_0:  w = (u-8)*d, 32-wide blocks, fp16 d
+ * Staging layout of one [N][K] matrix (K % 32 == 0; G128S: K % 128 == 0):
+ *   Q4NX : codes u8 [N][K/2] (low nibble = even k), scales bf16 [N][K/32], mins bf16 [N][K/32]
+ *   Q4S  : codes u8 [N][K/2], scales bf16 [N][K/32]
+ *   G128S: codes u8 [N][K/2], scales bf16 [N][K/128]
+ *   Q4_0 : GGUF block_q4_0 rows [N][K/32] x {fp16 d, u8 qs[16]} (element j <- qs[j] & 15,
+ *          element j+16 <- qs[j] >> 4)
+ * Handles made by the reference calls keep the reference's buffer sizes (onpu_geometry2's
+ * nbytes, which the staging layout always fits in); *_new3 handles use onpu_stage_bytes().
+ */
+#ifndef ONPU_H
+#define ONPU_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ONPU_FMT_Q4NX = 0, ONPU_FMT_Q4S = 1, ONPU_FMT_G128S = 2, ONPU_FMT_Q4_0 = 3 };
+
+/* ---- device (onpu_api.cpp:59-60) */
+int onpu_ok(void);                 /* 1 when a gfx950 GPU is usable */
+int onpu_batched_ok(void);         /* 1: several rows per call are supported */
+
+/* ---- geometry (onpu_api.cpp:64-69): the reference's Mat (model.py:151-187), so that
+ * check_geometry (model.py:353-360) accepts this library; formats 2 and 3 report the q4s sizes */
+void onpu_geometry2(int64_t N, int64_t K, int ncols, int sym, int64_t * out /* [8] */);
+void onpu_geometry(int64_t N, int64_t K, int ncols, int64_t * out);
+
+/* ---- stats (onpu_api.cpp:72-80) and shapes (:82-84) */
+void onpu_stats(int64_t * calls, double * wait_s);
+int onpu_has_shape(int tiles, int kc, int batched);
+
+/* ---- dense matrices (onpu_api.cpp:87-156) */
+void * onpu_dense_new2(int64_t N, int64_t K, int sym);
+void * onpu_dense_new(int64_t N, int64_t K);
+uint8_t * onpu_dense_buf(void * h);
+int64_t onpu_dense_bytes(void * h);
+void onpu_dense_sync(void * h);
+void onpu_dense_free(void * h);
+void onpu_dense_mv(void * h, const float * x, int64_t rows, float * y);
+
+/* ---- expert banks: E experts of [N][K], expert e's staging at e * onpu_bank_expert_bytes
+ * (onpu_api.cpp:159-250) */
+void * onpu_bank_new2(int64_t N, int64_t K, int64_t E, int ncols, int sym);
+void * onpu_bank_new(int64_t N, int64_t K, int64_t E, int ncols);
+uint8_t * onpu_bank_buf(void * h);
+int64_t onpu_bank_expert_bytes(void * h);
+void onpu_bank_sync(void * h);
+void onpu_bank_free(void * h);
+/* y [T][k][N]: slot (t, j) -> expert ids[t*k+j] applied to x [T][K] (x_per_slot 0) or [T][k][K] */
+void onpu_bank_run(void * h, const float * x, int x_per_slot, int64_t T, const int32_t * ids, int k, float * y);
+
+/* ---- routed-expert FFN (onpu_api.cpp:261-278): y [T][N of dn] = sum_j w[t*k+j] *
+ * dn_e(act(gu_e x_t + gu_bias[e]) ) + dn_bias[e]; act 0: silu(h[:I]) * h[I:], act 1: gpt-oss */
+void onpu_moe_ffn(void * gu, void * dn, const float * x, int64_t T, const int32_t * ids, int k, const float * w,
+                  int act, float alpha, float limit, const float * gu_bias, const float * dn_bias, float * y);
+/* the CPU helpers of onpu_cpu.cpp:233-274, computed on the GPU (host pointers in and out) */
+void onpu_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * gu_bias, int act,
+                  float alpha, float limit, float * a);
+void onpu_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * ids, const float * w,
+                  const float * bias, float * y);
+
+/* ---- fused expert FFN (onpu_api.cpp:292-496): gate_up, SiLU * up and down of a token's experts
+ * without host round trips. perm is the identity here (rows keep the [gate | up] order). */
+void * onpu_ffn_new(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int sym);
+void * onpu_ffn_gu(void * h);
+void * onpu_ffn_dn(void * h);
+int onpu_ffn_fused(void * h);
+void onpu_ffn_perm(void * h, int32_t * out /* [Ng] */);
+int onpu_ffn_run(void * h, const float * x, const int32_t * ids, int k, const float * w, float * y);
+int onpu_ffn_run_many(void * h, const float * x, int64_t T, const int32_t * ids, int k, const float * w, float * y);
+void onpu_ffn_free(void * h);
+
+/* ---- packing (onpu_api.cpp:499-529): quantize fp32 W [N][K] with the reference's search
+ * quantizers (q4nx / q4s per 32; g128s per 128; Q4_0 as ggml) into the staging layout; returns
+ * onpu_geometry2's nbytes (0: unsupported) */
+int64_t onpu_pack(const float * W, int64_t N, int64_t K, int ncols, int sym, uint8_t * out, int threads);
+void onpu_quant_dequant(const float * W, int64_t N, int64_t K, int sym, float * out, int threads);
+
+/* ================================================================ MI355X-native extensions
+ * No counterpart in the reference: device-pointer entry points for callers whose activations
+ * already live in HBM (torch tensors, a serving loop), plus introspection for parity checks. */
+const char * onpu_last_error(void);
+int64_t onpu_stage_bytes(int fmt, int64_t N, int64_t K);
+/* handles whose staging stride is onpu_stage_bytes (no reference padding) */
+void * onpu_dense_new3(int64_t N, int64_t K, int fmt);
+void * onpu_bank_new3(int64_t N, int64_t K, int64_t E, int fmt);
+void * onpu_ffn_new3(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int fmt);
+/* upload staging-layout bytes from caller memory without keeping a staging copy;
+ * bank: experts [e0, e0 + n), stage holds n consecutive experts of onpu_stage_bytes each */
+int onpu_dense_load(void * h, const void * stage);
+int onpu_bank_load(void * h, int64_t e0, int64_t n, const void * stage);
+/* N, K, fmt, E, row tiles, K blocks, HBM bytes per expert, HBM base address */
+void onpu_dense_info(void * h, int64_t * out /* [8] */);
+/* dequantized weights of expert e as the GPU stores them: fp32 (bf16 = 0) or bf16 RNE bits */
+int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
+/* y [M][N] = x [M][K] . W^T on `stream` (hipStream_t; NULL: the default stream); x bf16 in HBM,
+ * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels, larger M the MFMA GEMM. */
+int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
+/* logits fp32 [M][N] and argmax [M] (first maximum) */
+int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream);
+/* router: logits fp32 [T][E] -> ids [T][k], w [T][k] (softmax, top-k by probability, ties to the
+ * lower id, renormalised when renorm != 0) */
+int onpu_moe_route_dev(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
+                       void * stream);
+/* routed-expert FFN on device data: x bf16 [T][Kg], ids/w [T][k] -> y [T][Nd] (bf16 or fp32).
+ * h: an onpu_ffn_new / onpu_ffn_new3 handle. Uses workspace owned by h. */
+int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, int k, const float * w, void * y,
+                     int y_f32, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,662 @@
+// libonpu_hip: the reference's libonpu C ABI (llama/ggml-opennpu/onpu_api.cpp, onpu_cpu.cpp) over
+// HIP on one MI355X, plus device-pointer entry points. Declarations and conventions:
+// include/onpu.h.
+//
+// A handle (Mat4) holds one matrix or an expert bank: the weights in HBM in the tiled layout of
+// onpu_common.h, and (lazily) a host staging buffer in the staging layout that *_sync uploads.
+// Host-pointer calls take the library mutex and run on the library's stream; *_dev calls run on
+// the caller's stream and touch only the handle's own workspace.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "onpu.h"
+#include "onpu_common.h"
+#include "onpu_host.h"
+#include "onpu_launch.h"
+
+using namespace onpu;
+
+namespace {
+
+std::mutex g_mu;                          // serialises host-pointer calls (as onpu_api.cpp:53)
+thread_local std::string g_err;
+std::atomic<int64_t> g_calls{0};
+double g_wait_s = 0;                      // guarded by g_mu
+
+[[noreturn]] void die(const char * what, hipError_t e) {
+    std::fprintf(stderr, "libonpu_hip: %s failed: %s\n", what, hipGetErrorString(e));
+    std::abort();
+}
+void set_err(const char * what, hipError_t e) {
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+}
+void set_err(const char * what) { g_err = what; }
+
+// void calls abort on a HIP failure (the reference throws across extern "C"); int calls return -1
+#define HIPX(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) die(#call, e_); } while (0)
+#define HIPR(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { set_err(#call, e_); return -1; } } while (0)
+
+struct Device {
+    int ok = 0;
+    hipStream_t stream = nullptr;
+};
+
+Device & device() {
+    static Device d;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n < 1) return;
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, 0) != hipSuccess) return;
+        if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+            std::fprintf(stderr, "libonpu_hip: device 0 is %s; this library is built for gfx950 only\n",
+                         p.gcnArchName);
+            return;
+        }
+        if (hipSetDevice(0) != hipSuccess) return;
+        if (hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking) != hipSuccess) return;
+        d.ok = 1;
+    });
+    return d;
+}
+
+struct DBuf {                              // grow-only device buffer (freed with its owner)
+    void * p = nullptr;
+    size_t n = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= n) return hipSuccess;
+        if (p) (void) hipFree(p);
+        p = nullptr;
+        n = 0;
+        const hipError_t e = hipMalloc(&p, std::max<size_t>(bytes, 256));
+        if (e == hipSuccess) n = std::max<size_t>(bytes, 256);
+        return e;
+    }
+    void release() {
+        if (p) (void) hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    template <class T> T * as(size_t byte_off = 0) const { return (T *) ((char *) p + byte_off); }
+};
+
+struct Mat4 {                              // one [N][K] matrix (E = 1) or a bank of E experts
+    int fmt = 0;
+    int64_t N = 0, K = 0, E = 1;
+    Tiled g{};
+    int64_t dstride = 0;                   // HBM bytes per expert (tiled layout, 256-aligned)
+    uint8_t * dev = nullptr;
+    uint8_t * stage = nullptr;             // host staging, E * sstride bytes (lazy)
+    int64_t sstride = 0;
+    DBuf ws[6];                            // workspace of the calls on this handle
+};
+
+struct Ffn {
+    Mat4 * gu = nullptr, * dn = nullptr;
+    bool fused = false;
+    DBuf ws[12];
+};
+
+int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+
+Mat4 * make_mat(int64_t N, int64_t K, int64_t E, int fmt, int64_t sstride) {
+    if (!device().ok || !fmt_valid(fmt) || N <= 0 || K <= 0 || E <= 0 || K % fmt_group(fmt) != 0) return nullptr;
+    if (sstride < stage_bytes(fmt, N, K)) return nullptr;
+    auto * m = new Mat4;
+    m->fmt = fmt;
+    m->N = N;
+    m->K = K;
+    m->E = E;
+    m->g = tiled_geom(fmt, N, K);
+    m->dstride = round_up(m->g.bytes, 256);
+    m->sstride = sstride;
+    if (hipMalloc((void **) &m->dev, (size_t) (m->dstride * E)) != hipSuccess) {
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+void free_mat(Mat4 * m) {
+    if (!m) return;
+    if (m->dev) (void) hipFree(m->dev);
+    std::free(m->stage);
+    for (auto & b : m->ws) b.release();
+    delete m;
+}
+
+uint8_t * stage_of(Mat4 * m) {
+    if (!m->stage) {
+        m->stage = (uint8_t *) std::calloc((size_t) (m->E * m->sstride), 1);
+        if (!m->stage) { std::fprintf(stderr, "libonpu_hip: out of host memory for staging\n"); std::abort(); }
+    }
+    return m->stage;
+}
+
+// experts [e0, e0 + n) from staging bytes (stride src_stride per expert) -> HBM tiled layout
+hipError_t upload(Mat4 * m, int64_t e0, int64_t n, const uint8_t * src, int64_t src_stride, hipStream_t s) {
+    void * tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, (size_t) (n * src_stride));
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(tmp, src, (size_t) (n * src_stride), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = launch_repack(m->fmt, (const uint8_t *) tmp, src_stride, m->N, m->K, m->dev + e0 * m->dstride, m->dstride,
+                          n, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void) hipFree(tmp);
+    return e;
+}
+
+// ------------------------------------------------------------------ launch plans
+int env_int(const char * name, int dflt) {
+    const char * v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+
+struct Plan {
+    int mb = 1, rt = 1, waves = 1;
+    int64_t bpw = 1;
+};
+
+// waves split K; rt row tiles per workgroup; enough waves in flight to cover HBM latency
+Plan plan_gemv(int64_t NT, int64_t KB, int M, int64_t slots, bool act) {
+    Plan p;
+    p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    p.rt = act ? 2 : 1;
+    if (!act && p.mb == 1) p.rt = NT >= 4096 ? 4 : (NT >= 1536 ? 2 : 1);
+    const int maxw = p.mb == 1 ? 16 : 8;
+    const int64_t wg = (act ? NT / 2 : (NT + p.rt - 1) / p.rt) * slots;
+    p.waves = 1;
+    while (p.waves < maxw && 2 * p.waves <= KB && (wg * p.waves < 4096 || KB / p.waves > 8)) p.waves *= 2;
+    const int ew = env_int("ONPU_GEMV_WAVES", 0), er = env_int("ONPU_GEMV_RT", 0);
+    if (ew > 0 && ew <= maxw) p.waves = ew;
+    if (!act && er > 0 && p.mb == 1 && (er == 1 || er == 2 || er == 4)) p.rt = er;
+    p.bpw = (KB + p.waves - 1) / p.waves;
+    return p;
+}
+
+// y [M][N] = x [M][K] (bf16, device) . W_e^T, M rows
+hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const uint8_t * W = m->dev + e * m->dstride;
+    if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0) {
+        const Plan p = plan_gemv(m->g.NT, m->g.KB, (int) M, 1, false);
+        QArgs a{};
+        a.W = W; a.estride = 0; a.ids = nullptr;
+        a.N = m->N; a.K = m->K; a.NT = m->g.NT; a.KB = m->g.KB;
+        a.x = x; a.ldx = m->K; a.xslot = 0; a.xdiv = 1; a.M = (int) M;
+        a.y = y; a.ldy = m->N; a.yslot = 0; a.yf32 = yf32;
+        a.bpw = p.bpw;
+        dim3 grid((unsigned) ((m->g.NT + p.rt - 1) / p.rt), 1);
+        return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, grid, p.waves, s);
+    }
+    GArgs a{};
+    a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
+    a.x = x; a.ldx = m->K; a.y = y; a.ldy = m->N; a.yf32 = yf32;
+    const int ntw = env_int("ONPU_GEMM_NTW", 2) == 4 ? 4 : 2;
+    return launch_qgemm(m->fmt, a, ntw, s);
+}
+
+// per-slot products: slot r = t * k + j -> expert ids[r] on x row (x_per_slot ? r : t); y [T*k][N]
+hipError_t bank_core(Mat4 * m, const uint16_t * x, int x_per_slot, int64_t T, const int32_t * ids, int k, void * y,
+                     int yf32, hipStream_t s) {
+    const int64_t slots = T * k, chunk = (65535 / k) * k;     // grid.y limit; chunks start on a token
+    const Plan p = plan_gemv(m->g.NT, m->g.KB, 1, slots, false);
+    for (int64_t s0 = 0; s0 < slots; s0 += chunk) {
+        const int64_t ns = std::min<int64_t>(chunk, slots - s0);
+        QArgs a{};
+        a.W = m->dev; a.estride = m->dstride; a.ids = ids + s0;
+        a.N = m->N; a.K = m->K; a.NT = m->g.NT; a.KB = m->g.KB;
+        // slot r of this chunk reads x row r / xdiv from the chunk's first row
+        a.xdiv = x_per_slot ? 1 : k;
+        a.x = x + (x_per_slot ? s0 : s0 / k) * m->K;
+        a.ldx = m->K; a.xslot = m->K; a.M = 1;
+        a.y = (char *) y + s0 * m->N * (yf32 ? 4 : 2); a.ldy = m->N; a.yslot = m->N; a.yf32 = yf32;
+        a.bpw = p.bpw;
+        dim3 grid((unsigned) ((m->g.NT + p.rt - 1) / p.rt), (unsigned) ns);
+        hipError_t e = launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, grid, p.waves, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// routed-expert FFN on device data (act 0, no biases): x bf16 [T][H], ids/w [T][k] -> y [T][Nd]
+hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids, int k, const float * w, void * y,
+                    int yf32, hipStream_t s) {
+    Mat4 * gu = f->gu, * dn = f->dn;
+    const int64_t I = gu->N / 2, Nd = dn->N;
+    const int64_t n = T * k;
+    const int decode_max = env_int("ONPU_MOE_DECODE_MAX", 4);
+    hipError_t e;
+    if (T <= decode_max && k <= 16) {
+        // gate_up with SiLU(gate) * up per slot, then down with the weighted slot sum per token
+        e = f->ws[0].ensure((size_t) (n * I * 2));
+        if (e != hipSuccess) return e;
+        uint16_t * act = f->ws[0].as<uint16_t>();
+        const Plan pg = plan_gemv(gu->g.NT, gu->g.KB, 1, n, true);
+        QArgs a{};
+        a.W = gu->dev; a.estride = gu->dstride; a.ids = ids;
+        a.N = gu->N; a.K = gu->K; a.NT = gu->g.NT; a.KB = gu->g.KB;
+        a.x = x; a.ldx = gu->K; a.xslot = gu->K; a.xdiv = k; a.M = 1;
+        a.y = act; a.ldy = I; a.yslot = I; a.yf32 = 0; a.bpw = pg.bpw;
+        e = launch_qgemv(gu->fmt, EPI_ACT_, a, 1, 2, dim3((unsigned) (I / 16), (unsigned) n), pg.waves, s);
+        if (e != hipSuccess) return e;
+        int ksplit = 1;
+        while (k * ksplit * 2 <= 16 && ksplit * 2 <= dn->g.KB) ksplit *= 2;
+        QArgs b{};
+        b.W = dn->dev; b.estride = dn->dstride; b.ids = ids;
+        b.N = Nd; b.K = dn->K; b.NT = dn->g.NT; b.KB = dn->g.KB;
+        b.x = act; b.ldx = I; b.xslot = I; b.xdiv = 1; b.M = 1;
+        b.y = y; b.ldy = Nd; b.yslot = Nd; b.yf32 = yf32;
+        b.wslot = w; b.nslot = k; b.ksplit = ksplit;
+        b.bpw = (dn->g.KB + ksplit - 1) / ksplit;
+        return launch_qgemv(dn->fmt, EPI_SLOTSUM_, b, 1, 1, dim3((unsigned) dn->g.NT, (unsigned) T), k * ksplit, s);
+    }
+    // prompts: tokens grouped per expert (one pass over each routed expert's weights per 64 rows)
+    const int rows_per_item = 64, mb = 4;
+    const int64_t E = gu->E, maxitems = n / rows_per_item + E;
+    if ((e = f->ws[1].ensure((size_t) (E + 1) * 4)) != hipSuccess) return e;
+    if ((e = f->ws[2].ensure((size_t) n * 4)) != hipSuccess) return e;
+    if ((e = f->ws[3].ensure((size_t) n * 4)) != hipSuccess) return e;
+    if ((e = f->ws[4].ensure((size_t) (maxitems * 3 + 1) * 4)) != hipSuccess) return e;
+    if ((e = f->ws[5].ensure((size_t) (n * I * 2))) != hipSuccess) return e;
+    if ((e = f->ws[6].ensure((size_t) (n * Nd * 4))) != hipSuccess) return e;
+    int32_t * off = f->ws[1].as<int32_t>(), * perm = f->ws[2].as<int32_t>(), * inv = f->ws[3].as<int32_t>();
+    int32_t * items = f->ws[4].as<int32_t>(), * nitems = items + maxitems * 3;
+    uint16_t * act = f->ws[5].as<uint16_t>();
+    float * o = f->ws[6].as<float>();
+    if ((e = launch_moe_permute(ids, n, (int) E, rows_per_item, off, perm, items, nitems, s)) != hipSuccess) return e;
+    if ((e = launch_invert(perm, n, inv, s)) != hipSuccess) return e;
+    MArgs a{};
+    a.W = gu->dev; a.estride = gu->dstride; a.NT = gu->g.NT; a.KB = gu->g.KB; a.N = gu->N; a.K = gu->K;
+    a.x = x; a.ldx = gu->K; a.y = act; a.ldy = I; a.perm = perm; a.items = items; a.nitems = nitems; a.k = k;
+    int wg = 1;                            // LDS: wg * 2 tiles * mb * 1 KiB <= 32 KiB
+    while (wg < 4 && 2 * wg <= gu->g.KB) wg *= 2;
+    a.bpw = (gu->g.KB + wg - 1) / wg;
+    if ((e = launch_moe_grouped(gu->fmt, 0, a, mb, dim3((unsigned) (I / 16), (unsigned) maxitems), wg, s)) !=
+        hipSuccess)
+        return e;
+    MArgs b{};
+    b.W = dn->dev; b.estride = dn->dstride; b.NT = dn->g.NT; b.KB = dn->g.KB; b.N = Nd; b.K = dn->K;
+    b.x = act; b.ldx = I; b.y = o; b.ldy = Nd; b.perm = perm; b.items = items; b.nitems = nitems; b.k = k;
+    int wd = 1;
+    while (wd < 8 && 2 * wd <= dn->g.KB) wd *= 2;
+    b.bpw = (dn->g.KB + wd - 1) / wd;
+    if ((e = launch_moe_grouped(dn->fmt, 1, b, mb, dim3((unsigned) dn->g.NT, (unsigned) maxitems), wd, s)) !=
+        hipSuccess)
+        return e;
+    return launch_moe_combine(o, inv, w, T, k, Nd, y, yf32, s);
+}
+
+// expert ids from the caller index HBM: reject out-of-range ids before any launch
+void check_ids(const int32_t * ids, int64_t n, int64_t E, const char * who) {
+    for (int64_t i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= E) {
+            std::fprintf(stderr, "libonpu_hip: %s: expert id %d at %lld outside [0, %lld)\n", who, (int) ids[i],
+                         (long long) i, (long long) E);
+            std::abort();
+        }
+}
+
+// host fp32 rows -> bf16 on the device (the reference converts on the host, opennpu_core.hpp:418-424)
+hipError_t x_to_dev(DBuf & fbuf, DBuf & bbuf, const float * x, int64_t n, hipStream_t s) {
+    hipError_t e = fbuf.ensure((size_t) n * 4);
+    if (e == hipSuccess) e = bbuf.ensure((size_t) n * 2);
+    if (e == hipSuccess) e = hipMemcpyAsync(fbuf.p, x, (size_t) n * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = launch_f32_to_bf16(fbuf.as<float>(), n, bbuf.as<uint16_t>(), s);
+    return e;
+}
+
+struct Timer {
+    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+    ~Timer() {
+        g_wait_s += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        g_calls++;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+const char * onpu_last_error(void) { return g_err.c_str(); }
+
+int onpu_ok(void) { return device().ok; }
+int onpu_batched_ok(void) { return device().ok; }
+
+void onpu_geometry2(int64_t N, int64_t K, int ncols, int sym, int64_t * out) {
+    const RefGeom g = ref_geometry(N, K, ncols, sym != 0);
+    const int64_t v[8] = {g.R, g.S, g.tiles, g.kc, g.ks, g.rows_col, g.cb, g.nbytes};
+    for (int i = 0; i < 8; i++) out[i] = g.ok ? v[i] : 0;
+}
+void onpu_geometry(int64_t N, int64_t K, int ncols, int64_t * out) { onpu_geometry2(N, K, ncols, 0, out); }
+
+void onpu_stats(int64_t * calls, double * wait_s) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    *calls = g_calls.load();
+    *wait_s = g_wait_s;
+}
+
+// every (tiles, kc) is served: the HIP kernels take any shape
+int onpu_has_shape(int, int, int) { return device().ok; }
+
+int64_t onpu_stage_bytes(int fmt, int64_t N, int64_t K) {
+    return fmt_valid(fmt) && K % fmt_group(fmt) == 0 ? stage_bytes(fmt, N, K) : 0;
+}
+
+// ---------------------------------------------------------------- dense
+void * onpu_dense_new2(int64_t N, int64_t K, int sym) {
+    const RefGeom g = ref_geometry(N, K, 8, sym != 0);
+    if (!g.ok) return nullptr;
+    return make_mat(N, K, 1, sym, g.nbytes);
+}
+void * onpu_dense_new(int64_t N, int64_t K) { return onpu_dense_new2(N, K, 0); }
+void * onpu_dense_new3(int64_t N, int64_t K, int fmt) {
+    if (!fmt_valid(fmt) || K % fmt_group(fmt) != 0) return nullptr;
+    return make_mat(N, K, 1, fmt, stage_bytes(fmt, N, K));
+}
+uint8_t * onpu_dense_buf(void * h) { return stage_of((Mat4 *) h); }
+int64_t onpu_dense_bytes(void * h) { return ((Mat4 *) h)->sstride; }
+
+void onpu_dense_sync(void * h) {
+    auto * m = (Mat4 *) h;
+    std::lock_guard<std::mutex> lk(g_mu);
+    HIPX(upload(m, 0, m->E, stage_of(m), m->sstride, device().stream));
+}
+
+void onpu_dense_free(void * h) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    free_mat((Mat4 *) h);
+}
+
+int onpu_dense_load(void * h, const void * stage) {
+    auto * m = (Mat4 *) h;
+    std::lock_guard<std::mutex> lk(g_mu);
+    HIPR(upload(m, 0, 1, (const uint8_t *) stage, stage_bytes(m->fmt, m->N, m->K), device().stream));
+    return 0;
+}
+
+void onpu_dense_info(void * h, int64_t * out) {
+    auto * m = (Mat4 *) h;
+    const int64_t v[8] = {m->N, m->K, m->fmt, m->E, m->g.NT, m->g.KB, m->dstride, (int64_t) (uintptr_t) m->dev};
+    for (int i = 0; i < 8; i++) out[i] = v[i];
+}
+
+int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16) {
+    auto * m = (Mat4 *) h;
+    if (e < 0 || e >= m->E) { set_err("onpu_dense_dequant: expert out of range"); return -1; }
+    std::lock_guard<std::mutex> lk(g_mu);
+    const hipStream_t s = device().stream;
+    const size_t bytes = (size_t) (m->N * m->K * (bf16 ? 2 : 4));
+    HIPR(m->ws[0].ensure(bytes));
+    HIPR(launch_dequant(m->fmt, m->dev + e * m->dstride, m->N, m->K, m->ws[0].p, bf16, s));
+    HIPR(hipMemcpyAsync(out_host, m->ws[0].p, bytes, hipMemcpyDeviceToHost, s));
+    HIPR(hipStreamSynchronize(s));
+    return 0;
+}
+
+void onpu_dense_mv(void * h, const float * x, int64_t rows, float * y) {
+    auto * m = (Mat4 *) h;
+    if (rows <= 0) return;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Timer tm;
+    const hipStream_t s = device().stream;
+    HIPX(x_to_dev(m->ws[0], m->ws[1], x, rows * m->K, s));
+    HIPX(m->ws[2].ensure((size_t) (rows * m->N * 4)));
+    HIPX(mv_core(m, 0, m->ws[1].as<uint16_t>(), rows, m->ws[2].p, 1, s));
+    HIPX(hipMemcpyAsync(y, m->ws[2].p, (size_t) (rows * m->N * 4), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+}
+
+int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream) {
+    auto * m = (Mat4 *) h;
+    HIPR(mv_core(m, 0, (const uint16_t *) x, M, y, y_f32, (hipStream_t) stream));
+    return 0;
+}
+
+int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream) {
+    auto * m = (Mat4 *) h;
+    HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
+    HIPR(launch_argmax(logits, M, m->N, argmax, (hipStream_t) stream));
+    return 0;
+}
+
+// ---------------------------------------------------------------- banks
+void * onpu_bank_new2(int64_t N, int64_t K, int64_t E, int ncols, int sym) {
+    const RefGeom g = ref_geometry(N, K, ncols, sym != 0);
+    if (!g.ok) return nullptr;
+    return make_mat(N, K, E, sym, g.nbytes);
+}
+void * onpu_bank_new(int64_t N, int64_t K, int64_t E, int ncols) { return onpu_bank_new2(N, K, E, ncols, 0); }
+void * onpu_bank_new3(int64_t N, int64_t K, int64_t E, int fmt) {
+    if (!fmt_valid(fmt) || K % fmt_group(fmt) != 0) return nullptr;
+    return make_mat(N, K, E, fmt, stage_bytes(fmt, N, K));
+}
+uint8_t * onpu_bank_buf(void * h) { return stage_of((Mat4 *) h); }
+int64_t onpu_bank_expert_bytes(void * h) { return ((Mat4 *) h)->sstride; }
+void onpu_bank_sync(void * h) { onpu_dense_sync(h); }
+void onpu_bank_free(void * h) { onpu_dense_free(h); }
+
+int onpu_bank_load(void * h, int64_t e0, int64_t n, const void * stage) {
+    auto * m = (Mat4 *) h;
+    if (e0 < 0 || n < 0 || e0 + n > m->E) { set_err("onpu_bank_load: experts out of range"); return -1; }
+    std::lock_guard<std::mutex> lk(g_mu);
+    HIPR(upload(m, e0, n, (const uint8_t *) stage, stage_bytes(m->fmt, m->N, m->K), device().stream));
+    return 0;
+}
+
+void onpu_bank_run(void * h, const float * x, int x_per_slot, int64_t T, const int32_t * ids, int k, float * y) {
+    auto * m = (Mat4 *) h;
+    if (T <= 0 || k <= 0) return;
+    check_ids(ids, T * k, m->E, "onpu_bank_run");
+    std::lock_guard<std::mutex> lk(g_mu);
+    Timer tm;
+    const hipStream_t s = device().stream;
+    const int64_t xrows = x_per_slot ? T * k : T;
+    HIPX(x_to_dev(m->ws[0], m->ws[1], x, xrows * m->K, s));
+    HIPX(m->ws[2].ensure((size_t) (T * k * 4)));
+    HIPX(hipMemcpyAsync(m->ws[2].p, ids, (size_t) (T * k * 4), hipMemcpyHostToDevice, s));
+    HIPX(m->ws[3].ensure((size_t) (T * k * m->N * 4)));
+    HIPX(bank_core(m, m->ws[1].as<uint16_t>(), x_per_slot, T, m->ws[2].as<int32_t>(), k, m->ws[3].p, 1, s));
+    HIPX(hipMemcpyAsync(y, m->ws[3].p, (size_t) (T * k * m->N * 4), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+}
+
+void onpu_moe_ffn(void * gu_h, void * dn_h, const float * x, int64_t T, const int32_t * ids, int k, const float * w,
+                  int act, float alpha, float limit, const float * gu_bias, const float * dn_bias, float * y) {
+    auto * gu = (Mat4 *) gu_h, * dn = (Mat4 *) dn_h;
+    if (T <= 0 || k <= 0) return;
+    check_ids(ids, T * k, std::min(gu->E, dn->E), "onpu_moe_ffn");
+    std::lock_guard<std::mutex> lk(g_mu);
+    Timer tm;
+    const hipStream_t s = device().stream;
+    const int64_t n = T * k, Ng = gu->N, I = Ng / 2, Nd = dn->N, E = gu->E;
+    DBuf * b = gu->ws;                     // gu's workspace: x f32/bf16, ids, h, a (f32, bf16)
+    DBuf * c = dn->ws;                     // dn's workspace: w, o, y, biases
+    HIPX(x_to_dev(b[0], b[1], x, T * gu->K, s));
+    HIPX(b[2].ensure((size_t) n * 4));
+    HIPX(hipMemcpyAsync(b[2].p, ids, (size_t) n * 4, hipMemcpyHostToDevice, s));
+    HIPX(b[3].ensure((size_t) (n * Ng * 4)));
+    HIPX(bank_core(gu, b[1].as<uint16_t>(), 0, T, b[2].as<int32_t>(), k, b[3].p, 1, s));
+    const float * gb = nullptr, * db = nullptr;
+    if (gu_bias) {
+        HIPX(c[3].ensure((size_t) (E * Ng * 4)));
+        HIPX(hipMemcpyAsync(c[3].p, gu_bias, (size_t) (E * Ng * 4), hipMemcpyHostToDevice, s));
+        gb = c[3].as<float>();
+    }
+    if (dn_bias) {
+        HIPX(c[4].ensure((size_t) (E * Nd * 4)));
+        HIPX(hipMemcpyAsync(c[4].p, dn_bias, (size_t) (E * Nd * 4), hipMemcpyHostToDevice, s));
+        db = c[4].as<float>();
+    }
+    HIPX(b[4].ensure((size_t) (n * I * 4)));
+    HIPX(launch_moe_act(b[3].as<float>(), n, Ng, b[2].as<int32_t>(), gb, act, alpha, limit, b[4].as<float>(), s));
+    HIPX(b[5].ensure((size_t) (n * I * 2)));
+    HIPX(launch_f32_to_bf16(b[4].as<float>(), n * I, b[5].as<uint16_t>(), s));
+    HIPX(c[0].ensure((size_t) n * 4));
+    HIPX(hipMemcpyAsync(c[0].p, w, (size_t) n * 4, hipMemcpyHostToDevice, s));
+    HIPX(c[1].ensure((size_t) (n * Nd * 4)));
+    HIPX(bank_core(dn, b[5].as<uint16_t>(), 1, T, b[2].as<int32_t>(), k, c[1].p, 1, s));
+    HIPX(c[2].ensure((size_t) (T * Nd * 4)));
+    HIPX(launch_moe_sum(c[1].as<float>(), T, k, Nd, b[2].as<int32_t>(), c[0].as<float>(), db, c[2].as<float>(), s));
+    HIPX(hipMemcpyAsync(y, c[2].p, (size_t) (T * Nd * 4), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+}
+
+// the CPU helpers of onpu_cpu.cpp:233-274, computed on the GPU
+void onpu_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * gu_bias, int act,
+                  float alpha, float limit, float * a) {
+    if (rows <= 0) return;
+    std::lock_guard<std::mutex> lk(g_mu);
+    static DBuf bh, bi, bb, ba;
+    const hipStream_t s = device().stream;
+    int64_t E = 0;
+    if (gu_bias)
+        for (int64_t r = 0; r < rows; r++) E = std::max<int64_t>(E, (int64_t) ids[r] + 1);
+    HIPX(bh.ensure((size_t) (rows * Ng * 4)));
+    HIPX(hipMemcpyAsync(bh.p, h, (size_t) (rows * Ng * 4), hipMemcpyHostToDevice, s));
+    if (gu_bias) {
+        HIPX(bi.ensure((size_t) rows * 4));
+        HIPX(hipMemcpyAsync(bi.p, ids, (size_t) rows * 4, hipMemcpyHostToDevice, s));
+        HIPX(bb.ensure((size_t) (E * Ng * 4)));
+        HIPX(hipMemcpyAsync(bb.p, gu_bias, (size_t) (E * Ng * 4), hipMemcpyHostToDevice, s));
+    }
+    HIPX(ba.ensure((size_t) (rows * (Ng / 2) * 4)));
+    HIPX(launch_moe_act(bh.as<float>(), rows, Ng, gu_bias ? bi.as<int32_t>() : nullptr,
+                        gu_bias ? bb.as<float>() : nullptr, act, alpha, limit, ba.as<float>(), s));
+    HIPX(hipMemcpyAsync(a, ba.p, (size_t) (rows * (Ng / 2) * 4), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+}
+
+void onpu_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * ids, const float * w,
+                  const float * bias, float * y) {
+    if (T <= 0) return;
+    std::lock_guard<std::mutex> lk(g_mu);
+    static DBuf bo, bi, bw, bb, by;
+    const hipStream_t s = device().stream;
+    const int64_t n = T * k;
+    int64_t E = 0;
+    for (int64_t r = 0; r < n; r++) E = std::max<int64_t>(E, (int64_t) ids[r] + 1);
+    HIPX(bo.ensure((size_t) (n * N * 4)));
+    HIPX(hipMemcpyAsync(bo.p, o, (size_t) (n * N * 4), hipMemcpyHostToDevice, s));
+    HIPX(bi.ensure((size_t) n * 4));
+    HIPX(hipMemcpyAsync(bi.p, ids, (size_t) n * 4, hipMemcpyHostToDevice, s));
+    HIPX(bw.ensure((size_t) n * 4));
+    HIPX(hipMemcpyAsync(bw.p, w, (size_t) n * 4, hipMemcpyHostToDevice, s));
+    if (bias) {
+        HIPX(bb.ensure((size_t) (E * N * 4)));
+        HIPX(hipMemcpyAsync(bb.p, bias, (size_t) (E * N * 4), hipMemcpyHostToDevice, s));
+    }
+    HIPX(by.ensure((size_t) (T * N * 4)));
+    HIPX(launch_moe_sum(bo.as<float>(), T, k, N, bi.as<int32_t>(), bw.as<float>(), bias ? bb.as<float>() : nullptr,
+                        by.as<float>(), s));
+    HIPX(hipMemcpyAsync(y, by.p, (size_t) (T * N * 4), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+}
+
+// ---------------------------------------------------------------- fused expert FFN
+static void * ffn_make(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int fmt, int64_t sg, int64_t sd) {
+    Mat4 * gu = make_mat(Ng, Kg, E, fmt, sg);
+    Mat4 * dn = gu ? make_mat(Nd, Kd, E, fmt, sd) : nullptr;
+    if (!gu || !dn) { free_mat(gu); return nullptr; }
+    auto * f = new Ffn;
+    f->gu = gu;
+    f->dn = dn;
+    // the fused kernels pair gate row tile t with up row tile t + I/16
+    f->fused = Ng % 32 == 0 && Kd == Ng / 2;
+    return f;
+}
+
+void * onpu_ffn_new(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int sym) {
+    const RefGeom gg = ref_geometry(Ng, Kg, 1, sym != 0), gd = ref_geometry(Nd, Kd, 1, sym != 0);
+    if (!gg.ok || !gd.ok) return nullptr;
+    return ffn_make(Ng, Kg, Nd, Kd, E, sym, gg.nbytes, gd.nbytes);
+}
+void * onpu_ffn_new3(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int fmt) {
+    if (!fmt_valid(fmt) || Kg % fmt_group(fmt) != 0 || Kd % fmt_group(fmt) != 0) return nullptr;
+    return ffn_make(Ng, Kg, Nd, Kd, E, fmt, stage_bytes(fmt, Ng, Kg), stage_bytes(fmt, Nd, Kd));
+}
+void * onpu_ffn_gu(void * h) { return ((Ffn *) h)->gu; }
+void * onpu_ffn_dn(void * h) { return ((Ffn *) h)->dn; }
+int onpu_ffn_fused(void * h) { return ((Ffn *) h)->fused ? 1 : 0; }
+void onpu_ffn_perm(void * h, int32_t * out) {
+    for (int64_t i = 0; i < ((Ffn *) h)->gu->N; i++) out[i] = (int32_t) i;
+}
+void onpu_ffn_free(void * h) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto * f = (Ffn *) h;
+    free_mat(f->gu);
+    free_mat(f->dn);
+    for (auto & b : f->ws) b.release();
+    delete f;
+}
+
+static int ffn_host(Ffn * f, const float * x, int64_t T, const int32_t * ids, int k, const float * w, float * y) {
+    if (!f->fused) return 0;
+    check_ids(ids, T * k, f->gu->E, "onpu_ffn_run");
+    std::lock_guard<std::mutex> lk(g_mu);
+    Timer tm;
+    const hipStream_t s = device().stream;
+    DBuf * b = f->ws + 7;
+    const int64_t n = T * k, Nd = f->dn->N;
+    HIPX(x_to_dev(b[0], b[1], x, T * f->gu->K, s));
+    HIPX(b[2].ensure((size_t) n * 8));
+    HIPX(hipMemcpyAsync(b[2].p, ids, (size_t) n * 4, hipMemcpyHostToDevice, s));
+    HIPX(hipMemcpyAsync(b[2].as<char>((size_t) n * 4), w, (size_t) n * 4, hipMemcpyHostToDevice, s));
+    HIPX(b[3].ensure((size_t) (T * Nd * 4)));
+    HIPX(ffn_core(f, b[1].as<uint16_t>(), T, b[2].as<int32_t>(), k, b[2].as<float>((size_t) n * 4), b[3].p, 1, s));
+    HIPX(hipMemcpyAsync(y, b[3].p, (size_t) (T * Nd * 4), hipMemcpyDeviceToHost, s));
+    HIPX(hipStreamSynchronize(s));
+    return 1;
+}
+
+int onpu_ffn_run(void * h, const float * x, const int32_t * ids, int k, const float * w, float * y) {
+    return ffn_host((Ffn *) h, x, 1, ids, k, w, y);
+}
+int onpu_ffn_run_many(void * h, const float * x, int64_t T, const int32_t * ids, int k, const float * w, float * y) {
+    return T > 0 ? ffn_host((Ffn *) h, x, T, ids, k, w, y) : 1;
+}
+
+int onpu_moe_route_dev(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
+                       void * stream) {
+    HIPR(launch_route(logits, T, E, k, renorm, ids, w, (hipStream_t) stream));
+    return 0;
+}
+
+int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, int k, const float * w, void * y,
+                     int y_f32, void * stream) {
+    auto * f = (Ffn *) h;
+    if (!f->fused) { set_err("onpu_moe_ffn_dev: this FFN shape has no fused path"); return -1; }
+    HIPR(ffn_core(f, (const uint16_t *) x, T, ids, k, w, y, y_f32, (hipStream_t) stream));
+    return 0;
+}
+
+// ---------------------------------------------------------------- packing
+int64_t onpu_pack(const float * W, int64_t N, int64_t K, int ncols, int sym, uint8_t * out, int threads) {
+    const RefGeom g = ref_geometry(N, K, ncols, sym != 0);
+    if (!g.ok || !fmt_valid(sym) || K % fmt_group(sym) != 0) return 0;
+    const int64_t sb = stage_bytes(sym, N, K);
+    if (sb > g.nbytes) return 0;
+    if (!pack_staging(sym, W, N, K, out, threads)) return 0;
+    std::memset(out + sb, 0, (size_t) (g.nbytes - sb));
+    return g.nbytes;
+}
+
+void onpu_quant_dequant(const float * W, int64_t N, int64_t K, int sym, float * out, int threads) {
+    if (!fmt_valid(sym) || K % fmt_group(sym) != 0) return;
+    std::vector<uint8_t> st((size_t) stage_bytes(sym, N, K));
+    pack_staging(sym, W, N, K, st.data(), threads);
+    dequant_staging(sym, st.data(), N, K, out, threads);
+}
+
+}  // extern "C"

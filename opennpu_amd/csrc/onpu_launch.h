@@ -1,0 +1,69 @@
+// Kernel argument blocks and launchers shared by onpu_kernels.hip and onpu_api.cpp.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// k_qgemv: y = x . deq(W)^T for M <= 64 rows of x, per slot (expert) and epilogue
+struct QArgs {
+    const uint8_t * W;        // tiled weights; expert e at W + e * estride
+    int64_t estride;
+    const int32_t * ids;      // expert of each slot (nullptr: one dense matrix)
+    int64_t N, K, NT, KB;
+    const uint16_t * x;       // bf16 rows; slot s reads x + (s / xdiv) * xslot, row stride ldx
+    int64_t ldx, xslot, xdiv;
+    int M;
+    void * y;                 // bf16 or fp32 (yf32); slot s writes y + s * yslot, row stride ldy
+    int64_t ldy, yslot;
+    int yf32;
+    const float * wslot;      // EPI_SLOTSUM: routing weights [tokens][nslot]
+    int nslot, ksplit;        // EPI_SLOTSUM: waves = nslot * ksplit
+    int64_t bpw;              // K blocks (128 wide) per wave
+};
+
+// k_qgemm: prefill, Y[M][N] = X[M][K] . deq(W)^T
+struct GArgs {
+    const uint8_t * W;
+    int64_t NT, KB, N, K, M;
+    const uint16_t * x;
+    int64_t ldx;
+    void * y;
+    int64_t ldy;
+    int yf32;
+};
+
+// grouped MoE products over a device work list (expert, first position, rows)
+struct MArgs {
+    const uint8_t * W;
+    int64_t estride, NT, KB, N, K;
+    const uint16_t * x;       // gate_up: token rows [T][K]; down: act rows in permuted order
+    int64_t ldx;
+    void * y;                 // gate_up: act bf16 [T*k][N/2]; down: fp32 [T*k][N]
+    int64_t ldy;
+    const int32_t * perm;     // permuted position -> entry t * k + j
+    const int32_t * items;    // [nitems][3]
+    const int32_t * nitems;
+    int k;
+    int64_t bpw;
+};
+
+hipError_t launch_repack(int fmt, const uint8_t * st, int64_t sstride, int64_t N, int64_t K, uint8_t * out,
+                         int64_t ostride, int64_t E, hipStream_t s);
+hipError_t launch_dequant(int fmt, const uint8_t * W, int64_t N, int64_t K, void * out, int bf16, hipStream_t s);
+hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, dim3 grid, int waves, hipStream_t s);
+hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
+hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
+                        hipStream_t s);
+hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_per_item, int32_t * off, int32_t * perm,
+                              int32_t * items, int32_t * nitems, hipStream_t s);
+hipError_t launch_moe_grouped(int fmt, int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s);
+hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
+hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
+                              void * y, int yf32, hipStream_t s);
+hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, hipStream_t s);
+hipError_t launch_f32_to_bf16(const float * in, int64_t n, uint16_t * out, hipStream_t s);
+hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * bias, int act,
+                          float alpha, float limit, float * o, hipStream_t s);
+hipError_t launch_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * ids, const float * w,
+                          const float * bias, float * y, hipStream_t s);
+
+enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };

@@ -1,0 +1,130 @@
+"""Device-resident operators over libonpu_hip's *_dev entry points, for callers holding torch
+tensors in HBM (tests, the benchmark, a serving loop). torch supplies device memory and the
+stream; every product is computed by the library's HIP kernels.
+
+  QMatrix   one int4 matrix (any format): mv (y = x W^T), argmax (LM head), dequant
+  QFfn      routed-expert FFN bank (gate_up + down): route, ffn
+"""
+import ctypes as C
+
+import numpy as np
+
+from ._lib import check, require_gpu
+
+
+def _stream():
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def _np_ptr(a):
+    return C.c_void_p(a.ctypes.data)
+
+
+class QMatrix:
+    """An [N][K] int4 matrix resident in HBM (tiled layout), loaded from staging bytes."""
+
+    def __init__(self, N, K, fmt, stage=None):
+        self.L = require_gpu()
+        self.N, self.K, self.fmt = int(N), int(K), int(fmt)
+        self.h = self.L.onpu_dense_new3(self.N, self.K, self.fmt)
+        if not self.h:
+            raise ValueError(f"unsupported matrix [{N}, {K}] fmt {fmt}")
+        if stage is not None:
+            self.load(stage)
+
+    def load(self, stage):
+        stage = np.ascontiguousarray(stage, np.uint8)
+        assert stage.size == self.L.onpu_stage_bytes(self.fmt, self.N, self.K)
+        check(self.L.onpu_dense_load(self.h, _np_ptr(stage)), "onpu_dense_load")
+
+    def mv(self, x, out=None, f32=False):
+        """x: bf16 cuda tensor [M][K] -> y [M][N] (bf16, or fp32 when f32)."""
+        import torch
+        assert x.dtype == torch.bfloat16 and x.is_cuda and x.is_contiguous() and x.shape[-1] == self.K
+        M = x.numel() // self.K
+        if out is None:
+            out = torch.empty((M, self.N), dtype=torch.float32 if f32 else torch.bfloat16, device=x.device)
+        check(self.L.onpu_dense_mv_dev(self.h, _ptr(x), M, _ptr(out), int(out.dtype == torch.float32), _stream()),
+              "onpu_dense_mv_dev")
+        return out
+
+    def argmax(self, x, logits=None, idx=None):
+        """LM head: fp32 logits [M][N] and their argmax [M] (int32)."""
+        import torch
+        M = x.numel() // self.K
+        if logits is None:
+            logits = torch.empty((M, self.N), dtype=torch.float32, device=x.device)
+        if idx is None:
+            idx = torch.empty((M,), dtype=torch.int32, device=x.device)
+        check(self.L.onpu_dense_argmax_dev(self.h, _ptr(x), M, _ptr(logits), _ptr(idx), _stream()),
+              "onpu_dense_argmax_dev")
+        return logits, idx
+
+    def dequant(self, bf16=False):
+        """Dequantized weights as the GPU holds them: fp32 [N][K] or bf16 bits (uint16)."""
+        out = np.empty((self.N, self.K), np.uint16 if bf16 else np.float32)
+        check(self.L.onpu_dense_dequant(self.h, 0, _np_ptr(out), int(bf16)), "onpu_dense_dequant")
+        return out
+
+    def info(self):
+        out = (C.c_int64 * 8)()
+        self.L.onpu_dense_info(self.h, out)
+        return tuple(out)
+
+    def free(self):
+        if self.h:
+            self.L.onpu_dense_free(self.h)
+            self.h = None
+
+
+class QFfn:
+    """E routed experts: gate_up [Ng = 2I][Kg] and down [Nd][Kd = I], one HBM pool each."""
+
+    def __init__(self, E, H, I, fmt, Nd=None):
+        self.L = require_gpu()
+        self.E, self.H, self.I, self.fmt = int(E), int(H), int(I), int(fmt)
+        self.Nd = int(Nd if Nd is not None else H)
+        self.h = self.L.onpu_ffn_new3(2 * self.I, self.H, self.Nd, self.I, self.E, self.fmt)
+        if not self.h:
+            raise ValueError("unsupported expert shapes")
+        self.gu = self.L.onpu_ffn_gu(self.h)
+        self.dn = self.L.onpu_ffn_dn(self.h)
+
+    def load(self, gu_stage, dn_stage, e0=0):
+        """gu_stage / dn_stage: n experts' staging bytes, concatenated."""
+        gu_stage = np.ascontiguousarray(gu_stage, np.uint8)
+        dn_stage = np.ascontiguousarray(dn_stage, np.uint8)
+        sg = self.L.onpu_stage_bytes(self.fmt, 2 * self.I, self.H)
+        n = gu_stage.size // sg
+        check(self.L.onpu_bank_load(self.gu, e0, n, _np_ptr(gu_stage)), "onpu_bank_load")
+        check(self.L.onpu_bank_load(self.dn, e0, n, _np_ptr(dn_stage)), "onpu_bank_load")
+
+    def route(self, logits, k, renorm=True):
+        """logits fp32 cuda [T][E] -> ids int32 [T][k], w fp32 [T][k]."""
+        import torch
+        T = logits.shape[0]
+        ids = torch.empty((T, k), dtype=torch.int32, device=logits.device)
+        w = torch.empty((T, k), dtype=torch.float32, device=logits.device)
+        check(self.L.onpu_moe_route_dev(_ptr(logits), T, logits.shape[1], k, int(renorm), _ptr(ids), _ptr(w),
+                                        _stream()), "onpu_moe_route_dev")
+        return ids, w
+
+    def ffn(self, x, ids, w, out=None, f32=False):
+        """x bf16 [T][H], ids/w [T][k] -> y [T][Nd] = sum_j w_j down_e(silu(gate_e x) * up_e x)."""
+        import torch
+        T, k = ids.shape
+        if out is None:
+            out = torch.empty((T, self.Nd), dtype=torch.float32 if f32 else torch.bfloat16, device=x.device)
+        check(self.L.onpu_moe_ffn_dev(self.h, _ptr(x), T, _ptr(ids), k, _ptr(w), _ptr(out),
+                                      int(out.dtype == torch.float32), _stream()), "onpu_moe_ffn_dev")
+        return out
+
+    def free(self):
+        if self.h:
+            self.L.onpu_ffn_free(self.h)
+            self.h = None

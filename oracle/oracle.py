@@ -1,0 +1,246 @@
+"""ORACLE — test infrastructure only.
+
+Python access to the C restatement in oracle/oracle.c (built by oracle/Makefile into
+oracle/_build/liboracle.so) plus numpy restatements used beside it. Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker: nothing in the product path calls it.
+
+Each function cites the reference file:line it restates; tests/test_oracle.py pins each one
+against library routines, closed forms, invariants or brute force (see oracle.c's header).
+"""
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "liboracle.so"
+
+FMT_Q4NX, FMT_Q4S, FMT_G128S, FMT_Q4_0 = 0, 1, 2, 3
+_lib = None
+
+
+def build():
+    """Compile oracle.c (gcc) into oracle/_build/liboracle.so."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        P, I64, I32 = C.c_void_p, C.c_int64, C.c_int
+        L.orc_f2bf.restype, L.orc_f2bf.argtypes = C.c_uint16, [C.c_float]
+        L.orc_bf2f.restype, L.orc_bf2f.argtypes = C.c_float, [C.c_uint16]
+        L.orc_h2f.restype, L.orc_h2f.argtypes = C.c_float, [C.c_uint16]
+        L.orc_group.restype, L.orc_group.argtypes = I64, [I32]
+        L.orc_stage_bytes.restype, L.orc_stage_bytes.argtypes = I64, [I32, I64, I64]
+        L.orc_unpack.argtypes = [I32, P, I64, I64, P]
+        L.orc_dequant.argtypes = [I32, P, I64, I64, P]
+        L.orc_dequant_bf16.argtypes = [I32, P, I64, I64, P]
+        L.orc_qmm_rows.argtypes = [I32, P, I64, I64, P, I64, I64, I64, P]
+        L.orc_matmul_f64.argtypes = [P, I64, I64, P, I64, P]
+        L.orc_route.argtypes = [P, I64, I32, I32, I32, P, P]
+        L.orc_silu_mul.argtypes = [P, I64, I64, P]
+        L.orc_gptoss_act.argtypes = [P, I64, I64, C.c_float, C.c_float, P]
+        L.orc_moe_sum.argtypes = [P, I64, I32, I64, P, P, P, P]
+        L.orc_argmax.argtypes = [P, I64, I64, P]
+        L.orc_geometry.argtypes = [I64, I64, I32, I32, P]
+        L.orc_quant_sym32.argtypes = [P, P, P]
+        L.orc_quant_asym32.argtypes = [P, P, P, P]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ------------------------------------------------------------------ scalars
+def f2bf(x):
+    """float32 array -> bf16 bit patterns (uint16), RNE (opennpu_core.hpp:50-56)."""
+    x = np.ascontiguousarray(x, np.float32)
+    return np.fromiter((lib().orc_f2bf(float(v)) for v in x.ravel()), np.uint16, x.size).reshape(x.shape)
+
+
+def f2bf_np(x):
+    """The same RNE rounding vectorised in numpy (used for large arrays)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 64).astype(np.uint16), r)
+
+
+def bf2f(h):
+    """bf16 bits -> float32 (opennpu_core.hpp:57-62)."""
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ------------------------------------------------------------------ formats
+def group(fmt):
+    return 128 if fmt == FMT_G128S else 32
+
+
+def stage_bytes(fmt, N, K):
+    return int(lib().orc_stage_bytes(fmt, N, K))
+
+
+def unpack(fmt, st, N, K):
+    """Stored codes u [N][K] (uint8 0..15)."""
+    out = np.empty((N, K), np.uint8)
+    lib().orc_unpack(fmt, _p(np.ascontiguousarray(st)), N, K, _p(out))
+    return out
+
+
+def dequant(fmt, st, N, K):
+    """fp32 dequantized weights [N][K] (onpu_api.cpp:508-529 semantics)."""
+    out = np.empty((N, K), np.float32)
+    lib().orc_dequant(fmt, _p(np.ascontiguousarray(st)), N, K, _p(out))
+    return out
+
+
+def dequant_bf16(fmt, st, N, K):
+    """bf16 (RNE) of the dequantized weights, as bit patterns [N][K] (gemv_any.cc:65,106-107)."""
+    out = np.empty((N, K), np.uint16)
+    lib().orc_dequant_bf16(fmt, _p(np.ascontiguousarray(st)), N, K, _p(out))
+    return out
+
+
+def qmm(fmt, st, N, K, xb, n0=0, n1=None):
+    """fp64 y[M][n1-n0] = x . dequant(W)^T for rows [n0, n1) (reference.py:24-28,55 pattern,
+    accumulated in fp64). xb: bf16 bits [M][K]."""
+    n1 = N if n1 is None else n1
+    xb = np.ascontiguousarray(xb, np.uint16).reshape(-1, K)
+    M = xb.shape[0]
+    y = np.empty((M, n1 - n0), np.float64)
+    lib().orc_qmm_rows(fmt, _p(np.ascontiguousarray(st)), N, K, _p(xb), M, n0, n1, _p(y))
+    return y
+
+
+def matmul_f64(W, x):
+    """fp64 brute force y[M][N] = x[M][K] . W[N][K]^T (W float32, x float64)."""
+    W = np.ascontiguousarray(W, np.float32)
+    x = np.ascontiguousarray(x, np.float64)
+    N, K = W.shape
+    M = x.shape[0]
+    y = np.empty((M, N), np.float64)
+    lib().orc_matmul_f64(_p(W), N, K, _p(x), M, _p(y))
+    return y
+
+
+def qmm_f32_torch(fmt, st, N, K, xb):
+    """The reference's own CPU pattern: dequantize W to fp32, then x @ W.T in torch fp32
+    (opennpu/native/reference.py:24-28,55). Used as the cpu_baseline workload."""
+    import torch
+    W = torch.from_numpy(dequant(fmt, st, N, K))
+    x = torch.from_numpy(bf2f(xb).reshape(-1, K))
+    return (x @ W.T).numpy()
+
+
+# ------------------------------------------------------------------ MoE pieces
+def route(logits, k, renorm=True):
+    """softmax -> top-k -> renorm (moe_runtime.py:333-341, reference.py:72-76); ties to the lower id."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    lib().orc_route(_p(logits), T, E, k, int(renorm), _p(ids), _p(w))
+    return ids, w
+
+
+def silu_mul(h):
+    """act 0: silu(h[:, :I]) * h[:, I:] in fp32 (onpu_cpu.cpp:253)."""
+    h = np.ascontiguousarray(h, np.float32)
+    rows, Ng = h.shape
+    a = np.empty((rows, Ng // 2), np.float32)
+    lib().orc_silu_mul(_p(h), rows, Ng, _p(a))
+    return a
+
+
+def gptoss_act(h, alpha, limit):
+    """act 1 (onpu_cpu.cpp:245-250)."""
+    h = np.ascontiguousarray(h, np.float32)
+    rows, Ng = h.shape
+    a = np.empty((rows, Ng // 2), np.float32)
+    lib().orc_gptoss_act(_p(h), rows, Ng, alpha, limit, _p(a))
+    return a
+
+
+def moe_sum(o, ids, w, bias=None):
+    """y[t] = sum_j w[t,j] (o[t,j] + bias[ids[t,j]]) (onpu_cpu.cpp:259-274). o: [T][k][N]."""
+    o = np.ascontiguousarray(o, np.float32)
+    T, k, N = o.shape
+    y = np.empty((T, N), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_moe_sum(_p(o), T, k, N, _p(np.ascontiguousarray(ids, np.int32)),
+                      _p(np.ascontiguousarray(w, np.float32)), None if b is None else _p(b), _p(y))
+    return y
+
+
+def argmax(v):
+    """first maximum per row (engine.py:358)."""
+    v = np.ascontiguousarray(v, np.float32)
+    rows, N = v.shape
+    out = np.empty(rows, np.int32)
+    lib().orc_argmax(_p(v), rows, N, _p(out))
+    return out
+
+
+def moe_layer(fmt, gu_st, dn_st, E, H, I, x_bf, ids, w):
+    """A routed-expert FFN layer as reference.py:71-84 computes it (dequantized experts, fp32 act),
+    with the two rounding points of the device path: gate_up in fp64 -> fp32, act -> bf16 RNE as the
+    down input (the device input conversion, opennpu_core.hpp:418-424), down in fp64, weighted sum.
+    gu_st / dn_st: E staging blobs; returns y [T][H] float64."""
+    T, k = ids.shape
+    y = np.zeros((T, H), np.float64)
+    xb = np.asarray(x_bf, np.uint16).reshape(T, H)
+    for e in np.unique(ids):
+        rows, slots = np.nonzero(ids == e)
+        g = qmm(fmt, gu_st[e], 2 * I, H, xb[rows]).astype(np.float32)
+        a = f2bf_np(silu_mul(g))
+        d = qmm(fmt, dn_st[e], H, I, a)
+        y[rows] += w[rows, slots][:, None].astype(np.float64) * d
+    return y
+
+
+# ------------------------------------------------------------------ geometry / quantizers
+def geometry(N, K, ncols, sym):
+    """Reference Mat geometry (model.py:151-187): R, S, tiles, kc, ks, rows_col, cb, nbytes."""
+    out = np.zeros(8, np.int64)
+    lib().orc_geometry(N, K, ncols, int(sym), _p(out))
+    return tuple(int(v) for v in out)
+
+
+def quant_sym32(x):
+    """q4s search quantizer for 32 weights (opennpu_core.hpp:142-169): (codes, bf16 d bits)."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(32, np.uint8)
+    d = np.zeros(1, np.uint16)
+    lib().orc_quant_sym32(_p(x), _p(q), _p(d))
+    return q, int(d[0])
+
+
+def quant_asym32(x):
+    """q4nx search quantizer for 32 weights (opennpu_core.hpp:103-138): (codes, s bits, m bits)."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(32, np.uint8)
+    s = np.zeros(1, np.uint16)
+    m = np.zeros(1, np.uint16)
+    lib().orc_quant_asym32(_p(x), _p(q), _p(s), _p(m))
+    return q, int(s[0]), int(m[0])
+
+
+def max_rel_err(y, r):
+    """max|y - r| / max|r| (the tolerance BASELINE states; offload.py:313-315 reports rel-L2)."""
+    y = np.asarray(y, np.float64)
+    r = np.asarray(r, np.float64)
+    return float(np.abs(y - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+if __name__ == "__main__":
+    build()
+    print("oracle built:", LIB, os.path.getsize(LIB), "bytes")

@@ -1,0 +1,143 @@
+"""GPU parity of the dense int4 path (decode GEMV family, prefill GEMM, LM head) against the oracle.
+
+The product is called through libonpu_hip's C ABI (opennpu_amd.device wraps the *_dev entry
+points); the oracle is oracle/oracle.c (fp64 dequantize-then-matmul of reference.py:24-28,55).
+Tolerances: bf16 outputs max|y-r|/max|r| <= 1e-2 and per element within the bf16 rounding bound
+(conftest.check_bf16_out); fp32 logits <= 1e-3 (and <= 1e-4 observed bound).
+"""
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+from opennpu_amd import synthetic as syn
+from tests.conftest import check_bf16_out, check_f32_out, from_torch, to_torch_bf16
+
+pytestmark = pytest.mark.gpu
+FMTS = [orc.FMT_Q4NX, orc.FMT_Q4S, orc.FMT_G128S, orc.FMT_Q4_0]
+
+
+def _mv(fmt, N, K, M, seed, f32=False):
+    from opennpu_amd.device import QMatrix
+    st = syn.weights(fmt, N, K, seed)
+    xb = syn.activations(M, K, seed + 7919)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        y = from_torch(q.mv(to_torch_bf16(xb).reshape(M, K), f32=f32))
+    finally:
+        q.free()
+    return st, xb, y
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_bit_exact(gpu, fmt):
+    """unpack + dequant in HBM layout == the reference's dequant, bit for bit (fp32 and bf16 RNE)."""
+    from opennpu_amd.device import QMatrix
+    for (N, K) in [(48, 256), (37, 384), (16, 2048)] + ([] if fmt == orc.FMT_G128S else [(21, 160)]):
+        st = syn.weights(fmt, N, K, 11 + N)
+        q = QMatrix(N, K, fmt, st)
+        try:
+            w = q.dequant()
+            wb = q.dequant(bf16=True)
+        finally:
+            q.free()
+        ref = orc.dequant(fmt, st, N, K)
+        assert np.array_equal(w.view(np.uint32), ref.view(np.uint32)), (fmt, N, K)
+        assert np.array_equal(wb, orc.dequant_bf16(fmt, st, N, K)), (fmt, N, K)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16, 17, 33, 64])
+def test_gemv_small(gpu, fmt, M):
+    for (N, K) in [(16, 128), (72, 512), (300, 1024)] + ([] if fmt == orc.FMT_G128S else [(129, 2080)]):
+        st, xb, y = _mv(fmt, N, K, M, 100 * M + N)
+        check_bf16_out(y, orc.qmm(fmt, st, N, K, xb), what=f"fmt {fmt} N {N} K {K} M {M}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("name,N,K", [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096),
+                                      ("down", 4096, 12288)])
+def test_gemv_qwen3_8b(gpu, name, N, K, M):
+    """Qwen3-8B decode layer shapes (g128s), every output row against the oracle."""
+    st, xb, y = _mv(orc.FMT_G128S, N, K, M, 1 + K + N)
+    check_bf16_out(y, orc.qmm(orc.FMT_G128S, st, N, K, xb), what=f"{name} M {M}")
+
+
+def test_gemv_config0(gpu):
+    """M=1, K=N=4096 g128s, seed 0."""
+    st, xb, y = _mv(orc.FMT_G128S, 4096, 4096, 1, 0)
+    check_bf16_out(y, orc.qmm(orc.FMT_G128S, st, 4096, 4096, xb), what="config0")
+
+
+def test_gemv_fp32_out(gpu):
+    st, xb, y = _mv(orc.FMT_Q4S, 520, 1024, 3, 5, f32=True)
+    check_f32_out(y, orc.qmm(orc.FMT_Q4S, st, 520, 1024, xb))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M", [65, 130, 256])
+def test_gemm_ragged(gpu, fmt, M):
+    """prefill GEMM path (M > 64), ragged M and N."""
+    N, K = 200, 640 if fmt != orc.FMT_G128S else 768
+    st, xb, y = _mv(fmt, N, K, M, 3 * M)
+    check_bf16_out(y, orc.qmm(fmt, st, N, K, xb), what=f"gemm fmt {fmt} M {M}")
+
+
+@pytest.mark.parametrize("name,N,K", [("up", 14336, 4096), ("down", 4096, 14336)])
+def test_gemm_llama_ffn(gpu, name, N, K):
+    """Llama-3.1-8B FFN prefill at M=2048: all rows of a 128-column slice plus 48 full rows."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    M = 2048
+    st = syn.weights(orc.FMT_G128S, N, K, 17)
+    xb = syn.activations(M, K, 18)
+    q = QMatrix(N, K, orc.FMT_G128S, st)
+    try:
+        y = q.mv(to_torch_bf16(xb).reshape(M, K))
+        torch.cuda.synchronize()
+        yc = from_torch(y[:, 1000:1128])
+        rows = np.random.default_rng(0).choice(M, 48, replace=False)
+        yr = from_torch(y[torch.as_tensor(rows, device=y.device)])
+    finally:
+        q.free()
+    check_bf16_out(yc, orc.qmm(orc.FMT_G128S, st, N, K, xb, 1000, 1128), what=f"{name} column slice")
+    check_bf16_out(yr, orc.qmm(orc.FMT_G128S, st, N, K, xb[rows]), what=f"{name} rows")
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_lm_head_q4_0(gpu, M):
+    """151936 x 4096 GGUF Q4_0 LM head: fp32 logits and argmax (first maximum)."""
+    from opennpu_amd.device import QMatrix
+    N, K = 151936, 4096
+    st = syn.weights(orc.FMT_Q4_0, N, K, 4)
+    xb = syn.activations(M, K, 5 + M)
+    q = QMatrix(N, K, orc.FMT_Q4_0, st)
+    try:
+        lg, idx = q.argmax(to_torch_bf16(xb).reshape(M, K))
+        lg, idx = from_torch(lg), idx.cpu().numpy()
+    finally:
+        q.free()
+    ref = orc.qmm(orc.FMT_Q4_0, st, N, K, xb)
+    check_f32_out(lg, ref, what="lm head")
+    assert np.array_equal(idx, orc.argmax(lg)), "argmax of the returned logits"
+    top2 = np.sort(ref, axis=1)[:, -2:]
+    for m in range(M):
+        if top2[m, 1] - top2[m, 0] > 1e-3 * np.abs(ref).max():
+            assert idx[m] == int(np.argmax(ref[m])), f"row {m}"
+
+
+def test_rows_zero_and_reuse(gpu):
+    """M = 0 is a no-op; one handle serves several calls with different M."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    N, K = 64, 256
+    st = syn.weights(orc.FMT_G128S, N, K, 9)
+    q = QMatrix(N, K, orc.FMT_G128S, st)
+    try:
+        out = torch.zeros((1, N), dtype=torch.bfloat16, device="cuda")
+        q.mv(torch.zeros((0, K), dtype=torch.bfloat16, device="cuda"), out=out[:0])
+        for M in (3, 1, 9):
+            xb = syn.activations(M, K, M)
+            y = from_torch(q.mv(to_torch_bf16(xb).reshape(M, K)))
+            check_bf16_out(y, orc.qmm(orc.FMT_G128S, st, N, K, xb), what=f"M {M}")
+    finally:
+        q.free()

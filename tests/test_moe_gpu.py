@@ -1,0 +1,83 @@
+"""GPU parity of the MoE path (router, permutation + grouped products, fused decode FFN) against
+the oracle's restatement of reference.py:71-84 (softmax -> top-k -> renorm, dequantized experts,
+silu(gate) * up, weighted sum), with the device path's rounding point (act -> bf16)."""
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+from opennpu_amd import synthetic as syn
+from tests.conftest import check_bf16_out, from_torch, to_torch_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _experts(fmt, E, H, I, seed):
+    gu = [syn.weights(fmt, 2 * I, H, seed + 2 * e) for e in range(E)]
+    dn = [syn.weights(fmt, H, I, seed + 2 * e + 1) for e in range(E)]
+    return gu, dn
+
+
+def _ffn(fmt, E, H, I, gu, dn):
+    from opennpu_amd.device import QFfn
+    f = QFfn(E, H, I, fmt)
+    f.load(np.concatenate(gu), np.concatenate(dn))
+    return f
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 128, 8), (7, 64, 4), (512, 128, 8), (33, 16, 2)])
+def test_route(gpu, T, E, k):
+    import torch
+    from opennpu_amd.device import QFfn
+    lg = syn.logits(T, E, T + E)
+    f = QFfn(2, 128, 128, orc.FMT_G128S)          # any handle: routing needs no weights
+    try:
+        ids, w = f.route(torch.from_numpy(lg).cuda(), k)
+        ids, w = ids.cpu().numpy(), w.cpu().numpy()
+    finally:
+        f.free()
+    rid, rw = orc.route(lg, k)
+    assert np.array_equal(ids, rid)
+    np.testing.assert_allclose(w, rw, rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+
+
+@pytest.mark.parametrize("fmt", [orc.FMT_G128S, orc.FMT_Q4S, orc.FMT_Q4NX])
+@pytest.mark.parametrize("T", [1, 3, 8, 40])
+def test_moe_ffn_small(gpu, fmt, T):
+    """decode (T <= 4: fused gate_up/act + down/slot sum) and grouped (T > 4) paths."""
+    import torch
+    E, H, I, k = 16, 256, 128, 4
+    gu, dn = _experts(fmt, E, H, I, 1000 + T)
+    xb = syn.activations(T, H, T)
+    rid, rw = orc.route(syn.logits(T, E, 5 + T), k)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        y = f.ffn(to_torch_bf16(xb).reshape(T, H), torch.from_numpy(rid).cuda(), torch.from_numpy(rw).cuda())
+        y = from_torch(y)
+    finally:
+        f.free()
+    ref = orc.moe_layer(fmt, gu, dn, E, H, I, xb, rid, rw)
+    check_bf16_out(y, ref, what=f"moe fmt {fmt} T {T}", floor=2e-4)
+
+
+@pytest.mark.parametrize("T,check_tokens", [(1, 1), (512, 24)])
+def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
+    """128 experts, H=2048, I=768, top-8 (router on device), g128s; a subset of tokens checked."""
+    import torch
+    E, H, I, k = 128, 2048, 768, 8
+    fmt = orc.FMT_G128S
+    gu, dn = _experts(fmt, E, H, I, 77)
+    xb = syn.activations(T, H, 78)
+    lg = syn.logits(T, E, 79)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        ids, w = f.route(torch.from_numpy(lg).cuda(), k)
+        y = from_torch(f.ffn(to_torch_bf16(xb).reshape(T, H), ids, w))
+        ids, w = ids.cpu().numpy(), w.cpu().numpy()
+    finally:
+        f.free()
+    rid, rw = orc.route(lg, k)
+    assert np.array_equal(ids, rid)
+    tok = np.random.default_rng(1).choice(T, check_tokens, replace=False)
+    ref = orc.moe_layer(fmt, gu, dn, E, H, I, xb[tok], rid[tok], rw[tok])
+    check_bf16_out(y[tok], ref, what=f"qwen3-30b-a3b T {T}", floor=2e-4)
