@@ -135,12 +135,16 @@ void orc_dequant_bf16(int fmt, const uint8_t * st, int64_t N, int64_t K, uint16_
  * x is bf16 (the device input is bf16 RNE of the fp32 activations, opennpu_core.hpp:418-424).
  * Rows [n0, n1) only, so callers can check a slice of a very large matrix. */
 void orc_qmm_rows(int fmt, const uint8_t * st, int64_t N, int64_t K, const uint16_t * xb, int64_t M,
-                  int64_t n0, int64_t n1, double * y /* [M][n1-n0] */) {
+                  int64_t n0, int64_t n1, double * y /* [M][n1-n0] */, int bf16w) {
+    /* bf16w: the weights the device's bf16 MAC sees, RNE of the dequant (gemv_any.cc:65,106-107) */
     double * xd = (double *) malloc(sizeof(double) * (size_t) (M * K));
     float * w = (float *) malloc(sizeof(float) * (size_t) K);
     for (int64_t i = 0; i < M * K; i++) xd[i] = (double) orc_bf2f(xb[i]);
     for (int64_t n = n0; n < n1; n++) {
-        for (int64_t k = 0; k < K; k++) w[k] = wq_at(fmt, st, N, K, n, k);
+        for (int64_t k = 0; k < K; k++) {
+            w[k] = wq_at(fmt, st, N, K, n, k);
+            if (bf16w) w[k] = orc_bf2f(orc_f2bf(w[k]));
+        }
         for (int64_t m = 0; m < M; m++) {
             const double * xr = xd + m * K;
             double acc = 0.0;

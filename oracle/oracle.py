@@ -42,7 +42,7 @@ def lib():
         L.orc_unpack.argtypes = [I32, P, I64, I64, P]
         L.orc_dequant.argtypes = [I32, P, I64, I64, P]
         L.orc_dequant_bf16.argtypes = [I32, P, I64, I64, P]
-        L.orc_qmm_rows.argtypes = [I32, P, I64, I64, P, I64, I64, I64, P]
+        L.orc_qmm_rows.argtypes = [I32, P, I64, I64, P, I64, I64, I64, P, I32]
         L.orc_matmul_f64.argtypes = [P, I64, I64, P, I64, P]
         L.orc_route.argtypes = [P, I64, I32, I32, I32, P, P]
         L.orc_silu_mul.argtypes = [P, I64, I64, P]
@@ -110,14 +110,15 @@ def dequant_bf16(fmt, st, N, K):
     return out
 
 
-def qmm(fmt, st, N, K, xb, n0=0, n1=None):
+def qmm(fmt, st, N, K, xb, n0=0, n1=None, bf16w=False):
     """fp64 y[M][n1-n0] = x . dequant(W)^T for rows [n0, n1) (reference.py:24-28,55 pattern,
-    accumulated in fp64). xb: bf16 bits [M][K]."""
+    accumulated in fp64). xb: bf16 bits [M][K]. bf16w: with the weights rounded to bf16 (RNE) as the
+    reference device's MAC sees them (gemv_any.cc:65,106-107)."""
     n1 = N if n1 is None else n1
     xb = np.ascontiguousarray(xb, np.uint16).reshape(-1, K)
     M = xb.shape[0]
     y = np.empty((M, n1 - n0), np.float64)
-    lib().orc_qmm_rows(fmt, _p(np.ascontiguousarray(st)), N, K, _p(xb), M, n0, n1, _p(y))
+    lib().orc_qmm_rows(fmt, _p(np.ascontiguousarray(st)), N, K, _p(xb), M, n0, n1, _p(y), int(bf16w))
     return y
 
 
