@@ -1,0 +1,328 @@
+"""Benchmark of the int4 weight-only matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+
+Headline workload (one "step"): the int4 weight stream of one Qwen3-8B decode token, i.e. the 36
+layers' g128s GEMVs at M=1: fused QKV 6144x4096, o 4096x4096, fused gate+up 24576x4096 and down
+4096x12288, each layer with its own HBM copy of the weights (3.58 GB per step, far above the
+256 MB Infinity Cache). The step is captured once in a HIP graph and replayed. value = algorithmic
+bytes per step (int4 codes + bf16 scales + x + y) / time, in GB/s.
+
+Also measured in the same run (the "configs" object): M=4 and M=8 decode steps, a single
+4096x4096 GEMV rotated over 64 copies, the Llama-3.1-8B prefill FFN GEMMs (M=2048, TFLOPS), the
+Qwen3-30B-A3B MoE layer (decode M=1 and prefill M=512, router included), and the 151936x4096
+Q4_0 LM head with argmax (M=1, 5). The roofline object is the dominant kernel: the gate+up GEMV,
+timed with HIP events over a graph of back-to-back launches on its stream. The cpu_baseline leg
+times the reference's own CPU pattern (dequantize to fp32, then x @ W^T in torch fp32,
+opennpu/native/reference.py:24-28,55) on one layer of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "int4 GEMV HBM GB/s (% peak) + prefill GEMM TFLOPS at 8B / 30B-A3B shapes"
+HBM_PEAK = 8.0e12            # MI355X HBM3E, B/s
+BF16_PEAK = 2.5e15           # MI355X dense bf16 MFMA, flop/s
+G128S, Q4_0 = 2, 3
+LAYERS = 36                  # Qwen3-8B
+QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def wbytes(fmt, N, K):
+    """algorithmic weight bytes: int4 codes + scales"""
+    if fmt == Q4_0:
+        return N * (K // 32) * 18
+    return N * K // 2 + N * (K // 128) * 2
+
+
+class GraphStep:
+    """A list of launches captured in one HIP graph (falls back to eager launches)."""
+
+    def __init__(self, fn, torch):
+        self.torch, self.fn = torch, fn
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()                              # warm: first launches load the code object
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.g = None
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            self.g = g
+        except Exception as e:  # noqa: BLE001 - eager launches still measure the kernels
+            log(f"graph capture failed ({e}); timing eager launches")
+        self.mode = "hip_graph" if self.g is not None else "eager"
+
+    def __call__(self):
+        if self.g is not None:
+            self.g.replay()
+        else:
+            self.fn()
+
+
+def time_it(torch, step, iters, warmup):
+    """mean seconds per call of step(), HIP events on the current stream"""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / iters
+
+
+def bf16_tensor(torch, bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+# ------------------------------------------------------------------ workloads
+def decode_layers(torch, QMatrix, syn, Ms, steps, warmup):
+    """the headline step at each M; returns {M: result} and the gate+up roofline measurement"""
+    mats = {}
+    for name, N, K in QWEN3_8B:
+        st = syn.weights(G128S, N, K, 100 + N + K)
+        mats[name] = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
+        del st
+    res, graphs = {}, {}
+    for M in Ms:
+        xs = {K: bf16_tensor(torch, syn.activations(M, K, K + M)).reshape(M, K) for K in (4096, 12288)}
+        ys = {name: torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for name, N, _ in QWEN3_8B}
+
+        def step(M=M, xs=xs, ys=ys):
+            for layer in range(LAYERS):
+                for name, N, K in QWEN3_8B:
+                    mats[name][layer].mv(xs[K], out=ys[name])
+
+        g = GraphStep(step, torch)
+        # the graph's outputs equal eager launches' (last layer's gate+up)
+        g()
+        torch.cuda.synchronize()
+        y_graph = ys["gate_up"].clone()
+        mats["gate_up"][LAYERS - 1].mv(xs[4096], out=ys["gate_up"])
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, ys["gate_up"]), "graph replay differs from eager launches"
+        t = time_it(torch, g, steps, warmup)
+        byts = LAYERS * sum(wbytes(G128S, N, K) + M * K * 2 + M * N * 2 for _, N, K in QWEN3_8B)
+        res[M] = {"ms_per_step": t * 1e3, "GBps": byts / t / 1e9, "hbm_frac": byts / t / HBM_PEAK,
+                  "bytes_per_step": byts, "tokens_per_s_equiv": M / t, "launch": g.mode}
+        # per-matrix kernels: a graph of the 36 copies of each matrix, back to back
+        per = {}
+        for name, N, K in QWEN3_8B:
+            def one(name=name, K=K):
+                for layer in range(LAYERS):
+                    mats[name][layer].mv(xs[K], out=ys[name])
+            gm = GraphStep(one, torch)
+            tm = time_it(torch, gm, max(20, steps // 2), 3) / LAYERS
+            b1 = wbytes(G128S, N, K) + M * K * 2 + M * N * 2
+            per[name] = {"us": tm * 1e6, "GBps": b1 / tm / 1e9, "hbm_frac": b1 / tm / HBM_PEAK, "bytes": b1}
+        res[M]["per_matrix"] = per
+        graphs[M] = g
+    for v in mats.values():
+        for q in v:
+            q.free()
+    return res
+
+
+def config0(torch, QMatrix, syn, iters):
+    N = K = 4096
+    st = syn.weights(G128S, N, K, 0)
+    copies = [QMatrix(N, K, G128S, st) for _ in range(64)]     # 555 MB rotation
+    x = bf16_tensor(torch, syn.activations(1, K, 1)).reshape(1, K)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        for q in copies:
+            q.mv(x, out=y)
+    g = GraphStep(step, torch)
+    t = time_it(torch, g, iters, 3) / len(copies)
+    b = wbytes(G128S, N, K) + K * 2 + N * 2
+    for q in copies:
+        q.free()
+    return {"us_per_call": t * 1e6, "GBps": b / t / 1e9, "hbm_frac": b / t / HBM_PEAK, "bytes": b}
+
+
+def prefill(torch, QMatrix, syn, iters):
+    out = {}
+    M = 2048
+    for name, N, K in [("up", 14336, 4096), ("down", 4096, 14336)]:
+        q = QMatrix(N, K, G128S, syn.weights(G128S, N, K, 7))
+        x = bf16_tensor(torch, syn.activations(M, K, 8)).reshape(M, K)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        g = GraphStep(lambda: q.mv(x, out=y), torch)
+        t = time_it(torch, g, iters, 3)
+        fl = 2.0 * M * N * K
+        out[name] = {"us_per_call": t * 1e6, "TFLOPS": fl / t / 1e12, "mfma_frac": fl / t / BF16_PEAK}
+        q.free()
+    return out
+
+
+def moe(torch, QFfn, syn, iters):
+    E, H, I, k = 128, 2048, 768, 8
+    gu = np.concatenate([syn.weights(G128S, 2 * I, H, 300 + e) for e in range(E)])
+    dn = np.concatenate([syn.weights(G128S, H, I, 600 + e) for e in range(E)])
+    nl = 4                                                   # 4 layers x 311 MB rotation
+    ffns = []
+    for _ in range(nl):
+        f = QFfn(E, H, I, G128S)
+        f.load(gu, dn)
+        ffns.append(f)
+    per_expert = wbytes(G128S, 2 * I, H) + wbytes(G128S, H, I)
+    out = {}
+    for T in (1, 512):
+        lg = torch.from_numpy(syn.logits(T, E, 9)).cuda()
+        x = bf16_tensor(torch, syn.activations(T, H, 10)).reshape(T, H)
+        y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        ids, _ = ffns[0].route(lg, k)
+        hit = len(np.unique(ids.cpu().numpy()))
+
+        def step(lg=lg, x=x, y=y):
+            for f in ffns:
+                i, w = f.route(lg, k)
+                f.ffn(x, i, w, out=y)
+        g = GraphStep(step, torch)
+        t = time_it(torch, g, iters, 3) / nl
+        byts = hit * per_expert + T * H * 2 * 2 + T * E * 4
+        fl = 2.0 * T * k * (2 * I * H + H * I)
+        out[f"M{T}"] = {"us_per_layer": t * 1e6, "GBps": byts / t / 1e9, "hbm_frac": byts / t / HBM_PEAK,
+                        "TFLOPS": fl / t / 1e12, "mfma_frac": fl / t / BF16_PEAK, "experts_hit": hit,
+                        "tokens_per_s": T / t}
+    for f in ffns:
+        f.free()
+    return out
+
+
+def lm_head(torch, QMatrix, syn, iters):
+    N, K = 151936, 4096
+    st = syn.weights(Q4_0, N, K, 11)
+    copies = [QMatrix(N, K, Q4_0, st) for _ in range(2)]      # 700 MB rotation
+    out = {}
+    for M in (1, 5):
+        x = bf16_tensor(torch, syn.activations(M, K, 12)).reshape(M, K)
+        lg = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        idx = torch.empty((M,), dtype=torch.int32, device="cuda")
+
+        def step(x=x, lg=lg, idx=idx):
+            for q in copies:
+                q.argmax(x, lg, idx)
+        g = GraphStep(step, torch)
+        t = time_it(torch, g, iters, 3) / len(copies)
+        b = wbytes(Q4_0, N, K) + M * K * 2 + M * N * 4
+        out[f"M{M}"] = {"us_per_call": t * 1e6, "GBps": b / t / 1e9, "hbm_frac": b / t / HBM_PEAK}
+    for q in copies:
+        q.free()
+    return out
+
+
+def cpu_baseline(syn, seconds=12.0):
+    """The reference's CPU pattern on one Qwen3-8B layer at M=1: dequantize W to fp32 (timed once),
+    then x @ W^T in torch fp32 (timed, repeated for about `seconds`)."""
+    import torch
+    import oracle.oracle as orc
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    Ws, xs, wb = [], [], 0
+    t0 = time.perf_counter()
+    for name, N, K in QWEN3_8B:
+        st = syn.weights(G128S, N, K, 100 + N + K)
+        Ws.append(torch.from_numpy(orc.dequant(G128S, st, N, K)))
+        xs.append(torch.from_numpy(orc.bf2f(syn.activations(1, K, K + 1)).reshape(1, K)))
+        wb += wbytes(G128S, N, K) + K * 2 + N * 2
+    t_deq = time.perf_counter() - t0
+    for W, x in zip(Ws, xs):
+        (x @ W.T)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for W, x in zip(Ws, xs):
+            (x @ W.T)
+        reps += 1
+        if time.perf_counter() - t0 > seconds:
+            break
+    t = (time.perf_counter() - t0) / reps
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": wb / t / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"one Qwen3-8B layer (4 g128s matrices, {wb / 1e6:.1f} MB int4+scales), M=1: "
+                       f"torch fp32 x @ W^T on pre-dequantized weights, {reps} reps in {reps * t:.1f} s; "
+                       f"{t * 1e3:.2f} ms/layer ({t * LAYERS * 1e3:.0f} ms per 36-layer step); "
+                       f"dequant of the layer outside the timed region took {t_deq:.2f} s (oracle C, 1 thread)"),
+            "cpu_model": cpu}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="headline step only (no extra configs, no CPU leg)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the int4 path on a single MI355X; --gpus {args.gpus} "
+              "is not supported (see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from opennpu_amd import require_gpu, synthetic as syn
+    from opennpu_amd.device import QFfn, QMatrix
+    require_gpu()
+    torch.cuda.set_device(0)
+    t_all = time.perf_counter()
+    log("decode layers ...")
+    dec = decode_layers(torch, QMatrix, syn, (1,) if args.quick else (1, 4, 8), args.steps, args.warmup)
+    head = dec[1]
+    configs = {"qwen3_8b_decode": {f"M{M}": v for M, v in dec.items()}}
+    if not args.quick:
+        log("config 0 ...")
+        configs["gemv_4096"] = config0(torch, QMatrix, syn, 50)
+        log("prefill ...")
+        configs["llama31_8b_prefill_ffn"] = prefill(torch, QMatrix, syn, 20)
+        log("moe ...")
+        configs["qwen3_30b_a3b_moe"] = moe(torch, QFfn, syn, 30)
+        log("lm head ...")
+        configs["lm_head_q4_0"] = lm_head(torch, QMatrix, syn, 30)
+    gu = head["per_matrix"]["gate_up"]
+    roof = {"kernel": "k_qgemv<g128s, MB=1, RT=2> (gate+up 24576x4096, M=1)", "bound": "hbm",
+            "achieved": gu["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": gu["GBps"] / (HBM_PEAK / 1e9),
+            "traffic": None, "bytes_per_launch": gu["bytes"], "us_per_launch": gu["us"]}
+    cpu = None
+    if not (args.quick or args.no_cpu):
+        log("cpu baseline ...")
+        cpu = cpu_baseline(syn)
+    out = {"metric": METRIC, "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "Qwen3-8B decode token: 36 layers x int4 g128s GEMVs (QKV 6144x4096, o 4096x4096, "
+                                  "gate+up 24576x4096, down 4096x12288), M=1, one HBM copy per layer",
+                      "bytes_per_step": head["bytes_per_step"], "hbm_frac": head["hbm_frac"],
+                      "tokens_per_s_equiv": head["tokens_per_s_equiv"], "launch": head["launch"]},
+           "roofline": roof, "cpu_baseline": cpu, "configs": configs,
+           "wall_s": time.perf_counter() - t_all}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
