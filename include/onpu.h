@@ -112,6 +112,9 @@ void * onpu_ffn_new3(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, 
  * bank: experts [e0, e0 + n), stage holds n consecutive experts of onpu_stage_bytes each */
 int onpu_dense_load(void * h, const void * stage);
 int onpu_bank_load(void * h, int64_t e0, int64_t n, const void * stage);
+/* the decode-GEMV launch plan (host only): mb, rt, nb, xl, tw, kw, bpw, grid x, built, max waves
+ * for an [N][K] matrix of fmt at M rows over `slots` slots; epi 0 store, 1 SiLU-gate, 2 slot sum */
+void onpu_plan_gemv(int fmt, int64_t N, int64_t K, int M, int64_t slots, int epi, int64_t * out /* [10] */);
 /* N, K, fmt, E, row tiles, K blocks, HBM bytes per expert, HBM base address */
 void onpu_dense_info(void * h, int64_t * out /* [8] */);
 /* dequantized weights of expert e as the GPU stores them: fp32 (bf16 = 0) or bf16 RNE bits */

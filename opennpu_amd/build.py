@@ -18,14 +18,17 @@ OUT = HERE / "libonpu_hip.so"
 BUILD = HERE / "_build"
 ARCH = os.environ.get("ONPU_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ["onpu_kernels.hip", "onpu_api.cpp", "onpu_quant.cpp"]
+# (source, extra defines, object name): onpu_fmt.hip is built once per weight format
+SOURCES = [("onpu_kernels.hip", [], "onpu_kernels"), ("onpu_api.cpp", [], "onpu_api"), ("onpu_quant.cpp", [], "onpu_quant")] + \
+    [("onpu_fmt.hip", [f"-DONPU_FMT_ID={i}"], f"onpu_fmt{i}") for i in range(4)]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(CSRC), "-I", str(ROOT / "include"),
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
 
 
-def _compile(src):
-    obj = BUILD / (src + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(job):
+    src, defs, name = job
+    obj = BUILD / (name + ".o")
+    cmd = [HIPCC, *FLAGS, *defs, "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
@@ -35,7 +38,7 @@ def _compile(src):
 
 def build(verbose=True):
     BUILD.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(len(SOURCES)) as ex:
+    with ThreadPoolExecutor(min(len(SOURCES), os.cpu_count() or 4)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), "-lpthread"]

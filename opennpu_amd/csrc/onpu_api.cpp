@@ -164,24 +164,80 @@ int env_int(const char * name, int dflt) {
 }
 
 struct Plan {
-    int mb = 1, rt = 1, waves = 1;
-    int64_t bpw = 1;
+    int mb = 1, rt = 1, nb = 2, xl = 0, tw = 1, kw = 1;
+    int64_t bpw = 1, gx = 1;                 // K blocks per wave; grid.x (tile groups / tw)
+    int waves() const { return tw * kw; }
 };
 
-// waves split K; rt row tiles per workgroup; enough waves in flight to cover HBM latency
-Plan plan_gemv(int64_t NT, int64_t KB, int M, int64_t slots, bool act) {
+// Workgroup = tw tile groups x kw K parts; each wave streams bpw K blocks of its tile group (rt row
+// tiles) through a two-chunk pipeline of nb blocks. The plan aims at ~2048 waves with an equal
+// contiguous share of 4..16 blocks (4..16 KiB of nibbles) each, at most 2 tile groups per
+// workgroup with at least 512 workgroups, and x staged in LDS (xl) when M rows of K fit in 48 KiB.
+// ACT pairs gate tile t with up tile t + NT/2, so tw divides NT/2 there. (Sweeps of kw, tw and nb
+// over the Qwen3-8B and 151936-row LM-head shapes on MI355X put the optimum there.)
+Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
+    (void) fmt;
     Plan p;
     p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-    p.rt = act ? 2 : 1;
-    if (!act && p.mb == 1) p.rt = NT >= 4096 ? 4 : (NT >= 1536 ? 2 : 1);
-    const int maxw = p.mb == 1 ? 16 : 8;
-    const int64_t wg = (act ? NT / 2 : (NT + p.rt - 1) / p.rt) * slots;
-    p.waves = 1;
-    while (p.waves < maxw && 2 * p.waves <= KB && (wg * p.waves < 4096 || KB / p.waves > 8)) p.waves *= 2;
-    const int ew = env_int("ONPU_GEMV_WAVES", 0), er = env_int("ONPU_GEMV_RT", 0);
-    if (ew > 0 && ew <= maxw) p.waves = ew;
-    if (!act && er > 0 && p.mb == 1 && (er == 1 || er == 2 || er == 4)) p.rt = er;
-    p.bpw = (KB + p.waves - 1) / p.waves;
+    p.rt = epi == EPI_ACT_ ? 2 : 1;
+    const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2;
+    p.xl = (p.mb == 1 && xbytes <= 48 * 1024) ? 1 : 0;
+    const int ex = env_int("ONPU_GEMV_XL", -1);
+    if (ex == 0) p.xl = 0;
+    const int64_t groups = epi == EPI_ACT_ ? NT / 2 : NT;
+    const int64_t per = std::min<int64_t>(16, std::max<int64_t>(4, (groups * slots * KB + 2047) / 2048));
+    int64_t kw = std::min<int64_t>(16, std::max<int64_t>(1, (KB + per - 1) / per));
+    const int ekw = env_int("ONPU_GEMV_KW", 0);
+    if (ekw > 0) kw = std::min<int64_t>(ekw, KB);
+    p.bpw = (KB + kw - 1) / kw;
+    p.kw = (int) ((KB + p.bpw - 1) / p.bpw);
+    p.nb = p.bpw >= 2 ? 2 : 1;
+    const int en = env_int("ONPU_GEMV_NB", 0);
+    if (en > 0) p.nb = en;
+    // the largest built chunk size not above the wish, with x in LDS if built, else from global;
+    // (rt, nb = 1, xl = 0) is built for every epilogue and MB
+    int pick = 0;
+    for (int xl : {p.xl, 0}) {
+        for (int nb = p.nb; nb >= 1 && !pick; nb--)
+            if (qgemv_has_variant(epi, p.mb, p.rt, nb, xl)) { p.nb = nb; p.xl = xl; pick = 1; }
+        if (pick) break;
+    }
+    if (!pick) { p.nb = 1; p.xl = 0; }
+    const int maxw = std::min(qgemv_max_waves(p.mb, p.rt, p.nb, p.xl), 32 / (p.rt * p.mb));   // LDS <= 32 KiB
+    if (p.kw > maxw) {                               // more K per wave
+        p.kw = maxw;
+        p.bpw = (KB + p.kw - 1) / p.kw;
+        p.kw = (int) ((KB + p.bpw - 1) / p.bpw);
+    }
+    int tw = std::max(1, std::min(2, maxw / p.kw));
+    while (tw > 1 && (tw * p.kw * p.rt * p.mb > 32 || (groups + tw - 1) / tw * slots < 512 ||
+                      (epi == EPI_ACT_ && groups % tw != 0)))
+        tw--;
+    const int etw = env_int("ONPU_GEMV_TW", 0);
+    if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= 32 && !(epi == EPI_ACT_ && groups % etw))
+        tw = etw;
+    p.tw = tw;
+    p.gx = (groups + tw - 1) / tw;
+    return p;
+}
+
+// MoE decode down projection with the weighted slot sum: one workgroup per row tile holds the k
+// slots x ksplit K parts (kw = k * ksplit waves, returned in kw); kw = 0 when k slots do not fit
+Plan plan_slotsum(int64_t KB, int k) {
+    Plan p;
+    p.rt = 1;
+    p.tw = 1;
+    int ksplit = 1;
+    while (k * ksplit * 2 <= 16 && ksplit * 2 <= KB) ksplit *= 2;
+    p.bpw = (KB + ksplit - 1) / ksplit;
+    p.kw = 0;
+    for (int nb : {3, 2, 1})                         // largest chunk whose launch bound holds the waves
+        if (nb <= std::max<int64_t>(1, p.bpw) && qgemv_has_variant(EPI_SLOTSUM_, 1, 1, nb, 0) &&
+            k * ksplit <= qgemv_max_waves(1, 1, nb, 0)) {
+            p.nb = nb;
+            p.kw = k * ksplit;
+            break;
+        }
     return p;
 }
 
@@ -190,15 +246,14 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
     if (M <= 0) return hipSuccess;
     const uint8_t * W = m->dev + e * m->dstride;
     if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0) {
-        const Plan p = plan_gemv(m->g.NT, m->g.KB, (int) M, 1, false);
+        const Plan p = plan_gemv(m->fmt, m->g.NT, m->g.KB, (int) M, 1, EPI_STORE_);
         QArgs a{};
         a.W = W; a.estride = 0; a.ids = nullptr;
         a.N = m->N; a.K = m->K; a.NT = m->g.NT; a.KB = m->g.KB;
         a.x = x; a.ldx = m->K; a.xslot = 0; a.xdiv = 1; a.M = (int) M;
         a.y = y; a.ldy = m->N; a.yslot = 0; a.yf32 = yf32;
-        a.bpw = p.bpw;
-        dim3 grid((unsigned) ((m->g.NT + p.rt - 1) / p.rt), 1);
-        return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, grid, p.waves, s);
+        a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
+        return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
     }
     GArgs a{};
     a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
@@ -211,7 +266,7 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
 hipError_t bank_core(Mat4 * m, const uint16_t * x, int x_per_slot, int64_t T, const int32_t * ids, int k, void * y,
                      int yf32, hipStream_t s) {
     const int64_t slots = T * k, chunk = (65535 / k) * k;     // grid.y limit; chunks start on a token
-    const Plan p = plan_gemv(m->g.NT, m->g.KB, 1, slots, false);
+    const Plan p = plan_gemv(m->fmt, m->g.NT, m->g.KB, 1, slots, EPI_STORE_);
     for (int64_t s0 = 0; s0 < slots; s0 += chunk) {
         const int64_t ns = std::min<int64_t>(chunk, slots - s0);
         QArgs a{};
@@ -222,9 +277,9 @@ hipError_t bank_core(Mat4 * m, const uint16_t * x, int x_per_slot, int64_t T, co
         a.x = x + (x_per_slot ? s0 : s0 / k) * m->K;
         a.ldx = m->K; a.xslot = m->K; a.M = 1;
         a.y = (char *) y + s0 * m->N * (yf32 ? 4 : 2); a.ldy = m->N; a.yslot = m->N; a.yf32 = yf32;
-        a.bpw = p.bpw;
-        dim3 grid((unsigned) ((m->g.NT + p.rt - 1) / p.rt), (unsigned) ns);
-        hipError_t e = launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, grid, p.waves, s);
+        a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
+        hipError_t e = launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, (unsigned) ns),
+                                    p.waves(), s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -243,24 +298,27 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
         e = f->ws[0].ensure((size_t) (n * I * 2));
         if (e != hipSuccess) return e;
         uint16_t * act = f->ws[0].as<uint16_t>();
-        const Plan pg = plan_gemv(gu->g.NT, gu->g.KB, 1, n, true);
+        const Plan pg = plan_gemv(gu->fmt, gu->g.NT, gu->g.KB, 1, n, EPI_ACT_);
         QArgs a{};
         a.W = gu->dev; a.estride = gu->dstride; a.ids = ids;
         a.N = gu->N; a.K = gu->K; a.NT = gu->g.NT; a.KB = gu->g.KB;
         a.x = x; a.ldx = gu->K; a.xslot = gu->K; a.xdiv = k; a.M = 1;
-        a.y = act; a.ldy = I; a.yslot = I; a.yf32 = 0; a.bpw = pg.bpw;
-        e = launch_qgemv(gu->fmt, EPI_ACT_, a, 1, 2, dim3((unsigned) (I / 16), (unsigned) n), pg.waves, s);
+        a.y = act; a.ldy = I; a.yslot = I; a.yf32 = 0; a.bpw = pg.bpw; a.tw = pg.tw;
+        a.xls = gu->g.KB * 128 + 8;
+        e = launch_qgemv(gu->fmt, EPI_ACT_, a, 1, 2, pg.nb, pg.xl, dim3((unsigned) pg.gx, (unsigned) n), pg.waves(), s);
         if (e != hipSuccess) return e;
-        int ksplit = 1;
-        while (k * ksplit * 2 <= 16 && ksplit * 2 <= dn->g.KB) ksplit *= 2;
+        const Plan pd = plan_slotsum(dn->g.KB, k);
+        if (!pd.kw) return hipErrorInvalidValue;
+        const int ksplit = pd.kw / k;
         QArgs b{};
         b.W = dn->dev; b.estride = dn->dstride; b.ids = ids;
         b.N = Nd; b.K = dn->K; b.NT = dn->g.NT; b.KB = dn->g.KB;
         b.x = act; b.ldx = I; b.xslot = I; b.xdiv = 1; b.M = 1;
         b.y = y; b.ldy = Nd; b.yslot = Nd; b.yf32 = yf32;
-        b.wslot = w; b.nslot = k; b.ksplit = ksplit;
-        b.bpw = (dn->g.KB + ksplit - 1) / ksplit;
-        return launch_qgemv(dn->fmt, EPI_SLOTSUM_, b, 1, 1, dim3((unsigned) dn->g.NT, (unsigned) T), k * ksplit, s);
+        b.wslot = w; b.nslot = k; b.ksplit = ksplit; b.tw = 1;
+        b.bpw = pd.bpw;
+        return launch_qgemv(dn->fmt, EPI_SLOTSUM_, b, 1, 1, pd.nb, 0, dim3((unsigned) dn->g.NT, (unsigned) T), pd.kw,
+                            s);
     }
     // prompts: tokens grouped per expert (one pass over each routed expert's weights per 64 rows)
     const int rows_per_item = 64, mb = 4;
@@ -349,6 +407,16 @@ void onpu_stats(int64_t * calls, double * wait_s) {
 
 // every (tiles, kc) is served: the HIP kernels take any shape
 int onpu_has_shape(int, int, int) { return device().ok; }
+
+// the GEMV launch plan for an [N][K] matrix of fmt at M rows over `slots` (host only, no GPU):
+// out = mb, rt, nb, xl, tw, kw, bpw, gx, built (1 if that kernel variant exists), max waves
+void onpu_plan_gemv(int fmt, int64_t N, int64_t K, int M, int64_t slots, int epi, int64_t * out) {
+    const Tiled g = tiled_geom(fmt, N, K);
+    const Plan p = epi == EPI_SLOTSUM_ ? plan_slotsum(g.KB, (int) slots) : plan_gemv(fmt, g.NT, g.KB, M, slots, epi);
+    const int64_t v[10] = {p.mb, p.rt, p.nb, p.xl, p.tw, p.kw, p.bpw, p.gx,
+                           qgemv_has_variant(epi, p.mb, p.rt, p.nb, p.xl), qgemv_max_waves(p.mb, p.rt, p.nb, p.xl)};
+    for (int i = 0; i < 10; i++) out[i] = v[i];
+}
 
 int64_t onpu_stage_bytes(int fmt, int64_t N, int64_t K) {
     return fmt_valid(fmt) && K % fmt_group(fmt) == 0 ? stage_bytes(fmt, N, K) : 0;

@@ -1,0 +1,58 @@
+// The format-specific kernels of libonpu_hip: compiled once per weight format with
+// -DONPU_FMT_ID=<0..3> (onpu_common.h OnpuFmt), so the variants build in parallel.
+#include "onpu_kern.h"
+
+#ifndef ONPU_FMT_ID
+#error "compile with -DONPU_FMT_ID=<format>"
+#endif
+#define ONPU_CAT2(a, b) a##b
+#define ONPU_CAT(a, b) ONPU_CAT2(a, b)
+#define FN(name) ONPU_CAT(name##_f, ONPU_FMT_ID)
+
+static constexpr int F = ONPU_FMT_ID;
+
+hipError_t FN(repack)(const uint8_t * st, int64_t sstride, int64_t N, int64_t K, int64_t KB, int64_t NT, uint8_t * out,
+                      int64_t ostride, int64_t E, hipStream_t s) {
+    k_repack<F><<<dim3((unsigned) KB, (unsigned) NT, (unsigned) E), 64, 0, s>>>(st, sstride, N, K, KB, out, ostride);
+    return hipGetLastError();
+}
+
+hipError_t FN(dequant)(const uint8_t * W, int64_t N, int64_t K, int64_t KB, int64_t NT, void * out, int bf16,
+                       hipStream_t s) {
+    k_dequant<F><<<dim3((unsigned) KB, (unsigned) NT), 64, 0, s>>>(W, N, K, KB, out, bf16);
+    return hipGetLastError();
+}
+
+hipError_t FN(qgemv)(int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves, size_t lds,
+                     hipStream_t s) {
+#define X(e_, mb_, rt_, nb_, xl_)                                                           \
+    if (epi == e_ && mb == mb_ && rt == rt_ && nb == nb_ && xl == xl_) {                   \
+        k_qgemv<F, mb_, rt_, nb_, e_, xl_><<<grid, waves * 64, lds, s>>>(a);               \
+        return hipGetLastError();                                                          \
+    }
+    ONPU_QGEMV_VARIANTS(X)
+#undef X
+    return hipErrorInvalidValue;
+}
+
+hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
+    const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * ntw - 1) / (4 * ntw);
+    const dim3 grid((unsigned) (gm * gn));
+    if (ntw == 4) k_qgemm<F, 4><<<grid, 256, 0, s>>>(a);
+    else k_qgemm<F, 2><<<grid, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t FN(moe)(int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s) {
+    const size_t lds = (size_t) waves * (which == 0 ? 2 : 1) * mb * 256 * sizeof(float);
+    if (which == 0) {
+        if (mb == 1) k_moe_gu<F, 1, 2><<<grid, waves * 64, lds, s>>>(a);
+        else if (mb == 2) k_moe_gu<F, 2, 2><<<grid, waves * 64, lds, s>>>(a);
+        else k_moe_gu<F, 4, 1><<<grid, waves * 64, lds, s>>>(a);
+    } else {
+        if (mb == 1) k_moe_dn<F, 1, 2><<<grid, waves * 64, lds, s>>>(a);
+        else if (mb == 2) k_moe_dn<F, 2, 2><<<grid, waves * 64, lds, s>>>(a);
+        else k_moe_dn<F, 4, 1><<<grid, waves * 64, lds, s>>>(a);
+    }
+    return hipGetLastError();
+}

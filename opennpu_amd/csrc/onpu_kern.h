@@ -1,0 +1,666 @@
+// Templated device code of libonpu_hip for gfx950: the tiled-layout kernels instantiated once per
+// weight format (onpu_fmt.hip, compiled with ONPU_FMT_ID = 0..3).
+//
+//   k_repack     staging layout -> tiled HBM layout (onpu_common.h), once per weight upload
+//   k_dequant    tiled -> fp32 or bf16 (RNE) dequantized weights (parity checks)
+//   k_qgemv      M <= 64 rows: the decode GEMV family. Integer MFMA on biased codes (128 + u) in
+//                bf16, group scales applied in fp32 between MFMA steps, x column sums from an
+//                extra MFMA against ones; epilogues: store, SiLU(gate) * up, MoE slot sum
+//   k_qgemm      M > 64 (prefill): x tile in LDS, int4 tile dequantized to bf16 RNE((u-8)s) in
+//                registers and fed to v_mfma_f32_16x16x32_bf16, fp32 accumulate
+//   k_moe_gu/dn  grouped expert products over a device work list
+#pragma once
+#include <hip/hip_runtime.h>
+#include "onpu_common.h"
+#include "onpu_launch.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define DEV static __device__ __forceinline__
+
+// LDS views: pointers into the dynamic shared array travel through generic pointers; casting them
+// back to address space 3 makes the accesses ds_read / ds_write (a generic "flat" access counts
+// against both the vector-memory and LDS counters and forces waits on the weight prefetch)
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+#define LDS_U32X4(p) ((lds_u32x4 *) (p))
+
+
+DEV f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// D_j -> 8 bf16 holding 128 + u (bf16 0x43XX = 128 + XX for XX < 128), in B-operand order:
+// r.x = (d & M) | mag, r.y = ((d >> 4) & M) | mag, r.z = ((d >> 8) & M) | mag, r.w = ((d >> 12) & M) | mag.
+// Seven VALU ops with v_and_or_b32 (the compiler splits it into and + or). The block ends with
+// s_nop 1: an MFMA may read these registers as its B operand right after the asm, and the ISA wants
+// two wait states between a VALU write and that read (the compiler cannot see inside the asm).
+DEV u32x4 unpack_biased(uint32_t d, uint32_t mag) {
+    u32x4 r;
+    asm("v_and_or_b32 %0, %4, %5, %6\n\t"
+        "v_lshrrev_b32 %1, 4, %4\n\t"
+        "v_and_or_b32 %1, %1, %5, %6\n\t"
+        "v_lshrrev_b32 %2, 8, %4\n\t"
+        "v_and_or_b32 %2, %2, %5, %6\n\t"
+        "v_lshrrev_b32 %3, 12, %4\n\t"
+        "v_and_or_b32 %3, %3, %5, %6\n\t"
+        "s_nop 1"
+        : "=&v"(r.x), "=&v"(r.y), "=&v"(r.z), "=&v"(r.w)
+        : "v"(d), "s"(0x000F000Fu), "v"(mag));
+    return r;
+}
+
+// code u (0..15) of element e of D_j
+DEV uint32_t code_of(uint32_t d, int e) { return (d >> (4 * nib_pos(e))) & 0xfu; }
+
+DEV float scale_f32(int fmt, uint32_t bits) {
+    return fmt == ONPU_Q4_0 ? f16_to_f32((uint16_t) bits) : bf16_to_f32((uint16_t) bits);
+}
+
+// dequantized weight (fp32) as the reference defines it: (u - 8) * s, or u * s + m for q4nx.
+// u * s is exact in fp32 (4-bit times 8/11-bit), so fmaf rounds exactly once, like mul-then-add.
+DEV float dq_val(int fmt, uint32_t u, float s, float m) {
+    return fmt_has_min(fmt) ? fmaf((float) u, s, m) : fmaf((float) u, s, -8.0f * s);
+}
+
+// two fp32 -> packed bf16 (round to nearest even: v_cvt_pk_bf16_f32), low half = lo
+DEV uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    bf2 h;
+    h.x = (__bf16) lo;
+    h.y = (__bf16) hi;
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// ------------------------------------------------------------------ repack
+// grid (KB, NT, E), 64 threads. st: staging of E experts (stride sstride bytes); out: tiled
+// (stride ostride bytes per expert)
+template <int FMT>
+__global__ __launch_bounds__(64) void k_repack(const uint8_t * __restrict__ st, int64_t sstride, int64_t N,
+                                               int64_t K, int64_t KB, uint8_t * __restrict__ out, int64_t ostride) {
+    const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
+    const int64_t b = blockIdx.x, t = blockIdx.y;
+    st += (int64_t) blockIdx.z * sstride;
+    uint8_t * blk = out + (int64_t) blockIdx.z * ostride + (t * KB + b) * fmt_blk(FMT);
+    const int64_t n = 16 * t + r;
+    const uint32_t pad = fmt_has_min(FMT) ? 0u : 8u;
+    u32x4 dv;
+    for (int j = 0; j < 4; j++) {
+        const int64_t k0 = 128 * b + 32 * j + 8 * q;
+        uint32_t d = 0;
+        if (FMT == ONPU_Q4_0) {
+            for (int e = 0; e < 8; e++) {
+                const int64_t k = k0 + e;
+                uint32_t u = pad;
+                if (n < N && k < K) {
+                    const uint8_t * bq = st + (n * (K / 32) + k / 32) * 18 + 2;
+                    const int jj = (int) (k % 32);
+                    u = jj < 16 ? (bq[jj] & 0xfu) : (bq[jj - 16] >> 4);
+                }
+                d |= u << (4 * nib_pos(e));
+            }
+        } else {
+            uint32_t w = 0x88888888u * (pad == 8u);
+            if (n < N && k0 < K) w = *(const uint32_t *) (st + n * (K / 2) + k0 / 2);   // 8 codes, k0 % 8 == 0
+            for (int e = 0; e < 8; e++) d |= ((w >> (4 * e)) & 0xfu) << (4 * nib_pos(e));
+        }
+        dv[j] = d;
+    }
+    *(u32x4 *) (blk + 16 * lane) = dv;
+    // group parameters [16 rows][GPB] (+ min)
+    constexpr int G = FMT == ONPU_G128S ? 128 : 32, GPB = 128 / G;
+    if (lane < 16 * GPB) {
+        const int rr = lane / GPB, g = lane % GPB;
+        const int64_t nn = 16 * t + rr, gi = b * GPB + g;          // group index along K
+        uint16_t s = 0, mn = 0;
+        if (nn < N && gi * G < K) {
+            if (FMT == ONPU_Q4_0) {
+                const uint8_t * bb = st + (nn * (K / 32) + gi) * 18;
+                s = (uint16_t) (bb[0] | (bb[1] << 8));
+            } else {
+                const uint16_t * sc = (const uint16_t *) (st + N * K / 2);
+                s = sc[nn * (K / G) + gi];
+                if (fmt_has_min(FMT)) mn = sc[N * (K / G) + nn * (K / G) + gi];
+            }
+        }
+        uint16_t * p = (uint16_t *) (blk + 1024);
+        if (fmt_has_min(FMT)) { p[2 * lane] = s; p[2 * lane + 1] = mn; }
+        else p[lane] = s;
+    }
+}
+
+// Raw group parameters of lane row r in one block (loaded early, decoded at compute time):
+// G128S one u16 scale, Q4S / Q4_0 four u16 scales, Q4NX four {u16 scale, u16 min} pairs.
+template <int FMT> struct Par { uint32_t v[FMT == ONPU_Q4NX ? 4 : (FMT == ONPU_G128S ? 1 : 2)]; };
+
+template <int FMT>
+DEV Par<FMT> par_zero() {
+    Par<FMT> p;
+    for (auto & x : p.v) x = 0u;
+    return p;
+}
+
+template <int FMT>
+DEV Par<FMT> load_par(const uint8_t * blk, int r) {
+    Par<FMT> p;
+    if (FMT == ONPU_G128S) p.v[0] = *(const uint16_t *) (blk + 1024 + 2 * r);
+    else if (FMT == ONPU_Q4NX) {
+        const u32x4 q = __builtin_nontemporal_load((const u32x4 *) (blk + 1024 + 16 * r));
+        for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];
+    } else {
+        const u32x2 q = __builtin_nontemporal_load((const u32x2 *) (blk + 1024 + 8 * r));
+        p.v[0] = q.x;
+        p.v[1 % (sizeof(p.v) / 4)] = q.y;
+    }
+    return p;
+}
+
+// scale and additive offset per MFMA step such that w = s * (128 + u) + boff
+// (sym: boff = -136 s; q4nx: boff = m - 128 s)
+template <int FMT>
+DEV void decode_par(const Par<FMT> & p, float (&s)[4], float (&bo)[4]) {
+    if (FMT == ONPU_G128S) {
+        const float v = bf16_to_f32((uint16_t) p.v[0]);
+        for (int j = 0; j < 4; j++) { s[j] = v; bo[j] = -136.0f * v; }
+    } else if (FMT == ONPU_Q4NX) {
+        for (int j = 0; j < 4; j++) {
+            const uint32_t pj = p.v[j % (sizeof(p.v) / 4)];
+            s[j] = bf16_to_f32((uint16_t) (pj & 0xffff));
+            bo[j] = bf16_to_f32((uint16_t) (pj >> 16)) - 128.0f * s[j];
+        }
+    } else {
+        for (int j = 0; j < 4; j++) {
+            const uint32_t bits = (p.v[(j >> 1) % (sizeof(p.v) / 4)] >> (16 * (j & 1))) & 0xffff;
+            s[j] = scale_f32(FMT, bits);
+            bo[j] = -136.0f * s[j];
+        }
+    }
+}
+
+// raw parameters for dequant (s, m) per step
+template <int FMT>
+DEV void load_sm(const uint8_t * blk, int r, float (&s)[4], float (&m)[4]) {
+    if (FMT == ONPU_G128S) {
+        const float v = bf16_to_f32(*(const uint16_t *) (blk + 1024 + 2 * r));
+        for (int j = 0; j < 4; j++) { s[j] = v; m[j] = 0.f; }
+    } else if (FMT == ONPU_Q4NX) {
+        const u32x4 p = *(const u32x4 *) (blk + 1024 + 16 * r);
+        for (int j = 0; j < 4; j++) {
+            s[j] = bf16_to_f32((uint16_t) (p[j] & 0xffff));
+            m[j] = bf16_to_f32((uint16_t) (p[j] >> 16));
+        }
+    } else {
+        const u32x2 p = *(const u32x2 *) (blk + 1024 + 8 * r);
+        for (int j = 0; j < 4; j++) {
+            s[j] = scale_f32(FMT, (p[j >> 1] >> (16 * (j & 1))) & 0xffff);
+            m[j] = 0.f;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ dequant (parity checks)
+// grid (KB, NT), 64 threads; out [N][K] fp32 (bf16 = 0) or bf16 RNE bits (bf16 = 1)
+template <int FMT>
+__global__ __launch_bounds__(64) void k_dequant(const uint8_t * __restrict__ W, int64_t N, int64_t K, int64_t KB,
+                                                void * __restrict__ out, int bf16) {
+    const int lane = threadIdx.x, q = lane >> 4, r = lane & 15;
+    const int64_t b = blockIdx.x, t = blockIdx.y, n = 16 * t + r;
+    const uint8_t * blk = W + (t * KB + b) * fmt_blk(FMT);
+    const u32x4 dv = *(const u32x4 *) (blk + 16 * lane);
+    float s[4], m[4];
+    load_sm<FMT>(blk, r, s, m);
+    if (n >= N) return;
+    for (int j = 0; j < 4; j++)
+        for (int e = 0; e < 8; e += 2) {
+            const int64_t k = 128 * b + 32 * j + 8 * q + e;   // K % 32 == 0: k < K covers k + 1
+            if (k >= K) continue;
+            const float v0 = dq_val(FMT, code_of(dv[j], e), s[j], m[j]);
+            const float v1 = dq_val(FMT, code_of(dv[j], e + 1), s[j], m[j]);
+            if (bf16) *(uint32_t *) ((uint16_t *) out + n * K + k) = pack_bf16x2(v0, v1);
+            else { ((float *) out)[n * K + k] = v0; ((float *) out)[n * K + k + 1] = v1; }
+        }
+}
+
+// ------------------------------------------------------------------ decode GEMV family
+// Per wave: RT row tiles x a run of K blocks. A operand = x rows (16 per MFMA block, MB blocks),
+// B operand = unpacked biased codes. For each MFMA step j (32 k, one 32-group):
+//   cg = x . (128 + u)^T,  cs = x . 1  (column sums of x, shared by all row tiles)
+//   acc += s_j * cg + boff_j * cs
+template <int FMT, int MB, int RT>
+DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FMT> (&par)[RT],
+                    const u32x4 (&xa)[MB][4], uint32_t mag, f32x4 (&acc)[RT][MB]) {
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    if (FMT == ONPU_G128S) {
+        f32x4 cs[MB];
+        for (int mb = 0; mb < MB; mb++) {
+            cs[mb] = z;
+            for (int j = 0; j < 4; j++) cs[mb] = mfma(xa[mb][j], ones, cs[mb]);
+        }
+        for (int rt = 0; rt < RT; rt++) {
+            if (!valid[rt]) continue;
+            f32x4 cg[MB];
+            for (int mb = 0; mb < MB; mb++) cg[mb] = z;
+            for (int j = 0; j < 4; j++) {
+                const u32x4 bw = unpack_biased(wv[rt][j], mag);
+                for (int mb = 0; mb < MB; mb++) cg[mb] = mfma(xa[mb][j], bw, cg[mb]);
+            }
+            float s[4], bo[4];
+            decode_par<FMT>(par[rt], s, bo);
+            for (int mb = 0; mb < MB; mb++)
+                for (int v = 0; v < 4; v++) acc[rt][mb][v] += s[0] * cg[mb][v] + bo[0] * cs[mb][v];
+        }
+    } else {
+        f32x4 cs[MB][4];
+        for (int mb = 0; mb < MB; mb++)
+            for (int j = 0; j < 4; j++) cs[mb][j] = mfma(xa[mb][j], ones, z);
+        for (int rt = 0; rt < RT; rt++) {
+            if (!valid[rt]) continue;
+            float s[4], bo[4];
+            decode_par<FMT>(par[rt], s, bo);
+            for (int j = 0; j < 4; j++) {
+                const u32x4 bw = unpack_biased(wv[rt][j], mag);
+                for (int mb = 0; mb < MB; mb++) {
+                    const f32x4 cg = mfma(xa[mb][j], bw, z);
+                    for (int v = 0; v < 4; v++) acc[rt][mb][v] += s[j] * cg[v] + bo[j] * cs[mb][j][v];
+                }
+            }
+        }
+    }
+}
+
+// Where the A operand (x rows) comes from: global rows (optionally gathered through xrows) or the
+// workgroup's LDS copy xs[M][xls] (bf16, zero past K).
+struct XSrc {
+    const uint16_t * x;
+    int64_t ldx;
+    const int32_t * xrows;
+    const uint16_t * xs;
+    int64_t xls;
+};
+
+// x fragments of block b: lane (r, q) of A-block mb holds x[row(16 mb + r)][128 b + 32 j + 8 q .. +7]
+// (XL: from the LDS copy, else from global rows; a compile-time choice so that the LDS path has
+// no global load the waits would have to cover)
+template <int MB, bool XL>
+DEV void load_x(const XSrc & X, int M, int64_t K, int64_t b, int r, int q, u32x4 (&xa)[MB][4]) {
+    for (int mb = 0; mb < MB; mb++) {
+        const int m = 16 * mb + r;
+        int64_t row = m;
+        bool ok = m < M;
+        if (!XL && X.xrows && ok) { row = X.xrows[m]; ok = row >= 0; }
+        for (int j = 0; j < 4; j++) {
+            const int64_t k = 128 * b + 32 * j + 8 * q;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (ok && k < K) {
+                if (XL) v = *LDS_U32X4(X.xs + m * X.xls + k);
+                else v = *(const u32x4 *) (X.x + row * X.ldx + k);
+            }
+            xa[mb][j] = v;
+        }
+    }
+}
+
+// One chunk of NB blocks x RT row tiles: weights (non-temporal: each byte is read once), parameters
+// and which (block, tile) pairs are real. The loads are unconditional (an out-of-range pair reads
+// the always-valid block `safe` and is flagged), so the hardware wait counts stay exact across the
+// two-chunk pipeline instead of falling back to waiting for every outstanding load.
+template <int FMT, int RT, int NB>
+struct WChunk {
+    u32x4 wv[NB][RT];
+    Par<FMT> par[NB][RT];
+    bool ok[NB][RT];
+};
+
+template <int FMT, int RT, int NB>
+DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], const uint8_t * safe, int64_t c0,
+                    int64_t b1, int lane, int r) {
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const uint8_t * p[NB][RT];
+    for (int i = 0; i < NB; i++)
+        for (int rt = 0; rt < RT; rt++) {
+            c.ok[i][rt] = tb[rt] != nullptr && c0 + i < b1;
+            p[i][rt] = c.ok[i][rt] ? tb[rt] + (c0 + i) * BLK : safe;
+        }
+    for (int i = 0; i < NB; i++)
+        for (int rt = 0; rt < RT; rt++) {
+            c.wv[i][rt] = __builtin_nontemporal_load((const u32x4 *) (p[i][rt] + 16 * lane));
+            c.par[i][rt] = load_par<FMT>(p[i][rt], r);
+        }
+}
+
+// The MFMAs of one chunk (blocks c0 .. c0 + NB - 1, those below b1)
+template <int FMT, int MB, int RT, int NB, bool XL>
+DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, const XSrc & X, int M, int64_t K,
+                       int r, int q, uint32_t mag, f32x4 (&acc)[RT][MB]) {
+    if (XL) {                             // x from LDS, one block at a time (short latency)
+        for (int i = 0; i < NB; i++) {
+            if (c0 + i >= b1) break;
+            u32x4 xa[MB][4];
+            load_x<MB, true>(X, M, K, c0 + i, r, q, xa);
+            qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa, mag, acc);
+        }
+    } else {                              // x from global memory: the chunk's x loads first
+        u32x4 xa[NB][MB][4];
+        for (int i = 0; i < NB; i++) load_x<MB, false>(X, M, c0 + i < b1 ? K : 0, c0 + i, r, q, xa[i]);
+        for (int i = 0; i < NB; i++)
+            if (c0 + i < b1) qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], mag, acc);
+    }
+}
+
+// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks of NB blocks with two
+// chunk buffers: the loads of chunk i + 1 are in flight while chunk i is computed, so each wave
+// streams its K range with NB..2 NB blocks (x RT tiles) outstanding. pre() runs before the first
+// loads are issued and post() right after (the workgroup's LDS staging of x: its loads first, then
+// the LDS writes and the barrier while the weights stream); every wave calls both, also one with no
+// blocks. safe: any valid block (the target of out-of-range loads).
+template <int FMT, int MB, int RT, int NB, bool XL, class Pre, class Post>
+DEV void qacc_run(const uint8_t * const (&tb)[RT], const uint8_t * safe, int64_t b0, int64_t b1, const XSrc & X, int M,
+                  int64_t K, Pre pre, Post post, f32x4 (&acc)[RT][MB]) {
+    const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
+    const uint32_t mag = 0x43004300u;
+    for (int rt = 0; rt < RT; rt++)
+        for (int mb = 0; mb < MB; mb++) acc[rt][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    WChunk<FMT, RT, NB> ca, cb;
+    pre();
+    load_chunk<FMT, RT, NB>(ca, tb, safe, b0, b1, lane, r);
+    post();
+    // Every iteration issues both loads, past b1 too (they read `safe` and are flagged): with no
+    // conditional loads the compiler's wait counts see exactly the chunk a computation needs.
+    for (int64_t c0 = b0; c0 < b1; c0 += 2 * NB) {
+        load_chunk<FMT, RT, NB>(cb, tb, safe, c0 + NB, b1, lane, r);
+        compute_chunk<FMT, MB, RT, NB, XL>(ca, c0, b1, X, M, K, r, q, mag, acc);
+        load_chunk<FMT, RT, NB>(ca, tb, safe, c0 + 2 * NB, b1, lane, r);
+        compute_chunk<FMT, MB, RT, NB, XL>(cb, c0 + NB, b1, X, M, K, r, q, mag, acc);
+    }
+}
+
+// Epilogues
+enum { EPI_STORE = 0, EPI_ACT = 1, EPI_SLOTSUM = 2 };
+
+DEV void store_out(void * y, int yf32, int64_t idx, float v) {
+    if (yf32) ((float *) y)[idx] = v;
+    else ((uint16_t *) y)[idx] = f32_to_bf16(v);
+}
+
+DEV float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+constexpr int qgemv_lb(int MB, int RT, int NB, int XL) { return (MB == 1 && RT * NB <= (XL ? 4 : 2)) ? 1024 : 512; }
+
+// grid: (tile groups, slots), block: waves * 64 threads. A workgroup holds a.tw tile groups x KW
+// K parts (KW = waves / a.tw): wave w works on tile group w / KW (RT row tiles: t and t + stride,
+// stride = gridDim.x * a.tw) and K part w % KW. Dynamic LDS: the cross-wave reduction buffer
+// (waves * RT * MB KiB), then with XL the x rows [M][xls] bf16 shared by all waves.
+//   STORE  : slot = blockIdx.y; y[m][n] = sum of the K parts
+//   ACT    : RT = 2, tiles (gate t, up t + stride); out[m][16 t + r] = silu(g) * u
+//   SLOTSUM: a.tw = 1; wave w -> slot w / ksplit (its expert and x row), K part w % ksplit;
+//            out = sum_s w_s y_s
+template <int FMT, int MB, int RT, int NB, int EPI, int XL>
+__global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
+    extern __shared__ float red[];
+    // the wave index is uniform across a wave: readfirstlane lets the compiler keep tile bases,
+    // block ranges and their guards in scalar registers
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const int ntw = EPI == EPI_SLOTSUM ? 1 : a.tw, KW = nw / ntw;
+    int64_t slot;
+    int kpart, twi;
+    if (EPI == EPI_SLOTSUM) {
+        slot = (int64_t) blockIdx.y * a.nslot + wave / a.ksplit;
+        kpart = wave % a.ksplit;
+        twi = 0;
+    } else {
+        slot = blockIdx.y;
+        twi = wave / KW;
+        kpart = wave % KW;
+    }
+    const int64_t e = a.ids ? (int64_t) a.ids[slot] : 0;
+    const uint8_t * W = a.W + e * a.estride;
+    const uint16_t * x = a.x + (slot / a.xdiv) * a.xslot;
+    const uint8_t * tb[RT];
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const int64_t stride = (int64_t) gridDim.x * ntw, tg0 = (int64_t) blockIdx.x * ntw;
+    for (int rt = 0; rt < RT; rt++) {
+        const int64_t t = tg0 + twi + rt * stride;
+        tb[rt] = t < a.NT ? W + t * a.KB * BLK : nullptr;
+    }
+    const int64_t b0 = (int64_t) kpart * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
+    constexpr int PER = RT * MB * 256;
+    uint16_t * xs = (uint16_t *) (red + nw * PER);
+    const XSrc X{x, a.ldx, nullptr, XL ? xs : nullptr, a.xls};
+    // XL: the workgroup copies x [M][K] into LDS in 16 B units u = tid + i * blockDim; rows are
+    // zero-padded from K to Kpad = 128 * KB. The first 4 units per thread are loaded before the
+    // weight loads are issued (pre) and stored after (post); any further ones are copied in post.
+    const uint32_t kp8 = (uint32_t) a.KB * 16, nunits = (uint32_t) a.M * kp8, bd = blockDim.x;
+    u32x4 xv[4];
+    auto xunit = [&](uint32_t u) {
+        const uint32_t m = u / kp8, k = (u - m * kp8) * 8;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (k < a.K) v = *(const u32x4 *) (x + (int64_t) m * a.ldx + k);
+        return v;
+    };
+    auto xslot = [&](uint32_t u) {
+        const uint32_t m = u / kp8;
+        return LDS_U32X4(xs + (int64_t) m * a.xls + (u - m * kp8) * 8);
+    };
+    auto pre = [&]() {
+        if (!XL) return;
+        for (int i = 0; i < 4; i++) {
+            const uint32_t u = threadIdx.x + i * bd;
+            xv[i] = u < nunits ? xunit(u) : (u32x4){0u, 0u, 0u, 0u};
+        }
+    };
+    auto post = [&]() {
+        if (!XL) return;
+        for (int i = 0; i < 4; i++) {
+            const uint32_t u = threadIdx.x + i * bd;
+            if (u < nunits) *xslot(u) = xv[i];
+        }
+        for (uint32_t u = threadIdx.x + 4 * bd; u < nunits; u += bd) *xslot(u) = xunit(u);
+        __syncthreads();
+    };
+    f32x4 acc[RT][MB];
+    qacc_run<FMT, MB, RT, NB, XL != 0>(tb, W, b0, b1, X, a.M, a.K, pre, post, acc);
+
+    // cross-wave reduction through LDS: red[wave][((rt * MB + mb) * 4 + v) * 64 + lane]
+    for (int rt = 0; rt < RT; rt++)
+        for (int mb = 0; mb < MB; mb++)
+            for (int v = 0; v < 4; v++) red[wave * PER + ((rt * MB + mb) * 4 + v) * 64 + lane] = acc[rt][mb][v];
+    __syncthreads();
+    const int nout = EPI == EPI_ACT ? MB * 256 : PER;
+    for (int oo = threadIdx.x; oo < ntw * nout; oo += blockDim.x) {
+        const int tw = oo / nout, o = oo % nout;
+        const int rt = o / (MB * 256), mb = (o / 256) % MB, v = (o / 64) % 4, l = o % 64;
+        const int m = 16 * mb + 4 * (l >> 4) + v;
+        const int64_t n = 16 * (tg0 + tw + rt * stride) + (l & 15);
+        if (m >= a.M) continue;
+        const float * rp = red + (int64_t) tw * KW * PER + o;
+        if (EPI == EPI_SLOTSUM) {
+            const float * ws = a.wslot + (int64_t) blockIdx.y * a.nslot;
+            float s = 0.f;
+            for (int sl = 0; sl < a.nslot; sl++) {
+                float p = 0.f;
+                for (int kp = 0; kp < a.ksplit; kp++) p += red[(sl * a.ksplit + kp) * PER + o];
+                s += ws[sl] * p;
+            }
+            if (n < a.N) store_out(a.y, a.yf32, (int64_t) blockIdx.y * a.yslot + (int64_t) m * a.ldy + n, s);
+        } else if (EPI == EPI_ACT) {
+            float g = 0.f, u = 0.f;
+            for (int kp = 0; kp < KW; kp++) { g += rp[kp * PER]; u += rp[kp * PER + MB * 256]; }
+            if (n < a.N / 2)
+                store_out(a.y, a.yf32, (int64_t) slot * a.yslot + (int64_t) m * a.ldy + n, silu_f(g) * u);
+        } else {
+            float s = 0.f;
+            for (int kp = 0; kp < KW; kp++) s += rp[kp * PER];
+            if (n < a.N) store_out(a.y, a.yf32, (int64_t) slot * a.yslot + (int64_t) m * a.ldy + n, s);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ prefill GEMM
+// Y[M][N] = X[M][K] . deq(W)^T. WG: 4 waves, tile BM = 128 rows of X x BN = 64 * NTW row tiles... each wave
+// owns NTW row tiles (16 rows each) and all 128 X rows: 8 A-blocks x NTW accumulators.
+// Per K block (128): X tile (128 x 128 bf16, 32 KiB) staged in LDS as MFMA fragments
+// [mb][j][lane] (16 B each); each wave loads its own weight blocks and dequantizes them to bf16
+// RNE((u - 8) s) (the reference's device weight, gemv_any.cc:65,106-107) in registers.
+template <int FMT, int NTW>
+__global__ __launch_bounds__(256) void k_qgemm(GArgs a) {
+    __shared__ u32x4 xs[8 * 4 * 64];                 // 32 KiB
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r = lane & 15;
+    // XCD-aware order: consecutive logical tiles land on the same XCD (WG i runs on XCD i % 8)
+    const int64_t nwg = (int64_t) gridDim.x, wg = blockIdx.x;
+    int64_t lid = wg;
+    if (nwg % 8 == 0) lid = (wg % 8) * (nwg / 8) + wg / 8;
+    const int64_t gm = (a.M + 127) / 128;
+    const int64_t mblk = lid % gm, nblk = lid / gm;
+    const int64_t m0 = mblk * 128;
+    const int64_t t0 = nblk * (4 * NTW) + wave * NTW;       // first row tile of this wave
+    const uint8_t * tb[NTW];
+    for (int i = 0; i < NTW; i++) tb[i] = (t0 + i) < a.NT ? a.W + (t0 + i) * a.KB * BLK : nullptr;
+
+    f32x4 acc[8][NTW];
+    for (int mb = 0; mb < 8; mb++)
+        for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // X tile loader: 2048 chunks of 16 B (128 rows x 16 chunks), 8 per thread
+    u32x4 xr[8];
+    auto load_xt = [&](int64_t b) {
+        for (int i = 0; i < 8; i++) {
+            const int c = tid + 256 * i, row = c >> 4, c16 = c & 15;
+            const int64_t m = m0 + row, k = 128 * b + 8 * c16;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (m < a.M && k < a.K) v = *(const u32x4 *) (a.x + m * a.ldx + k);
+            xr[i] = v;
+        }
+    };
+    auto store_xt = [&]() {
+        for (int i = 0; i < 8; i++) {
+            const int c = tid + 256 * i, row = c >> 4, c16 = c & 15;
+            const int j = c16 >> 2, qq = c16 & 3, mb = row >> 4, rr = row & 15;
+            xs[(mb * 4 + j) * 64 + qq * 16 + rr] = xr[i];
+        }
+    };
+    u32x4 wr[NTW];
+    float ws[NTW][4], wm[NTW][4];
+    auto load_w = [&](int64_t b) {
+        for (int i = 0; i < NTW; i++) {
+            if (tb[i]) {
+                const uint8_t * blk = tb[i] + b * BLK;
+                wr[i] = *(const u32x4 *) (blk + 16 * lane);
+                load_sm<FMT>(blk, r, ws[i], wm[i]);
+            } else {
+                wr[i] = (u32x4){0u, 0u, 0u, 0u};
+                for (int j = 0; j < 4; j++) { ws[i][j] = 0.f; wm[i][j] = 0.f; }
+            }
+        }
+    };
+    load_xt(0);
+    load_w(0);
+    for (int64_t b = 0; b < a.KB; b++) {
+        __syncthreads();                 // previous block's reads of xs are done
+        store_xt();
+        // dequantize this block's weights to bf16 B operands
+        u32x4 bw[NTW][4];
+        for (int i = 0; i < NTW; i++)
+            for (int j = 0; j < 4; j++) {
+                const uint32_t d = wr[i][j];
+                uint32_t o[4];
+                for (int p = 0; p < 4; p++)
+                    o[p] = pack_bf16x2(dq_val(FMT, code_of(d, 2 * p), ws[i][j], wm[i][j]),
+                                       dq_val(FMT, code_of(d, 2 * p + 1), ws[i][j], wm[i][j]));
+                bw[i][j] = (u32x4){o[0], o[1], o[2], o[3]};
+            }
+        __syncthreads();
+        if (b + 1 < a.KB) { load_xt(b + 1); load_w(b + 1); }
+        for (int j = 0; j < 4; j++)
+            for (int mb = 0; mb < 8; mb++) {
+                const u32x4 xa = xs[(mb * 4 + j) * 64 + lane];
+                for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa, bw[i][j], acc[mb][i]);
+            }
+    }
+    // store: lane holds rows 4 (l >> 4) + v of A-block mb, column r of row tile t0 + i
+    for (int mb = 0; mb < 8; mb++)
+        for (int i = 0; i < NTW; i++) {
+            const int64_t n = 16 * (t0 + i) + r;
+            if (n >= a.N) continue;
+            for (int v = 0; v < 4; v++) {
+                const int64_t m = m0 + 16 * mb + 4 * q + v;
+                if (m < a.M) store_out(a.y, a.yf32, m * a.ldy + n, acc[mb][i][v]);
+            }
+        }
+}
+
+// grouped gate_up (+ SiLU * up) over work items: blockIdx.y = item, blockIdx.x = gate tile t.
+// Rows of the item: perm[first .. first + rows) -> token = entry / k (x row), output row = position.
+template <int FMT, int MB, int NB>
+__global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_gu(MArgs a) {
+    extern __shared__ float red[];
+    const int item = blockIdx.y;
+    if (item >= *a.nitems) return;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
+    const uint8_t * W = a.W + (int64_t) e * a.estride;
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    // x rows of this item: token = perm / k
+    __shared__ int32_t xr[64];
+    if (threadIdx.x < 64) xr[threadIdx.x] = threadIdx.x < rows ? a.perm[first + threadIdx.x] / a.k : -1;
+    __syncthreads();
+    const uint8_t * tb[2];
+    int64_t tile[2] = {(int64_t) blockIdx.x, (int64_t) blockIdx.x + gridDim.x};
+    for (int rt = 0; rt < 2; rt++) tb[rt] = tile[rt] < a.NT ? W + tile[rt] * a.KB * BLK : nullptr;
+    const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
+    f32x4 acc[2][MB];
+    const XSrc X{a.x, a.ldx, xr, nullptr, 0};
+    qacc_run<FMT, MB, 2, NB, false>(tb, W, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
+    constexpr int PER = 2 * MB * 256;
+    for (int rt = 0; rt < 2; rt++)
+        for (int mb = 0; mb < MB; mb++)
+            for (int v = 0; v < 4; v++) red[wave * PER + ((rt * MB + mb) * 4 + v) * 64 + lane] = acc[rt][mb][v];
+    __syncthreads();
+    for (int o = threadIdx.x; o < MB * 256; o += blockDim.x) {
+        const int mb = (o / 256) % MB, v = (o / 64) % 4, l = o % 64;
+        const int m = 16 * mb + 4 * (l >> 4) + v;
+        const int64_t n = 16 * tile[0] + (l & 15);
+        if (m >= rows || n >= a.N / 2) continue;
+        float g = 0.f, u = 0.f;
+        for (int w = 0; w < nw; w++) { g += red[w * PER + o]; u += red[w * PER + MB * 256 + o]; }
+        ((uint16_t *) a.y)[(int64_t) (first + m) * a.ldy + n] = f32_to_bf16(silu_f(g) * u);
+    }
+}
+
+// grouped down over work items: rows are act rows at positions first .. first + rows (contiguous);
+// output o[position][N] fp32
+template <int FMT, int MB, int NB>
+__global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_dn(MArgs a) {
+    extern __shared__ float red[];
+    const int item = blockIdx.y;
+    if (item >= *a.nitems) return;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
+    const uint8_t * W = a.W + (int64_t) e * a.estride;
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const uint8_t * tb[1];
+    int64_t tile = blockIdx.x;
+    tb[0] = tile < a.NT ? W + tile * a.KB * BLK : nullptr;
+    const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
+    f32x4 acc[1][MB];
+    const XSrc X{a.x + (int64_t) first * a.ldx, a.ldx, nullptr, nullptr, 0};
+    qacc_run<FMT, MB, 1, NB, false>(tb, W, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
+    constexpr int PER = MB * 256;
+    for (int mb = 0; mb < MB; mb++)
+        for (int v = 0; v < 4; v++) red[wave * PER + (mb * 4 + v) * 64 + lane] = acc[0][mb][v];
+    __syncthreads();
+    for (int o = threadIdx.x; o < PER; o += blockDim.x) {
+        const int mb = o / 256, v = (o / 64) % 4, l = o % 64;
+        const int m = 16 * mb + 4 * (l >> 4) + v;
+        const int64_t n = 16 * tile + (l & 15);
+        if (m >= rows || n >= a.N) continue;
+        float s = 0.f;
+        for (int w = 0; w < nw; w++) s += red[w * PER + o];
+        ((float *) a.y)[(int64_t) (first + m) * a.ldy + n] = s;
+    }
+}
+

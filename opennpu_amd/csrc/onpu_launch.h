@@ -18,6 +18,8 @@ struct QArgs {
     const float * wslot;      // EPI_SLOTSUM: routing weights [tokens][nslot]
     int nslot, ksplit;        // EPI_SLOTSUM: waves = nslot * ksplit
     int64_t bpw;              // K blocks (128 wide) per wave
+    int64_t xls;              // LDS-staged x (XL variants): row stride in elements
+    int tw;                   // tile groups per workgroup (waves = tw * K parts); 1 for EPI_SLOTSUM
 };
 
 // k_qgemm: prefill, Y[M][N] = X[M][K] . deq(W)^T
@@ -49,7 +51,10 @@ struct MArgs {
 hipError_t launch_repack(int fmt, const uint8_t * st, int64_t sstride, int64_t N, int64_t K, uint8_t * out,
                          int64_t ostride, int64_t E, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t * W, int64_t N, int64_t K, void * out, int bf16, hipStream_t s);
-hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, dim3 grid, int waves, hipStream_t s);
+hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,
+                        hipStream_t s);
+int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl);
+int qgemv_max_waves(int mb, int rt, int nb, int xl);
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
 hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
                         hipStream_t s);
@@ -67,3 +72,26 @@ hipError_t launch_moe_sum(const float * o, int64_t T, int k, int64_t N, const in
                           const float * bias, float * y, hipStream_t s);
 
 enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
+
+// k_qgemv variants built for every format: X(epilogue, MB, RT, NB, XL). MB: 16-row x blocks;
+// RT: row tiles per workgroup; NB: K blocks each wave loads before computing; XL: x staged in LDS.
+#define ONPU_QGEMV_VARIANTS(X)                                                                          \
+    X(0, 1, 1, 1, 1) X(0, 1, 1, 2, 1) X(0, 1, 1, 4, 1) X(0, 1, 2, 2, 1)                                 \
+    X(0, 1, 1, 1, 0) X(0, 1, 1, 2, 0) X(0, 1, 2, 1, 0) X(0, 2, 1, 1, 0) X(0, 2, 1, 2, 0) X(0, 4, 1, 1, 0) \
+    X(1, 1, 2, 1, 1) X(1, 1, 2, 2, 1) X(1, 1, 2, 1, 0) X(1, 2, 2, 1, 0) X(1, 4, 2, 1, 0)                \
+    X(2, 1, 1, 1, 0) X(2, 1, 1, 2, 0) X(2, 1, 1, 3, 0)
+
+// per-format entry points (onpu_fmt.hip compiled with ONPU_FMT_ID = id)
+#define ONPU_FMT_DECL(id)                                                                                   \
+    hipError_t repack_f##id(const uint8_t * st, int64_t sstride, int64_t N, int64_t K, int64_t KB, int64_t NT,  \
+                            uint8_t * out, int64_t ostride, int64_t E, hipStream_t s);                    \
+    hipError_t dequant_f##id(const uint8_t * W, int64_t N, int64_t K, int64_t KB, int64_t NT, void * out, int bf16, \
+                             hipStream_t s);                                                              \
+    hipError_t qgemv_f##id(int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,       \
+                           size_t lds, hipStream_t s);                                                    \
+    hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
+    hipError_t moe_f##id(int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s);
+ONPU_FMT_DECL(0)
+ONPU_FMT_DECL(1)
+ONPU_FMT_DECL(2)
+ONPU_FMT_DECL(3)

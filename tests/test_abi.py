@@ -1,0 +1,134 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/onpu.h declares, and its
+host-only routines (reference geometry, staging sizes, launch plans, packing) behave; no GPU needed."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle.oracle as orc
+from opennpu_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_symbols():
+    text = (ROOT / "include" / "onpu.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(onpu_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_header_symbol():
+    L = _lib.lib()
+    syms = header_symbols()
+    assert len(syms) > 40
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    assert sorted(_lib.EXPORTS) == syms, "ctypes declarations and header differ"
+
+
+def test_no_gpu_here_means_not_ok():
+    import torch
+    L = _lib.lib()
+    if not torch.cuda.is_available():
+        assert L.onpu_ok() == 0
+        assert L.onpu_dense_new3(64, 128, 2) is None      # construction refuses without a GPU
+        with pytest.raises(RuntimeError):
+            _lib.require_gpu()
+
+
+# values of the reference Mat formula (model.py:151-187) at the benchmark shapes, as listed for
+# (N, K, ncols, sym) -> (R, S, tiles, kc, nbytes)
+GEOMETRY = [
+    ((4096, 4096, 8, 0), (4, 2, 4, 8, 10_485_760)),
+    ((6144, 4096, 8, 0), (4, 2, 6, 8, None)),
+    ((24576, 4096, 8, 0), (4, 2, 24, 8, None)),
+    ((4096, 12288, 8, 0), (1, 8, 16, 6, None)),
+    ((1536, 2048, 1, 0), (1, 1, 6, 8, None)),
+    ((2048, 768, 1, 0), (1, 1, 8, 3, None)),
+    ((151936, 4096, 8, 0), (4, 2, 149, 8, None)),
+]
+
+
+@pytest.mark.parametrize("args,want", GEOMETRY)
+def test_reference_geometry(args, want):
+    L = _lib.lib()
+    out = (C.c_int64 * 8)()
+    L.onpu_geometry2(*args, out)
+    got = tuple(out)
+    assert got == orc.geometry(*args)
+    R, S, tiles, kc, nbytes = want
+    assert got[:4] == (R, S, tiles, kc)
+    if nbytes is not None:
+        assert got[7] == nbytes
+    # every staging layout fits in the reference's buffer size for the same matrix
+    for fmt in (0, 1, 2, 3):
+        N, K = args[0], args[1]
+        if K % orc.group(fmt) == 0:
+            sym_out = (C.c_int64 * 8)()
+            L.onpu_geometry2(N, K, args[2], fmt, sym_out)
+            assert L.onpu_stage_bytes(fmt, N, K) == orc.stage_bytes(fmt, N, K) <= sym_out[7]
+
+
+SHAPES = [(16, 128), (72, 512), (300, 1024), (129, 2080), (6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288),
+          (1536, 2048), (2048, 768), (151936, 4096), (14336, 4096), (4096, 14336), (40, 32)]
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+def test_launch_plans_are_built_variants(fmt):
+    """Every plan the host picks names a kernel variant that exists, fits its launch bounds and
+    the 32 KiB reduction buffer, and covers all K blocks."""
+    L = _lib.lib()
+    out = (C.c_int64 * 10)()
+    for N, K in SHAPES:
+        if K % orc.group(fmt):
+            continue
+        KB = -(-K // 128)
+        for M in (1, 2, 5, 8, 16, 17, 33, 64):
+            for slots, epi in ((1, 0), (8, 0), (8, 1)):
+                if epi == 1 and (N % 32):
+                    continue
+                L.onpu_plan_gemv(fmt, N, K, M, slots, epi, out)
+                mb, rt, nb, xl, tw, kw, bpw, gx, built, maxw = tuple(out)
+                assert built, (fmt, N, K, M, epi, tuple(out))
+                assert tw * kw <= maxw and tw * kw * rt * mb <= 32
+                assert kw * bpw >= KB and (kw - 1) * bpw < KB
+                NT = -(-N // 16)
+                groups = NT // 2 if epi == 1 else NT
+                assert gx * tw >= groups
+                if epi == 1:
+                    assert gx * tw == groups
+                assert mb * 16 >= min(M, 64)
+        for k in (1, 2, 4, 6, 8, 16):              # MoE decode down projection, weighted slot sum
+            L.onpu_plan_gemv(fmt, N, K, 1, k, 2, out)
+            mb, rt, nb, xl, tw, kw, bpw, gx, built, maxw = tuple(out)
+            assert built and kw % k == 0 and kw <= maxw and kw <= 16, (N, K, k, tuple(out))
+            assert (kw // k) * bpw >= KB
+
+
+def test_pack_round_trip_q4s():
+    """onpu_pack writes the staging layout with the reference's q4s search quantizer; its
+    dequantization equals onpu_quant_dequant, and its codes and scales equal the oracle's."""
+    L = _lib.lib()
+    rng = np.random.default_rng(0)
+    N, K = 24, 256
+    W = rng.standard_normal((N, K)).astype(np.float32) * 0.05
+    g = (C.c_int64 * 8)()
+    L.onpu_geometry2(N, K, 8, 1, g)
+    out = np.zeros(g[7], np.uint8)
+    n = L.onpu_pack(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 8, 1, out.ctypes.data_as(C.POINTER(C.c_uint8)), 2)
+    assert n == g[7]
+    st = out[:orc.stage_bytes(1, N, K)]
+    deq = orc.dequant(1, st, N, K)
+    qd = np.empty_like(W)
+    L.onpu_quant_dequant(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 1, qd.ctypes.data_as(C.POINTER(C.c_float)), 2)
+    assert np.array_equal(deq, qd)
+    # 4-bit quantization noise of Gaussian weights: ~10% of their rms (the search may clip)
+    assert np.linalg.norm(deq - W) / np.linalg.norm(W) < 0.15
+    # codes and scales agree with the oracle's restatement of quant_sym32, group by group
+    for r in range(0, N, 7):
+        for gi in range(K // 32):
+            q, d = orc.quant_sym32(W[r, 32 * gi:32 * gi + 32])
+            assert np.array_equal(orc.unpack(1, st, N, K)[r, 32 * gi:32 * gi + 32], q)
+            assert st[N * K // 2:].view(np.uint16)[r * (K // 32) + gi] == d
