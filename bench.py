@@ -273,6 +273,30 @@ def cpu_baseline(syn, seconds=12.0):
             "cpu_model": cpu}
 
 
+def profile_target(torch, QMatrix, syn, reps=3):
+    """The roofline kernel alone, for hardware-counter runs: the gate+up GEMV (24576x4096 g128s,
+    M=1) over its 36 HBM copies, `reps` eager launches each, then one plain 512 MiB device copy
+    (torch copy_) whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters' unit."""
+    name, N, K = QWEN3_8B[2]
+    st = syn.weights(G128S, N, K, 100 + N + K)
+    mats = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
+    x = bf16_tensor(torch, syn.activations(1, K, K + 1)).reshape(1, K)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+    for _ in range(reps):
+        for q in mats:
+            q.mv(x, out=y)
+    torch.cuda.synchronize()
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for q in mats:
+        q.free()
+    print(json.dumps({"profile_target": f"{name} {N}x{K} g128s M=1", "launches": reps * LAYERS,
+                      "algorithmic_bytes_per_launch": wbytes(G128S, N, K) + K * 2 + N * 2,
+                      "calibration_copy_bytes": 512 << 20}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,6 +304,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline step only (no extra configs, no CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="only the roofline kernel plus a calibration copy, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the int4 path on a single MI355X; --gpus {args.gpus} "
@@ -290,6 +316,9 @@ def main():
     from opennpu_amd.device import QFfn, QMatrix
     require_gpu()
     torch.cuda.set_device(0)
+    if args.profile:
+        profile_target(torch, QMatrix, syn)
+        return
     t_all = time.perf_counter()
     log("decode layers ...")
     dec = decode_layers(torch, QMatrix, syn, (1,) if args.quick else (1, 4, 8), args.steps, args.warmup)

@@ -316,14 +316,16 @@ struct WChunk {
 };
 
 template <int FMT, int RT, int NB>
-DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], const uint8_t * safe, int64_t c0,
+DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], const uint8_t * last, int64_t c0,
                     int64_t b1, int lane, int r) {
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     const uint8_t * p[NB][RT];
     for (int i = 0; i < NB; i++)
         for (int rt = 0; rt < RT; rt++) {
+            // a block past b1 (or of a missing tile) re-reads `last`, the wave's own last block of
+            // tile 0: an address the wave fetches anyway, never one that every wave shares
             c.ok[i][rt] = tb[rt] != nullptr && c0 + i < b1;
-            p[i][rt] = c.ok[i][rt] ? tb[rt] + (c0 + i) * BLK : safe;
+            p[i][rt] = c.ok[i][rt] ? tb[rt] + (c0 + i) * BLK : last;
         }
     for (int i = 0; i < NB; i++)
         for (int rt = 0; rt < RT; rt++) {
@@ -351,30 +353,43 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
     }
 }
 
-// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks of NB blocks with two
-// chunk buffers: the loads of chunk i + 1 are in flight while chunk i is computed, so each wave
-// streams its K range with NB..2 NB blocks (x RT tiles) outstanding. pre() runs before the first
-// loads are issued and post() right after (the workgroup's LDS staging of x: its loads first, then
-// the LDS writes and the barrier while the weights stream); every wave calls both, also one with no
-// blocks. safe: any valid block (the target of out-of-range loads).
+// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks
+// of NB blocks with two chunk buffers: the loads of chunk i + 1 are in flight while chunk i is
+// computed, so each wave streams its K range with NB..2 NB blocks (x RT tiles) outstanding. Loads
+// are only issued for chunks that hold blocks, and every path into the loop head has exactly the
+// chunk `ca` outstanding, so the compiler's wait counts cover just the chunk being computed.
+// pre() runs before the first loads are issued and post() right after (the workgroup's LDS
+// staging of x: its loads first, then the LDS writes and the barrier while the weights stream);
+// every wave calls both, also one with no blocks.
 template <int FMT, int MB, int RT, int NB, bool XL, class Pre, class Post>
-DEV void qacc_run(const uint8_t * const (&tb)[RT], const uint8_t * safe, int64_t b0, int64_t b1, const XSrc & X, int M,
-                  int64_t K, Pre pre, Post post, f32x4 (&acc)[RT][MB]) {
+DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const XSrc & X, int M, int64_t K, Pre pre,
+                  Post post, f32x4 (&acc)[RT][MB]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
+    if (tb[0] == nullptr) b1 = b0;                 // no tile: no blocks (the epilogue skips its rows)
     const uint32_t mag = 0x43004300u;
     for (int rt = 0; rt < RT; rt++)
         for (int mb = 0; mb < MB; mb++) acc[rt][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const uint8_t * last = b0 < b1 ? tb[0] + (b1 - 1) * BLK : nullptr;
     WChunk<FMT, RT, NB> ca, cb;
     pre();
-    load_chunk<FMT, RT, NB>(ca, tb, safe, b0, b1, lane, r);
+    if (b0 < b1) load_chunk<FMT, RT, NB>(ca, tb, last, b0, b1, lane, r);
     post();
-    // Every iteration issues both loads, past b1 too (they read `safe` and are flagged): with no
-    // conditional loads the compiler's wait counts see exactly the chunk a computation needs.
-    for (int64_t c0 = b0; c0 < b1; c0 += 2 * NB) {
-        load_chunk<FMT, RT, NB>(cb, tb, safe, c0 + NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL>(ca, c0, b1, X, M, K, r, q, mag, acc);
-        load_chunk<FMT, RT, NB>(ca, tb, safe, c0 + 2 * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL>(cb, c0 + NB, b1, X, M, K, r, q, mag, acc);
+    if (b0 >= b1) return;
+    const int64_t nc = (b1 - b0 + NB - 1) / NB;     // chunks; chunk i starts at b0 + i * NB
+    int64_t i = 0;
+    for (; i + 2 < nc; i += 2) {                     // chunks i + 1 and i + 2 exist
+        load_chunk<FMT, RT, NB>(cb, tb, last, b0 + (i + 1) * NB, b1, lane, r);
+        compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        load_chunk<FMT, RT, NB>(ca, tb, last, b0 + (i + 2) * NB, b1, lane, r);
+        compute_chunk<FMT, MB, RT, NB, XL>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
+    }
+    if (i + 1 < nc) {                                // two chunks left: ca (loaded) and one more
+        load_chunk<FMT, RT, NB>(cb, tb, last, b0 + (i + 1) * NB, b1, lane, r);
+        compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
+    } else {
+        compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
     }
 }
 
@@ -462,7 +477,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         __syncthreads();
     };
     f32x4 acc[RT][MB];
-    qacc_run<FMT, MB, RT, NB, XL != 0>(tb, W, b0, b1, X, a.M, a.K, pre, post, acc);
+    qacc_run<FMT, MB, RT, NB, XL != 0>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
 
     // cross-wave reduction through LDS: red[wave][((rt * MB + mb) * 4 + v) * 64 + lane]
     for (int rt = 0; rt < RT; rt++)
@@ -614,7 +629,7 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_gu(MArgs a) {
     const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
     f32x4 acc[2][MB];
     const XSrc X{a.x, a.ldx, xr, nullptr, 0};
-    qacc_run<FMT, MB, 2, NB, false>(tb, W, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
+    qacc_run<FMT, MB, 2, NB, false>(tb, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
     constexpr int PER = 2 * MB * 256;
     for (int rt = 0; rt < 2; rt++)
         for (int mb = 0; mb < MB; mb++)
@@ -648,7 +663,7 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_dn(MArgs a) {
     const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
     f32x4 acc[1][MB];
     const XSrc X{a.x + (int64_t) first * a.ldx, a.ldx, nullptr, nullptr, 0};
-    qacc_run<FMT, MB, 1, NB, false>(tb, W, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
+    qacc_run<FMT, MB, 1, NB, false>(tb, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
     constexpr int PER = MB * 256;
     for (int mb = 0; mb < MB; mb++)
         for (int v = 0; v < 4; v++) red[wave * PER + (mb * 4 + v) * 64 + lane] = acc[0][mb][v];

@@ -46,6 +46,30 @@ def test_dequant_bit_exact(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+def test_golden_fixtures(gpu, fmt):
+    """the committed fixtures (tests/golden/golden.npz, built from the format definitions with
+    numpy alone): dequant bit-exact, y within the bf16 tolerance, through GEMV and GEMM"""
+    import torch
+    from pathlib import Path
+    from opennpu_amd.device import QMatrix
+    G = np.load(Path(__file__).resolve().parent / "golden" / "golden.npz")
+    N, K, M = (int(v) for v in G[f"f{fmt}_shape"])
+    q = QMatrix(N, K, fmt, G[f"f{fmt}_st"])
+    try:
+        assert np.array_equal(q.dequant().view(np.uint32), G[f"f{fmt}_w"].view(np.uint32))
+        y = from_torch(q.mv(to_torch_bf16(G[f"f{fmt}_x"]).reshape(M, K)))
+        check_bf16_out(y, G[f"f{fmt}_y"], what=f"golden fmt {fmt}")
+        # the same rows repeated past the GEMV limit run the MFMA GEMM
+        xr = np.tile(G[f"f{fmt}_x"], (80 // M + 1, 1))[:80]
+        yr = from_torch(q.mv(to_torch_bf16(xr).reshape(80, K)))
+        ref = np.tile(G[f"f{fmt}_y"], (80 // M + 1, 1))[:80]
+        assert np.abs(yr - ref).max() <= 1e-2 * np.abs(ref).max()
+    finally:
+        q.free()
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M", [1, 2, 5, 8, 16, 17, 33, 64])
 def test_gemv_small(gpu, fmt, M):
     for (N, K) in [(16, 128), (72, 512), (300, 1024)] + ([] if fmt == orc.FMT_G128S else [(129, 2080)]):

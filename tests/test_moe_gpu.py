@@ -41,6 +41,23 @@ def test_route(gpu, T, E, k):
     np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
 
 
+def test_route_golden(gpu):
+    """the committed router fixture (numpy softmax + stable sort), including a tie at the top that
+    goes to the lower expert id"""
+    import torch
+    from pathlib import Path
+    from opennpu_amd.device import QFfn
+    G = np.load(Path(__file__).resolve().parent / "golden" / "golden.npz")
+    f = QFfn(2, 128, 128, orc.FMT_G128S)
+    try:
+        ids, w = f.route(torch.from_numpy(G["route_logits"]).cuda(), 8)
+        ids, w = ids.cpu().numpy(), w.cpu().numpy()
+    finally:
+        f.free()
+    assert np.array_equal(ids, G["route_ids"])
+    np.testing.assert_allclose(w, G["route_w"], rtol=2e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("fmt", [orc.FMT_G128S, orc.FMT_Q4S, orc.FMT_Q4NX])
 @pytest.mark.parametrize("T", [1, 3, 8, 40])
 def test_moe_ffn_small(gpu, fmt, T):
