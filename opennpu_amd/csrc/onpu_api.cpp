@@ -255,11 +255,23 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
         return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
     }
-    GArgs a{};
-    a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
-    a.x = x; a.ldx = m->K; a.y = y; a.ldy = m->N; a.yf32 = yf32;
-    const int ntw = env_int("ONPU_GEMM_NTW", 2) == 4 ? 4 : 2;
-    return launch_qgemm(m->fmt, a, ntw, s);
+    // 4 weight tiles per wave (workgroup tile 128 x 256) when that still gives two workgroups per CU,
+    // else 2 (128 x 128)
+    const int64_t wg4 = ((M + 127) / 128) * ((m->g.NT + 15) / 16);
+    int ntw = wg4 >= 512 ? 4 : 2;
+    const int entw = env_int("ONPU_GEMM_NTW", 0);
+    if (entw == 2 || entw == 4) ntw = entw;
+    // the kernel addresses X with 32-bit buffer offsets: launches of at most 2^31 bytes of X rows
+    const int64_t rows_max = std::max<int64_t>(128, (((int64_t) 1 << 31) - 1) / (m->K * 2) / 128 * 128);
+    for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
+        GArgs a{};
+        a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = std::min(rows_max, M - r0);
+        a.x = x + r0 * m->K; a.ldx = m->K; a.ldy = m->N; a.yf32 = yf32;
+        a.y = (char *) y + r0 * m->N * (yf32 ? 4 : 2);
+        const hipError_t e = launch_qgemm(m->fmt, a, ntw, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // per-slot products: slot r = t * k + j -> expert ids[r] on x row (x_per_slot ? r : t); y [T*k][N]

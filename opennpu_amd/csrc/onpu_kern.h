@@ -515,90 +515,155 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
 }
 
 // ------------------------------------------------------------------ prefill GEMM
-// Y[M][N] = X[M][K] . deq(W)^T. WG: 4 waves, tile BM = 128 rows of X x BN = 64 * NTW row tiles... each wave
-// owns NTW row tiles (16 rows each) and all 128 X rows: 8 A-blocks x NTW accumulators.
-// Per K block (128): X tile (128 x 128 bf16, 32 KiB) staged in LDS as MFMA fragments
-// [mb][j][lane] (16 B each); each wave loads its own weight blocks and dequantizes them to bf16
-// RNE((u - 8) s) (the reference's device weight, gemv_any.cc:65,106-107) in registers.
+// The 8 weights of dword d (B-operand order: element e at nibble (e >> 1) + 4 (e & 1)) dequantized
+// to bf16 RNE(w), w = (u - 8) s or u s + m: the weight the reference device feeds its MAC
+// (gemv_any.cc:65,106-107). Nibbles are split into bytes (lo: even nibbles, hi: odd), converted
+// with v_cvt_f32_ubyteN, one fma each (exact: u s fits fp32) and packed by v_cvt_pk_bf16_f32.
+template <int FMT>
+DEV u32x4 dequant8(uint32_t d, float s, float c) {
+    const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+    auto f = [&](uint32_t w, int byte) { return fmaf((float) ((w >> (8 * byte)) & 0xffu), s, c); };
+    return (u32x4){pack_bf16x2(f(lo, 0), f(lo, 2)), pack_bf16x2(f(hi, 0), f(hi, 2)), pack_bf16x2(f(lo, 1), f(lo, 3)),
+                   pack_bf16x2(f(hi, 1), f(hi, 3))};
+}
+
+// scale s and additive constant c of MFMA step j such that w = u * s + c
+template <int FMT>
+DEV void par_sc(const Par<FMT> & p, int j, float & s, float & c) {
+    if (FMT == ONPU_G128S) {
+        s = bf16_to_f32((uint16_t) p.v[0]);
+        c = -8.0f * s;
+    } else if (FMT == ONPU_Q4NX) {
+        const uint32_t pj = p.v[j % (sizeof(p.v) / 4)];
+        s = bf16_to_f32((uint16_t) (pj & 0xffff));
+        c = bf16_to_f32((uint16_t) (pj >> 16));
+    } else {
+        s = scale_f32(FMT, (p.v[(j >> 1) % (sizeof(p.v) / 4)] >> (16 * (j & 1))) & 0xffff);
+        c = -8.0f * s;
+    }
+}
+
+// Y[M][N] = X[M][K] . deq(W)^T for M > 64. Workgroup: 4 waves, tile 128 rows of X x 64 NTW rows of
+// W; wave w owns NTW 16-row weight tiles and all 128 X rows (8 x NTW accumulators of 16 x 16).
+// Per 128-wide K block the X tile (32 KiB of MFMA A fragments [mb][j][lane]) sits in one of two
+// LDS buffers. The buffers are filled straight from global memory by buffer_load_dwordx4 ... lds
+// (lane l of a wave writes 16 B at base + 16 l, so one load fills one A fragment; rows past M and
+// k past K read out of the buffer's range and land as zeros), so X never occupies registers.
+// Each wave dequantizes its own weight blocks in registers one 32-wide K step at a time and runs
+// 8 NTW MFMAs per step. The next block's X and weights are in flight while the current block
+// computes; one barrier per block. Workgroups are numbered so that consecutive tiles share an XCD
+// (workgroup i runs on XCD i % 8), M tile fastest: concurrent workgroups of an XCD reuse the same
+// weight tiles from its L2. The host keeps M * ldx * 2 below 2^31 (32-bit buffer offsets).
+typedef __attribute__((address_space(3))) void lds_void;
+
+// one 128-wide K block of the GEMM: 4 steps of (dequantize NTW weight fragments, 8 NTW MFMAs)
 template <int FMT, int NTW>
-__global__ __launch_bounds__(256) void k_qgemm(GArgs a) {
-    __shared__ u32x4 xs[8 * 4 * 64];                 // 32 KiB
+DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int nt_ok, int lane,
+                    f32x4 (&acc)[8][NTW]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        u32x4 bw[NTW];
+#pragma unroll
+        for (int i = 0; i < NTW; i++) {
+            float sc, cc;
+            par_sc<FMT>(pr[i], j, sc, cc);
+            bw[i] = dequant8<FMT>(wr[i][j], sc, cc);
+        }
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++) {
+            const u32x4 xa = *LDS_U32X4(&xsb[(mb * 4 + j) * 64 + lane]);
+#pragma unroll
+            for (int i = 0; i < NTW; i++)
+                if (i < nt_ok) acc[mb][i] = mfma(xa, bw[i], acc[mb][i]);
+        }
+    }
+}
+
+// the X tile of block b into LDS buffer buf: wave w fills fragments f = 8 w + i, (mb, j) =
+// (f / 4, f % 4); lane (q, r) brings row m0 + 16 mb + r, k = 128 b + 32 j + 8 q
+DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const GArgs & a, int64_t m0, int64_t b, int wave, int q,
+                     int r, u32x4 * buf) {
+    for (int i = 0; i < 8; i++) {
+        const int f = 8 * wave + i, mb = f >> 2, j = f & 3;
+        const int64_t m = m0 + 16 * mb + r, k = 128 * b + 32 * j + 8 * q;
+        const uint32_t off = (m < a.M && k < a.K) ? (uint32_t) ((m * a.ldx + k) * 2) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, 0, 0, 0);
+    }
+}
+
+template <int FMT, int NTW>
+DEV void gemm_load_w(const uint8_t * const (&tb)[NTW], int64_t b, int lane, int r, u32x4 (&w)[NTW],
+                     Par<FMT> (&p)[NTW]) {
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r = lane & 15;
-    // XCD-aware order: consecutive logical tiles land on the same XCD (WG i runs on XCD i % 8)
+    for (int i = 0; i < NTW; i++) {
+        const uint8_t * blk = tb[i] + b * BLK;
+        w[i] = *(const u32x4 *) (blk + 16 * lane);
+        p[i] = load_par<FMT>(blk, r);
+    }
+}
+
+template <int FMT, int NTW>
+__global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
+    __shared__ u32x4 xs0[8 * 4 * 64], xs1[8 * 4 * 64];     // 2 x 32 KiB
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15;
+    const int q = lane >> 4;
     const int64_t nwg = (int64_t) gridDim.x, wg = blockIdx.x;
     int64_t lid = wg;
     if (nwg % 8 == 0) lid = (wg % 8) * (nwg / 8) + wg / 8;
     const int64_t gm = (a.M + 127) / 128;
     const int64_t mblk = lid % gm, nblk = lid / gm;
     const int64_t m0 = mblk * 128;
-    const int64_t t0 = nblk * (4 * NTW) + wave * NTW;       // first row tile of this wave
+    const int64_t t0 = nblk * (4 * NTW) + wave * NTW;     // first weight tile of this wave
+    // tiles past NT (the last column of workgroups) read tile t0's blocks and are not computed
+    int nt_ok = (int) (a.NT - t0 < NTW ? a.NT - t0 : NTW);
+    if (nt_ok < 0) nt_ok = 0;
     const uint8_t * tb[NTW];
-    for (int i = 0; i < NTW; i++) tb[i] = (t0 + i) < a.NT ? a.W + (t0 + i) * a.KB * BLK : nullptr;
+    for (int i = 0; i < NTW; i++) tb[i] = a.W + (i < nt_ok ? t0 + i : (nt_ok > 0 ? t0 : 0)) * a.KB * BLK;
 
     f32x4 acc[8][NTW];
+#pragma unroll
     for (int mb = 0; mb < 8; mb++)
+#pragma unroll
         for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-    // X tile loader: 2048 chunks of 16 B (128 rows x 16 chunks), 8 per thread
-    u32x4 xr[8];
-    auto load_xt = [&](int64_t b) {
-        for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i, row = c >> 4, c16 = c & 15;
-            const int64_t m = m0 + row, k = 128 * b + 8 * c16;
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (m < a.M && k < a.K) v = *(const u32x4 *) (a.x + m * a.ldx + k);
-            xr[i] = v;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
+    u32x4 wr[NTW], wn[NTW];
+    Par<FMT> pr[NTW], pn[NTW];
+    gemm_load_x(xr, a, m0, 0, wave, q, r, xs0);
+    gemm_load_w<FMT, NTW>(tb, 0, lane, r, wr, pr);
+    __builtin_amdgcn_s_waitcnt(0x0f70);                  // vmcnt(0): the DMA into xs0 is done
+    __syncthreads();
+    for (int64_t b = 0; b < a.KB; b += 2) {
+        // even block from xs0 while block b + 1 streams into xs1
+        const bool more1 = b + 1 < a.KB;
+        if (more1) {
+            gemm_load_x(xr, a, m0, b + 1, wave, q, r, xs1);
+            gemm_load_w<FMT, NTW>(tb, b + 1, lane, r, wn, pn);
         }
-    };
-    auto store_xt = [&]() {
-        for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i, row = c >> 4, c16 = c & 15;
-            const int j = c16 >> 2, qq = c16 & 3, mb = row >> 4, rr = row & 15;
-            xs[(mb * 4 + j) * 64 + qq * 16 + rr] = xr[i];
-        }
-    };
-    u32x4 wr[NTW];
-    float ws[NTW][4], wm[NTW][4];
-    auto load_w = [&](int64_t b) {
-        for (int i = 0; i < NTW; i++) {
-            if (tb[i]) {
-                const uint8_t * blk = tb[i] + b * BLK;
-                wr[i] = *(const u32x4 *) (blk + 16 * lane);
-                load_sm<FMT>(blk, r, ws[i], wm[i]);
-            } else {
-                wr[i] = (u32x4){0u, 0u, 0u, 0u};
-                for (int j = 0; j < 4; j++) { ws[i][j] = 0.f; wm[i][j] = 0.f; }
-            }
-        }
-    };
-    load_xt(0);
-    load_w(0);
-    for (int64_t b = 0; b < a.KB; b++) {
-        __syncthreads();                 // previous block's reads of xs are done
-        store_xt();
-        // dequantize this block's weights to bf16 B operands
-        u32x4 bw[NTW][4];
-        for (int i = 0; i < NTW; i++)
-            for (int j = 0; j < 4; j++) {
-                const uint32_t d = wr[i][j];
-                uint32_t o[4];
-                for (int p = 0; p < 4; p++)
-                    o[p] = pack_bf16x2(dq_val(FMT, code_of(d, 2 * p), ws[i][j], wm[i][j]),
-                                       dq_val(FMT, code_of(d, 2 * p + 1), ws[i][j], wm[i][j]));
-                bw[i][j] = (u32x4){o[0], o[1], o[2], o[3]};
-            }
+        gemm_block<FMT, NTW>(xs0, wr, pr, nt_ok, lane, acc);
+        if (!more1) break;
+        for (int i = 0; i < NTW; i++) { wr[i] = wn[i]; pr[i] = pn[i]; }
+        __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
-        if (b + 1 < a.KB) { load_xt(b + 1); load_w(b + 1); }
-        for (int j = 0; j < 4; j++)
-            for (int mb = 0; mb < 8; mb++) {
-                const u32x4 xa = xs[(mb * 4 + j) * 64 + lane];
-                for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa, bw[i][j], acc[mb][i]);
-            }
+        // odd block from xs1 while block b + 2 streams into xs0
+        const bool more2 = b + 2 < a.KB;
+        if (more2) {
+            gemm_load_x(xr, a, m0, b + 2, wave, q, r, xs0);
+            gemm_load_w<FMT, NTW>(tb, b + 2, lane, r, wn, pn);
+        }
+        gemm_block<FMT, NTW>(xs1, wr, pr, nt_ok, lane, acc);
+        if (!more2) break;
+        for (int i = 0; i < NTW; i++) { wr[i] = wn[i]; pr[i] = pn[i]; }
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
     }
-    // store: lane holds rows 4 (l >> 4) + v of A-block mb, column r of row tile t0 + i
+    // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
+#pragma unroll
     for (int mb = 0; mb < 8; mb++)
+#pragma unroll
         for (int i = 0; i < NTW; i++) {
+            if (i >= nt_ok) continue;
             const int64_t n = 16 * (t0 + i) + r;
             if (n >= a.N) continue;
             for (int v = 0; v < 4; v++) {
