@@ -255,12 +255,12 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
         return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
     }
-    // 4 weight tiles per wave (workgroup tile 128 x 256) when that still gives two workgroups per CU,
-    // else 2 (128 x 128)
-    const int64_t wg4 = ((M + 127) / 128) * ((m->g.NT + 15) / 16);
-    int ntw = wg4 >= 512 ? 4 : 2;
+    // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
+    // workgroups, else 2 (128 x 128); 4 (128 x 256) runs out of registers and is slower
+    const int64_t wg3 = ((M + 127) / 128) * ((m->g.NT + 11) / 12);
+    int ntw = wg3 >= 512 ? 3 : 2;
     const int entw = env_int("ONPU_GEMM_NTW", 0);
-    if (entw == 2 || entw == 4) ntw = entw;
+    if (entw >= 2 && entw <= 4) ntw = entw;
     // the kernel addresses X with 32-bit buffer offsets: launches of at most 2^31 bytes of X rows
     const int64_t rows_max = std::max<int64_t>(128, (((int64_t) 1 << 31) - 1) / (m->K * 2) / 128 * 128);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {

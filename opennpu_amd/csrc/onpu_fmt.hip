@@ -39,6 +39,7 @@ hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
     const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * ntw - 1) / (4 * ntw);
     const dim3 grid((unsigned) (gm * gn));
     if (ntw == 4) k_qgemm<F, 4><<<grid, 256, 0, s>>>(a);
+    else if (ntw == 3) k_qgemm<F, 3><<<grid, 256, 0, s>>>(a);
     else k_qgemm<F, 2><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }

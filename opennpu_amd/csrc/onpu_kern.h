@@ -521,7 +521,11 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
 // with v_cvt_f32_ubyteN, one fma each (exact: u s fits fp32) and packed by v_cvt_pk_bf16_f32.
 template <int FMT>
 DEV u32x4 dequant8(uint32_t d, float s, float c) {
-    const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+    // the masks are opaque to the optimizer, which would otherwise fold each byte extraction into a
+    // 4-bit field extract (v_bfe) plus v_cvt_f32_ubyte0: two ops per weight instead of one
+    uint32_t lo, hi;
+    asm("v_and_b32 %0, %1, %2" : "=v"(lo) : "v"(d), "v"(0x0f0f0f0fu));
+    asm("v_and_b32 %0, %1, %2" : "=v"(hi) : "v"(d >> 4), "v"(0x0f0f0f0fu));
     auto f = [&](uint32_t w, int byte) { return fmaf((float) ((w >> (8 * byte)) & 0xffu), s, c); };
     return (u32x4){pack_bf16x2(f(lo, 0), f(lo, 2)), pack_bf16x2(f(hi, 0), f(hi, 2)), pack_bf16x2(f(lo, 1), f(lo, 3)),
                    pack_bf16x2(f(hi, 1), f(hi, 3))};
@@ -556,49 +560,93 @@ DEV void par_sc(const Par<FMT> & p, int j, float & s, float & c) {
 // weight tiles from its L2. The host keeps M * ldx * 2 below 2^31 (32-bit buffer offsets).
 typedef __attribute__((address_space(3))) void lds_void;
 
-// one 128-wide K block of the GEMM: 4 steps of (dequantize NTW weight fragments, 8 NTW MFMAs)
+// one 128-wide K block of the GEMM: 4 steps of (dequantize NTW weight fragments, 8 NTW MFMAs).
+// NTW = 2: the A fragments of step j + 1 are read from LDS before step j's MFMAs are issued, and
+// step j's dequant runs while step j's reads are in flight. NTW = 4 has no registers to spare for
+// that and reads each step's fragments at the step's start.
 template <int FMT, int NTW>
-DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int nt_ok, int lane,
+DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int lane,
                     f32x4 (&acc)[8][NTW]) {
+    constexpr bool PIPE = NTW <= 3;
+    u32x4 xa[PIPE ? 2 : 1][8];
+    if (PIPE) {
+#pragma unroll
+        for (int mb = 0; mb < 8; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + 0) * 64 + lane]);
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        u32x4 bw[NTW];
+        const int cur = PIPE ? (j & 1) : 0;
+        if (!PIPE) {
 #pragma unroll
-        for (int i = 0; i < NTW; i++) {
-            float sc, cc;
-            par_sc<FMT>(pr[i], j, sc, cc);
-            bw[i] = dequant8<FMT>(wr[i][j], sc, cc);
+            for (int mb = 0; mb < 8; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + j) * 64 + lane]);
         }
+        if (PIPE) {
+            u32x4 bw[NTW];
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++) {
-            const u32x4 xa = *LDS_U32X4(&xsb[(mb * 4 + j) * 64 + lane]);
+            for (int i = 0; i < NTW; i++) {
+                float sc, cc;
+                par_sc<FMT>(pr[i], j, sc, cc);
+                bw[i] = dequant8<FMT>(wr[i][j], sc, cc);
+            }
+            if (j < 3) {
 #pragma unroll
-            for (int i = 0; i < NTW; i++)
-                if (i < nt_ok) acc[mb][i] = mfma(xa, bw[i], acc[mb][i]);
+                for (int mb = 0; mb < 8; mb++) xa[(j + 1) & 1][mb] = *LDS_U32X4(&xsb[(mb * 4 + j + 1) * 64 + lane]);
+            }
+#pragma unroll
+            for (int mb = 0; mb < 8; mb++)
+#pragma unroll
+                for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa[cur][mb], bw[i], acc[mb][i]);
+        } else {                          // one weight fragment live at a time
+#pragma unroll
+            for (int i = 0; i < NTW; i++) {
+                float sc, cc;
+                par_sc<FMT>(pr[i], j, sc, cc);
+                const u32x4 bw = dequant8<FMT>(wr[i][j], sc, cc);
+#pragma unroll
+                for (int mb = 0; mb < 8; mb++) acc[mb][i] = mfma(xa[0][mb], bw, acc[mb][i]);
+            }
         }
+        // keep each step's work within the step: hoisting later steps forward only lengthens live
+        // ranges past the register budget
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// the X tile of block b into LDS buffer buf: wave w fills fragments f = 8 w + i, (mb, j) =
-// (f / 4, f % 4); lane (q, r) brings row m0 + 16 mb + r, k = 128 b + 32 j + 8 q
-DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const GArgs & a, int64_t m0, int64_t b, int wave, int q,
-                     int r, u32x4 * buf) {
+// The X tile of block b into LDS buffer buf: wave w fills fragments f = 8 w + i, (mb, j) =
+// (f / 4, f % 4); lane (q, r) brings row m0 + 16 mb + r, k = 128 b + 32 j + 8 q. xo[i] is the
+// lane's byte offset of its element at b = 0 (0x80000000, past the buffer, for rows >= M: those
+// land as zeros); block b adds 256 b in the scalar offset. kfix: the last block when K % 128 != 0
+// (its k >= K lanes read past the buffer too).
+DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xo)[8], int64_t b, bool kfix, int64_t K,
+                     int wave, int q, u32x4 * buf) {
+#pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int f = 8 * wave + i, mb = f >> 2, j = f & 3;
-        const int64_t m = m0 + 16 * mb + r, k = 128 * b + 32 * j + 8 * q;
-        const uint32_t off = (m < a.M && k < a.K) ? (uint32_t) ((m * a.ldx + k) * 2) : 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, 0, 0, 0);
+        const int f = 8 * wave + i, j = f & 3;
+        uint32_t off = xo[i];
+        if (kfix && 128 * b + 32 * j + 8 * q >= K) off = 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b), 0, 0);
     }
 }
 
+// weight block b of the wave's NTW tiles (buffer loads: one lane offset, the block in the scalar offset)
 template <int FMT, int NTW>
-DEV void gemm_load_w(const uint8_t * const (&tb)[NTW], int64_t b, int lane, int r, u32x4 (&w)[NTW],
+DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int lane, int r, u32x4 (&w)[NTW],
                      Par<FMT> (&p)[NTW]) {
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const uint32_t sb = (uint32_t) (b * BLK);
+#pragma unroll
     for (int i = 0; i < NTW; i++) {
-        const uint8_t * blk = tb[i] + b * BLK;
-        w[i] = *(const u32x4 *) (blk + 16 * lane);
-        p[i] = load_par<FMT>(blk, r);
+        w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs[i], 16 * lane, sb, 0));
+        if (FMT == ONPU_G128S) {
+            p[i].v[0] = __builtin_amdgcn_raw_buffer_load_b16(wrs[i], 1024 + 2 * r, sb, 0);
+        } else if (FMT == ONPU_Q4NX) {
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs[i], 1024 + 16 * r, sb, 0));
+            for (int jj = 0; jj < 4; jj++) p[i].v[jj % (sizeof(p[i].v) / 4)] = v[jj];
+        } else {
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs[i], 1024 + 8 * r, sb, 0));
+            p[i].v[0] = v.x;
+            p[i].v[1 % (sizeof(p[i].v) / 4)] = v.y;
+        }
     }
 }
 
@@ -611,53 +659,67 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
     const int64_t nwg = (int64_t) gridDim.x, wg = blockIdx.x;
     int64_t lid = wg;
     if (nwg % 8 == 0) lid = (wg % 8) * (nwg / 8) + wg / 8;
-    const int64_t gm = (a.M + 127) / 128;
-    const int64_t mblk = lid % gm, nblk = lid / gm;
+    // groups of GMS M tiles x all N columns, M fastest: the 64 workgroups an XCD runs at once cover
+    // GMS M tiles x 64 / GMS N columns, so each X tile and each weight tile is read by many of them
+    constexpr int64_t GMS = 4;
+    const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * NTW - 1) / (4 * NTW);
+    const int64_t grp = lid / (GMS * gn), in = lid % (GMS * gn);
+    const int64_t gms = gm - grp * GMS < GMS ? gm - grp * GMS : GMS;       // M tiles in this group
+    const int64_t mblk = grp * GMS + in % gms, nblk = in / gms;
     const int64_t m0 = mblk * 128;
     const int64_t t0 = nblk * (4 * NTW) + wave * NTW;     // first weight tile of this wave
-    // tiles past NT (the last column of workgroups) read tile t0's blocks and are not computed
+    // tiles past NT (the last column of workgroups) recompute tile t0 (or 0) and are not stored
     int nt_ok = (int) (a.NT - t0 < NTW ? a.NT - t0 : NTW);
     if (nt_ok < 0) nt_ok = 0;
-    const uint8_t * tb[NTW];
-    for (int i = 0; i < NTW; i++) tb[i] = a.W + (i < nt_ok ? t0 + i : (nt_ok > 0 ? t0 : 0)) * a.KB * BLK;
+    __amdgpu_buffer_rsrc_t wrs[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; i++) {
+        const int64_t t = i < nt_ok ? t0 + i : (nt_ok > 0 ? t0 : 0);
+        wrs[i] = __builtin_amdgcn_make_buffer_rsrc((void *) (a.W + t * a.KB * BLK), (short) 0,
+                                                   (int) (uint32_t) (a.KB * BLK), 0x00020000);
+    }
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
+    uint32_t xo[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int f = 8 * wave + i, mb = f >> 2, j = f & 3;
+        const int64_t m = m0 + 16 * mb + r;
+        xo[i] = m < a.M ? (uint32_t) ((m * a.ldx + 32 * j + 8 * q) * 2) : 0x80000000u;
+    }
+    const bool ktail = a.K % 128 != 0;
 
     f32x4 acc[8][NTW];
 #pragma unroll
     for (int mb = 0; mb < 8; mb++)
 #pragma unroll
         for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
-    u32x4 wr[NTW], wn[NTW];
-    Par<FMT> pr[NTW], pn[NTW];
-    gemm_load_x(xr, a, m0, 0, wave, q, r, xs0);
-    gemm_load_w<FMT, NTW>(tb, 0, lane, r, wr, pr);
+    // two register sets for the weights, alternating with the two LDS buffers (no copies)
+    u32x4 wa[NTW], wb[NTW];
+    Par<FMT> pa[NTW], pb[NTW];
+    gemm_load_x(xr, xo, 0, ktail && a.KB == 1, a.K, wave, q, xs0);
+    gemm_load_w<FMT, NTW>(wrs, 0, lane, r, wa, pa);
     __builtin_amdgcn_s_waitcnt(0x0f70);                  // vmcnt(0): the DMA into xs0 is done
     __syncthreads();
-    for (int64_t b = 0; b < a.KB; b += 2) {
-        // even block from xs0 while block b + 1 streams into xs1
-        const bool more1 = b + 1 < a.KB;
-        if (more1) {
-            gemm_load_x(xr, a, m0, b + 1, wave, q, r, xs1);
-            gemm_load_w<FMT, NTW>(tb, b + 1, lane, r, wn, pn);
-        }
-        gemm_block<FMT, NTW>(xs0, wr, pr, nt_ok, lane, acc);
-        if (!more1) break;
-        for (int i = 0; i < NTW; i++) { wr[i] = wn[i]; pr[i] = pn[i]; }
+    // pairs of blocks, one loop exit (acc merges once); an odd last block after the loop
+    int64_t b = 0;
+    for (; b + 2 <= a.KB; b += 2) {
+        // even block from (xs0, wa) while block b + 1 streams into (xs1, wb)
+        gemm_load_x(xr, xo, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, xs1);
+        gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wb, pb);
+        gemm_block<FMT, NTW>(xs0, wa, pa, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
-        // odd block from xs1 while block b + 2 streams into xs0
-        const bool more2 = b + 2 < a.KB;
-        if (more2) {
-            gemm_load_x(xr, a, m0, b + 2, wave, q, r, xs0);
-            gemm_load_w<FMT, NTW>(tb, b + 2, lane, r, wn, pn);
+        // odd block from (xs1, wb) while block b + 2 streams into (xs0, wa)
+        if (b + 2 < a.KB) {
+            gemm_load_x(xr, xo, b + 2, ktail && b + 3 == a.KB, a.K, wave, q, xs0);
+            gemm_load_w<FMT, NTW>(wrs, b + 2, lane, r, wa, pa);
         }
-        gemm_block<FMT, NTW>(xs1, wr, pr, nt_ok, lane, acc);
-        if (!more2) break;
-        for (int i = 0; i < NTW; i++) { wr[i] = wn[i]; pr[i] = pn[i]; }
+        gemm_block<FMT, NTW>(xs1, wb, pb, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
+    if (b < a.KB) gemm_block<FMT, NTW>(xs0, wa, pa, lane, acc);
     // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
 #pragma unroll
     for (int mb = 0; mb < 8; mb++)
