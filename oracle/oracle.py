@@ -89,8 +89,16 @@ def stage_bytes(fmt, N, K):
     return int(lib().orc_stage_bytes(fmt, N, K))
 
 
+def _check(fmt, st, N, K):
+    if K % group(fmt) != 0:
+        raise ValueError(f"K = {K} is not a multiple of the format's group ({group(fmt)})")
+    if np.asarray(st).size < stage_bytes(fmt, N, K):
+        raise ValueError("staging buffer smaller than the format's size")
+
+
 def unpack(fmt, st, N, K):
     """Stored codes u [N][K] (uint8 0..15)."""
+    _check(fmt, st, N, K)
     out = np.empty((N, K), np.uint8)
     lib().orc_unpack(fmt, _p(np.ascontiguousarray(st)), N, K, _p(out))
     return out
@@ -98,6 +106,7 @@ def unpack(fmt, st, N, K):
 
 def dequant(fmt, st, N, K):
     """fp32 dequantized weights [N][K] (onpu_api.cpp:508-529 semantics)."""
+    _check(fmt, st, N, K)
     out = np.empty((N, K), np.float32)
     lib().orc_dequant(fmt, _p(np.ascontiguousarray(st)), N, K, _p(out))
     return out
@@ -105,6 +114,7 @@ def dequant(fmt, st, N, K):
 
 def dequant_bf16(fmt, st, N, K):
     """bf16 (RNE) of the dequantized weights, as bit patterns [N][K] (gemv_any.cc:65,106-107)."""
+    _check(fmt, st, N, K)
     out = np.empty((N, K), np.uint16)
     lib().orc_dequant_bf16(fmt, _p(np.ascontiguousarray(st)), N, K, _p(out))
     return out
@@ -114,6 +124,7 @@ def qmm(fmt, st, N, K, xb, n0=0, n1=None, bf16w=False):
     """fp64 y[M][n1-n0] = x . dequant(W)^T for rows [n0, n1) (reference.py:24-28,55 pattern,
     accumulated in fp64). xb: bf16 bits [M][K]. bf16w: with the weights rounded to bf16 (RNE) as the
     reference device's MAC sees them (gemv_any.cc:65,106-107)."""
+    _check(fmt, st, N, K)
     n1 = N if n1 is None else n1
     xb = np.ascontiguousarray(xb, np.uint16).reshape(-1, K)
     M = xb.shape[0]

@@ -214,7 +214,7 @@ def test_argmax_golden_first_maximum():
 def test_moe_layer_against_dense_composition():
     """the routed layer = sum over slots of w * down(bf16(silu(gate) * up)) with dense numpy products"""
     rng = np.random.default_rng(6)
-    E, H, I, T, k = 4, 128, 64, 3, 2
+    E, H, I, T, k = 4, 128, 128, 3, 2
     gu = [syn.weights(orc.FMT_G128S, 2 * I, H, 50 + e) for e in range(E)]
     dn = [syn.weights(orc.FMT_G128S, H, I, 60 + e) for e in range(E)]
     x = orc.f2bf(rng.standard_normal((T, H)).astype(np.float32))
@@ -277,3 +277,10 @@ def test_quant_asym32_exact_grid_round_trip():
         q, sb, mb = orc.quant_asym32((u * s + m).astype(np.float32))
         sf, mf = orc.bf2f(np.array([sb, mb], np.uint16))
         assert np.array_equal((q * sf + mf).astype(np.float32), (u * s + m).astype(np.float32))
+
+
+def test_oracle_rejects_shapes_outside_the_format():
+    with pytest.raises(ValueError):
+        orc.dequant(orc.FMT_G128S, np.zeros(64 * 32, np.uint8), 64, 64)      # K not a multiple of 128
+    with pytest.raises(ValueError):
+        orc.qmm(orc.FMT_Q4S, np.zeros(10, np.uint8), 4, 64, np.zeros((1, 64), np.uint16))   # short buffer
