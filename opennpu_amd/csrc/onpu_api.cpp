@@ -176,11 +176,10 @@ struct Plan {
 // ACT pairs gate tile t with up tile t + NT/2, so tw divides NT/2 there. (Sweeps of kw, tw and nb
 // over the Qwen3-8B and 151936-row LM-head shapes on MI355X put the optimum there.)
 Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
-    (void) fmt;
     Plan p;
     p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     p.rt = epi == EPI_ACT_ ? 2 : 1;
-    const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2;
+    const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2 + KB * (fmt == ONPU_G128S ? 1 : 4) * 64;
     p.xl = (p.mb == 1 && xbytes <= 48 * 1024) ? 1 : 0;
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;

@@ -229,17 +229,13 @@ __global__ __launch_bounds__(64) void k_dequant(const uint8_t * __restrict__ W, 
 // B operand = unpacked biased codes. For each MFMA step j (32 k, one 32-group):
 //   cg = x . (128 + u)^T,  cs = x . 1  (column sums of x, shared by all row tiles)
 //   acc += s_j * cg + boff_j * cs
+// cs[mb][j] comes from the caller (G128S: cs[mb][0] is the sum over the whole block), in the MFMA
+// C layout: lane (q, r) holds the sums of rows 16 mb + 4 q + v.
 template <int FMT, int MB, int RT>
 DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FMT> (&par)[RT],
-                    const u32x4 (&xa)[MB][4], uint32_t mag, f32x4 (&acc)[RT][MB]) {
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+                    const u32x4 (&xa)[MB][4], const f32x4 (&cs)[MB][4], uint32_t mag, f32x4 (&acc)[RT][MB]) {
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     if (FMT == ONPU_G128S) {
-        f32x4 cs[MB];
-        for (int mb = 0; mb < MB; mb++) {
-            cs[mb] = z;
-            for (int j = 0; j < 4; j++) cs[mb] = mfma(xa[mb][j], ones, cs[mb]);
-        }
         for (int rt = 0; rt < RT; rt++) {
             if (!valid[rt]) continue;
             f32x4 cg[MB];
@@ -251,12 +247,9 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
             float s[4], bo[4];
             decode_par<FMT>(par[rt], s, bo);
             for (int mb = 0; mb < MB; mb++)
-                for (int v = 0; v < 4; v++) acc[rt][mb][v] += s[0] * cg[mb][v] + bo[0] * cs[mb][v];
+                for (int v = 0; v < 4; v++) acc[rt][mb][v] += s[0] * cg[mb][v] + bo[0] * cs[mb][0][v];
         }
     } else {
-        f32x4 cs[MB][4];
-        for (int mb = 0; mb < MB; mb++)
-            for (int j = 0; j < 4; j++) cs[mb][j] = mfma(xa[mb][j], ones, z);
         for (int rt = 0; rt < RT; rt++) {
             if (!valid[rt]) continue;
             float s[4], bo[4];
@@ -272,6 +265,21 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
     }
 }
 
+// column sums of x for one block from an MFMA against ones (x from global memory)
+template <int FMT, int MB>
+DEV void xsum_mfma(const u32x4 (&xa)[MB][4], f32x4 (&cs)[MB][4]) {
+    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < MB; mb++) {
+        if (FMT == ONPU_G128S) {
+            cs[mb][0] = z;
+            for (int j = 0; j < 4; j++) cs[mb][0] = mfma(xa[mb][j], ones, cs[mb][0]);
+        } else {
+            for (int j = 0; j < 4; j++) cs[mb][j] = mfma(xa[mb][j], ones, z);
+        }
+    }
+}
+
 // Where the A operand (x rows) comes from: global rows (optionally gathered through xrows) or the
 // workgroup's LDS copy xs[M][xls] (bf16, zero past K).
 struct XSrc {
@@ -280,6 +288,7 @@ struct XSrc {
     const int32_t * xrows;
     const uint16_t * xs;
     int64_t xls;
+    const float * xsum;       // XL: LDS column sums [group][16] of x's 32- (G128S: 128-) groups
 };
 
 // x fragments of block b: lane (r, q) of A-block mb holds x[row(16 mb + r)][128 b + 32 j + 8 q .. +7]
@@ -343,24 +352,34 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
             if (c0 + i >= b1) break;
             u32x4 xa[MB][4];
             load_x<MB, true>(X, M, K, c0 + i, r, q, xa);
-            qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa, mag, acc);
+            f32x4 cs[MB][4];
+            constexpr int GPB = FMT == ONPU_G128S ? 1 : 4;
+            for (int mb = 0; mb < MB; mb++)
+                for (int j = 0; j < GPB; j++)
+                    cs[mb][j] = *(const __attribute__((address_space(3))) f32x4 *) (X.xsum + ((c0 + i) * GPB + j) * 16 +
+                                                                                   16 * mb + 4 * q);
+            qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, acc);
         }
     } else {                              // x from global memory: the chunk's x loads first
         u32x4 xa[NB][MB][4];
         for (int i = 0; i < NB; i++) load_x<MB, false>(X, M, c0 + i < b1 ? K : 0, c0 + i, r, q, xa[i]);
         for (int i = 0; i < NB; i++)
-            if (c0 + i < b1) qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], mag, acc);
+            if (c0 + i < b1) {
+                f32x4 cs[MB][4];
+                xsum_mfma<FMT, MB>(xa[i], cs);
+                qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], cs, mag, acc);
+            }
     }
 }
 
-// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks
-// of NB blocks with two chunk buffers: the loads of chunk i + 1 are in flight while chunk i is
-// computed, so each wave streams its K range with NB..2 NB blocks (x RT tiles) outstanding. Loads
-// are only issued for chunks that hold blocks, and every path into the loop head has exactly the
-// chunk `ca` outstanding, so the compiler's wait counts cover just the chunk being computed.
-// pre() runs before the first loads are issued and post() right after (the workgroup's LDS
-// staging of x: its loads first, then the LDS writes and the barrier while the weights stream);
-// every wave calls both, also one with no blocks.
+// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks of NB blocks with two
+// chunk buffers: the loads of chunk i + 1 are in flight while chunk i is computed, so each wave
+// streams its K range with NB..2 NB blocks (x RT tiles) outstanding. Loads are only issued for
+// chunks that hold blocks, and every path into the loop head has exactly the chunk `ca`
+// outstanding, so the compiler's wait counts cover just the chunk being computed. pre() runs
+// before the first loads are issued and post() right after (the workgroup's LDS staging of x: its
+// loads first, then the LDS writes and the barrier while the weights stream); every wave calls
+// both, also one with no blocks. (Issuing both chunks before the barrier measured slower.)
 template <int FMT, int MB, int RT, int NB, bool XL, class Pre, class Post>
 DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const XSrc & X, int M, int64_t K, Pre pre,
                   Post post, f32x4 (&acc)[RT][MB]) {
@@ -444,7 +463,10 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     const int64_t b0 = (int64_t) kpart * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
     constexpr int PER = RT * MB * 256;
     uint16_t * xs = (uint16_t *) (red + nw * PER);
-    const XSrc X{x, a.ldx, nullptr, XL ? xs : nullptr, a.xls};
+    // XL: column sums of x per 32-group (G128S: per 128) after the x rows: xsum[group][16 rows]
+    constexpr int GS = FMT == ONPU_G128S ? 128 : 32, UPG = GS / 8;       // 16 B units per group
+    float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
+    const XSrc X{x, a.ldx, nullptr, XL ? xs : nullptr, a.xls, XL ? xsum : nullptr};
     // XL: the workgroup copies x [M][K] into LDS in 16 B units u = tid + i * blockDim; rows are
     // zero-padded from K to Kpad = 128 * KB. The first 4 units per thread are loaded before the
     // weight loads are issued (pre) and stored after (post); any further ones are copied in post.
@@ -467,13 +489,25 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
             xv[i] = u < nunits ? xunit(u) : (u32x4){0u, 0u, 0u, 0u};
         }
     };
+    // unit u's 8 values summed in fp32, then over the UPG consecutive lanes holding one group (the
+    // units of a group are consecutive in u, and u = tid + i * blockDim keeps them in one wave)
+    auto stage = [&](uint32_t u, u32x4 v) {
+        if (u < nunits) *xslot(u) = v;
+        float t = 0.f;
+        for (int d = 0; d < 4; d++) t += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+        for (int o = UPG / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+        if (u < nunits && u % UPG == 0) {
+            const uint32_t m = u / kp8, g = (u - m * kp8) / UPG;
+            xsum[g * 16 + m] = t;
+        }
+    };
     auto post = [&]() {
         if (!XL) return;
-        for (int i = 0; i < 4; i++) {
-            const uint32_t u = threadIdx.x + i * bd;
-            if (u < nunits) *xslot(u) = xv[i];
+        for (int i = 0; i < 4; i++) stage(threadIdx.x + i * bd, xv[i]);
+        for (uint32_t u0 = 4 * bd; u0 < nunits; u0 += bd) {          // same trip count for every lane
+            const uint32_t u = u0 + threadIdx.x;
+            stage(u, u < nunits ? xunit(u) : (u32x4){0u, 0u, 0u, 0u});
         }
-        for (uint32_t u = threadIdx.x + 4 * bd; u < nunits; u += bd) *xslot(u) = xunit(u);
         __syncthreads();
     };
     f32x4 acc[RT][MB];
@@ -755,7 +789,7 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_gu(MArgs a) {
     for (int rt = 0; rt < 2; rt++) tb[rt] = tile[rt] < a.NT ? W + tile[rt] * a.KB * BLK : nullptr;
     const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
     f32x4 acc[2][MB];
-    const XSrc X{a.x, a.ldx, xr, nullptr, 0};
+    const XSrc X{a.x, a.ldx, xr, nullptr, 0, nullptr};
     qacc_run<FMT, MB, 2, NB, false>(tb, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
     constexpr int PER = 2 * MB * 256;
     for (int rt = 0; rt < 2; rt++)
@@ -789,7 +823,7 @@ __global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_dn(MArgs a) {
     tb[0] = tile < a.NT ? W + tile * a.KB * BLK : nullptr;
     const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
     f32x4 acc[1][MB];
-    const XSrc X{a.x + (int64_t) first * a.ldx, a.ldx, nullptr, nullptr, 0};
+    const XSrc X{a.x + (int64_t) first * a.ldx, a.ldx, nullptr, nullptr, 0, nullptr};
     qacc_run<FMT, MB, 1, NB, false>(tb, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
     constexpr int PER = MB * 256;
     for (int mb = 0; mb < MB; mb++)

@@ -205,13 +205,16 @@ int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl) {
 
 int qgemv_max_waves(int mb, int rt, int nb, int xl) { return qgemv_lb(mb, rt, nb, xl) / 64; }
 
-// LDS per workgroup: the reduction buffer plus, with xl, the staged x rows (<= 64 KiB together)
+// LDS per workgroup: the reduction buffer plus, with xl, the staged x rows and their column sums
+// (<= 64 KiB together)
 hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,
                         hipStream_t s) {
     if (waves < 1 || waves > qgemv_max_waves(mb, rt, nb, xl) || !qgemv_has_variant(epi, mb, rt, nb, xl))
         return hipErrorInvalidValue;
     const size_t red = (size_t) waves * rt * mb * 1024;
-    const size_t xb = xl ? (size_t) a.M * a.xls * 2 : 0;
+    // x rows, then the column sums [KB * groups per block][16] floats
+    const size_t xb = xl ? (size_t) a.M * a.xls * 2 + (size_t) a.KB * (fmt == 2 ? 1 : 4) * 64 : 0;
+    if (xl && a.M > 16) return hipErrorInvalidValue;
     if (red > 32768 || red + xb > 65536) return hipErrorInvalidValue;
     if (xl && a.xls < a.KB * 128) return hipErrorInvalidValue;
     switch (fmt) {
