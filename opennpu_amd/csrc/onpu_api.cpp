@@ -505,8 +505,13 @@ int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, 
 
 int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream) {
     auto * m = (Mat4 *) h;
+    if (M <= 0) return 0;
+    // per-part maxima of the two-pass argmax: workspace of the handle (allocated on the first call
+    // with this many rows; calls that overlap on one handle must not share it)
+    HIPR(m->ws[5].ensure((size_t) (M * ARGMAX_PARTS * 8)));
     HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
-    HIPR(launch_argmax(logits, M, m->N, argmax, (hipStream_t) stream));
+    HIPR(launch_argmax(logits, M, m->N, argmax, m->ws[5].as<float>(), m->ws[5].as<int32_t>((size_t) M * ARGMAX_PARTS * 4),
+                       (hipStream_t) stream));
     return 0;
 }
 

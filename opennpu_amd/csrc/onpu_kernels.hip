@@ -3,44 +3,77 @@
 #include "onpu_kern.h"
 
 // ------------------------------------------------------------------ router
-// one wave per token: softmax over E <= 256 logits, top-k (ties to the lower id), renormalised
+// Wave-wide reductions with DPP inside each 16-lane row and readlane across the four rows (no LDS
+// round trips): every lane gets the result.
+template <int CTRL>
+DEV uint32_t dpp_u(uint32_t v) { return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xf, 0xf, false); }
+DEV float readlane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+DEV uint32_t wave_umax(uint32_t v) {
+    v = max(v, dpp_u<0x111>(v));                      // row_shr:1 (lanes without a source see 0)
+    v = max(v, dpp_u<0x112>(v));                      // row_shr:2
+    v = max(v, dpp_u<0x114>(v));                      // row_shr:4
+    v = max(v, dpp_u<0x118>(v));                      // row_shr:8: lane 15 of each row has the row's max
+    const uint32_t a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
+    return max(max(a, b), max(c, d));
+}
+
+DEV float wave_fsum(float v) {
+    v += __uint_as_float(dpp_u<0xB1>(__float_as_uint(v)));   // quad_perm [1,0,3,2]
+    v += __uint_as_float(dpp_u<0x4E>(__float_as_uint(v)));   // quad_perm [2,3,0,1]
+    v += __uint_as_float(dpp_u<0x124>(__float_as_uint(v)));  // row_ror:4
+    v += __uint_as_float(dpp_u<0x128>(__float_as_uint(v)));  // row_ror:8: every lane has its row's sum
+    return (readlane_f(v, 0) + readlane_f(v, 16)) +
+           (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+// float <-> unsigned key with the same order
+DEV uint32_t ord_key(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+DEV float ord_val(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k); }
+
+// one wave per token: softmax over E <= 256 logits, top-k by probability (ties to the lower id),
+// renormalised (moe_runtime.py:333-341). Lane l holds experts 4 l .. 4 l + 3, so the lowest lane
+// holding the maximum also holds its lowest id.
 __global__ __launch_bounds__(64) void k_route(const float * __restrict__ logits, int64_t T, int E, int k, int renorm,
                                               int32_t * __restrict__ ids, float * __restrict__ w) {
     const int64_t t = blockIdx.x;
     const int lane = threadIdx.x;
     const float * l = logits + t * E;
     float v[4];
-    float mx = -INFINITY;
+    uint32_t mk = 0;
     for (int i = 0; i < 4; i++) {
-        const int e = lane + 64 * i;
+        const int e = 4 * lane + i;
         v[i] = e < E ? l[e] : -INFINITY;
-        mx = fmaxf(mx, v[i]);
+        mk = max(mk, ord_key(v[i]));
     }
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float mx = ord_val(wave_umax(mk));
     float p[4], sum = 0.f;
     for (int i = 0; i < 4; i++) {
-        const int e = lane + 64 * i;
+        const int e = 4 * lane + i;
         p[i] = e < E ? expf(v[i] - mx) : 0.f;
         sum += p[i];
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    sum = wave_fsum(sum);
+    // selection keys: probability bits + 1 (p >= 0, so the bits order like the values); 0 = taken
+    uint32_t key[4];
+    for (int i = 0; i < 4; i++) key[i] = 4 * lane + i < E ? __float_as_uint(p[i]) + 1u : 0u;
     float ws = 0.f;
     for (int j = 0; j < k; j++) {
-        // argmax over (p, -id)
-        float bv = -1.f;
-        int bi = 0x7fffffff;
-        for (int i = 0; i < 4; i++) {
-            const int e = lane + 64 * i;
-            if (e < E && (p[i] > bv || (p[i] == bv && e < bi))) { bv = p[i]; bi = e; }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        uint32_t lb = 0;
+        int li = 0;
         for (int i = 0; i < 4; i++)
-            if (lane + 64 * i == bi) p[i] = -2.f;        // taken
-        const float pj = bv / sum;
+            if (key[i] > lb) { lb = key[i]; li = i; }
+        const uint32_t best = wave_umax(lb);
+        const uint64_t hold = __ballot(lb == best);
+        const int first = __builtin_ctzll(hold);
+        const int bi = 4 * first + __builtin_amdgcn_readlane(li, first);
+        for (int i = 0; i < 4; i++)
+            if (lane == first && i == li) key[i] = 0u;
+        const float pj = __uint_as_float(best - 1u) / sum;
         ws += pj;
         if (lane == 0) { ids[t * k + j] = bi; w[t * k + j] = pj; }
     }
@@ -104,30 +137,46 @@ __global__ void k_invert(const int32_t * __restrict__ perm, int64_t n, int32_t *
 }
 
 // ------------------------------------------------------------------ argmax
-// one workgroup per row: first maximum of logits[row][0..N)
-__global__ __launch_bounds__(1024) void k_argmax(const float * __restrict__ v, int64_t N, int32_t * __restrict__ out) {
-    const float * x = v + (int64_t) blockIdx.x * N;
+// first maximum of logits[row][0..N): pass 1 splits each row over gridDim.x workgroups, each leaving
+// its (value, index) in pv / pi [row][part]; pass 2 reduces a row's parts with one wave. Ties go to
+// the lower index in both passes.
+DEV void argmax_merge(float & bv, int & bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+DEV void argmax_wave(float & bv, int & bi) {
+    for (int o = 32; o > 0; o >>= 1) argmax_merge(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float * __restrict__ v, int64_t N, float * __restrict__ pv,
+                                                     int32_t * __restrict__ pi) {
+    const int64_t row = blockIdx.y, parts = gridDim.x;
+    const int64_t per = (N + parts - 1) / parts, n0 = blockIdx.x * per, n1 = n0 + per < N ? n0 + per : N;
+    const float * x = v + row * N;
     float bv = -INFINITY;
-    int bi = (int) N;
-    for (int n = threadIdx.x; n < (int) N; n += blockDim.x) {
-        const float f = x[n];
-        if (f > bv || (f == bv && n < bi)) { bv = f; bi = n; }
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    __shared__ float sv[16];
-    __shared__ int si[16];
+    int bi = 0x7fffffff;
+    for (int64_t n = n0 + threadIdx.x; n < n1; n += blockDim.x) argmax_merge(bv, bi, x[n], (int) n);
+    argmax_wave(bv, bi);
+    __shared__ float sv[4];
+    __shared__ int si[4];
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < (int) (blockDim.x >> 6); w++)
-            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-        out[blockIdx.x] = (int32_t) bi;
+        for (int w = 1; w < 4; w++) argmax_merge(bv, bi, sv[w], si[w]);
+        pv[row * parts + blockIdx.x] = bv;
+        pi[row * parts + blockIdx.x] = bi;
     }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_final(const float * __restrict__ pv, const int32_t * __restrict__ pi,
+                                                     int parts, int64_t N, int32_t * __restrict__ out) {
+    const int64_t row = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int p = threadIdx.x; p < parts; p += 64) argmax_merge(bv, bi, pv[row * parts + p], pi[row * parts + p]);
+    argmax_wave(bv, bi);
+    if (threadIdx.x == 0) out[row] = bi < N ? bi : 0;       // a row of NaNs: 0
 }
 
 // ------------------------------------------------------------------ small helpers
@@ -277,8 +326,11 @@ hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float 
     return hipSuccess;
 }
 
-hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, hipStream_t s) {
-    k_argmax<<<dim3((unsigned) rows), 1024, 0, s>>>(v, N, out);
+hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, float * pv, int32_t * pi,
+                         hipStream_t s) {
+    k_argmax_part<<<dim3(ARGMAX_PARTS, (unsigned) rows), 256, 0, s>>>(v, N, pv, pi);
+    CHECK_LAUNCH();
+    k_argmax_final<<<dim3((unsigned) rows), 64, 0, s>>>(pv, pi, ARGMAX_PARTS, N, out);
     CHECK_LAUNCH();
     return hipSuccess;
 }

@@ -64,7 +64,10 @@ hipError_t launch_moe_grouped(int fmt, int which, const MArgs & a, int mb, dim3 
 hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
 hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
-hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, hipStream_t s);
+// pv / pi: workspace of rows * ARGMAX_PARTS floats / ints
+constexpr int ARGMAX_PARTS = 64;
+hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, float * pv, int32_t * pi,
+                         hipStream_t s);
 hipError_t launch_f32_to_bf16(const float * in, int64_t n, uint16_t * out, hipStream_t s);
 hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * bias, int act,
                           float alpha, float limit, float * o, hipStream_t s);
