@@ -170,8 +170,8 @@ struct Plan {
 };
 
 // Workgroup = tw tile groups x kw K parts; each wave streams bpw K blocks of its tile group (rt row
-// tiles) through a two-chunk pipeline of nb blocks. The plan aims at ~2048 waves with an equal
-// contiguous share of 4..16 blocks (4..16 KiB of nibbles) each, at most 2 tile groups per
+// tiles) through a two-chunk pipeline of nb blocks. The plan aims at ~4096 waves with an equal
+// contiguous share of 4..8 blocks (4..8 KiB of nibbles) each, at most 2 tile groups per
 // workgroup with at least 512 workgroups, and x staged in LDS (xl) when M rows of K fit in 48 KiB.
 // ACT pairs gate tile t with up tile t + NT/2, so tw divides NT/2 there. (Sweeps of kw, tw and nb
 // over the Qwen3-8B and 151936-row LM-head shapes on MI355X put the optimum there.)
@@ -184,7 +184,7 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
     const int64_t groups = epi == EPI_ACT_ ? NT / 2 : NT;
-    const int64_t per = std::min<int64_t>(16, std::max<int64_t>(4, (groups * slots * KB + 2047) / 2048));
+    const int64_t per = std::min<int64_t>(8, std::max<int64_t>(4, (groups * slots * KB + 4095) / 4096));
     int64_t kw = std::min<int64_t>(16, std::max<int64_t>(1, (KB + per - 1) / per));
     const int ekw = env_int("ONPU_GEMV_KW", 0);
     if (ekw > 0) kw = std::min<int64_t>(ekw, KB);

@@ -231,9 +231,19 @@ __global__ __launch_bounds__(64) void k_dequant(const uint8_t * __restrict__ W, 
 //   acc += s_j * cg + boff_j * cs
 // cs[mb][j] comes from the caller (G128S: cs[mb][0] is the sum over the whole block), in the MFMA
 // C layout: lane (q, r) holds the sums of rows 16 mb + 4 q + v.
+// mrows: rows of x (uniform); with one A block only rows v < mrows of lanes q = 0 can be stored,
+// so for mrows == 1 the accumulate touches row 0 alone.
+DEV void acc4(f32x4 & acc, float s, float bo, const f32x4 & cg, const f32x4 & cs, int rows) {
+    acc[0] = fmaf(s, cg[0], fmaf(bo, cs[0], acc[0]));
+    if (rows > 1)
+        for (int v = 1; v < 4; v++) acc[v] = fmaf(s, cg[v], fmaf(bo, cs[v], acc[v]));
+}
+
 template <int FMT, int MB, int RT>
 DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FMT> (&par)[RT],
-                    const u32x4 (&xa)[MB][4], const f32x4 (&cs)[MB][4], uint32_t mag, f32x4 (&acc)[RT][MB]) {
+                    const u32x4 (&xa)[MB][4], const f32x4 (&cs)[MB][4], uint32_t mag, int mrows,
+                    f32x4 (&acc)[RT][MB]) {
+    const int rows = MB > 1 ? 4 : mrows;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     if (FMT == ONPU_G128S) {
         for (int rt = 0; rt < RT; rt++) {
@@ -246,8 +256,7 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
             }
             float s[4], bo[4];
             decode_par<FMT>(par[rt], s, bo);
-            for (int mb = 0; mb < MB; mb++)
-                for (int v = 0; v < 4; v++) acc[rt][mb][v] += s[0] * cg[mb][v] + bo[0] * cs[mb][0][v];
+            for (int mb = 0; mb < MB; mb++) acc4(acc[rt][mb], s[0], bo[0], cg[mb], cs[mb][0], rows);
         }
     } else {
         for (int rt = 0; rt < RT; rt++) {
@@ -258,7 +267,7 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
                 const u32x4 bw = unpack_biased(wv[rt][j], mag);
                 for (int mb = 0; mb < MB; mb++) {
                     const f32x4 cg = mfma(xa[mb][j], bw, z);
-                    for (int v = 0; v < 4; v++) acc[rt][mb][v] += s[j] * cg[v] + bo[j] * cs[mb][j][v];
+                    acc4(acc[rt][mb], s[j], bo[j], cg, cs[mb][j], rows);
                 }
             }
         }
@@ -296,6 +305,16 @@ struct XSrc {
 // no global load the waits would have to cover)
 template <int MB, bool XL>
 DEV void load_x(const XSrc & X, int M, int64_t K, int64_t b, int r, int q, u32x4 (&xa)[MB][4]) {
+    if (XL) {
+        // LDS rows are zero-padded to 128 KB columns; rows >= M read row M - 1 (their MFMA rows are
+        // never stored), so the reads need no masks
+        for (int mb = 0; mb < MB; mb++) {
+            const int m = 16 * mb + r < M ? 16 * mb + r : M - 1;
+            const uint16_t * base = X.xs + (uint32_t) m * (uint32_t) X.xls + (uint32_t) b * 128u + 8u * q;
+            for (int j = 0; j < 4; j++) xa[mb][j] = *LDS_U32X4(base + 32 * j);
+        }
+        return;
+    }
     for (int mb = 0; mb < MB; mb++) {
         const int m = 16 * mb + r;
         int64_t row = m;
@@ -358,7 +377,7 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
                 for (int j = 0; j < GPB; j++)
                     cs[mb][j] = *(const __attribute__((address_space(3))) f32x4 *) (X.xsum + ((c0 + i) * GPB + j) * 16 +
                                                                                    16 * mb + 4 * q);
-            qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, acc);
+            qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, M, acc);
         }
     } else {                              // x from global memory: the chunk's x loads first
         u32x4 xa[NB][MB][4];
@@ -367,7 +386,7 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
             if (c0 + i < b1) {
                 f32x4 cs[MB][4];
                 xsum_mfma<FMT, MB>(xa[i], cs);
-                qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], cs, mag, acc);
+                qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], cs, mag, M, acc);
             }
     }
 }
