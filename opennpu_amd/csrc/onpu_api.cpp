@@ -171,8 +171,10 @@ struct Plan {
 
 // Workgroup = tw tile groups x kw K parts; each wave streams bpw K blocks of its tile group (rt row
 // tiles) through a two-chunk pipeline of nb blocks. The plan aims at ~4096 waves with an equal
-// contiguous share of 4..8 blocks (4..8 KiB of nibbles) each, at most 2 tile groups per
-// workgroup with at least 512 workgroups, and x staged in LDS (xl) when M rows of K fit in 48 KiB.
+// contiguous share of 4..8 blocks (4..8 KiB of nibbles) each (up to 16 when there are 4096 or
+// more tile groups, as for a vocabulary-sized LM head), at most 2 tile groups per workgroup (4
+// with several x rows, whose LDS staging then serves more tiles) with at least 512 workgroups,
+// and x staged in LDS (xl) when M rows of K and their column sums fit in 52 KiB.
 // ACT pairs gate tile t with up tile t + NT/2, so tw divides NT/2 there. (Sweeps of kw, tw and nb
 // over the Qwen3-8B and 151936-row LM-head shapes on MI355X put the optimum there.)
 Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
@@ -180,11 +182,12 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     p.rt = epi == EPI_ACT_ ? 2 : 1;
     const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2 + KB * (fmt == ONPU_G128S ? 1 : 4) * 64;
-    p.xl = (p.mb == 1 && xbytes <= 48 * 1024) ? 1 : 0;
+    p.xl = (p.mb == 1 && xbytes <= 52 * 1024) ? 1 : 0;   // + reduction buffer <= 64 KiB (checked at launch)
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
     const int64_t groups = epi == EPI_ACT_ ? NT / 2 : NT;
-    const int64_t per = std::min<int64_t>(8, std::max<int64_t>(4, (groups * slots * KB + 4095) / 4096));
+    const int64_t per = std::min<int64_t>(groups * slots >= 4096 ? 16 : 8,
+                                          std::max<int64_t>(4, (groups * slots * KB + 4095) / 4096));
     int64_t kw = std::min<int64_t>(16, std::max<int64_t>(1, (KB + per - 1) / per));
     const int ekw = env_int("ONPU_GEMV_KW", 0);
     if (ekw > 0) kw = std::min<int64_t>(ekw, KB);
@@ -202,18 +205,20 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
         if (pick) break;
     }
     if (!pick) { p.nb = 1; p.xl = 0; }
-    const int maxw = std::min(qgemv_max_waves(p.mb, p.rt, p.nb, p.xl), 32 / (p.rt * p.mb));   // LDS <= 32 KiB
+    // the reduction buffer (waves x rt x mb KiB) <= 32 KiB and, with x in LDS, <= 64 KiB together
+    const int64_t red_kib = p.xl ? std::min<int64_t>(32, (65536 - xbytes) / 1024) : 32;
+    const int maxw = std::max(1, std::min(qgemv_max_waves(p.mb, p.rt, p.nb, p.xl), (int) (red_kib / (p.rt * p.mb))));
     if (p.kw > maxw) {                               // more K per wave
         p.kw = maxw;
         p.bpw = (KB + p.kw - 1) / p.kw;
         p.kw = (int) ((KB + p.bpw - 1) / p.bpw);
     }
-    int tw = std::max(1, std::min(2, maxw / p.kw));
-    while (tw > 1 && (tw * p.kw * p.rt * p.mb > 32 || (groups + tw - 1) / tw * slots < 512 ||
+    int tw = std::max(1, std::min(M > 1 ? 4 : 2, maxw / p.kw));
+    while (tw > 1 && (tw * p.kw * p.rt * p.mb > red_kib || (groups + tw - 1) / tw * slots < 512 ||
                       (epi == EPI_ACT_ && groups % tw != 0)))
         tw--;
     const int etw = env_int("ONPU_GEMV_TW", 0);
-    if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= 32 && !(epi == EPI_ACT_ && groups % etw))
+    if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= red_kib && !(epi == EPI_ACT_ && groups % etw))
         tw = etw;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;

@@ -75,8 +75,11 @@ ONPU_HD float bf16_to_f32(uint16_t h) {
     return v.f;
 }
 
-// IEEE binary16 -> f32, exact
+// IEEE binary16 -> f32, exact (device: one v_cvt_f32_f16; fp16 denormals are kept by default)
 ONPU_HD float f16_to_f32(uint16_t h) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return (float) __builtin_bit_cast(_Float16, h);
+#endif
     const uint32_t s = (uint32_t) (h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
     union { float f; uint32_t u; } v;
     if (e == 0) {
