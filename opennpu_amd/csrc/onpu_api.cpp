@@ -337,7 +337,7 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
                             s);
     }
     // prompts: tokens grouped per expert (one pass over each routed expert's weights per 64 rows)
-    const int rows_per_item = 64, mb = 4;
+    const int rows_per_item = 64;                 // the grouped GEMM's 4 A blocks of 16 rows
     const int64_t E = gu->E, maxitems = n / rows_per_item + E;
     if ((e = f->ws[1].ensure((size_t) (E + 1) * 4)) != hipSuccess) return e;
     if ((e = f->ws[2].ensure((size_t) n * 4)) != hipSuccess) return e;
@@ -354,21 +354,14 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
     MArgs a{};
     a.W = gu->dev; a.estride = gu->dstride; a.NT = gu->g.NT; a.KB = gu->g.KB; a.N = gu->N; a.K = gu->K;
     a.x = x; a.ldx = gu->K; a.y = act; a.ldy = I; a.perm = perm; a.items = items; a.nitems = nitems; a.k = k;
-    int wg = 1;                            // LDS: wg * 2 tiles * mb * 1 KiB <= 32 KiB
-    while (wg < 4 && 2 * wg <= gu->g.KB) wg *= 2;
-    a.bpw = (gu->g.KB + wg - 1) / wg;
-    if ((e = launch_moe_grouped(gu->fmt, 0, a, mb, dim3((unsigned) (I / 16), (unsigned) maxitems), wg, s)) !=
-        hipSuccess)
-        return e;
+    a.xbytes = T * gu->K * 2;
+    // grouped GEMMs: X tiles in LDS, weights dequantized in registers
     MArgs b{};
     b.W = dn->dev; b.estride = dn->dstride; b.NT = dn->g.NT; b.KB = dn->g.KB; b.N = Nd; b.K = dn->K;
     b.x = act; b.ldx = I; b.y = o; b.ldy = Nd; b.perm = perm; b.items = items; b.nitems = nitems; b.k = k;
-    int wd = 1;
-    while (wd < 8 && 2 * wd <= dn->g.KB) wd *= 2;
-    b.bpw = (dn->g.KB + wd - 1) / wd;
-    if ((e = launch_moe_grouped(dn->fmt, 1, b, mb, dim3((unsigned) dn->g.NT, (unsigned) maxitems), wd, s)) !=
-        hipSuccess)
-        return e;
+    b.xbytes = n * I * 2;
+    if ((e = launch_moe_gemm(gu->fmt, 0, a, maxitems, s)) != hipSuccess) return e;
+    if ((e = launch_moe_gemm(dn->fmt, 1, b, maxitems, s)) != hipSuccess) return e;
     return launch_moe_combine(o, inv, w, T, k, Nd, y, yf32, s);
 }
 

@@ -44,16 +44,8 @@ hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t FN(moe)(int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s) {
-    const size_t lds = (size_t) waves * (which == 0 ? 2 : 1) * mb * 256 * sizeof(float);
-    if (which == 0) {
-        if (mb == 1) k_moe_gu<F, 1, 2><<<grid, waves * 64, lds, s>>>(a);
-        else if (mb == 2) k_moe_gu<F, 2, 2><<<grid, waves * 64, lds, s>>>(a);
-        else k_moe_gu<F, 4, 1><<<grid, waves * 64, lds, s>>>(a);
-    } else {
-        if (mb == 1) k_moe_dn<F, 1, 2><<<grid, waves * 64, lds, s>>>(a);
-        else if (mb == 2) k_moe_dn<F, 2, 2><<<grid, waves * 64, lds, s>>>(a);
-        else k_moe_dn<F, 4, 1><<<grid, waves * 64, lds, s>>>(a);
-    }
+hipError_t FN(moe_gemm)(int which, const MArgs & a, dim3 grid, hipStream_t s) {
+    if (which == 0) k_moe_gemm<F, 0><<<grid, 256, 0, s>>>(a);
+    else k_moe_gemm<F, 1><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }

@@ -8,7 +8,7 @@
 //                extra MFMA against ones; epilogues: store, SiLU(gate) * up, MoE slot sum
 //   k_qgemm      M > 64 (prefill): x tile in LDS, int4 tile dequantized to bf16 RNE((u-8)s) in
 //                registers and fed to v_mfma_f32_16x16x32_bf16, fp32 accumulate
-//   k_moe_gu/dn  grouped expert products over a device work list
+//   k_moe_gemm   grouped expert products (MoE prompts) over a device work list
 #pragma once
 #include <hip/hip_runtime.h>
 #include "onpu_common.h"
@@ -613,25 +613,26 @@ DEV void par_sc(const Par<FMT> & p, int j, float & s, float & c) {
 // weight tiles from its L2. The host keeps M * ldx * 2 below 2^31 (32-bit buffer offsets).
 typedef __attribute__((address_space(3))) void lds_void;
 
-// one 128-wide K block of the GEMM: 4 steps of (dequantize NTW weight fragments, 8 NTW MFMAs).
-// NTW = 2: the A fragments of step j + 1 are read from LDS before step j's MFMAs are issued, and
+// one 128-wide K block of the GEMM: 4 steps of (dequantize NTW weight fragments, MBG NTW MFMAs),
+// X from the LDS fragments [mb][j][lane] of MBG 16-row A blocks.
+// NTW <= 3: the A fragments of step j + 1 are read from LDS before step j's MFMAs are issued, and
 // step j's dequant runs while step j's reads are in flight. NTW = 4 has no registers to spare for
 // that and reads each step's fragments at the step's start.
-template <int FMT, int NTW>
+template <int FMT, int NTW, int MBG>
 DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int lane,
-                    f32x4 (&acc)[8][NTW]) {
+                    f32x4 (&acc)[MBG][NTW]) {
     constexpr bool PIPE = NTW <= 3;
-    u32x4 xa[PIPE ? 2 : 1][8];
+    u32x4 xa[PIPE ? 2 : 1][MBG];
     if (PIPE) {
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + 0) * 64 + lane]);
+        for (int mb = 0; mb < MBG; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + 0) * 64 + lane]);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int cur = PIPE ? (j & 1) : 0;
         if (!PIPE) {
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + j) * 64 + lane]);
+            for (int mb = 0; mb < MBG; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + j) * 64 + lane]);
         }
         if (PIPE) {
             u32x4 bw[NTW];
@@ -643,10 +644,11 @@ DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&
             }
             if (j < 3) {
 #pragma unroll
-                for (int mb = 0; mb < 8; mb++) xa[(j + 1) & 1][mb] = *LDS_U32X4(&xsb[(mb * 4 + j + 1) * 64 + lane]);
+                for (int mb = 0; mb < MBG; mb++)
+                    xa[(j + 1) & 1][mb] = *LDS_U32X4(&xsb[(mb * 4 + j + 1) * 64 + lane]);
             }
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++)
+            for (int mb = 0; mb < MBG; mb++)
 #pragma unroll
                 for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa[cur][mb], bw[i], acc[mb][i]);
         } else {                          // one weight fragment live at a time
@@ -656,7 +658,7 @@ DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&
                 par_sc<FMT>(pr[i], j, sc, cc);
                 const u32x4 bw = dequant8<FMT>(wr[i][j], sc, cc);
 #pragma unroll
-                for (int mb = 0; mb < 8; mb++) acc[mb][i] = mfma(xa[0][mb], bw, acc[mb][i]);
+                for (int mb = 0; mb < MBG; mb++) acc[mb][i] = mfma(xa[0][mb], bw, acc[mb][i]);
             }
         }
         // keep each step's work within the step: hoisting later steps forward only lengthens live
@@ -760,7 +762,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         // even block from (xs0, wa) while block b + 1 streams into (xs1, wb)
         gemm_load_x(xr, xo, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, xs1);
         gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wb, pb);
-        gemm_block<FMT, NTW>(xs0, wa, pa, lane, acc);
+        gemm_block<FMT, NTW, 8>(xs0, wa, pa, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
         // odd block from (xs1, wb) while block b + 2 streams into (xs0, wa)
@@ -768,11 +770,11 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
             gemm_load_x(xr, xo, b + 2, ktail && b + 3 == a.KB, a.K, wave, q, xs0);
             gemm_load_w<FMT, NTW>(wrs, b + 2, lane, r, wa, pa);
         }
-        gemm_block<FMT, NTW>(xs1, wb, pb, lane, acc);
+        gemm_block<FMT, NTW, 8>(xs1, wb, pb, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
-    if (b < a.KB) gemm_block<FMT, NTW>(xs0, wa, pa, lane, acc);
+    if (b < a.KB) gemm_block<FMT, NTW, 8>(xs0, wa, pa, lane, acc);
     // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
 #pragma unroll
     for (int mb = 0; mb < 8; mb++)
@@ -788,74 +790,98 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         }
 }
 
-// grouped gate_up (+ SiLU * up) over work items: blockIdx.y = item, blockIdx.x = gate tile t.
-// Rows of the item: perm[first .. first + rows) -> token = entry / k (x row), output row = position.
-template <int FMT, int MB, int NB>
-__global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_gu(MArgs a) {
-    extern __shared__ float red[];
+// ------------------------------------------------------------------ MoE prefill: grouped GEMM
+// Work item = (expert e, first permuted position, rows <= 64) from k_moe_permute; blockIdx.y =
+// item, blockIdx.x = a group of output columns. Workgroup: 4 waves x 2 weight tiles, 64 rows of X
+// (the item's rows, gathered) as 4 A blocks; per 128-wide K block the X tile (16 KiB of A
+// fragments) is filled by buffer loads straight to LDS, each lane from its own row (rows past the
+// item land as zeros), and each wave dequantizes its two weight tiles in registers (the k_qgemm
+// scheme over one expert's weights).
+//   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = 4 blockIdx.x + w and up tile
+//           g + NT / 2; act[position][16 g + r] = bf16(silu(gate) * up)
+//   WHICH 1 (down): wave w holds tiles 8 blockIdx.x + 2 w + {0, 1}; o[position][n] = fp32
+// X rows: WHICH 0 token perm[position] / k of x [T][K]; WHICH 1 position of act [T k][K].
+template <int FMT, int WHICH>
+__global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
+    constexpr int MBG = 4;
+    __shared__ u32x4 xs0[MBG * 4 * 64], xs1[MBG * 4 * 64];     // 2 x 16 KiB
     const int item = blockIdx.y;
     if (item >= *a.nitems) return;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15;
+    const int q = lane >> 4;
     const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
     const uint8_t * W = a.W + (int64_t) e * a.estride;
-    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
-    // x rows of this item: token = perm / k
-    __shared__ int32_t xr[64];
-    if (threadIdx.x < 64) xr[threadIdx.x] = threadIdx.x < rows ? a.perm[first + threadIdx.x] / a.k : -1;
-    __syncthreads();
-    const uint8_t * tb[2];
-    int64_t tile[2] = {(int64_t) blockIdx.x, (int64_t) blockIdx.x + gridDim.x};
-    for (int rt = 0; rt < 2; rt++) tb[rt] = tile[rt] < a.NT ? W + tile[rt] * a.KB * BLK : nullptr;
-    const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
-    f32x4 acc[2][MB];
-    const XSrc X{a.x, a.ldx, xr, nullptr, 0, nullptr};
-    qacc_run<FMT, MB, 2, NB, false>(tb, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
-    constexpr int PER = 2 * MB * 256;
-    for (int rt = 0; rt < 2; rt++)
-        for (int mb = 0; mb < MB; mb++)
-            for (int v = 0; v < 4; v++) red[wave * PER + ((rt * MB + mb) * 4 + v) * 64 + lane] = acc[rt][mb][v];
-    __syncthreads();
-    for (int o = threadIdx.x; o < MB * 256; o += blockDim.x) {
-        const int mb = (o / 256) % MB, v = (o / 64) % 4, l = o % 64;
-        const int m = 16 * mb + 4 * (l >> 4) + v;
-        const int64_t n = 16 * tile[0] + (l & 15);
-        if (m >= rows || n >= a.N / 2) continue;
-        float g = 0.f, u = 0.f;
-        for (int w = 0; w < nw; w++) { g += red[w * PER + o]; u += red[w * PER + MB * 256 + o]; }
-        ((uint16_t *) a.y)[(int64_t) (first + m) * a.ldy + n] = f32_to_bf16(silu_f(g) * u);
+    int64_t t[2];
+    if (WHICH == 0) { t[0] = (int64_t) blockIdx.x * 4 + wave; t[1] = t[0] + a.NT / 2; }
+    else { t[0] = (int64_t) blockIdx.x * 8 + 2 * wave; t[1] = t[0] + 1; }
+    const bool ok0 = WHICH == 0 ? t[0] < a.NT / 2 : t[0] < a.NT;
+    const bool ok1 = WHICH == 0 ? ok0 : t[1] < a.NT;
+    __amdgpu_buffer_rsrc_t wrs[2];
+    for (int i = 0; i < 2; i++) {
+        const int64_t tt = (i == 0 ? ok0 : ok1) ? t[i] : 0;
+        wrs[i] = __builtin_amdgcn_make_buffer_rsrc((void *) (W + tt * a.KB * BLK), (short) 0,
+                                                   (int) (uint32_t) (a.KB * BLK), 0x00020000);
     }
-}
-
-// grouped down over work items: rows are act rows at positions first .. first + rows (contiguous);
-// output o[position][N] fp32
-template <int FMT, int MB, int NB>
-__global__ __launch_bounds__(MB == 1 ? 1024 : 512) void k_moe_dn(MArgs a) {
-    extern __shared__ float red[];
-    const int item = blockIdx.y;
-    if (item >= *a.nitems) return;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
-    const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
-    const uint8_t * W = a.W + (int64_t) e * a.estride;
-    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
-    const uint8_t * tb[1];
-    int64_t tile = blockIdx.x;
-    tb[0] = tile < a.NT ? W + tile * a.KB * BLK : nullptr;
-    const int64_t b0 = (int64_t) wave * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
-    f32x4 acc[1][MB];
-    const XSrc X{a.x + (int64_t) first * a.ldx, a.ldx, nullptr, nullptr, 0, nullptr};
-    qacc_run<FMT, MB, 1, NB, false>(tb, b0, b1, X, rows, a.K, [] {}, [] {}, acc);
-    constexpr int PER = MB * 256;
-    for (int mb = 0; mb < MB; mb++)
-        for (int v = 0; v < 4; v++) red[wave * PER + (mb * 4 + v) * 64 + lane] = acc[0][mb][v];
-    __syncthreads();
-    for (int o = threadIdx.x; o < PER; o += blockDim.x) {
-        const int mb = o / 256, v = (o / 64) % 4, l = o % 64;
-        const int m = 16 * mb + 4 * (l >> 4) + v;
-        const int64_t n = 16 * tile + (l & 15);
-        if (m >= rows || n >= a.N) continue;
-        float s = 0.f;
-        for (int w = 0; w < nw; w++) s += red[w * PER + o];
-        ((float *) a.y)[(int64_t) (first + m) * a.ldy + n] = s;
+    // this wave's 4 X fragments f = 4 wave + i: (mb, j) = (f / 4, f % 4) = (wave, i)
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) a.xbytes, 0x00020000);
+    const int row = 16 * wave + r;
+    uint32_t xrow = 0x80000000u;
+    if (row < rows) {
+        const int64_t src = WHICH == 0 ? (int64_t) (a.perm[first + row] / a.k) : (int64_t) (first + row);
+        xrow = (uint32_t) (src * a.ldx * 2);
     }
+    const bool ktail = a.K % 128 != 0;
+    auto load_xt = [&](int64_t b, u32x4 * buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t off = xrow == 0x80000000u ? xrow : xrow + (uint32_t) (32 * i + 8 * q) * 2;
+            if (ktail && 128 * b + 32 * i + 8 * q >= a.K) off = 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + (4 * wave + i) * 64), 16, off,
+                                                     (uint32_t) (256 * b), 0, 0);
+        }
+    };
+    f32x4 acc[MBG][2];
+#pragma unroll
+    for (int mb = 0; mb < MBG; mb++) acc[mb][0] = acc[mb][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    u32x4 wa[2], wb[2];
+    Par<FMT> pa[2], pb[2];
+    load_xt(0, xs0);
+    gemm_load_w<FMT, 2>(wrs, 0, lane, r, wa, pa);
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    int64_t b = 0;
+    for (; b + 2 <= a.KB; b += 2) {
+        load_xt(b + 1, xs1);
+        gemm_load_w<FMT, 2>(wrs, b + 1, lane, r, wb, pb);
+        gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
+        if (b + 2 < a.KB) {
+            load_xt(b + 2, xs0);
+            gemm_load_w<FMT, 2>(wrs, b + 2, lane, r, wa, pa);
+        }
+        gemm_block<FMT, 2, MBG>(xs1, wb, pb, lane, acc);
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
+    }
+    if (b < a.KB) gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
+    // lane (q, r) holds rows 4 q + v of A block mb, column r of its tiles
+#pragma unroll
+    for (int mb = 0; mb < MBG; mb++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int rr = 16 * mb + 4 * q + v;
+            if (rr >= rows) continue;
+            const int64_t pos = first + rr;
+            if (WHICH == 0) {
+                if (ok0)
+                    ((uint16_t *) a.y)[pos * a.ldy + 16 * t[0] + r] =
+                        f32_to_bf16(silu_f(acc[mb][0][v]) * acc[mb][1][v]);
+            } else {
+                if (ok0 && 16 * t[0] + r < a.N) ((float *) a.y)[pos * a.ldy + 16 * t[0] + r] = acc[mb][0][v];
+                if (ok1 && 16 * t[1] + r < a.N) ((float *) a.y)[pos * a.ldy + 16 * t[1] + r] = acc[mb][1][v];
+            }
+        }
 }
-

@@ -285,13 +285,16 @@ hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_moe_grouped(int fmt, int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s) {
-    if ((size_t) waves * (which == 0 ? 2 : 1) * mb * 1024 > 32768) return hipErrorInvalidValue;
+hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s) {
+    if (a.xbytes <= 0 || a.xbytes >= ((int64_t) 1 << 31) || maxitems <= 0 || maxitems > 65535) return hipErrorInvalidValue;
+    if (which == 0 && (a.NT % 2 || a.N != 16 * a.NT)) return hipErrorInvalidValue;   // gate | up halves of whole tiles
+    const int64_t gx = which == 0 ? (a.NT / 2 + 3) / 4 : (a.NT + 7) / 8;
+    const dim3 grid((unsigned) gx, (unsigned) maxitems);
     switch (fmt) {
-        case 0: return moe_f0(which, a, mb, grid, waves, s);
-        case 1: return moe_f1(which, a, mb, grid, waves, s);
-        case 2: return moe_f2(which, a, mb, grid, waves, s);
-        case 3: return moe_f3(which, a, mb, grid, waves, s);
+        case 0: return moe_gemm_f0(which, a, grid, s);
+        case 1: return moe_gemm_f1(which, a, grid, s);
+        case 2: return moe_gemm_f2(which, a, grid, s);
+        case 3: return moe_gemm_f3(which, a, grid, s);
     }
     return hipErrorInvalidValue;
 }

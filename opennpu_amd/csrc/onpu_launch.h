@@ -33,7 +33,7 @@ struct GArgs {
     int yf32;
 };
 
-// grouped MoE products over a device work list (expert, first position, rows)
+// grouped MoE products (k_moe_gemm) over a device work list (expert, first position, rows)
 struct MArgs {
     const uint8_t * W;
     int64_t estride, NT, KB, N, K;
@@ -45,7 +45,7 @@ struct MArgs {
     const int32_t * items;    // [nitems][3]
     const int32_t * nitems;
     int k;
-    int64_t bpw;
+    int64_t xbytes;           // k_moe_gemm: bytes of x (buffer range of the gathered rows, < 2^31)
 };
 
 hipError_t launch_repack(int fmt, const uint8_t * st, int64_t sstride, int64_t N, int64_t K, uint8_t * out,
@@ -60,7 +60,8 @@ hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renor
                         hipStream_t s);
 hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_per_item, int32_t * off, int32_t * perm,
                               int32_t * items, int32_t * nitems, hipStream_t s);
-hipError_t launch_moe_grouped(int fmt, int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s);
+// grouped GEMM over the work items (k_moe_gemm): grid.x column groups (gate_up: NT / 8, down: NT / 8)
+hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s);
 hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
 hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
@@ -93,7 +94,7 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
     hipError_t qgemv_f##id(int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,       \
                            size_t lds, hipStream_t s);                                                    \
     hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
-    hipError_t moe_f##id(int which, const MArgs & a, int mb, dim3 grid, int waves, hipStream_t s);
+    hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);
 ONPU_FMT_DECL(0)
 ONPU_FMT_DECL(1)
 ONPU_FMT_DECL(2)

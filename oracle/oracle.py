@@ -202,19 +202,20 @@ def argmax(v):
     return out
 
 
-def moe_layer(fmt, gu_st, dn_st, E, H, I, x_bf, ids, w):
+def moe_layer(fmt, gu_st, dn_st, E, H, I, x_bf, ids, w, bf16w=False):
     """A routed-expert FFN layer as reference.py:71-84 computes it (dequantized experts, fp32 act),
     with the two rounding points of the device path: gate_up in fp64 -> fp32, act -> bf16 RNE as the
     down input (the device input conversion, opennpu_core.hpp:418-424), down in fp64, weighted sum.
-    gu_st / dn_st: E staging blobs; returns y [T][H] float64."""
+    gu_st / dn_st: E staging blobs; returns y [T][H] float64. bf16w: the expert weights rounded to
+    bf16 (RNE) as the reference device's MAC sees them (gemv_any.cc:65,106-107)."""
     T, k = ids.shape
     y = np.zeros((T, H), np.float64)
     xb = np.asarray(x_bf, np.uint16).reshape(T, H)
     for e in np.unique(ids):
         rows, slots = np.nonzero(ids == e)
-        g = qmm(fmt, gu_st[e], 2 * I, H, xb[rows]).astype(np.float32)
+        g = qmm(fmt, gu_st[e], 2 * I, H, xb[rows], bf16w=bf16w).astype(np.float32)
         a = f2bf_np(silu_mul(g))
-        d = qmm(fmt, dn_st[e], H, I, a)
+        d = qmm(fmt, dn_st[e], H, I, a, bf16w=bf16w)
         y[rows] += w[rows, slots][:, None].astype(np.float64) * d
     return y
 
