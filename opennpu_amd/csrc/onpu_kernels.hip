@@ -61,7 +61,9 @@ __global__ __launch_bounds__(64) void k_route(const float * __restrict__ logits,
     // selection keys: probability bits + 1 (p >= 0, so the bits order like the values); 0 = taken
     uint32_t key[4];
     for (int i = 0; i < 4; i++) key[i] = 4 * lane + i < E ? __float_as_uint(p[i]) + 1u : 0u;
-    float ws = 0.f;
+    // lane j keeps the j-th pick; one coalesced store per output at the end
+    float ws = 0.f, my_p = 0.f;
+    int my_id = 0;
     for (int j = 0; j < k; j++) {
         uint32_t lb = 0;
         int li = 0;
@@ -75,10 +77,12 @@ __global__ __launch_bounds__(64) void k_route(const float * __restrict__ logits,
             if (lane == first && i == li) key[i] = 0u;
         const float pj = __uint_as_float(best - 1u) / sum;
         ws += pj;
-        if (lane == 0) { ids[t * k + j] = bi; w[t * k + j] = pj; }
+        if (lane == j) { my_id = bi; my_p = pj; }
     }
-    if (renorm && lane == 0)
-        for (int j = 0; j < k; j++) w[t * k + j] = w[t * k + j] / ws;
+    if (lane < k) {
+        ids[t * k + lane] = my_id;
+        w[t * k + lane] = renorm ? my_p / ws : my_p;
+    }
 }
 
 // ------------------------------------------------------------------ MoE permutation
@@ -96,9 +100,21 @@ __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict
     __syncthreads();
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&cnt[ids[i]], 1);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t s = 0, it = 0;
-        for (int e = 0; e < E; e++) {
+    if (threadIdx.x < 64) {
+        // wave 0: lane l owns experts [l * EP, (l + 1) * EP); exclusive scans of rows and items
+        const int lane = threadIdx.x, EP = (E + 63) / 64, e0 = lane * EP, e1 = e0 + EP < E ? e0 + EP : E;
+        int32_t rs = 0, is = 0;
+        for (int e = e0; e < e1; e++) {
+            rs += cnt[e];
+            is += (cnt[e] + rows_per_item - 1) / rows_per_item;
+        }
+        int32_t ri = rs, ii = is;                     // inclusive scans across lanes
+        for (int o = 1; o < 64; o <<= 1) {
+            const int32_t a = __shfl_up(ri, o), b = __shfl_up(ii, o);
+            if (lane >= o) { ri += a; ii += b; }
+        }
+        int32_t s = ri - rs, it = ii - is;            // exclusive: this lane's first row / item
+        for (int e = e0; e < e1; e++) {
             pos[e] = s;
             off[e] = s;
             for (int32_t r0 = 0; r0 < cnt[e]; r0 += rows_per_item) {
@@ -109,8 +125,10 @@ __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict
             }
             s += cnt[e];
         }
-        off[E] = s;
-        *nitems = it;
+        if (lane == 63) {
+            off[E] = ri;
+            *nitems = ii;
+        }
     }
     __syncthreads();
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
