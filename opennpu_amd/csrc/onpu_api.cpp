@@ -174,7 +174,8 @@ struct Plan {
 // contiguous share of 4..8 blocks (4..8 KiB of nibbles) each (up to 16 when there are 4096 or
 // more tile groups, as for a vocabulary-sized LM head), at most 2 tile groups per workgroup (4
 // with several x rows, whose LDS staging then serves more tiles) with at least 512 workgroups,
-// and x staged in LDS (xl) when M rows of K and their column sums fit in 52 KiB.
+// and x staged in LDS (xl) when M rows of K and their column sums fit in 52 KiB (112 KiB with
+// 1024 or more tile groups).
 // ACT pairs gate tile t with up tile t + NT/2, so tw divides NT/2 there. (Sweeps of kw, tw and nb
 // over the Qwen3-8B and 151936-row LM-head shapes on MI355X put the optimum there.)
 Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
@@ -182,7 +183,10 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     p.rt = epi == EPI_ACT_ ? 2 : 1;
     const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2 + KB * (fmt == ONPU_G128S ? 1 : 4) * 64;
-    p.xl = (p.mb == 1 && xbytes <= 52 * 1024) ? 1 : 0;   // + reduction buffer <= 64 KiB (checked at launch)
+    // gfx950 gives a workgroup up to 160 KiB of LDS. x in LDS up to 52 KiB keeps several workgroups
+    // per CU; up to 112 KiB (one workgroup per CU) only pays off with many tile groups to share it
+    const int64_t groups0 = epi == EPI_ACT_ ? NT / 2 : NT;
+    p.xl = (p.mb == 1 && (xbytes <= 52 * 1024 || (xbytes <= 112 * 1024 && groups0 * slots >= 1024))) ? 1 : 0;
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
     const int64_t groups = epi == EPI_ACT_ ? NT / 2 : NT;
@@ -205,8 +209,8 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
         if (pick) break;
     }
     if (!pick) { p.nb = 1; p.xl = 0; }
-    // the reduction buffer (waves x rt x mb KiB) <= 32 KiB and, with x in LDS, <= 64 KiB together
-    const int64_t red_kib = p.xl ? std::min<int64_t>(32, (65536 - xbytes) / 1024) : 32;
+    // the reduction buffer (waves x rt x mb KiB) <= 32 KiB and, with x in LDS, <= 160 KiB together
+    const int64_t red_kib = p.xl ? std::min<int64_t>(32, (163840 - xbytes) / 1024) : 32;
     const int maxw = std::max(1, std::min(qgemv_max_waves(p.mb, p.rt, p.nb, p.xl), (int) (red_kib / (p.rt * p.mb))));
     if (p.kw > maxw) {                               // more K per wave
         p.kw = maxw;

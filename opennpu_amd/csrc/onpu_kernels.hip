@@ -273,7 +273,7 @@ int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl) {
 int qgemv_max_waves(int mb, int rt, int nb, int xl) { return qgemv_lb(mb, rt, nb, xl) / 64; }
 
 // LDS per workgroup: the reduction buffer plus, with xl, the staged x rows and their column sums
-// (<= 64 KiB together)
+// (<= 160 KiB together)
 hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,
                         hipStream_t s) {
     if (waves < 1 || waves > qgemv_max_waves(mb, rt, nb, xl) || !qgemv_has_variant(epi, mb, rt, nb, xl))
@@ -282,7 +282,7 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
     // x rows, then the column sums [KB * groups per block][16] floats
     const size_t xb = xl ? (size_t) a.M * a.xls * 2 + (size_t) a.KB * (fmt == 2 ? 1 : 4) * 64 : 0;
     if (xl && a.M > 16) return hipErrorInvalidValue;
-    if (red > 32768 || red + xb > 65536) return hipErrorInvalidValue;
+    if (red > 32768 || red + xb > 163840) return hipErrorInvalidValue;      // gfx950: 160 KiB per workgroup
     if (xl && a.xls < a.KB * 128) return hipErrorInvalidValue;
     switch (fmt) {
         case 0: return qgemv_f0(epi, a, mb, rt, nb, xl, grid, waves, red + xb, s);

@@ -93,10 +93,10 @@ def test_launch_plans_are_built_variants(fmt):
                 mb, rt, nb, xl, tw, kw, bpw, gx, built, maxw = tuple(out)
                 assert built, (fmt, N, K, M, epi, tuple(out))
                 assert tw * kw <= maxw and tw * kw * rt * mb <= 32
-                if xl:                             # x rows + column sums + reduction <= 64 KiB
+                if xl:                             # x rows + column sums + reduction <= 160 KiB
                     gpb = 1 if fmt == orc.FMT_G128S else 4
                     xb = M * (KB * 128 + 8) * 2 + KB * gpb * 64
-                    assert mb == 1 and xb + tw * kw * rt * mb * 1024 <= 65536, (fmt, N, K, M, tuple(out))
+                    assert mb == 1 and xb + tw * kw * rt * mb * 1024 <= 163840, (fmt, N, K, M, tuple(out))
                 assert kw * bpw >= KB and (kw - 1) * bpw < KB
                 NT = -(-N // 16)
                 groups = NT // 2 if epi == 1 else NT
