@@ -95,7 +95,7 @@ def bf16_tensor(torch, bits):
 
 
 # ------------------------------------------------------------------ workloads
-def decode_layers(torch, QMatrix, syn, Ms, steps, warmup):
+def decode_layers(torch, QMatrix, QChain, syn, Ms, steps, warmup):
     """the headline step at each M; returns {M: result} and the gate+up roofline measurement"""
     mats = {}
     for name, N, K in QWEN3_8B:
@@ -124,6 +124,22 @@ def decode_layers(torch, QMatrix, syn, Ms, steps, warmup):
         byts = LAYERS * sum(wbytes(G128S, N, K) + M * K * 2 + M * N * 2 for _, N, K in QWEN3_8B)
         res[M] = {"ms_per_step": t * 1e3, "GBps": byts / t / 1e9, "hbm_frac": byts / t / HBM_PEAK,
                   "bytes_per_step": byts, "tokens_per_s_equiv": M / t, "launch": g.mode}
+        # the same 144 GEMVs as one chained launch (grid barrier between consecutive GEMVs)
+        order = [(name, layer) for layer in range(LAYERS) for name, _, _ in QWEN3_8B]
+        kdim = {name: K for name, _, K in QWEN3_8B}
+        ch = QChain([mats[nm][ly] for nm, ly in order], [xs[kdim[nm]] for nm, ly in order], [ys[nm] for nm, ly in order])
+        gc = GraphStep(ch.run, torch)
+        gc()
+        torch.cuda.synchronize()
+        # the chain's split of K may differ from the single launches': equal to fp32 rounding
+        d = (ys["gate_up"].float() - y_graph.float()).abs().max() / y_graph.float().abs().max()
+        assert d <= 1e-2, f"chained gate+up differs from the per-launch result by {d:.3e}"
+        tc = time_it(torch, gc, steps, warmup)
+        if ch.status() != 0:
+            raise RuntimeError("chained decode: a grid barrier wait timed out")
+        res[M]["chained"] = {"ms_per_step": tc * 1e3, "GBps": byts / tc / 1e9, "hbm_frac": byts / tc / HBM_PEAK,
+                             "launch": "one chained launch per step (" + gc.mode + ")"}
+        ch.free()
         # per-matrix kernels: a graph of the 36 copies of each matrix, back to back
         per = {}
         for name, N, K in QWEN3_8B:
@@ -313,7 +329,7 @@ def main():
         sys.exit(2)
     import torch
     from opennpu_amd import require_gpu, synthetic as syn
-    from opennpu_amd.device import QFfn, QMatrix
+    from opennpu_amd.device import QChain, QFfn, QMatrix
     require_gpu()
     torch.cuda.set_device(0)
     if args.profile:
@@ -321,7 +337,7 @@ def main():
         return
     t_all = time.perf_counter()
     log("decode layers ...")
-    dec = decode_layers(torch, QMatrix, syn, (1,) if args.quick else (1, 4, 8), args.steps, args.warmup)
+    dec = decode_layers(torch, QMatrix, QChain, syn, (1,) if args.quick else (1, 4, 8), args.steps, args.warmup)
     head = dec[1]
     configs = {"qwen3_8b_decode": {f"M{M}": v for M, v in dec.items()}}
     if not args.quick:

@@ -47,6 +47,7 @@ void set_err(const char * what) { g_err = what; }
 
 struct Device {
     int ok = 0;
+    int cus = 0;
     hipStream_t stream = nullptr;
 };
 
@@ -64,6 +65,7 @@ Device & device() {
             return;
         }
         if (hipSetDevice(0) != hipSuccess) return;
+        d.cus = p.multiProcessorCount;
         if (hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking) != hipSuccess) return;
         d.ok = 1;
     });
@@ -725,6 +727,85 @@ int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, i
     if (!f->fused) { set_err("onpu_moe_ffn_dev: this FFN shape has no fused path"); return -1; }
     HIPR(ffn_core(f, (const uint16_t *) x, T, ids, k, w, y, y_f32, (hipStream_t) stream));
     return 0;
+}
+
+// ---------------------------------------------------------------- chained decode GEMVs
+struct Chain {
+    int fmt = 0, n = 0, M = 0, yf32 = 0, grid = 0, per_cu = 0;
+    size_t lds = 0;
+    int64_t xls = 0;
+    DBuf entries, bar;
+};
+
+void * onpu_chain_new(void * const * handles, const void * const * xs, void * const * ys, int n, int64_t M,
+                      int y_f32) {
+    if (!device().ok || n < 1 || M < 1 || M > 16) { set_err("onpu_chain_new: needs a GPU, n >= 1, 1 <= M <= 16"); return nullptr; }
+    const int fmt = ((Mat4 *) handles[0])->fmt;
+    int64_t kbmax = 0;
+    std::vector<ChainEntry> es((size_t) n);
+    for (int i = 0; i < n; i++) {
+        const Mat4 * m = (const Mat4 *) handles[i];
+        if (m->fmt != fmt || m->E != 1) { set_err("onpu_chain_new: entries need one format and dense handles"); return nullptr; }
+        ChainEntry & e = es[(size_t) i];
+        e.W = m->dev; e.x = (const uint16_t *) xs[i]; e.y = ys[i];
+        e.NT = m->g.NT; e.KB = m->g.KB; e.N = m->N; e.K = m->K;
+        // K split across 8 waves for up to 512 row tiles, else 4 (2 tiles per workgroup), else 2
+        e.kw = e.NT <= 512 ? 8 : (e.NT <= 4096 ? 4 : 2);
+        while (e.kw > 1 && e.kw > e.KB) e.kw /= 2;
+        e.tw = CHAIN_WAVES / e.kw;
+        e.bpw = (e.KB + e.kw - 1) / e.kw;
+        e.groups = (e.NT + e.tw - 1) / e.tw;
+        kbmax = std::max(kbmax, e.KB);
+    }
+    auto * c = new Chain;
+    c->fmt = fmt; c->n = n; c->M = (int) M; c->yf32 = y_f32;
+    c->xls = kbmax * 128 + 8;
+    c->lds = (size_t) CHAIN_WAVES * 256 * 4 + (size_t) M * c->xls * 2 + (size_t) kbmax * (fmt == ONPU_G128S ? 1 : 4) * 64;
+    const int per_cu = chain_occupancy(fmt, c->lds);
+    if (c->lds > 163840 || per_cu < 1) { set_err("onpu_chain_new: x rows do not fit in LDS"); delete c; return nullptr; }
+    c->per_cu = per_cu;
+    c->grid = std::min(per_cu, std::max(1, env_int("ONPU_CHAIN_PER_CU", 2))) * device().cus;
+    hipError_t e = c->entries.ensure(sizeof(ChainEntry) * (size_t) n);
+    if (e == hipSuccess) e = c->bar.ensure(sizeof(int32_t) * (size_t) (n + 1));
+    if (e == hipSuccess) e = hipMemcpy(c->entries.p, es.data(), sizeof(ChainEntry) * (size_t) n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(c->bar.p, 0, sizeof(int32_t) * (size_t) (n + 1));
+    if (e != hipSuccess) { set_err(hipGetErrorString(e)); delete c; return nullptr; }
+    return c;
+}
+
+int onpu_chain_run(void * h, void * stream) {
+    auto * c = (Chain *) h;
+    ChainArgs a{};
+    a.e = c->entries.as<ChainEntry>(); a.n = c->n; a.M = c->M; a.yf32 = c->yf32;
+    a.bar = c->bar.as<int32_t>(); a.xls = c->xls; a.spin = 4u << 20;
+    HIPR(launch_chain(c->fmt, a, c->grid, c->lds, (hipStream_t) stream));
+    return 0;
+}
+
+int onpu_chain_status(void * h) {
+    auto * c = (Chain *) h;
+    int32_t flag = 0;
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(&flag, c->bar.as<int32_t>(sizeof(int32_t) * (size_t) c->n), 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    return flag ? 1 : 0;
+}
+
+void onpu_chain_info(void * h, int64_t * out) {
+    auto * c = (Chain *) h;
+    out[0] = c->n; out[1] = c->grid; out[2] = (int64_t) c->lds; out[3] = c->xls;
+    out[4] = c->per_cu;
+    int32_t b0 = -1;
+    if (hipDeviceSynchronize() == hipSuccess) (void) hipMemcpy(&b0, c->bar.p, 4, hipMemcpyDeviceToHost);
+    out[5] = b0;                           // arrivals at the first barrier of the last run
+}
+
+void onpu_chain_free(void * h) {
+    auto * c = (Chain *) h;
+    if (!c) return;
+    c->entries.release();
+    c->bar.release();
+    delete c;
 }
 
 // ---------------------------------------------------------------- packing

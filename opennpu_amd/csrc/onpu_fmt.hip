@@ -49,3 +49,15 @@ hipError_t FN(moe_gemm)(int which, const MArgs & a, dim3 grid, hipStream_t s) {
     else k_moe_gemm<F, 1><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }
+
+hipError_t FN(chain)(const ChainArgs & a, int grid, size_t lds, hipStream_t s) {
+    k_qgemv_chain<F><<<grid, (CHAIN_WAVES + 1) * 64, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+int FN(chain_occ)(size_t lds) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qgemv_chain<F>, (CHAIN_WAVES + 1) * 64, lds) != hipSuccess)
+        return 0;
+    return nb;
+}

@@ -391,29 +391,27 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
     }
 }
 
-// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks of NB blocks with two
-// chunk buffers: the loads of chunk i + 1 are in flight while chunk i is computed, so each wave
-// streams its K range with NB..2 NB blocks (x RT tiles) outstanding. Loads are only issued for
-// chunks that hold blocks, and every path into the loop head has exactly the chunk `ca`
-// outstanding, so the compiler's wait counts cover just the chunk being computed. pre() runs
-// before the first loads are issued and post() right after (the workgroup's LDS staging of x: its
-// loads first, then the LDS writes and the barrier while the weights stream); every wave calls
-// both, also one with no blocks. (Issuing both chunks before the barrier measured slower.)
-template <int FMT, int MB, int RT, int NB, bool XL, class Pre, class Post>
-DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const XSrc & X, int M, int64_t K, Pre pre,
-                  Post post, f32x4 (&acc)[RT][MB]) {
-    const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
-    if (tb[0] == nullptr) b1 = b0;                 // no tile: no blocks (the epilogue skips its rows)
-    const uint32_t mag = 0x43004300u;
-    for (int rt = 0; rt < RT; rt++)
-        for (int mb = 0; mb < MB; mb++) acc[rt][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+// the first chunk's loads (qacc_run's prologue; a chained launch issues them before a barrier).
+// Returns the wave's last block (the target of out-of-range slots); b1 drops to b0 without a tile.
+template <int FMT, int RT, int NB>
+DEV const uint8_t * qacc_start(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], int64_t b0, int64_t & b1) {
+    const int lane = threadIdx.x & 63, r = lane & 15;
+    if (tb[0] == nullptr) b1 = b0;
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     const uint8_t * last = b0 < b1 ? tb[0] + (b1 - 1) * BLK : nullptr;
-    WChunk<FMT, RT, NB> ca, cb;
-    pre();
     if (b0 < b1) load_chunk<FMT, RT, NB>(ca, tb, last, b0, b1, lane, r);
-    post();
+    return last;
+}
+
+// the chunk loop after qacc_start (acc accumulates; the caller zeroes it); b1 and last as
+// qacc_start left them
+template <int FMT, int MB, int RT, int NB, bool XL>
+DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], const uint8_t * last, int64_t b0,
+                   int64_t b1, const XSrc & X, int M, int64_t K, f32x4 (&acc)[RT][MB]) {
+    const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
     if (b0 >= b1) return;
+    const uint32_t mag = 0x43004300u;
+    WChunk<FMT, RT, NB> cb;
     const int64_t nc = (b1 - b0 + NB - 1) / NB;     // chunks; chunk i starts at b0 + i * NB
     int64_t i = 0;
     for (; i + 2 < nc; i += 2) {                     // chunks i + 1 and i + 2 exist
@@ -429,6 +427,26 @@ DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const
     } else {
         compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
     }
+}
+
+// One wave: tiles tb[rt] (nullptr: no tile) over blocks [b0, b1), in chunks of NB blocks with two
+// chunk buffers: the loads of chunk i + 1 are in flight while chunk i is computed, so each wave
+// streams its K range with NB..2 NB blocks (x RT tiles) outstanding. Loads are only issued for
+// chunks that hold blocks, and every path into the loop head has exactly the chunk `ca`
+// outstanding, so the compiler's wait counts cover just the chunk being computed. pre() runs
+// before the first loads are issued and post() right after (the workgroup's LDS staging of x: its
+// loads first, then the LDS writes and the barrier while the weights stream); every wave calls
+// both, also one with no blocks. (Issuing both chunks before the barrier measured slower.)
+template <int FMT, int MB, int RT, int NB, bool XL, class Pre, class Post>
+DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const XSrc & X, int M, int64_t K, Pre pre,
+                  Post post, f32x4 (&acc)[RT][MB]) {
+    for (int rt = 0; rt < RT; rt++)
+        for (int mb = 0; mb < MB; mb++) acc[rt][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    WChunk<FMT, RT, NB> ca;
+    pre();
+    const uint8_t * last = qacc_start<FMT, RT, NB>(ca, tb, b0, b1);
+    post();
+    qacc_rest<FMT, MB, RT, NB, XL>(ca, tb, last, b0, b1, X, M, K, acc);
 }
 
 // Epilogues
@@ -884,4 +902,124 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
                 if (ok1 && 16 * t[1] + r < a.N) ((float *) a.y)[pos * a.ldy + 16 * t[1] + r] = acc[mb][1][v];
             }
         }
+}
+
+
+// ------------------------------------------------------------------ chained decode GEMVs
+// One launch runs a.n GEMVs in order (M <= 16 rows, x staged in LDS). Workgroup: CHAIN_WAVES compute
+// waves + one control wave. Entry i's tile groups (tw tiles x kw K parts, tw kw = CHAIN_WAVES) go to
+// workgroups g = blockIdx.x, + gridDim.x, ... Between entries every workgroup meets at a grid
+// barrier, so entry i + 1 may read entry i's output; around it:
+//   compute waves: store y, wait for their stores, then issue the first weight chunk of their
+//     first tile group of entry i + 1 (weights do not depend on x: they stream during the barrier)
+//   control wave: arrive (release at agent scope), poll the counter (bounded: past a.spin polls it
+//     flags a.bar[n] and proceeds, so no wave can wait forever), acquire, then stage x_{i+1} and its
+//     column sums in LDS by itself, so the compute waves never wait on loads younger than their
+//     prefetch.
+// Every workgroup must be resident at once (the host sizes the grid from the occupancy).
+DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, uint16_t * xs,
+                       float * xsum) {
+    const int lane = threadIdx.x & 63, upg = gs / 8;
+    const uint32_t kp8 = (uint32_t) KB * 16, nunits = (uint32_t) M * kp8;
+    for (uint32_t u0 = 0; u0 < nunits; u0 += 64) {               // same trip count for every lane
+        const uint32_t u = u0 + lane;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        uint32_t m = 0, kk = 0;
+        if (u < nunits) {
+            m = u / kp8;
+            kk = (u - m * kp8) * 8;
+            if (kk < K) v = *(const u32x4 *) (x + (int64_t) m * K + kk);
+            *LDS_U32X4(xs + (int64_t) m * xls + kk) = v;
+        }
+        float t = 0.f;
+        for (int d = 0; d < 4; d++) t += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+        for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+        if (u < nunits && u % upg == 0) xsum[(kk / gs) * 16 + m] = t;
+    }
+}
+
+// Two workgroups of 9 waves per CU can put 6 waves on one SIMD: the launch bound asks for 6 waves
+// per SIMD (<= 80 VGPRs) so that the two always fit together.
+template <int FMT>
+__global__ __launch_bounds__((CHAIN_WAVES + 1) * 64, 6) void k_qgemv_chain(ChainArgs a) {
+    constexpr int NB = 2, GS = FMT == ONPU_G128S ? 128 : 32;
+    constexpr int BLK = 1024 + 16 * (128 / GS) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    extern __shared__ float red[];                  // [CHAIN_WAVES][256] floats, x rows, column sums
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool ctrl = wave == CHAIN_WAVES;
+    const int64_t P = gridDim.x, w = blockIdx.x;
+    uint16_t * xs = (uint16_t *) (red + CHAIN_WAVES * 256);
+    float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
+    const XSrc X{nullptr, 0, nullptr, xs, a.xls, xsum};
+    WChunk<FMT, 1, NB> ca;
+    const uint8_t * last = nullptr;
+    int64_t pb0 = 0, pb1 = 0;                       // the prefetched range of the next entry
+    bool pre = false;
+    // entry 0: the first chunks, and x_0 by the control wave (no barrier before it)
+    auto prefetch = [&](const ChainEntry & F) {
+        pre = false;
+        if (ctrl || w >= F.groups) return;
+        const int twi = wave / F.kw, kp = wave % F.kw;
+        const int64_t t = w * F.tw + twi;
+        const uint8_t * tb[1] = {t < F.NT ? F.W + t * F.KB * BLK : nullptr};
+        pb0 = (int64_t) kp * F.bpw;
+        pb1 = pb0 + F.bpw < F.KB ? pb0 + F.bpw : F.KB;
+        last = qacc_start<FMT, 1, NB>(ca, tb, pb0, pb1);
+        pre = true;
+    };
+    prefetch(a.e[0]);
+    if (ctrl) chain_stage_x(a.e[0].x, a.M, a.e[0].K, a.e[0].KB, a.xls, GS, xs, xsum);
+    __syncthreads();
+    for (int i = 0; i < a.n; i++) {
+        const ChainEntry & E = a.e[i];
+        const int twi = wave / E.kw, kp = wave % E.kw;
+        for (int64_t g = w; g < E.groups; g += P) {          // same trip count for the whole workgroup
+            f32x4 acc[1][1];
+            acc[0][0] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (!ctrl) {
+                const int64_t t = g * E.tw + twi;
+                const uint8_t * tb[1] = {t < E.NT ? E.W + t * E.KB * BLK : nullptr};
+                int64_t b0 = (int64_t) kp * E.bpw, b1 = b0 + E.bpw < E.KB ? b0 + E.bpw : E.KB;
+                if (!(pre && g == w)) last = qacc_start<FMT, 1, NB>(ca, tb, b0, b1);
+                else b1 = pb1;
+                qacc_rest<FMT, 1, 1, NB, true>(ca, tb, last, b0, b1, X, a.M, E.K, acc);
+                for (int v = 0; v < 4; v++) red[wave * 256 + v * 64 + lane] = acc[0][0][v];
+            }
+            __syncthreads();
+            // tile group g: tiles g tw + twi, each summed over its kw K parts
+            for (int o = threadIdx.x; o < E.tw * 256; o += blockDim.x) {
+                const int ti = o / 256, v = (o / 64) % 4, l = o % 64;
+                const int m = 4 * (l >> 4) + v;
+                const int64_t n = 16 * (g * E.tw + ti) + (l & 15);
+                if (m >= a.M || n >= E.N) continue;
+                float sum = 0.f;
+                for (int k2 = 0; k2 < E.kw; k2++) sum += red[(ti * E.kw + k2) * 256 + v * 64 + l];
+                store_out(E.y, a.yf32, (int64_t) m * E.N + n, sum);
+            }
+            __syncthreads();
+        }
+        pre = false;
+        if (i + 1 == a.n) break;
+        // the barrier between entries i and i + 1
+        __builtin_amdgcn_s_waitcnt(0x0f70);                  // this wave's y stores are done
+        prefetch(a.e[i + 1]);
+        __syncthreads();                                     // every wave's stores are done
+        if (ctrl) {
+            if (lane == 0) {
+                __hip_atomic_fetch_add(a.bar + i, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                uint32_t polls = 0;
+                while (__hip_atomic_load(a.bar + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (int32_t) P) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++polls > a.spin) {
+                        __hip_atomic_store(a.bar + a.n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            const ChainEntry & F = a.e[i + 1];
+            chain_stage_x(F.x, a.M, F.K, F.KB, a.xls, GS, xs, xsum);
+        }
+        __syncthreads();
+    }
 }

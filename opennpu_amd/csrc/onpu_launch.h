@@ -48,6 +48,24 @@ struct MArgs {
     int64_t xbytes;           // k_moe_gemm: bytes of x (buffer range of the gathered rows, < 2^31)
 };
 
+// chained decode GEMVs (k_qgemv_chain): entry i = y_i [M][N] = x_i [M][K] . W_i^T, in order, each
+// entry may read what earlier ones wrote
+struct ChainEntry {
+    const uint8_t * W;
+    const uint16_t * x;
+    void * y;
+    int64_t NT, KB, N, K, bpw, groups;
+    int tw, kw;               // tw * kw = CHAIN_WAVES
+};
+struct ChainArgs {
+    const ChainEntry * e;
+    int n, M, yf32;
+    int32_t * bar;            // [n] arrival counters, zero at launch; bar[n]: set when a wait timed out
+    int64_t xls;              // LDS row stride of x (elements) >= 128 KB of every entry
+    uint32_t spin;            // poll limit of one barrier wait
+};
+constexpr int CHAIN_WAVES = 8;    // compute waves per workgroup (plus one control wave)
+
 hipError_t launch_repack(int fmt, const uint8_t * st, int64_t sstride, int64_t N, int64_t K, uint8_t * out,
                          int64_t ostride, int64_t E, hipStream_t s);
 hipError_t launch_dequant(int fmt, const uint8_t * W, int64_t N, int64_t K, void * out, int bf16, hipStream_t s);
@@ -62,6 +80,10 @@ hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_pe
                               int32_t * items, int32_t * nitems, hipStream_t s);
 // grouped GEMM over the work items (k_moe_gemm): grid.x column groups (gate_up: NT / 8, down: NT / 8)
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s);
+// zero the chain's counters, then the chained kernel on `grid` workgroups (all resident at once)
+hipError_t launch_chain(int fmt, const ChainArgs & a, int grid, size_t lds, hipStream_t s);
+// workgroups of the chained kernel that fit one CU at this LDS size
+int chain_occupancy(int fmt, size_t lds);
 hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
 hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
@@ -94,7 +116,9 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
     hipError_t qgemv_f##id(int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,       \
                            size_t lds, hipStream_t s);                                                    \
     hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
-    hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);
+    hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
+    hipError_t chain_f##id(const ChainArgs & a, int grid, size_t lds, hipStream_t s);                    \
+    int chain_occ_f##id(size_t lds);
 ONPU_FMT_DECL(0)
 ONPU_FMT_DECL(1)
 ONPU_FMT_DECL(2)

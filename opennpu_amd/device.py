@@ -4,6 +4,7 @@ stream; every product is computed by the library's HIP kernels.
 
   QMatrix   one int4 matrix (any format): mv (y = x W^T), argmax (LM head), dequant
   QFfn      routed-expert FFN bank (gate_up + down): route, ffn
+  QChain    a fixed sequence of QMatrix GEMVs run in order in one launch (onpu_chain_*)
 """
 import ctypes as C
 
@@ -127,4 +128,40 @@ class QFfn:
     def free(self):
         if self.h:
             self.L.onpu_ffn_free(self.h)
+            self.h = None
+
+
+class QChain:
+    """GEMVs y_i = x_i . W_i^T over QMatrix handles, executed in order in one launch with a grid
+    barrier between entries (x_i may be an earlier entry's y). xs / ys: bf16 (ys fp32 if f32) cuda
+    tensors [M][K_i] / [M][N_i], fixed for the life of the chain; keep them alive."""
+
+    def __init__(self, mats, xs, ys, f32=False):
+        self.L = require_gpu()
+        n = len(mats)
+        assert n == len(xs) == len(ys) and n > 0
+        M = xs[0].numel() // mats[0].K
+        for q, x, y in zip(mats, xs, ys):
+            assert x.is_cuda and y.is_cuda and x.numel() == M * q.K and y.numel() == M * q.N
+        P = C.c_void_p * n
+        self._keep = (list(mats), list(xs), list(ys))
+        self.h = self.L.onpu_chain_new(P(*[C.c_void_p(q.h) for q in mats]), P(*[_ptr(x) for x in xs]),
+                                       P(*[_ptr(y) for y in ys]), n, M, int(f32))
+        if not self.h:
+            raise RuntimeError(f"onpu_chain_new: {self.L.onpu_last_error().decode()}")
+
+    def run(self):
+        check(self.L.onpu_chain_run(self.h, _stream()), "onpu_chain_run")
+
+    def status(self):
+        return self.L.onpu_chain_status(self.h)
+
+    def info(self):
+        out = (C.c_int64 * 6)()
+        self.L.onpu_chain_info(self.h, out)
+        return tuple(out)
+
+    def free(self):
+        if self.h:
+            self.L.onpu_chain_free(self.h)
             self.h = None
