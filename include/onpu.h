@@ -138,7 +138,7 @@ int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, i
  * y_i [M][N_i] = x_i [M][K_i] . W_i^T fixed at creation (handles, x and y device pointers; one
  * weight format; 1 <= M <= 16; y bf16 or fp32); onpu_chain_run executes them in order in ONE launch
  * on `stream`, with a grid-wide barrier between entries, so x_i may be the y_j of an earlier entry.
- * The weights of entry i + 1 start streaming while entry i finishes. All workgroups must be
+ * Weights stream ahead through each workgroup's LDS, across the barriers. All workgroups must be
  * resident together: do not run other kernels concurrently with a chain on the same GPU. A barrier
  * wait that exceeds its poll limit (about 0.1 s) gives up rather than hanging; onpu_chain_status
  * then reports 1 (results invalid). The launch is capturable in a HIP graph. */
@@ -147,8 +147,8 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
 int onpu_chain_run(void * chain, void * stream);
 int onpu_chain_status(void * chain);   /* synchronises the device; 0 ok, 1 a barrier timed out, -1 error */
 void onpu_chain_info(void * chain, int64_t * out /* [6]: n, workgroups, LDS bytes, x row stride,
-                                                   workgroups per CU that fit, arrivals at the first barrier
-                                                   of the last run (synchronises) */);
+                                                   weight-ring blocks per wave, barrier arrivals of the
+                                                   last run, (n - 1) x workgroups when whole (synchronises) */);
 void onpu_chain_free(void * chain);
 
 #ifdef __cplusplus

@@ -731,9 +731,9 @@ int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, i
 
 // ---------------------------------------------------------------- chained decode GEMVs
 struct Chain {
-    int fmt = 0, n = 0, M = 0, yf32 = 0, grid = 0, per_cu = 0;
+    int fmt = 0, n = 0, M = 0, yf32 = 0, grid = 0, ring = 0;
     size_t lds = 0;
-    int64_t xls = 0;
+    int64_t xls = 0, ring_off = 0;
     DBuf entries, bar;
 };
 
@@ -746,6 +746,10 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
     for (int i = 0; i < n; i++) {
         const Mat4 * m = (const Mat4 *) handles[i];
         if (m->fmt != fmt || m->E != 1) { set_err("onpu_chain_new: entries need one format and dense handles"); return nullptr; }
+        if (m->g.NT * m->g.KB * fmt_blk(fmt) > (int64_t) UINT32_MAX) {
+            set_err("onpu_chain_new: a chained matrix must be under 4 GiB");
+            return nullptr;
+        }
         ChainEntry & e = es[(size_t) i];
         e.W = m->dev; e.x = (const uint16_t *) xs[i]; e.y = ys[i];
         e.NT = m->g.NT; e.KB = m->g.KB; e.N = m->N; e.K = m->K;
@@ -760,15 +764,20 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
     auto * c = new Chain;
     c->fmt = fmt; c->n = n; c->M = (int) M; c->yf32 = y_f32;
     c->xls = kbmax * 128 + 8;
-    c->lds = (size_t) CHAIN_WAVES * 256 * 4 + (size_t) M * c->xls * 2 + (size_t) kbmax * (fmt == ONPU_G128S ? 1 : 4) * 64;
-    const int per_cu = chain_occupancy(fmt, c->lds);
-    if (c->lds > 163840 || per_cu < 1) { set_err("onpu_chain_new: x rows do not fit in LDS"); delete c; return nullptr; }
-    c->per_cu = per_cu;
-    c->grid = std::min(per_cu, std::max(1, env_int("ONPU_CHAIN_PER_CU", 2))) * device().cus;
+    // LDS: partial sums (two buffers), x rows, column sums, then the deepest weight ring that fits
+    c->ring_off = (int64_t) 2 * CHAIN_WAVES * 256 * 4 + M * c->xls * 2 + kbmax * (fmt == ONPU_G128S ? 1 : 4) * 64;
+    const int64_t blk = fmt_blk(fmt);
+    c->ring = -1;
+    for (int ri = 0; ri < 3 && c->ring < 0; ri++) {
+        const size_t lds = (size_t) (c->ring_off + (int64_t) CHAIN_WAVES * CHAIN_RING_SLOTS[ri] * blk);
+        if (lds <= 163840 && chain_occupancy(fmt, ri, lds) >= 1) { c->ring = ri; c->lds = lds; }
+    }
+    if (c->ring < 0) { set_err("onpu_chain_new: x rows do not fit in LDS"); delete c; return nullptr; }
+    c->grid = device().cus;                // one workgroup per CU: the ring takes most of its LDS
     hipError_t e = c->entries.ensure(sizeof(ChainEntry) * (size_t) n);
-    if (e == hipSuccess) e = c->bar.ensure(sizeof(int32_t) * (size_t) (n + 1));
+    if (e == hipSuccess) e = c->bar.ensure(sizeof(int32_t) * (size_t) CHAIN_BAR_INTS);
     if (e == hipSuccess) e = hipMemcpy(c->entries.p, es.data(), sizeof(ChainEntry) * (size_t) n, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(c->bar.p, 0, sizeof(int32_t) * (size_t) (n + 1));
+    if (e == hipSuccess) e = hipMemset(c->bar.p, 0, sizeof(int32_t) * (size_t) CHAIN_BAR_INTS);
     if (e != hipSuccess) { set_err(hipGetErrorString(e)); delete c; return nullptr; }
     return c;
 }
@@ -776,9 +785,9 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
 int onpu_chain_run(void * h, void * stream) {
     auto * c = (Chain *) h;
     ChainArgs a{};
-    a.e = c->entries.as<ChainEntry>(); a.n = c->n; a.M = c->M; a.yf32 = c->yf32;
-    a.bar = c->bar.as<int32_t>(); a.xls = c->xls; a.spin = 4u << 20;
-    HIPR(launch_chain(c->fmt, a, c->grid, c->lds, (hipStream_t) stream));
+    a.n = c->n; a.M = c->M; a.yf32 = c->yf32;
+    a.bar = c->bar.as<int32_t>(); a.xls = c->xls; a.ring = c->ring_off; a.spin = 4u << 20;
+    HIPR(launch_chain(c->fmt, c->ring, a, c->entries.as<ChainEntry>(), c->grid, c->lds, (hipStream_t) stream));
     return 0;
 }
 
@@ -786,7 +795,7 @@ int onpu_chain_status(void * h) {
     auto * c = (Chain *) h;
     int32_t flag = 0;
     if (hipDeviceSynchronize() != hipSuccess ||
-        hipMemcpy(&flag, c->bar.as<int32_t>(sizeof(int32_t) * (size_t) c->n), 4, hipMemcpyDeviceToHost) != hipSuccess)
+        hipMemcpy(&flag, c->bar.as<int32_t>(sizeof(int32_t) * (size_t) (CHAIN_BAR_INTS - 1)), 4, hipMemcpyDeviceToHost) != hipSuccess)
         return -1;
     return flag ? 1 : 0;
 }
@@ -794,10 +803,15 @@ int onpu_chain_status(void * h) {
 void onpu_chain_info(void * h, int64_t * out) {
     auto * c = (Chain *) h;
     out[0] = c->n; out[1] = c->grid; out[2] = (int64_t) c->lds; out[3] = c->xls;
-    out[4] = c->per_cu;
-    int32_t b0 = -1;
-    if (hipDeviceSynchronize() == hipSuccess) (void) hipMemcpy(&b0, c->bar.p, 4, hipMemcpyDeviceToHost);
-    out[5] = b0;                           // arrivals at the first barrier of the last run
+    out[4] = CHAIN_RING_SLOTS[c->ring];
+    std::vector<int32_t> ctr((size_t) CHAIN_BAR_INTS, 0);
+    int64_t arrivals = -1;
+    if (hipDeviceSynchronize() == hipSuccess &&
+        hipMemcpy(ctr.data(), c->bar.p, sizeof(int32_t) * ctr.size(), hipMemcpyDeviceToHost) == hipSuccess) {
+        arrivals = 0;
+        for (int j = 0; j < CHAIN_CTRS; j++) arrivals += ctr[(size_t) j * CHAIN_CTR_STRIDE];
+    }
+    out[5] = arrivals;                     // barrier arrivals of the last run: (n - 1) * grid when whole
 }
 
 void onpu_chain_free(void * h) {

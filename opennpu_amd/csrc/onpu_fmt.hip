@@ -50,14 +50,34 @@ hipError_t FN(moe_gemm)(int which, const MArgs & a, dim3 grid, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t FN(chain)(const ChainArgs & a, int grid, size_t lds, hipStream_t s) {
-    k_qgemv_chain<F><<<grid, (CHAIN_WAVES + 1) * 64, lds, s>>>(a);
+template <int S>
+static hipError_t chain_s(const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds, hipStream_t s) {
+    k_qgemv_chain<F, S><<<grid, (CHAIN_WAVES + 1) * 64, lds, s>>>(a, ents);
     return hipGetLastError();
 }
 
-int FN(chain_occ)(size_t lds) {
+hipError_t FN(chain)(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds, hipStream_t s) {
+    switch (ring) {
+        case 0: return chain_s<CHAIN_RING_SLOTS[0]>(a, ents, grid, lds, s);
+        case 1: return chain_s<CHAIN_RING_SLOTS[1]>(a, ents, grid, lds, s);
+        case 2: return chain_s<CHAIN_RING_SLOTS[2]>(a, ents, grid, lds, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int S>
+static int chain_occ_s(size_t lds) {
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qgemv_chain<F>, (CHAIN_WAVES + 1) * 64, lds) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qgemv_chain<F, S>, (CHAIN_WAVES + 1) * 64, lds) != hipSuccess)
         return 0;
     return nb;
+}
+
+int FN(chain_occ)(int ring, size_t lds) {
+    switch (ring) {
+        case 0: return chain_occ_s<CHAIN_RING_SLOTS[0]>(lds);
+        case 1: return chain_occ_s<CHAIN_RING_SLOTS[1]>(lds);
+        case 2: return chain_occ_s<CHAIN_RING_SLOTS[2]>(lds);
+    }
+    return 0;
 }

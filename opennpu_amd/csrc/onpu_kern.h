@@ -25,6 +25,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // back to address space 3 makes the accesses ds_read / ds_write (a generic "flat" access counts
 // against both the vector-memory and LDS counters and forces waits on the weight prefetch)
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+// global-memory view of a pointer that came from memory rather than a kernel argument (without it
+// the compiler emits flat loads, which also count against the LDS wait counter)
+#define GLB(T, p) ((__attribute__((address_space(1))) T *) (p))
 #define LDS_U32X4(p) ((lds_u32x4 *) (p))
 
 
@@ -146,12 +149,12 @@ DEV Par<FMT> par_zero() {
 template <int FMT>
 DEV Par<FMT> load_par(const uint8_t * blk, int r) {
     Par<FMT> p;
-    if (FMT == ONPU_G128S) p.v[0] = *(const uint16_t *) (blk + 1024 + 2 * r);
+    if (FMT == ONPU_G128S) p.v[0] = *GLB(const uint16_t, blk + 1024 + 2 * r);
     else if (FMT == ONPU_Q4NX) {
-        const u32x4 q = __builtin_nontemporal_load((const u32x4 *) (blk + 1024 + 16 * r));
+        const u32x4 q = __builtin_nontemporal_load(GLB(const u32x4, blk + 1024 + 16 * r));
         for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];
     } else {
-        const u32x2 q = __builtin_nontemporal_load((const u32x2 *) (blk + 1024 + 8 * r));
+        const u32x2 q = __builtin_nontemporal_load(GLB(const u32x2, blk + 1024 + 8 * r));
         p.v[0] = q.x;
         p.v[1 % (sizeof(p.v) / 4)] = q.y;
     }
@@ -357,7 +360,7 @@ DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], co
         }
     for (int i = 0; i < NB; i++)
         for (int rt = 0; rt < RT; rt++) {
-            c.wv[i][rt] = __builtin_nontemporal_load((const u32x4 *) (p[i][rt] + 16 * lane));
+            c.wv[i][rt] = __builtin_nontemporal_load(GLB(const u32x4, p[i][rt] + 16 * lane));
             c.par[i][rt] = load_par<FMT>(p[i][rt], r);
         }
 }
@@ -906,120 +909,250 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
 
 
 // ------------------------------------------------------------------ chained decode GEMVs
-// One launch runs a.n GEMVs in order (M <= 16 rows, x staged in LDS). Workgroup: CHAIN_WAVES compute
-// waves + one control wave. Entry i's tile groups (tw tiles x kw K parts, tw kw = CHAIN_WAVES) go to
-// workgroups g = blockIdx.x, + gridDim.x, ... Between entries every workgroup meets at a grid
-// barrier, so entry i + 1 may read entry i's output; around it:
-//   compute waves: store y, wait for their stores, then issue the first weight chunk of their
-//     first tile group of entry i + 1 (weights do not depend on x: they stream during the barrier)
-//   control wave: arrive (release at agent scope), poll the counter (bounded: past a.spin polls it
-//     flags a.bar[n] and proceeds, so no wave can wait forever), acquire, then stage x_{i+1} and its
-//     column sums in LDS by itself, so the compute waves never wait on loads younger than their
-//     prefetch.
+// One launch runs a.n GEMVs in order (M <= 16 rows, x staged in LDS), one workgroup per CU of
+// CHAIN_WAVES compute waves + one control wave. Entry i's tile groups (tw tiles x kw K parts,
+// tw kw = CHAIN_WAVES) go to workgroups g = blockIdx.x, + gridDim.x, ...
+// Weights stream through a ring of S block slots per compute wave, filled by buffer-to-LDS loads.
+// A wave's sequence of blocks over the whole chain is known up front (weights do not depend on x),
+// so the ring is refilled with the next block of the sequence as each block is consumed and keeps
+// S blocks in flight across entry boundaries and grid barriers: HBM streams while the grid waits.
+// Between entries every workgroup meets at a grid barrier (entry i + 1 may read entry i's output):
+//   compute waves: leave their partial sums in LDS; besides the ring's loads they only load x in
+//     the staging and wait for those loads completely, so the ring's wait count stays exact
+//   control wave: sums the K parts, stores y (agent-scope stores), waits for its stores, arrives
+//     and polls (chain_barrier; bounded: past a.spin polls it sets the error flag and proceeds, so
+//     no wave can wait forever)
+//   all waves: stage x_{i+1} (agent-scope loads) and its column sums in LDS.
 // Every workgroup must be resident at once (the host sizes the grid from the occupancy).
+// x rows [M][K] (bf16) into the LDS copy xs[M][xls] and the column sums of each group of gs, by the
+// whole workgroup: consecutive threads take consecutive 8-element units (coalesced loads, two per
+// thread in flight at once); a group's units sit in consecutive lanes of one wave and are summed
+// across them.
 DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, uint16_t * xs,
                        float * xsum) {
-    const int lane = threadIdx.x & 63, upg = gs / 8;
+    const uint32_t T = blockDim.x, tid = threadIdx.x, upg = gs / 8;
     const uint32_t kp8 = (uint32_t) KB * 16, nunits = (uint32_t) M * kp8;
-    for (uint32_t u0 = 0; u0 < nunits; u0 += 64) {               // same trip count for every lane
-        const uint32_t u = u0 + lane;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        uint32_t m = 0, kk = 0;
-        if (u < nunits) {
-            m = u / kp8;
-            kk = (u - m * kp8) * 8;
-            if (kk < K) v = *(const u32x4 *) (x + (int64_t) m * K + kk);
-            *LDS_U32X4(xs + (int64_t) m * xls + kk) = v;
+    for (uint32_t u0 = 0; u0 < nunits; u0 += 2 * T) {            // same trip count for the whole workgroup
+        uint64_t v[2][2];
+        uint32_t m[2], kk[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {                             // both loads first: one round trip
+            const uint32_t u = u0 + j * T + tid;
+            v[j][0] = v[j][1] = 0;
+            m[j] = u / kp8;
+            kk[j] = (u - m[j] * kp8) * 8;
+            if (u < nunits && kk[j] < K) {
+                const auto * p = GLB(uint64_t, x + (int64_t) m[j] * K + kk[j]);
+                v[j][0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v[j][1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
-        float t = 0.f;
-        for (int d = 0; d < 4; d++) t += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
-        for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
-        if (u < nunits && u % upg == 0) xsum[(kk / gs) * 16 + m] = t;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t u = u0 + j * T + tid;
+            const u32x4 w = {(uint32_t) v[j][0], (uint32_t) (v[j][0] >> 32), (uint32_t) v[j][1],
+                             (uint32_t) (v[j][1] >> 32)};
+            if (u < nunits) *LDS_U32X4(xs + (int64_t) m[j] * xls + kk[j]) = w;
+            float t = 0.f;
+            for (int d = 0; d < 4; d++) t += __uint_as_float(w[d] << 16) + __uint_as_float(w[d] & 0xffff0000u);
+            for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+            if (u < nunits && u % upg == 0) xsum[(kk[j] / gs) * 16 + m[j]] = t;
+        }
     }
 }
 
-// Two workgroups of 9 waves per CU can put 6 waves on one SIMD: the launch bound asks for 6 waves
-// per SIMD (<= 80 VGPRs) so that the two always fit together.
+// y of a chain entry is read by other workgroups after the barrier: agent-scope stores, which are
+// coherent across the XCDs' L2 caches once complete (no L2 write-back needed before arriving).
+DEV void chain_store(void * y, int yf32, int64_t idx, float v) {
+    if (yf32) __hip_atomic_store(GLB(uint32_t, y) + idx, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else __hip_atomic_store(GLB(uint16_t, y) + idx, f32_to_bf16(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Grid barrier of the control wave. Every wave of the workgroup has waited for its own stores to
+// complete and met at a workgroup barrier before this. Lane 0 arrives on counter w % CHAIN_CTRS;
+// lane j polls counter j until it holds epoch * (workgroups arriving on j). Both sides use
+// agent-scope atomics, and the x reads after the barrier are agent-scope loads, so no cache
+// write-back or invalidate is needed. A wait longer than spin polls sets the error flag and ends
+// the wait (the results are then wrong but the kernel still exits).
+DEV void chain_barrier(int32_t * bar, int64_t w, int64_t P, int epoch, uint32_t spin) {
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) __hip_atomic_fetch_add(bar + (w % CHAIN_CTRS) * CHAIN_CTR_STRIDE, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t cnt = lane < P ? (P - lane + CHAIN_CTRS - 1) / CHAIN_CTRS : 0;
+    const int32_t want = (int32_t) (cnt * epoch);
+    for (uint32_t polls = 0;; polls++) {
+        const int32_t got = __hip_atomic_load(bar + lane * CHAIN_CTR_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_ballot_w64(got < want) == 0) break;
+        if (polls >= spin) {
+            if (lane == 0) __hip_atomic_store(bar + CHAIN_BAR_INTS - 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// s_waitcnt immediates (gfx9 encoding): vmcnt(n) with the other counters free, and lgkmcnt(0)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
+
+// position in a wave's block sequence over the chain: block b (< b1) of tile t of entry e, tile
+// group g; e == a.n: past the end
+struct ChainCur {
+    int e;
+    int64_t g, t, b, b1;
+    const uint8_t * W;        // entry e's weights, its K blocks and bytes (kept so that refills
+    int64_t KB;               // load nothing but the block)
+    uint32_t bytes;
+};
+
+// the wave's tile and K blocks [b0, b1) in tile group g of entry E (empty past the last tile)
+DEV void chain_range(const ChainEntry & E, int64_t g, int wave, int64_t & t, int64_t & b0, int64_t & b1) {
+    const int twi = wave / E.kw, kp = wave % E.kw;
+    t = g * E.tw + twi;
+    b0 = (int64_t) kp * E.bpw;
+    b1 = b0 + E.bpw < E.KB ? b0 + E.bpw : E.KB;
+    if (t >= E.NT) b1 = b0;
+}
+
+// moves c forward to the next position that holds a block, or past the end
 template <int FMT>
-__global__ __launch_bounds__((CHAIN_WAVES + 1) * 64, 6) void k_qgemv_chain(ChainArgs a) {
-    constexpr int NB = 2, GS = FMT == ONPU_G128S ? 128 : 32;
+DEV void chain_settle(ChainCur & c, const ChainEntry * __restrict__ ents, int n, int64_t w, int64_t P, int wave) {
+    while (c.e < n && c.b >= c.b1) {
+        c.g += P;
+        if (c.g >= ents[c.e].groups) { c.e++; c.g = w; }
+        c.b = c.b1 = 0;
+        if (c.e < n && c.g < ents[c.e].groups) {
+            const ChainEntry & E = ents[c.e];
+            chain_range(E, c.g, wave, c.t, c.b, c.b1);
+            c.W = E.W;
+            c.KB = E.KB;
+            c.bytes = (uint32_t) (E.NT * E.KB * fmt_blk(FMT));
+        }
+    }
+}
+
+// two buffer-to-LDS loads of c's block into `slot`: 1 KiB of nibbles (16 bytes per lane) and the
+// parameters (4 bytes per lane, the lanes they need); past the end both read out of range (zeros,
+// no memory traffic), so every refill counts two loads
+template <int FMT>
+DEV void chain_issue(ChainCur & c, const ChainEntry * __restrict__ ents, int n, int64_t w, int64_t P, int wave,
+                     uint8_t * slot, int lane) {
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    constexpr int PW = (BLK - 1024) / 4;
+    const bool live = c.e < n;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *) c.W, (short) 0, (int) c.bytes,
+                                                                         0x00020000);
+    const uint32_t so = live ? (uint32_t) ((c.t * c.KB + c.b) * BLK) : 0u;
+    const uint32_t vo = live ? 16u * lane : 0x80000000u, vp = live ? 1024u + 4u * lane : 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *) slot, 16, vo, so, 0, 0);
+    if (lane < PW) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *) (slot + 1024), 4, vp, so, 0, 0);
+    if (live) {
+        c.b++;
+        chain_settle<FMT>(c, ents, n, w, P, wave);
+    }
+}
+
+// workgroup barrier that orders LDS only: a __syncthreads here would also wait for every
+// buffer-to-LDS load in flight (the ring), draining it at each barrier
+DEV void chain_sync() {
+    __builtin_amdgcn_s_waitcnt(LGKM0_IMM);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int FMT>
+DEV Par<FMT> load_par_lds(const uint8_t * blk, int r) {
+    Par<FMT> p;
+    typedef __attribute__((address_space(3))) const uint16_t lds_u16;
+    typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
+    if (FMT == ONPU_G128S) p.v[0] = *(lds_u16 *) (blk + 1024 + 2 * r);
+    else if (FMT == ONPU_Q4NX) {
+        const u32x4 q = *LDS_U32X4(blk + 1024 + 16 * r);
+        for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];
+    } else {
+        const u32x2 q = *(lds_u32x2 *) (blk + 1024 + 8 * r);
+        p.v[0] = q.x;
+        p.v[1 % (sizeof(p.v) / 4)] = q.y;
+    }
+    return p;
+}
+
+template <int FMT, int S>
+__global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArgs a, const ChainEntry * __restrict__ ents) {
+    constexpr int GS = FMT == ONPU_G128S ? 128 : 32;
     constexpr int BLK = 1024 + 16 * (128 / GS) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
-    extern __shared__ float red[];                  // [CHAIN_WAVES][256] floats, x rows, column sums
+    static_assert(2 * (S - 1) <= 63, "ring deeper than the load counter");
+    extern __shared__ float red[];      // [2][CHAIN_WAVES][256] partial sums, x rows, column sums, ring
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
     const bool ctrl = wave == CHAIN_WAVES;
     const int64_t P = gridDim.x, w = blockIdx.x;
-    uint16_t * xs = (uint16_t *) (red + CHAIN_WAVES * 256);
+    uint16_t * xs = (uint16_t *) (red + 2 * CHAIN_WAVES * 256);
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
+    uint8_t * ring = (uint8_t *) red + a.ring + (ctrl ? 0 : wave * S * BLK);
     const XSrc X{nullptr, 0, nullptr, xs, a.xls, xsum};
-    WChunk<FMT, 1, NB> ca;
-    const uint8_t * last = nullptr;
-    int64_t pb0 = 0, pb1 = 0;                       // the prefetched range of the next entry
-    bool pre = false;
-    // entry 0: the first chunks, and x_0 by the control wave (no barrier before it)
-    auto prefetch = [&](const ChainEntry & F) {
-        pre = false;
-        if (ctrl || w >= F.groups) return;
-        const int twi = wave / F.kw, kp = wave % F.kw;
-        const int64_t t = w * F.tw + twi;
-        const uint8_t * tb[1] = {t < F.NT ? F.W + t * F.KB * BLK : nullptr};
-        pb0 = (int64_t) kp * F.bpw;
-        pb1 = pb0 + F.bpw < F.KB ? pb0 + F.bpw : F.KB;
-        last = qacc_start<FMT, 1, NB>(ca, tb, pb0, pb1);
-        pre = true;
-    };
-    prefetch(a.e[0]);
-    if (ctrl) chain_stage_x(a.e[0].x, a.M, a.e[0].K, a.e[0].KB, a.xls, GS, xs, xsum);
-    __syncthreads();
+    ChainCur ic{0, w - P, 0, 0, 0, ents[0].W, 1, 0u};   // past the end, refills read entry 0 out of range
+    if (!ctrl) {
+        chain_settle<FMT>(ic, ents, a.n, w, P, wave);
+        for (int s = 0; s < S; s++) chain_issue<FMT>(ic, ents, a.n, w, P, wave, ring + s * BLK, lane);
+    }
+    chain_stage_x(ents[0].x, a.M, ents[0].K, ents[0].KB, a.xls, GS, xs, xsum);
+    chain_sync();
+    const uint32_t mag = 0x43004300u;
+    uint32_t k = 0;                     // blocks consumed: the next one sits in slot k % S
+    int rb = 0;                         // partial-sum buffer of the current tile group
     for (int i = 0; i < a.n; i++) {
-        const ChainEntry & E = a.e[i];
-        const int twi = wave / E.kw, kp = wave % E.kw;
+        const ChainEntry & E = ents[i];
+        const int etw = E.tw, ekw = E.kw, nout = etw * 16 * a.M;
+        const int64_t eN = E.N;
+        void * const ey = E.y;
         for (int64_t g = w; g < E.groups; g += P) {          // same trip count for the whole workgroup
-            f32x4 acc[1][1];
-            acc[0][0] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            float * rp = red + rb * CHAIN_WAVES * 256;
             if (!ctrl) {
-                const int64_t t = g * E.tw + twi;
-                const uint8_t * tb[1] = {t < E.NT ? E.W + t * E.KB * BLK : nullptr};
-                int64_t b0 = (int64_t) kp * E.bpw, b1 = b0 + E.bpw < E.KB ? b0 + E.bpw : E.KB;
-                if (!(pre && g == w)) last = qacc_start<FMT, 1, NB>(ca, tb, b0, b1);
-                else b1 = pb1;
-                qacc_rest<FMT, 1, 1, NB, true>(ca, tb, last, b0, b1, X, a.M, E.K, acc);
-                for (int v = 0; v < 4; v++) red[wave * 256 + v * 64 + lane] = acc[0][0][v];
+                f32x4 acc[1][1];
+                acc[0][0] = (f32x4){0.f, 0.f, 0.f, 0.f};
+                int64_t t, b0, b1;
+                chain_range(E, g, wave, t, b0, b1);
+                for (int64_t b = b0; b < b1; b++) {
+                    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (S - 1)));     // block k has landed
+                    uint8_t * sl = ring + (k % S) * BLK;
+                    WChunk<FMT, 1, 1> ch;
+                    ch.ok[0][0] = true;
+                    ch.wv[0][0] = *LDS_U32X4(sl + 16 * lane);
+                    ch.par[0][0] = load_par_lds<FMT>(sl, r);
+                    compute_chunk<FMT, 1, 1, 1, true>(ch, b, b1, X, a.M, E.K, r, q, mag, acc);
+                    __builtin_amdgcn_s_waitcnt(LGKM0_IMM);            // the slot's reads are done
+                    chain_issue<FMT>(ic, ents, a.n, w, P, wave, sl, lane);     // refill it
+                    k++;
+                }
+                for (int v = 0; v < 4; v++) rp[wave * 256 + v * 64 + lane] = acc[0][0][v];
             }
-            __syncthreads();
-            // tile group g: tiles g tw + twi, each summed over its kw K parts
-            for (int o = threadIdx.x; o < E.tw * 256; o += blockDim.x) {
-                const int ti = o / 256, v = (o / 64) % 4, l = o % 64;
-                const int m = 4 * (l >> 4) + v;
-                const int64_t n = 16 * (g * E.tw + ti) + (l & 15);
-                if (m >= a.M || n >= E.N) continue;
-                float sum = 0.f;
-                for (int k2 = 0; k2 < E.kw; k2++) sum += red[(ti * E.kw + k2) * 256 + v * 64 + l];
-                store_out(E.y, a.yf32, (int64_t) m * E.N + n, sum);
-            }
-            __syncthreads();
-        }
-        pre = false;
-        if (i + 1 == a.n) break;
-        // the barrier between entries i and i + 1
-        __builtin_amdgcn_s_waitcnt(0x0f70);                  // this wave's y stores are done
-        prefetch(a.e[i + 1]);
-        __syncthreads();                                     // every wave's stores are done
-        if (ctrl) {
-            if (lane == 0) {
-                __hip_atomic_fetch_add(a.bar + i, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-                uint32_t polls = 0;
-                while (__hip_atomic_load(a.bar + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (int32_t) P) {
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++polls > a.spin) {
-                        __hip_atomic_store(a.bar + a.n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
+            chain_sync();
+            if (ctrl) {                 // outputs (tile g tw + ti, row m, column c), summed over the kw K parts
+                for (int o = lane; o < nout; o += 64) {
+                    const int ti = o / (16 * a.M), m = (o / 16) % a.M, c = o % 16;
+                    const int64_t n = 16 * (g * etw + ti) + c;
+                    // the accumulator of row m, column c sits at lane c + 16 (m / 4), element m % 4
+                    const float * src = rp + ti * ekw * 256 + (m & 3) * 64 + c + 16 * (m >> 2);
+                    float sum = src[0];
+#pragma unroll
+                    for (int k2 = 1; k2 < CHAIN_WAVES; k2++)
+                        if (k2 < ekw) sum += src[k2 * 256];
+                    if (n < eN) chain_store(ey, a.yf32, (int64_t) m * eN + n, sum);
                 }
             }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            const ChainEntry & F = a.e[i + 1];
-            chain_stage_x(F.x, a.M, F.K, F.KB, a.xls, GS, xs, xsum);
+            rb ^= 1;
         }
-        __syncthreads();
+        if (i + 1 == a.n) break;
+        if (ctrl) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));              // the y stores are complete
+            chain_barrier(a.bar, w, P, i + 1, a.spin);
+        }
+        chain_sync();
+        const ChainEntry & F = ents[i + 1];
+        chain_stage_x(F.x, a.M, F.K, F.KB, a.xls, GS, xs, xsum);
+        chain_sync();
     }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));      // the ring's last (out-of-range) loads have landed
 }

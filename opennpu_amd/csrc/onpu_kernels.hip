@@ -317,29 +317,31 @@ hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems
     return hipErrorInvalidValue;
 }
 
-__global__ void k_chain_reset(int32_t * bar, int n) {
-    for (int i = threadIdx.x; i <= n; i += blockDim.x) bar[i] = 0;
+__global__ void k_chain_reset(int32_t * bar) {
+    for (int i = threadIdx.x; i < CHAIN_BAR_INTS; i += blockDim.x) bar[i] = 0;
 }
 
-hipError_t launch_chain(int fmt, const ChainArgs & a, int grid, size_t lds, hipStream_t s) {
-    if (a.n <= 0 || a.M < 1 || a.M > 16 || grid < 1 || lds > 163840) return hipErrorInvalidValue;
-    k_chain_reset<<<1, 256, 0, s>>>(a.bar, a.n);
+hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,
+                        hipStream_t s) {
+    if (a.n <= 0 || a.M < 1 || a.M > 16 || grid < 1 || lds > 163840 || ring < 0 || ring > 2)
+        return hipErrorInvalidValue;
+    k_chain_reset<<<1, 256, 0, s>>>(a.bar);
     CHECK_LAUNCH();
     switch (fmt) {
-        case 0: return chain_f0(a, grid, lds, s);
-        case 1: return chain_f1(a, grid, lds, s);
-        case 2: return chain_f2(a, grid, lds, s);
-        case 3: return chain_f3(a, grid, lds, s);
+        case 0: return chain_f0(ring, a, ents, grid, lds, s);
+        case 1: return chain_f1(ring, a, ents, grid, lds, s);
+        case 2: return chain_f2(ring, a, ents, grid, lds, s);
+        case 3: return chain_f3(ring, a, ents, grid, lds, s);
     }
     return hipErrorInvalidValue;
 }
 
-int chain_occupancy(int fmt, size_t lds) {
+int chain_occupancy(int fmt, int ring, size_t lds) {
     switch (fmt) {
-        case 0: return chain_occ_f0(lds);
-        case 1: return chain_occ_f1(lds);
-        case 2: return chain_occ_f2(lds);
-        case 3: return chain_occ_f3(lds);
+        case 0: return chain_occ_f0(ring, lds);
+        case 1: return chain_occ_f1(ring, lds);
+        case 2: return chain_occ_f2(ring, lds);
+        case 3: return chain_occ_f3(ring, lds);
     }
     return 0;
 }

@@ -57,14 +57,19 @@ struct ChainEntry {
     int64_t NT, KB, N, K, bpw, groups;
     int tw, kw;               // tw * kw = CHAIN_WAVES
 };
-struct ChainArgs {
-    const ChainEntry * e;
+struct ChainArgs {              // (the entries array is a kernel argument of its own)
     int n, M, yf32;
-    int32_t * bar;            // [n] arrival counters, zero at launch; bar[n]: set when a wait timed out
+    int32_t * bar;            // CHAIN_CTRS arrival counters CHAIN_CTR_STRIDE ints apart, zero at launch, then
+                              // the flag set when a wait timed out (CHAIN_BAR_INTS ints)
     int64_t xls;              // LDS row stride of x (elements) >= 128 KB of every entry
+    int64_t ring;             // LDS byte offset of the weight ring
     uint32_t spin;            // poll limit of one barrier wait
 };
 constexpr int CHAIN_WAVES = 8;    // compute waves per workgroup (plus one control wave)
+constexpr int CHAIN_RING_SLOTS[3] = {12, 8, 4};   // ring depths built, deepest first
+// Workgroup w arrives on counter w % CHAIN_CTRS (one counter per lane of the polling wave); the
+// counters sit 256 bytes apart so that arrivals on different counters do not queue on one line.
+constexpr int CHAIN_CTRS = 64, CHAIN_CTR_STRIDE = 64, CHAIN_BAR_INTS = CHAIN_CTRS * CHAIN_CTR_STRIDE + 1;
 
 hipError_t launch_repack(int fmt, const uint8_t * st, int64_t sstride, int64_t N, int64_t K, uint8_t * out,
                          int64_t ostride, int64_t E, hipStream_t s);
@@ -81,9 +86,11 @@ hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_pe
 // grouped GEMM over the work items (k_moe_gemm): grid.x column groups (gate_up: NT / 8, down: NT / 8)
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s);
 // zero the chain's counters, then the chained kernel on `grid` workgroups (all resident at once)
-hipError_t launch_chain(int fmt, const ChainArgs & a, int grid, size_t lds, hipStream_t s);
+// (ring: CHAIN_RING_SLOTS[ring] weight blocks per compute wave)
+hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,
+                        hipStream_t s);
 // workgroups of the chained kernel that fit one CU at this LDS size
-int chain_occupancy(int fmt, size_t lds);
+int chain_occupancy(int fmt, int ring, size_t lds);
 hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
 hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
@@ -117,8 +124,9 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
                            size_t lds, hipStream_t s);                                                    \
     hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
     hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
-    hipError_t chain_f##id(const ChainArgs & a, int grid, size_t lds, hipStream_t s);                    \
-    int chain_occ_f##id(size_t lds);
+    hipError_t chain_f##id(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,  \
+                           hipStream_t s);                                                                \
+    int chain_occ_f##id(int ring, size_t lds);
 ONPU_FMT_DECL(0)
 ONPU_FMT_DECL(1)
 ONPU_FMT_DECL(2)
