@@ -35,6 +35,10 @@ BF16_PEAK = 2.5e15           # MI355X dense bf16 MFMA, flop/s
 G128S, Q4_0 = 2, 3
 LAYERS = 36                  # Qwen3-8B
 QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288)]
+# HBM bytes moved per gate+up launch (M=1), from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of
+# `bench.py --profile`, each scaled by what the counter reads for a plain 512 MiB copy
+# (profiles/qgemv_g128s_gate_up_24576x4096_pmc.md); a hardware-counter figure, not re-measured here
+GATE_UP_TRAFFIC = 52_221_305
 
 
 def log(*a):
@@ -361,9 +365,10 @@ def main():
         log("lm head ...")
         configs["lm_head_q4_0"] = lm_head(torch, QMatrix, syn, 30)
     gu = head["per_matrix"]["gate_up"]
-    roof = {"kernel": "k_qgemv<g128s, MB=1, RT=2> (gate+up 24576x4096, M=1)", "bound": "hbm",
-            "achieved": gu["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": gu["GBps"] / (HBM_PEAK / 1e9),
-            "traffic": None, "bytes_per_launch": gu["bytes"], "us_per_launch": gu["us"]}
+    roof = {"kernel": "k_qgemv<g128s> gate+up 24576x4096, M=1 (768 workgroups x 8 waves, x in LDS)",
+            "bound": "hbm", "achieved": gu["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": gu["GBps"] / (HBM_PEAK / 1e9), "traffic": GATE_UP_TRAFFIC, "bytes_per_launch": gu["bytes"],
+            "us_per_launch": gu["us"]}
     cpu = None
     if not (args.quick or args.no_cpu):
         log("cpu baseline ...")
