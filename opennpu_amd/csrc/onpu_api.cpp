@@ -101,6 +101,7 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     uint8_t * stage = nullptr;             // host staging, E * sstride bytes (lazy)
     int64_t sstride = 0;
     DBuf ws[6];                            // workspace of the calls on this handle
+    DBuf gsk_ws, gsk_sync;                 // k_qgemm_sk partial tiles and slot counters (zeroed once)
 };
 
 struct Ffn {
@@ -134,6 +135,8 @@ void free_mat(Mat4 * m) {
     if (m->dev) (void) hipFree(m->dev);
     std::free(m->stage);
     for (auto & b : m->ws) b.release();
+    m->gsk_ws.release();
+    m->gsk_sync.release();
     delete m;
 }
 
@@ -252,6 +255,47 @@ Plan plan_slotsum(int64_t KB, int k) {
 }
 
 // y [M][N] = x [M][K] (bf16, device) . W_e^T, M rows
+// Stream-K plan of k_qgemm_sk for M rows: configuration, grid and K-block iterations per workgroup.
+// Every CU gets one workgroup and an equal share of the tiles * KB iterations when there are at least
+// as many tiles as CUs; with half as many, each tile is split in two K halves. False (use k_qgemm)
+// when neither holds or when some tile would be cut by more than one workgroup boundary.
+bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & grid, int64_t & ipw) {
+    cfg = env_int("ONPU_GSK_CFG", 0);
+    if (cfg < 0 || cfg > 2 || cus <= 0) return false;
+    const GskCfg c = GSK_CFGS[cfg];
+    const int64_t MT = 16 * c.mbg, TPW = (int64_t) c.ntw * c.wv;
+    const int64_t tiles = ((M + MT - 1) / MT) * ((NT + TPW - 1) / TPW), total = tiles * KB;
+    if (tiles >= cus) ipw = (total + cus - 1) / cus;
+    else if (2 * tiles >= cus && KB % 2 == 0) ipw = KB / 2;
+    else return false;
+    grid = (total + ipw - 1) / ipw;
+    if (grid > cus) return false;
+    int64_t last = -1;                     // tile of the previous interior boundary
+    for (int64_t j = 1; j < grid; j++) {
+        const int64_t B = j * ipw;
+        if (B % KB == 0) continue;
+        if (B / KB == last) return false;
+        last = B / KB;
+    }
+    return true;
+}
+
+// partial tiles for one workgroup per CU (the largest k_qgemm_sk slot) and the slot counters,
+// zeroed once here; the kernel leaves them zero
+hipError_t gsk_workspace(Mat4 * m) {
+    const int cus = device().cus;
+    size_t slot = 0;
+    for (const GskCfg & c : GSK_CFGS) slot = std::max(slot, (size_t) c.wv * c.mbg * c.ntw * 1024);
+    if (m->gsk_sync.n == 0) {
+        hipError_t e = m->gsk_ws.ensure(slot * (size_t) cus);
+        if (e != hipSuccess) return e;
+        const size_t sb = ((size_t) cus + 1) * GSK_SYNC_STRIDE * 4;
+        if ((e = m->gsk_sync.ensure(sb)) != hipSuccess) return e;
+        if ((e = hipMemset(m->gsk_sync.p, 0, sb)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
     if (M <= 0) return hipSuccess;
     const uint8_t * W = m->dev + e * m->dstride;
@@ -264,6 +308,18 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         a.y = y; a.ldy = m->N; a.yslot = 0; a.yf32 = yf32;
         a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
         return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
+    }
+    int cfg = 0;
+    int64_t grid = 0, ipw = 0;
+    if (env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ipw) &&
+        M * m->K * 2 < ((int64_t) 1 << 31)) {
+        hipError_t e = gsk_workspace(m);
+        if (e != hipSuccess) return e;
+        GArgs a{};
+        a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
+        a.x = x; a.ldx = m->K; a.y = y; a.ldy = m->N; a.yf32 = yf32;
+        a.ipw = ipw; a.ws = m->gsk_ws.as<float>(); a.sync = m->gsk_sync.as<int32_t>(); a.spin = 1u << 22;
+        return launch_qgemm_sk(m->fmt, a, cfg, (int) grid, s);
     }
     // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
     // workgroups, else 2 (128 x 128); 4 (128 x 256) runs out of registers and is slower

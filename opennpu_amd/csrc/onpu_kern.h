@@ -811,6 +811,226 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         }
 }
 
+// ------------------------------------------------------------------ prefill GEMM, 256-row tiles
+// Y = X . deq(W)^T with a workgroup tile of MT = 16 MBG rows of X by 16 NTW WV rows of W. Wave w
+// owns NTW weight tiles and all MT rows (MBG x NTW accumulators of 16 x 16), so one dequantized
+// weight fragment (23 VALU ops) feeds MBG MFMAs: at MBG = 16 that is 1.4 VALU ops per
+// v_mfma_f32_16x16x32_bf16, which the matrix pipe hides when two waves share a SIMD (the 128-row
+// k_qgemm leaves 2.9 per MFMA, which it does not). X blocks move HBM -> LDS by buffer-to-LDS loads
+// into two MBG * 4 KiB buffers, weights stream into two register sets, as in k_qgemm.
+// Work split (stream-K): the tiles' K blocks form one tile-major sequence of tiles * KB
+// iterations and workgroup g takes [g ipw, (g + 1) ipw), so every CU gets the same number of MFMAs
+// whatever the tile count. A tile cut by a workgroup boundary has two segments (the host keeps it
+// to two): the first to finish stores its fp32 accumulators to the boundary's slot with
+// agent-scope stores (coherent across the XCDs' L2 caches once complete, no cache write-back) and
+// raises the slot's flag; the second waits for the flag (raised by a workgroup already in its
+// epilogue, so the wait is short and bounded), adds the partial and stores Y. Two addends give
+// the same fp32 sum in either order, so Y does not depend on which segment finishes first. The
+// second also clears the slot's counter and flag, which are therefore zero between launches.
+
+// X fragments of block b for a workgroup of WV waves: wave w fills FPW = 4 MBG / WV fragments
+// f = FPW w + i, (mb, j) = (f / 4, f % 4). xrow[i / 4]: the lane's byte offset of row m0 + 16 mb + r
+// at k = 8 q (0x80000000, past the buffer, for rows >= M); kfix as in gemm_load_x.
+template <int FPW>
+DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow)[FPW / 4], int64_t b, bool kfix,
+                        int64_t K, int wave, int q, u32x4 * buf) {
+#pragma unroll
+    for (int i = 0; i < FPW; i++) {
+        const int f = FPW * wave + i, j = i & 3;
+        uint32_t off = xrow[i >> 2] == 0x80000000u ? 0x80000000u : xrow[i >> 2] + 64u * j;
+        if (kfix && 128 * b + 32 * j + 8 * q >= K) off = 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b), 0, 0);
+    }
+}
+
+// one 128-wide K block: 4 steps j x MBG / 8 half-steps of 8 A blocks. The A fragments of the next
+// half-step are read from LDS while the current one's MFMAs run, and the weight fragments of step
+// j + 1 are dequantized during step j (tile i in half-step i % H), so neither LDS latency nor the
+// dequant sits in front of an MFMA except at the block's start.
+template <int FMT, int NTW, int MBG>
+DEV void gemm_block_sk(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int lane,
+                       f32x4 (&acc)[MBG][NTW]) {
+#ifdef GSK_OLD_BLOCK
+    gemm_block<FMT, NTW, MBG>(xsb, wr, pr, lane, acc);
+    return;
+#endif
+    constexpr int HB = 8, H = MBG / HB, S = 4 * H;
+    u32x4 xa[2][HB], bw[2][NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; i++) {
+        float sc, cc;
+        par_sc<FMT>(pr[i], 0, sc, cc);
+        bw[0][i] = dequant8<FMT>(wr[i][0], sc, cc);
+    }
+#pragma unroll
+    for (int mb = 0; mb < HB; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + 0) * 64 + lane]);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const int j = s / H, h = s % H;
+        if (s + 1 < S) {
+            const int j1 = (s + 1) / H, h1 = (s + 1) % H;
+#pragma unroll
+            for (int mb = 0; mb < HB; mb++)
+                xa[(s + 1) & 1][mb] = *LDS_U32X4(&xsb[((h1 * HB + mb) * 4 + j1) * 64 + lane]);
+        }
+        if (j + 1 < 4) {
+#pragma unroll
+            for (int i = 0; i < NTW; i++) {
+                if (i % H != h) continue;
+                float sc, cc;
+                par_sc<FMT>(pr[i], j + 1, sc, cc);
+                bw[(j + 1) & 1][i] = dequant8<FMT>(wr[i][j + 1], sc, cc);
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < HB; mb++)
+#pragma unroll
+            for (int i = 0; i < NTW; i++)
+                acc[h * HB + mb][i] = mfma(xa[s & 1][mb], bw[j & 1][i], acc[h * HB + mb][i]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int FMT, int NTW, int MBG, int WV>
+__global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
+    extern __shared__ u32x4 gsk_lds[];                   // two X buffers of 4 MBG fragments
+    __shared__ int s_old;
+    constexpr int MT = 16 * MBG, NF = 4 * MBG, FPW = NF / WV, TPW = NTW * WV;
+    static_assert(FPW % 4 == 0 && MBG % 8 == 0, "fragment split");
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    constexpr uint32_t SLOT = (uint32_t) WV * MBG * NTW * 1024;       // bytes of one partial tile
+    u32x4 * xs0 = gsk_lds, * xs1 = gsk_lds + NF * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15;
+    const int q = lane >> 4;
+    // workgroup i runs on XCD i % 8: consecutive logical indices (adjacent iteration ranges, hence
+    // adjacent tiles) go to one XCD so that its L2 holds their shared X rows and weight columns
+    const int64_t G = gridDim.x, wg = blockIdx.x;
+    const int64_t lid = G % 8 == 0 ? (wg % 8) * (G / 8) + wg / 8 : wg;
+    constexpr int64_t GMS = 4;
+    const int64_t gm = (a.M + MT - 1) / MT, gn = (a.NT + TPW - 1) / TPW, total = gm * gn * a.KB;
+    const int64_t itb = lid * a.ipw, ite = itb + a.ipw < total ? itb + a.ipw : total;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
+    const bool ktail = a.K % 128 != 0;
+    for (int64_t it = itb; it < ite;) {
+        const int64_t t = it / a.KB, kb0 = it % a.KB, kb1 = a.KB - kb0 < ite - it ? a.KB : kb0 + (ite - it);
+        it += kb1 - kb0;
+        // tile -> (M block, N block): groups of GMS M blocks x all N blocks, M fastest
+        const int64_t grp = t / (GMS * gn), in = t % (GMS * gn);
+        const int64_t gms = gm - grp * GMS < GMS ? gm - grp * GMS : GMS;
+        const int64_t m0 = (grp * GMS + in % gms) * MT, t0 = (in / gms) * TPW + wave * NTW;
+        int nt_ok = (int) (a.NT - t0 < NTW ? a.NT - t0 : NTW);
+        if (nt_ok < 0) nt_ok = 0;
+        __amdgpu_buffer_rsrc_t wrs[NTW];
+#pragma unroll
+        for (int i = 0; i < NTW; i++) {
+            const int64_t tt = i < nt_ok ? t0 + i : (nt_ok > 0 ? t0 : 0);
+            wrs[i] = __builtin_amdgcn_make_buffer_rsrc((void *) (a.W + tt * a.KB * BLK), (short) 0,
+                                                       (int) (uint32_t) (a.KB * BLK), 0x00020000);
+        }
+        uint32_t xrow[FPW / 4];
+#pragma unroll
+        for (int g = 0; g < FPW / 4; g++) {
+            const int64_t m = m0 + 16 * ((FPW * wave) / 4 + g) + r;
+            xrow[g] = m < a.M ? (uint32_t) ((m * a.ldx + 8 * q) * 2) : 0x80000000u;
+        }
+        f32x4 acc[MBG][NTW];
+#pragma unroll
+        for (int mb = 0; mb < MBG; mb++)
+#pragma unroll
+            for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        u32x4 wc[NTW], wn[NTW];
+        Par<FMT> pc[NTW], pn[NTW];
+        __syncthreads();                                  // the previous segment is done with xs0 / xs1
+        gemm_load_x_sk<FPW>(xr, xrow, kb0, ktail && kb0 + 1 == a.KB, a.K, wave, q, xs0);
+        gemm_load_w<FMT, NTW>(wrs, kb0, lane, r, wc, pc);
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
+        // one block per iteration (a single MFMA code path keeps the accumulators in place): block
+        // b + 1 streams into the other LDS buffer and the other register set while b computes
+        u32x4 * cur = xs0, * nxt = xs1;
+        for (int64_t b = kb0; b < kb1; b++) {
+            if (b + 1 < kb1) {
+                gemm_load_x_sk<FPW>(xr, xrow, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, nxt);
+                gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wn, pn);
+            }
+            gemm_block_sk<FMT, NTW, MBG>(cur, wc, pc, lane, acc);
+            __builtin_amdgcn_s_waitcnt(0x0f70);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < NTW; i++) { wc[i] = wn[i]; pc[i] = pn[i]; }
+            u32x4 * t_ = cur; cur = nxt; nxt = t_;
+        }
+
+        // Y from the accumulators, plus (second segment) the other segment's partial tile, added
+        // at the store so that no updated copy of the accumulators has to be merged with them
+        auto store_tile = [&](bool addp, const __amdgpu_buffer_rsrc_t & wsr) {
+            // lane (q, r) holds rows 4 q + v of A block mb, column r of weight tile t0 + i
+#pragma unroll
+            for (int mb = 0; mb < MBG; mb++) {
+#pragma unroll
+                for (int i = 0; i < NTW; i++) {
+                    f32x4 v4 = acc[mb][i];
+                    if (addp)
+                        v4 += __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                       wsr, (uint32_t) ((((wave * MBG + mb) * NTW + i) * 64 + lane) * 16), 0, 16));
+                    if (i >= nt_ok) continue;
+                    const int64_t n = 16 * (t0 + i) + r;
+                    if (n >= a.N) continue;
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int64_t m = m0 + 16 * mb + 4 * q + v;
+                        if (m < a.M) store_out(a.y, a.yf32, m * a.ldy + n, v4[v]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        if (kb0 == 0 && kb1 == a.KB) {
+            store_tile(false, xr);
+            continue;
+        }
+        const int64_t slot = kb0 > 0 ? lid - 1 : lid;
+        int32_t * sc = a.sync + slot * GSK_SYNC_STRIDE;
+        if (tid == 0) s_old = __hip_atomic_fetch_add(sc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int old = s_old;
+        const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *) ((char *) a.ws + (int64_t) slot * SLOT), (short) 0, (int) SLOT, 0x00020000);
+        if (old == 0) {                                   // first segment: publish the partial
+#pragma unroll
+            for (int mb = 0; mb < MBG; mb++)
+#pragma unroll
+                for (int i = 0; i < NTW; i++)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mb][i]), wsr,
+                                                           (uint32_t) ((((wave * MBG + mb) * NTW + i) * 64 + lane) * 16),
+                                                           0, 16 /* sc1: agent scope */);
+            __builtin_amdgcn_s_waitcnt(0x0f70);           // the stores have completed
+            __syncthreads();
+            if (tid == 0) __hip_atomic_store(sc + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {                                          // second: wait for the partial, add, store
+            if (tid == 0) {
+                uint32_t polls = 0;
+                while (__hip_atomic_load(sc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+                    if (++polls > a.spin) {
+                        __hip_atomic_store(a.sync + (int64_t) G * GSK_SYNC_STRIDE, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+            __syncthreads();
+            store_tile(true, wsr);
+            if (tid == 0) {
+                __hip_atomic_store(sc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(sc + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ MoE prefill: grouped GEMM
 // Work item = (expert e, first permuted position, rows <= 64) from k_moe_permute; blockIdx.y =
 // item, blockIdx.x = a group of output columns. Workgroup: 4 waves x 2 weight tiles, 64 rows of X

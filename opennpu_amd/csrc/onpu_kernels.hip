@@ -303,6 +303,18 @@ hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s) {
+    if (cfg < 0 || cfg > 2 || grid <= 0 || a.ipw <= 0 || !a.ws || !a.sync) return hipErrorInvalidValue;
+    if (a.M * a.ldx * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;     // 32-bit X offsets
+    switch (fmt) {
+        case 0: return qgemm_sk_f0(a, cfg, grid, s);
+        case 1: return qgemm_sk_f1(a, cfg, grid, s);
+        case 2: return qgemm_sk_f2(a, cfg, grid, s);
+        case 3: return qgemm_sk_f3(a, cfg, grid, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s) {
     if (a.xbytes <= 0 || a.xbytes >= ((int64_t) 1 << 31) || maxitems <= 0 || maxitems > 65535) return hipErrorInvalidValue;
     if (which == 0 && (a.NT % 2 || a.N != 16 * a.NT)) return hipErrorInvalidValue;   // gate | up halves of whole tiles

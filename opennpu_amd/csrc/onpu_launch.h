@@ -22,7 +22,7 @@ struct QArgs {
     int tw;                   // tile groups per workgroup (waves = tw * K parts); 1 for EPI_SLOTSUM
 };
 
-// k_qgemm: prefill, Y[M][N] = X[M][K] . deq(W)^T
+// k_qgemm / k_qgemm_sk: prefill, Y[M][N] = X[M][K] . deq(W)^T
 struct GArgs {
     const uint8_t * W;
     int64_t NT, KB, N, K, M;
@@ -31,7 +31,15 @@ struct GArgs {
     void * y;
     int64_t ldy;
     int yf32;
+    // k_qgemm_sk only: K-block iterations per workgroup over the tile-major sequence of
+    // tiles * KB; fp32 partial tiles, one slot per workgroup boundary; per slot an arrival counter
+    // and a ready flag (GSK_SYNC_STRIDE ints apart, zero between launches), then one error flag
+    int64_t ipw;
+    float * ws;
+    int32_t * sync;
+    uint32_t spin;
 };
+constexpr int GSK_SYNC_STRIDE = 16;
 
 // grouped MoE products (k_moe_gemm) over a device work list (expert, first position, rows)
 struct MArgs {
@@ -79,6 +87,11 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
 int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl);
 int qgemv_max_waves(int mb, int rt, int nb, int xl);
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
+// k_qgemm_sk configurations: {weight tiles per wave, 16-row A blocks, waves}; rows and columns of
+// the workgroup tile are 16 * MBG and 16 * NTW * WV
+struct GskCfg { int ntw, mbg, wv; };
+constexpr GskCfg GSK_CFGS[3] = {{2, 16, 8}, {4, 16, 4}, {2, 16, 4}};
+hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s);
 hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
                         hipStream_t s);
 hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_per_item, int32_t * off, int32_t * perm,
@@ -123,6 +136,7 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
     hipError_t qgemv_f##id(int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,       \
                            size_t lds, hipStream_t s);                                                    \
     hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
+    hipError_t qgemm_sk_f##id(const GArgs & a, int cfg, int grid, hipStream_t s);                          \
     hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
     hipError_t chain_f##id(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,  \
                            hipStream_t s);                                                                \

@@ -115,6 +115,41 @@ def test_gemm_ragged(gpu, fmt, M):
     check_gemm(y, fmt, st, N, K, xb, what=f"gemm fmt {fmt} M {M}")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemm_stream_k(gpu, fmt, monkeypatch):
+    """256-row stream-K GEMM (k_qgemm_sk) on a ragged shape with more tiles than CUs, so that
+    workgroup boundaries cut tiles in two: a 400-column slice over all rows and 32 full rows against
+    the oracle; a second call gives the same bits (the slot counters were left at zero and the
+    result does not depend on which segment of a cut tile finished first); the 128-row kernel agrees
+    to fp32 summation order."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    M, N = 2100, 7400
+    K = 640 if fmt == orc.FMT_G128S else 608          # 608: a K tail inside the last 128-wide block
+    st = syn.weights(fmt, N, K, 23)
+    xb = syn.activations(M, K, 24)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        x = to_torch_bf16(xb).reshape(M, K)
+        y1 = q.mv(x, f32=True)
+        y2 = q.mv(x, f32=True)
+        monkeypatch.setenv("ONPU_GEMM_SK", "0")
+        y0 = q.mv(x, f32=True)
+        monkeypatch.delenv("ONPU_GEMM_SK")
+        yb = q.mv(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), "stream-K GEMM is not deterministic"
+        d = ((y1 - y0).abs().max() / y0.abs().max()).item()
+        assert d <= 1e-5, f"stream-K vs 128-row GEMM differ by {d:.3e} of max|y|"
+        rows = np.random.default_rng(1).choice(M, 32, replace=False)
+        yc = from_torch(yb[:, N - 400:])
+        yr = from_torch(yb[torch.as_tensor(rows, device=yb.device)])
+    finally:
+        q.free()
+    check_gemm(yc, fmt, st, N, K, xb, N - 400, N, what=f"stream-K fmt {fmt} column slice")
+    check_gemm(yr, fmt, st, N, K, xb[rows], what=f"stream-K fmt {fmt} rows")
+
+
 @pytest.mark.parametrize("name,N,K", [("up", 14336, 4096), ("down", 4096, 14336)])
 def test_gemm_llama_ffn(gpu, name, N, K):
     """Llama-3.1-8B FFN prefill at M=2048: all rows of a 128-column slice plus 48 full rows."""
