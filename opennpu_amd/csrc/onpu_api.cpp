@@ -259,12 +259,27 @@ Plan plan_slotsum(int64_t KB, int k) {
 // Every CU gets one workgroup and an equal share of the tiles * KB iterations when there are at least
 // as many tiles as CUs; with half as many, each tile is split in two K halves. False (use k_qgemm)
 // when neither holds or when some tile would be cut by more than one workgroup boundary.
-bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & grid, int64_t & ipw) {
-    cfg = env_int("ONPU_GSK_CFG", 0);
-    if (cfg < 0 || cfg > 2 || cus <= 0) return false;
+bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & grid, GArgs & a) {
+    cfg = 0;
+    if (cus <= 0) return false;
     const GskCfg c = GSK_CFGS[cfg];
     const int64_t MT = 16 * c.mbg, TPW = (int64_t) c.ntw * c.wv;
     const int64_t tiles = ((M + MT - 1) / MT) * ((NT + TPW - 1) / TPW), total = tiles * KB;
+    // two-phase: whole tiles in step, then the remainder cut once per tile at s, chosen so that
+    // s ~ c (KB - s) with c = ceil(R / (cus - R)) tail pieces per workgroup
+    const int64_t F = tiles / cus, R = tiles % cus;
+    if (env_int("ONPU_GSK_SCHED", 1) == 1 && (F > 0 || 2 * R >= cus) && (R == 0 || KB >= 2)) {
+        a.sched = 1;
+        a.F = F;
+        a.R = R;
+        a.c = R ? (R + (cus - R) - 1) / (cus - R) : 0;
+        a.s = R ? std::min<int64_t>(KB - 1, std::max<int64_t>(1, (a.c * KB + a.c / 2 + 1) / (a.c + 1))) : KB;
+        a.ipw = KB;
+        grid = cus;
+        return true;
+    }
+    a.sched = 0;
+    int64_t & ipw = a.ipw;
     if (tiles >= cus) ipw = (total + cus - 1) / cus;
     else if (2 * tiles >= cus && KB % 2 == 0) ipw = KB / 2;
     else return false;
@@ -310,16 +325,16 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
     }
     int cfg = 0;
-    int64_t grid = 0, ipw = 0;
-    if (env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ipw) &&
+    int64_t grid = 0;
+    GArgs ga{};
+    if (env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ga) &&
         M * m->K * 2 < ((int64_t) 1 << 31)) {
         hipError_t e = gsk_workspace(m);
         if (e != hipSuccess) return e;
-        GArgs a{};
-        a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
-        a.x = x; a.ldx = m->K; a.y = y; a.ldy = m->N; a.yf32 = yf32;
-        a.ipw = ipw; a.ws = m->gsk_ws.as<float>(); a.sync = m->gsk_sync.as<int32_t>(); a.spin = 1u << 22;
-        return launch_qgemm_sk(m->fmt, a, cfg, (int) grid, s);
+        ga.W = W; ga.NT = m->g.NT; ga.KB = m->g.KB; ga.N = m->N; ga.K = m->K; ga.M = M;
+        ga.x = x; ga.ldx = m->K; ga.y = y; ga.ldy = m->N; ga.yf32 = yf32;
+        ga.ws = m->gsk_ws.as<float>(); ga.sync = m->gsk_sync.as<int32_t>(); ga.spin = 1u << 22;
+        return launch_qgemm_sk(m->fmt, ga, cfg, (int) grid, s);
     }
     // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
     // workgroups, else 2 (128 x 128); 4 (128 x 256) runs out of registers and is slower

@@ -47,8 +47,6 @@ hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
 hipError_t FN(qgemm_sk)(const GArgs & a, int cfg, int grid, hipStream_t s) {
     const size_t lds = (size_t) 2 * 4 * GSK_CFGS[cfg].mbg * 1024;
     if (cfg == 0) k_qgemm_sk<F, 2, 16, 8><<<grid, 512, lds, s>>>(a);
-    else if (cfg == 1) k_qgemm_sk<F, 4, 16, 4><<<grid, 256, lds, s>>>(a);
-    else if (cfg == 2) k_qgemm_sk<F, 2, 16, 4><<<grid, 256, lds, s>>>(a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

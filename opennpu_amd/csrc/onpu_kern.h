@@ -818,10 +818,16 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
 // v_mfma_f32_16x16x32_bf16, which the matrix pipe hides when two waves share a SIMD (the 128-row
 // k_qgemm leaves 2.9 per MFMA, which it does not). X blocks move HBM -> LDS by buffer-to-LDS loads
 // into two MBG * 4 KiB buffers, weights stream into two register sets, as in k_qgemm.
-// Work split (stream-K): the tiles' K blocks form one tile-major sequence of tiles * KB
-// iterations and workgroup g takes [g ipw, (g + 1) ipw), so every CU gets the same number of MFMAs
-// whatever the tile count. A tile cut by a workgroup boundary has two segments (the host keeps it
-// to two): the first to finish stores its fp32 accumulators to the boundary's slot with
+// Work split, one workgroup per CU, every CU the same number of MFMAs whatever the tile count:
+//   two-phase (sched 1): F rounds in which workgroup g takes all of tile r G + g (the 32
+//     workgroups of an XCD hold a block of 4 M tiles x 8 N tiles and step through K together, so
+//     each X block and weight block they share is fetched into that XCD's L2 once), then the R
+//     remaining tiles cut at K block s: g < R takes [0, s) of tile F G + g (again in step), the
+//     other workgroups take [s, KB) of c tiles each;
+//   stream-K (sched 0): the tiles' K blocks as one tile-major sequence, workgroup g takes
+//     iterations [g ipw, (g + 1) ipw).
+// A cut tile has two segments (the host keeps it to two): the first to finish stores its fp32
+// accumulators to the tile's slot with
 // agent-scope stores (coherent across the XCDs' L2 caches once complete, no cache write-back) and
 // raises the slot's flag; the second waits for the flag (raised by a workgroup already in its
 // epilogue, so the wait is short and bounded), adds the partial and stores Y. Two addends give
@@ -850,10 +856,6 @@ DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow
 template <int FMT, int NTW, int MBG>
 DEV void gemm_block_sk(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int lane,
                        f32x4 (&acc)[MBG][NTW]) {
-#ifdef GSK_OLD_BLOCK
-    gemm_block<FMT, NTW, MBG>(xsb, wr, pr, lane, acc);
-    return;
-#endif
     constexpr int HB = 8, H = MBG / HB, S = 4 * H;
     u32x4 xa[2][HB], bw[2][NTW];
 #pragma unroll
@@ -912,9 +914,35 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
     const bool ktail = a.K % 128 != 0;
-    for (int64_t it = itb; it < ite;) {
-        const int64_t t = it / a.KB, kb0 = it % a.KB, kb1 = a.KB - kb0 < ite - it ? a.KB : kb0 + (ite - it);
-        it += kb1 - kb0;
+    int64_t it = itb;                                     // stream-K cursor
+    for (int64_t qs = 0;; qs++) {
+        int64_t t, kb0, kb1, slot;                        // this segment: tile, K blocks, partial slot
+        if (a.sched == 0) {
+            if (it >= ite) break;
+            t = it / a.KB;
+            kb0 = it % a.KB;
+            kb1 = a.KB - kb0 < ite - it ? a.KB : kb0 + (ite - it);
+            it += kb1 - kb0;
+            slot = kb0 > 0 ? lid - 1 : lid;               // the boundary that cuts the tile
+        } else {
+            if (qs < a.F) {
+                t = qs * G + lid;
+                kb0 = 0;
+                kb1 = a.KB;
+            } else if (lid < a.R) {
+                if (qs > a.F) break;
+                t = a.F * G + lid;
+                kb0 = 0;
+                kb1 = a.s;
+            } else {
+                const int64_t p = (lid - a.R) * a.c + (qs - a.F);
+                if (qs - a.F >= a.c || p >= a.R) break;
+                t = a.F * G + p;
+                kb0 = a.s;
+                kb1 = a.KB;
+            }
+            slot = t - a.F * G;
+        }
         // tile -> (M block, N block): groups of GMS M blocks x all N blocks, M fastest
         const int64_t grp = t / (GMS * gn), in = t % (GMS * gn);
         const int64_t gms = gm - grp * GMS < GMS ? gm - grp * GMS : GMS;
@@ -991,7 +1019,6 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
             store_tile(false, xr);
             continue;
         }
-        const int64_t slot = kb0 > 0 ? lid - 1 : lid;
         int32_t * sc = a.sync + slot * GSK_SYNC_STRIDE;
         if (tid == 0) s_old = __hip_atomic_fetch_add(sc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();

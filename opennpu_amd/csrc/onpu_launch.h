@@ -38,6 +38,11 @@ struct GArgs {
     float * ws;
     int32_t * sync;
     uint32_t spin;
+    // sched 1 (two-phase): rounds F of one whole tile per workgroup, then the R remaining tiles
+    // cut at K block s: workgroup g < R takes blocks [0, s) of tile F G + g, workgroup g >= R the
+    // blocks [s, KB) of c tiles. sched 0: the ipw ranges above.
+    int sched;
+    int64_t F, R, s, c;
 };
 constexpr int GSK_SYNC_STRIDE = 16;
 
@@ -87,10 +92,11 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
 int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl);
 int qgemv_max_waves(int mb, int rt, int nb, int xl);
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
-// k_qgemm_sk configurations: {weight tiles per wave, 16-row A blocks, waves}; rows and columns of
-// the workgroup tile are 16 * MBG and 16 * NTW * WV
+// k_qgemm_sk configuration: {weight tiles per wave, 16-row A blocks, waves}; rows and columns of the
+// workgroup tile are 16 * MBG and 16 * NTW * WV. (Measured on MI355X against 256 x 64 per wave with
+// one wave per SIMD and 256 x 32 with four waves: both slower, the first by ~30 %.)
 struct GskCfg { int ntw, mbg, wv; };
-constexpr GskCfg GSK_CFGS[3] = {{2, 16, 8}, {4, 16, 4}, {2, 16, 4}};
+constexpr GskCfg GSK_CFGS[1] = {{2, 16, 8}};
 hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s);
 hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
                         hipStream_t s);

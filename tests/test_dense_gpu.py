@@ -116,16 +116,18 @@ def test_gemm_ragged(gpu, fmt, M):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_gemm_stream_k(gpu, fmt, monkeypatch):
-    """256-row stream-K GEMM (k_qgemm_sk) on a ragged shape with more tiles than CUs, so that
-    workgroup boundaries cut tiles in two: a 400-column slice over all rows and 32 full rows against
-    the oracle; a second call gives the same bits (the slot counters were left at zero and the
-    result does not depend on which segment of a cut tile finished first); the 128-row kernel agrees
-    to fp32 summation order."""
+@pytest.mark.parametrize("M,N,K", [(2100, 7400, 640), (1000, 14300, 512)])
+def test_gemm_stream_k(gpu, fmt, M, N, K, monkeypatch):
+    """256-row GEMM with a split of K (k_qgemm_sk) on ragged shapes with more tiles than CUs:
+    2100 x 7400 has one round of whole tiles and 5 tiles cut in two; 1000 x 14300 has 224 tiles, each
+    cut into a head piece and a tail piece, seven tail pieces per workgroup. A 400-column slice over
+    all rows and 32 full rows against the oracle; a second call gives the same bits (the slot
+    counters were left at zero, and a cut tile's sum does not depend on which piece finished first);
+    the plain stream-K split and the 128-row kernel agree to fp32 summation order."""
     import torch
     from opennpu_amd.device import QMatrix
-    M, N = 2100, 7400
-    K = 640 if fmt == orc.FMT_G128S else 608          # 608: a K tail inside the last 128-wide block
+    if fmt != orc.FMT_G128S:
+        K -= 32                                       # a K tail inside the last 128-wide block
     st = syn.weights(fmt, N, K, 23)
     xb = syn.activations(M, K, 24)
     q = QMatrix(N, K, fmt, st)
@@ -133,21 +135,25 @@ def test_gemm_stream_k(gpu, fmt, monkeypatch):
         x = to_torch_bf16(xb).reshape(M, K)
         y1 = q.mv(x, f32=True)
         y2 = q.mv(x, f32=True)
+        monkeypatch.setenv("ONPU_GSK_SCHED", "0")
+        ys = q.mv(x, f32=True)
         monkeypatch.setenv("ONPU_GEMM_SK", "0")
         y0 = q.mv(x, f32=True)
         monkeypatch.delenv("ONPU_GEMM_SK")
+        monkeypatch.delenv("ONPU_GSK_SCHED")
         yb = q.mv(x)
         torch.cuda.synchronize()
-        assert torch.equal(y1, y2), "stream-K GEMM is not deterministic"
-        d = ((y1 - y0).abs().max() / y0.abs().max()).item()
-        assert d <= 1e-5, f"stream-K vs 128-row GEMM differ by {d:.3e} of max|y|"
+        assert torch.equal(y1, y2), "split-K GEMM is not deterministic"
+        for other, what in ((y0, "128-row GEMM"), (ys, "stream-K split")):
+            d = ((y1 - other).abs().max() / other.abs().max()).item()
+            assert d <= 1e-5, f"two-phase split vs {what} differ by {d:.3e} of max|y|"
         rows = np.random.default_rng(1).choice(M, 32, replace=False)
         yc = from_torch(yb[:, N - 400:])
         yr = from_torch(yb[torch.as_tensor(rows, device=yb.device)])
     finally:
         q.free()
-    check_gemm(yc, fmt, st, N, K, xb, N - 400, N, what=f"stream-K fmt {fmt} column slice")
-    check_gemm(yr, fmt, st, N, K, xb[rows], what=f"stream-K fmt {fmt} rows")
+    check_gemm(yc, fmt, st, N, K, xb, N - 400, N, what=f"split-K fmt {fmt} {M}x{N} column slice")
+    check_gemm(yr, fmt, st, N, K, xb[rows], what=f"split-K fmt {fmt} {M}x{N} rows")
 
 
 @pytest.mark.parametrize("name,N,K", [("up", 14336, 4096), ("down", 4096, 14336)])
