@@ -75,6 +75,8 @@ def _declare(lib):
         "onpu_dense_argmax_dev": (I32, [P, P, I64, P, P, P]),
         "onpu_moe_route_dev": (I32, [P, I64, I32, I32, I32, P, P, P]),
         "onpu_moe_ffn_dev": (I32, [P, P, I64, P, I32, P, P, I32, P]),
+        "onpu_moe_decode_dev": (I32, [P, P, P, I64, I32, I32, I32, P, P, P, I32, P]),
+        "onpu_moe_status": (I32, [P]),
         "onpu_chain_new": (P, [C.POINTER(P), C.POINTER(P), C.POINTER(P), I32, I64, I32]),
         "onpu_chain_run": (I32, [P, P]),
         "onpu_chain_status": (I32, [P]),

@@ -108,6 +108,7 @@ struct Ffn {
     Mat4 * gu = nullptr, * dn = nullptr;
     bool fused = false;
     DBuf ws[12];
+    DBuf md_act, md_sync;                  // k_moe_decode: act rows, counters (zeroed once)
 };
 
 int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
@@ -378,6 +379,35 @@ hipError_t bank_core(Mat4 * m, const uint16_t * x, int x_per_slot, int64_t T, co
     return hipSuccess;
 }
 
+// MoE decode in one launch (k_moe_decode; opt-in with ONPU_MOE_FUSED=1, slower than the router
+// kernel plus two GEMV launches on MI355X) when the shapes fit it: route from logits (non-null;
+// ids / w are then written) or take ids / w, then both expert products and the weighted sum.
+// hipErrorNotSupported: use the multi-launch path.
+hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, int64_t T, int k, int renorm, int E,
+                           int32_t * ids, float * w, void * y, int yf32, hipStream_t s) {
+    Mat4 * gu = f->gu, * dn = f->dn;
+    const int64_t I = gu->N / 2;
+    if (!env_int("ONPU_MOE_FUSED", 0) || gu->fmt != dn->fmt || gu->N % 2 ||
+        !moe_decode_fits(gu->K, I, dn->N, gu->g.KB, dn->g.KB, (int) T, k, E) || dn->K != I)
+        return hipErrorNotSupported;
+    hipError_t e = f->md_act.ensure((size_t) (MD_MAX_T * MD_MAX_K) * (size_t) I * 2);
+    if (e != hipSuccess) return e;
+    if (f->md_sync.n == 0) {
+        if ((e = f->md_sync.ensure(MD_SYNC_INTS * 4)) != hipSuccess) return e;
+        if ((e = hipMemset(f->md_sync.p, 0, MD_SYNC_INTS * 4)) != hipSuccess) return e;
+    }
+    MDArgs a{};
+    a.Wg = gu->dev; a.gstride = gu->dstride; a.gNT = gu->g.NT; a.gKB = gu->g.KB;
+    a.Wd = dn->dev; a.dstride = dn->dstride; a.dNT = dn->g.NT; a.dKB = dn->g.KB;
+    a.H = gu->K; a.I = I; a.Nd = dn->N;
+    a.x = x; a.logits = logits; a.E = E; a.k = k; a.renorm = renorm; a.T = (int) T;
+    a.ids = ids; a.w = w; a.act = f->md_act.as<uint16_t>(); a.y = y; a.yf32 = yf32;
+    a.sync = f->md_sync.as<int32_t>();
+    a.npairs = T * k * (I / 16); a.nunits = T * dn->g.NT;
+    a.spin = 1u << 20;
+    return launch_moe_decode(gu->fmt, a, device().cus, s);
+}
+
 // routed-expert FFN on device data (act 0, no biases): x bf16 [T][H], ids/w [T][k] -> y [T][Nd]
 hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids, int k, const float * w, void * y,
                     int yf32, hipStream_t s) {
@@ -387,6 +417,9 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
     const int decode_max = env_int("ONPU_MOE_DECODE_MAX", 4);
     hipError_t e;
     if (T <= decode_max && k <= 16) {
+        e = moe_decode_core(f, nullptr, x, T, k, 1, (int) gu->E, const_cast<int32_t *>(ids),
+                            const_cast<float *>(w), y, yf32, s);
+        if (e != hipErrorNotSupported) return e;
         // gate_up with SiLU(gate) * up per slot, then down with the weighted slot sum per token
         e = f->ws[0].ensure((size_t) (n * I * 2));
         if (e != hipSuccess) return e;
@@ -798,6 +831,33 @@ int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, i
     if (!f->fused) { set_err("onpu_moe_ffn_dev: this FFN shape has no fused path"); return -1; }
     HIPR(ffn_core(f, (const uint16_t *) x, T, ids, k, w, y, y_f32, (hipStream_t) stream));
     return 0;
+}
+
+int onpu_moe_decode_dev(void * h, const float * logits, const void * x, int64_t T, int E, int k, int renorm,
+                        int32_t * ids, float * w, void * y, int y_f32, void * stream) {
+    auto * f = (Ffn *) h;
+    if (!f->fused) { set_err("onpu_moe_decode_dev: this FFN shape has no fused path"); return -1; }
+    if (E != f->gu->E) { set_err("onpu_moe_decode_dev: E differs from the bank's expert count"); return -1; }
+    const hipError_t e = moe_decode_core(f, logits, (const uint16_t *) x, T, k, renorm, E, ids, w, y, y_f32,
+                                         (hipStream_t) stream);
+    if (e != hipErrorNotSupported) {
+        HIPR(e);
+        return 0;
+    }
+    HIPR(launch_route(logits, T, E, k, renorm, ids, w, (hipStream_t) stream));
+    HIPR(ffn_core(f, (const uint16_t *) x, T, ids, k, w, y, y_f32, (hipStream_t) stream));
+    return 0;
+}
+
+int onpu_moe_status(void * h) {
+    auto * f = (Ffn *) h;
+    if (f->md_sync.n == 0) return 0;
+    int32_t flag = 0;
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(&flag, f->md_sync.as<int32_t>(MD_SYNC_ERR * 4), 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (flag && hipMemset(f->md_sync.as<int32_t>(MD_SYNC_ERR * 4), 0, 4) != hipSuccess) return -1;
+    return flag ? 1 : 0;
 }
 
 // ---------------------------------------------------------------- chained decode GEMVs

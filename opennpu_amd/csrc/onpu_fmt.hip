@@ -51,6 +51,13 @@ hipError_t FN(qgemm_sk)(const GArgs & a, int cfg, int grid, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t FN(moe_decode)(const MDArgs & a, int gb, int grid, size_t lds, hipStream_t s) {
+    if (gb == 2 && a.dKB <= 6) k_moe_decode<F, 2, 6><<<grid, 512, lds, s>>>(a);
+    else if (gb <= 4 && a.dKB <= MD_MAX_DB) k_moe_decode<F, MD_MAX_GB, MD_MAX_DB><<<grid, 512, lds, s>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t FN(moe_gemm)(int which, const MArgs & a, dim3 grid, hipStream_t s) {
     if (which == 0) k_moe_gemm<F, 0><<<grid, 256, 0, s>>>(a);
     else k_moe_gemm<F, 1><<<grid, 256, 0, s>>>(a);

@@ -38,22 +38,19 @@ DEV f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 
 // D_j -> 8 bf16 holding 128 + u (bf16 0x43XX = 128 + XX for XX < 128), in B-operand order:
 // r.x = (d & M) | mag, r.y = ((d >> 4) & M) | mag, r.z = ((d >> 8) & M) | mag, r.w = ((d >> 12) & M) | mag.
-// Seven VALU ops with v_and_or_b32 (the compiler splits it into and + or). The block ends with
-// s_nop 1: an MFMA may read these registers as its B operand right after the asm, and the ISA wants
-// two wait states between a VALU write and that read (the compiler cannot see inside the asm).
+// Seven VALU ops: with the mask in an SGPR and mag in a VGPR, both opaque (gfx9 VOP3 takes no
+// literal), the compiler selects v_and_or_b32. Written as plain code, not inline asm, so that the compiler sees
+// VALU writes and keeps its MFMA hazard rules: an asm block may be given registers that an MFMA it
+// just issued still reads or writes (for M = 1 three of the four result registers of an MFMA are
+// dead, and the MFMA's late write-back then lands on the asm's output).
+// A value the optimizer cannot see through: an empty asm tied to its operand emits no instruction
+// and writes no register (so it raises no hazard), but the constant is no longer known.
+DEV uint32_t opaque_s(uint32_t v) { asm("" : "+s"(v)); return v; }
+DEV uint32_t opaque_v(uint32_t v) { asm("" : "+v"(v)); return v; }
+
 DEV u32x4 unpack_biased(uint32_t d, uint32_t mag) {
-    u32x4 r;
-    asm("v_and_or_b32 %0, %4, %5, %6\n\t"
-        "v_lshrrev_b32 %1, 4, %4\n\t"
-        "v_and_or_b32 %1, %1, %5, %6\n\t"
-        "v_lshrrev_b32 %2, 8, %4\n\t"
-        "v_and_or_b32 %2, %2, %5, %6\n\t"
-        "v_lshrrev_b32 %3, 12, %4\n\t"
-        "v_and_or_b32 %3, %3, %5, %6\n\t"
-        "s_nop 1"
-        : "=&v"(r.x), "=&v"(r.y), "=&v"(r.z), "=&v"(r.w)
-        : "v"(d), "s"(0x000F000Fu), "v"(mag));
-    return r;
+    const uint32_t M = opaque_s(0x000F000Fu), g = opaque_v(mag);
+    return (u32x4){(d & M) | g, ((d >> 4) & M) | g, ((d >> 8) & M) | g, ((d >> 12) & M) | g};
 }
 
 // code u (0..15) of element e of D_j
@@ -225,6 +222,84 @@ __global__ __launch_bounds__(64) void k_dequant(const uint8_t * __restrict__ W, 
             if (bf16) *(uint32_t *) ((uint16_t *) out + n * K + k) = pack_bf16x2(v0, v1);
             else { ((float *) out)[n * K + k] = v0; ((float *) out)[n * K + k + 1] = v1; }
         }
+}
+
+// ------------------------------------------------------------------ router
+// Wave-wide reductions with DPP inside each 16-lane row and readlane across the four rows (no LDS
+// round trips): every lane gets the result.
+template <int CTRL>
+DEV uint32_t dpp_u(uint32_t v) { return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xf, 0xf, false); }
+DEV float readlane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+DEV uint32_t wave_umax(uint32_t v) {
+    v = max(v, dpp_u<0x111>(v));                      // row_shr:1 (lanes without a source see 0)
+    v = max(v, dpp_u<0x112>(v));                      // row_shr:2
+    v = max(v, dpp_u<0x114>(v));                      // row_shr:4
+    v = max(v, dpp_u<0x118>(v));                      // row_shr:8: lane 15 of each row has the row's max
+    const uint32_t a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
+    const uint32_t c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
+    return max(max(a, b), max(c, d));
+}
+
+DEV float wave_fsum(float v) {
+    v += __uint_as_float(dpp_u<0xB1>(__float_as_uint(v)));   // quad_perm [1,0,3,2]
+    v += __uint_as_float(dpp_u<0x4E>(__float_as_uint(v)));   // quad_perm [2,3,0,1]
+    v += __uint_as_float(dpp_u<0x124>(__float_as_uint(v)));  // row_ror:4
+    v += __uint_as_float(dpp_u<0x128>(__float_as_uint(v)));  // row_ror:8: every lane has its row's sum
+    return (readlane_f(v, 0) + readlane_f(v, 16)) +
+           (readlane_f(v, 32) + readlane_f(v, 48));
+}
+
+// float <-> unsigned key with the same order
+DEV uint32_t ord_key(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+DEV float ord_val(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k); }
+
+
+// Router of one token on one wave: softmax over E <= 256 logits, top-k by probability (ties to the
+// lower id), renormalised when renorm (moe_runtime.py:333-341, reference.py:72-76). Lane l holds
+// experts 4 l .. 4 l + 3, so the lowest lane holding the maximum also holds its lowest id. Lane j < k
+// returns pick j (id and weight).
+DEV void route_token(const float * __restrict__ l, int E, int k, int renorm, int & my_id, float & my_w) {
+    const int lane = threadIdx.x & 63;
+    float v[4];
+    uint32_t mk = 0;
+    for (int i = 0; i < 4; i++) {
+        const int e = 4 * lane + i;
+        v[i] = e < E ? l[e] : -INFINITY;
+        mk = max(mk, ord_key(v[i]));
+    }
+    const float mx = ord_val(wave_umax(mk));
+    float p[4], sum = 0.f;
+    for (int i = 0; i < 4; i++) {
+        const int e = 4 * lane + i;
+        p[i] = e < E ? expf(v[i] - mx) : 0.f;
+        sum += p[i];
+    }
+    sum = wave_fsum(sum);
+    // selection keys: probability bits + 1 (p >= 0, so the bits order like the values); 0 = taken
+    uint32_t key[4];
+    for (int i = 0; i < 4; i++) key[i] = 4 * lane + i < E ? __float_as_uint(p[i]) + 1u : 0u;
+    float ws = 0.f, my_p = 0.f;
+    my_id = 0;
+    for (int j = 0; j < k; j++) {
+        uint32_t lb = 0;
+        int li = 0;
+        for (int i = 0; i < 4; i++)
+            if (key[i] > lb) { lb = key[i]; li = i; }
+        const uint32_t best = wave_umax(lb);
+        const uint64_t hold = __ballot(lb == best);
+        const int first = __builtin_ctzll(hold);
+        const int bi = 4 * first + __builtin_amdgcn_readlane(li, first);
+        for (int i = 0; i < 4; i++)
+            if (lane == first && i == li) key[i] = 0u;
+        const float pj = __uint_as_float(best - 1u) / sum;
+        ws += pj;
+        if (lane == j) { my_id = bi; my_p = pj; }
+    }
+    my_w = renorm ? my_p / ws : my_p;
 }
 
 // ------------------------------------------------------------------ decode GEMV family
@@ -595,11 +670,11 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
 // with v_cvt_f32_ubyteN, one fma each (exact: u s fits fp32) and packed by v_cvt_pk_bf16_f32.
 template <int FMT>
 DEV u32x4 dequant8(uint32_t d, float s, float c) {
-    // the masks are opaque to the optimizer, which would otherwise fold each byte extraction into a
-    // 4-bit field extract (v_bfe) plus v_cvt_f32_ubyte0: two ops per weight instead of one
-    uint32_t lo, hi;
-    asm("v_and_b32 %0, %1, %2" : "=v"(lo) : "v"(d), "v"(0x0f0f0f0fu));
-    asm("v_and_b32 %0, %1, %2" : "=v"(hi) : "v"(d >> 4), "v"(0x0f0f0f0fu));
+    // an opaque mask, so that the optimizer cannot fold each byte extraction into a 4-bit field
+    // extract (v_bfe) plus v_cvt_f32_ubyte0 (two ops per weight instead of one); plain code rather
+    // than an asm v_and_b32, so that MFMA hazards stay visible to the compiler
+    const uint32_t M = opaque_s(0x0f0f0f0fu);
+    const uint32_t lo = d & M, hi = (d >> 4) & M;
     auto f = [&](uint32_t w, int byte) { return fmaf((float) ((w >> (8 * byte)) & 0xffu), s, c); };
     return (u32x4){pack_bf16x2(f(lo, 0), f(lo, 2)), pack_bf16x2(f(hi, 0), f(hi, 2)), pack_bf16x2(f(lo, 1), f(lo, 3)),
                    pack_bf16x2(f(hi, 1), f(hi, 3))};
@@ -1154,6 +1229,265 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
         }
 }
 
+
+// ------------------------------------------------------------------ MoE decode in one launch
+// Opt-in (ONPU_MOE_FUSED=1): measured on MI355X for Qwen3-30B-A3B at T = 1 it takes ~19 us against
+// ~16 us for the router kernel plus the two GEMV launches. Routing and x staging finish at ~2.5 us,
+// the expert weights are in by ~6 us, but the handoff of act between workgroups (store
+// acknowledgement, arrival, poll, reload: four memory round trips) costs more than the two kernel
+// boundaries it removes.
+// T <= 4 tokens, k <= 8 routed experts each (the reference's fused expert FFN, onpu_api.cpp:292-496,
+// gemv_any.cc:34-50, and onpu_moe_ffn's act 0 path, onpu_api.cpp:261-278 with onpu_cpu.cpp:233-274):
+//   router (when logits are given): softmax -> top-k -> renorm, as k_route;
+//   phase A: slot s = t k + j, expert e = ids[s]: act[s][i] = bf16(silu(g_i) * u_i) with g, u the
+//            rows i and I + i of gate_up_e times x_t, for every 16-row tile pair (gate tile i / 16,
+//            up tile I / 16 + i / 16) ("pairs");
+//   phase B: y[t][n] = sum_j w[t][j] (down_e(j) . act[t k + j])[n] for every 16-row tile of down
+//            ("units"), the k slots summed in slot order.
+// One workgroup of 8 waves per CU. Workgroup g takes pairs g, g + G, ... (the 8 waves split each
+// pair's K blocks and meet in LDS) and units G - 1 - g, 2 G - 1 - g, ... (wave j takes slot j), so
+// with one token the workgroups with fewer pairs are the ones with a unit. All weight loads are
+// issued as soon as the routing is known: the unit's down tiles first, then the pairs' tiles.
+// A workgroup publishes each pair's 16 act values with two 16-byte agent-scope stores (coherent
+// across the XCDs' L2 caches once complete), waits for its stores to complete and adds its pair
+// count to sync[0]; a workgroup with units waits until sync[0] counts every pair (a wait on workgroups that never wait themselves,
+// bounded by a.spin polls; a timeout raises sync[MD_SYNC_ERR]), reads the act rows with agent-scope
+// loads and finishes its units. The last workgroup with units clears sync[0] and sync[MD_SYNC_DONE]
+// again, so the counters are zero between launches (and a captured graph replays without resets).
+
+// x rows [T][H] -> LDS xs[T][xl] (bf16, zero past H) and their group sums xg[T][KB * GPB], by the
+// whole workgroup: thread u takes 8 elements, a group's threads are consecutive lanes of one wave
+template <int FMT>
+DEV void md_stage_x(const uint16_t * __restrict__ x, int T, int64_t H, int64_t KB, int64_t xl, uint16_t * xs,
+                    float * xg) {
+    constexpr int GS = FMT == ONPU_G128S ? 128 : 32, UPG = GS / 8, GPB = 128 / GS;
+    const uint32_t kp8 = (uint32_t) KB * 16, nunits = (uint32_t) T * kp8;
+    for (uint32_t u0 = 0; u0 < nunits; u0 += blockDim.x) {       // same trip count for the workgroup
+        const uint32_t u = u0 + threadIdx.x, t = u / kp8, k = (u - t * kp8) * 8;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (u < nunits && k < H) v = *(const u32x4 *) (x + (int64_t) t * H + k);
+        if (u < nunits) *LDS_U32X4(xs + (int64_t) t * xl + k) = v;
+        float sum = 0.f;
+        for (int d = 0; d < 4; d++) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+        for (int o = UPG / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (u < nunits && (k / 8) % UPG == 0) xg[(int64_t) t * KB * GPB + k / GS] = sum;
+    }
+}
+
+// One wave's M = 1 products over NB blocks of RT row tiles (weights and parameters loaded earlier):
+// the x row from LDS (xr, blocks b0 ..), its group sums xg; acc[rt][0] lanes 0..15 hold the partials
+// of tile rows 0..15. Blocks i >= nb are skipped (their loads re-read a valid block).
+template <int FMT, int RT, int NB>
+DEV void md_accum(const u32x4 (&wv)[NB][RT], const Par<FMT> (&par)[NB][RT], int nb, const uint16_t * xr,
+                  const float * xg, int64_t b0, f32x4 (&acc)[RT][1]) {
+    const int q = (threadIdx.x & 63) >> 4;
+    constexpr int GPB = FMT == ONPU_G128S ? 1 : 4;
+    bool valid[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) valid[rt] = true;
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        if (i >= nb) break;
+        const int64_t b = b0 + i;
+        u32x4 xa[1][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) xa[0][j] = *LDS_U32X4(xr + b * 128 + 32 * j + 8 * q);
+        f32x4 cs[1][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float v = *(const __attribute__((address_space(3))) float *) (xg + b * GPB + (j < GPB ? j : 0));
+            cs[0][j] = (f32x4){v, v, v, v};
+        }
+        qacc_block<FMT, 1, RT>(valid, wv[i], par[i], xa, cs, 0x43004300u, 1, acc);
+    }
+}
+
+// weights of NB blocks b0 .. of RT tiles (bases tb[rt]); blocks past nb re-read block b0
+template <int FMT, int RT, int NB>
+DEV void md_load(const uint8_t * const (&tb)[RT], int64_t b0, int nb, u32x4 (&wv)[NB][RT], Par<FMT> (&par)[NB][RT]) {
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const int lane = threadIdx.x & 63, r = lane & 15;
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const uint8_t * p = tb[rt] + (b0 + (i < nb ? i : 0)) * BLK;
+            wv[i][rt] = __builtin_nontemporal_load(GLB(const u32x4, p + 16 * lane));
+            par[i][rt] = load_par<FMT>(p, r);
+        }
+}
+
+// GB: gate_up K blocks per wave (the 8 waves split the H / 128 blocks); DB: down K blocks (I / 128
+// rounded up), both at most as built
+template <int FMT, int GB, int DB>
+__global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
+    extern __shared__ float mds[];
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    constexpr int GS = FMT == ONPU_G128S ? 128 : 32, GPB = 128 / GS;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 15;
+    const int64_t G = gridDim.x, g = blockIdx.x;
+    const int k = a.k, T = a.T;
+    const int64_t IT = a.I / 16;
+    // LDS: ids / w, x rows and sums, the cross-wave buffer, then per wave one act row and its sums
+    int32_t * sids = (int32_t *) mds;
+    float * sw = mds + MD_MAX_T * MD_MAX_K;
+    const int64_t xl = a.gKB * 128, al = (int64_t) DB * 128;
+    uint16_t * xs = (uint16_t *) (mds + 2 * MD_MAX_T * MD_MAX_K);
+    float * xg = (float *) (xs + T * xl);
+    float * red = xg + (T * a.gKB * GPB + 3) / 4 * 4;          // [8][2][64], 16-byte aligned
+    uint16_t * ab = (uint16_t *) (red + MD_WAVES * 2 * 64);      // [8][al]
+    float * abg = (float *) (ab + MD_WAVES * al);                // [8][DB * GPB]
+
+    // routing (wave 0) while the other waves stage x
+    if (a.logits) {
+        if (wave == 0)
+            for (int t = 0; t < T; t++) {
+                int id;
+                float wt;
+                route_token(a.logits + (int64_t) t * a.E, a.E, k, a.renorm, id, wt);
+                if (lane < k) {
+                    sids[t * k + lane] = id;
+                    sw[t * k + lane] = wt;
+                    if (g == 0) {
+                        a.ids[t * k + lane] = id;
+                        a.w[t * k + lane] = wt;
+                    }
+                }
+            }
+    } else if (threadIdx.x < T * k) {
+        sids[threadIdx.x] = a.ids[threadIdx.x];
+        sw[threadIdx.x] = a.w[threadIdx.x];
+    }
+    md_stage_x<FMT>(a.x, T, a.H, a.gKB, xl, xs, xg);
+    __syncthreads();
+
+    // the first unit's down tiles (wave j < k: slot j of the unit's token), then the first pair
+    const int64_t u0 = G - 1 - g;
+    u32x4 dw[DB][1];
+    Par<FMT> dp[DB][1];
+    auto load_unit = [&](int64_t u) {
+        const int64_t t = u / a.dNT, h = u % a.dNT;
+        const int j = wave < k ? wave : 0;
+        const uint8_t * tb[1] = {a.Wd + (int64_t) sids[t * k + j] * a.dstride + h * a.dKB * BLK};
+        md_load<FMT, 1, DB>(tb, 0, (int) a.dKB, dw, dp);
+    };
+    if (u0 < a.nunits) load_unit(u0);
+    const int64_t gb0 = (int64_t) wave * GB, gnb = a.gKB - gb0 < GB ? (a.gKB - gb0 > 0 ? a.gKB - gb0 : 0) : GB;
+    u32x4 gw[2][GB][2];
+    Par<FMT> gp[2][GB][2];
+    auto load_pair = [&](int64_t p, int buf) {
+        const int64_t s = p / IT, gt = p % IT;
+        const uint8_t * e = a.Wg + (int64_t) sids[s] * a.gstride;
+        const uint8_t * tb[2] = {e + gt * a.gKB * BLK, e + (IT + gt) * a.gKB * BLK};
+        md_load<FMT, 2, GB>(tb, gnb > 0 ? gb0 : 0, gnb > 0 ? (int) gnb : 1, gw[buf], gp[buf]);
+    };
+    auto do_pair = [&](int64_t p, const u32x4 (&wv)[GB][2], const Par<FMT> (&pv)[GB][2]) {
+        f32x4 acc[2][1] = {{{0.f, 0.f, 0.f, 0.f}}, {{0.f, 0.f, 0.f, 0.f}}};
+        const int64_t s = p / IT, gt = p % IT, t = s / k;
+        if (gnb > 0) md_accum<FMT, 2, GB>(wv, pv, (int) gnb, xs + t * xl, xg + t * a.gKB * GPB, gb0, acc);
+        red[(wave * 2 + 0) * 64 + lane] = acc[0][0][0];
+        red[(wave * 2 + 1) * 64 + lane] = acc[1][0][0];
+        __syncthreads();
+        // wave 0: lane r < 16 forms act of tile row r; lane 0 gathers the 16 bf16 (32 bytes) and
+        // publishes them with two 16-byte agent-scope stores, waits for them, and arrives
+        if (wave == 0) {
+            float gs = 0.f, us = 0.f;
+            for (int w = 0; w < MD_WAVES; w++) { gs += red[(w * 2 + 0) * 64 + r]; us += red[(w * 2 + 1) * 64 + r]; }
+            const uint32_t h = f32_to_bf16(silu_f(gs) * us);
+            const uint32_t pr = h | (__shfl_down(h, 1) << 16);        // lanes 2i: rows 2i, 2i + 1
+            u32x4 lo, hi;
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                lo[d] = __shfl(pr, 2 * d);
+                hi[d] = __shfl(pr, 8 + 2 * d);
+            }
+            if (lane == 0) {
+                const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+                    (void *) (a.act + s * a.I + gt * 16), (short) 0, 32, 0x00020000);
+                __builtin_amdgcn_raw_buffer_store_b128(lo, ar, 0, 0, 16 /* sc1: agent scope */);
+                __builtin_amdgcn_raw_buffer_store_b128(hi, ar, 16, 0, 16);
+            }
+        }
+        __syncthreads();                               // red is reused by the next pair
+    };
+    int64_t mine = 0;                                  // pairs done by this workgroup
+    // phase A: pairs g, g + G, ... alternating between the two register sets, the next pair's loads
+    // in flight while the current one computes
+    if (g < a.npairs) load_pair(g, 0);
+    for (int64_t p = g; p < a.npairs; p += 2 * G) {
+        if (p + G < a.npairs) load_pair(p + G, 1);
+        do_pair(p, gw[0], gp[0]);
+        mine++;
+        if (p + G >= a.npairs) break;
+        if (p + 2 * G < a.npairs) load_pair(p + 2 * G, 0);
+        do_pair(p + G, gw[1], gp[1]);
+        mine++;
+    }
+    // publish: this workgroup's act stores have completed, then one arrival for all its pairs
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+    if (threadIdx.x == 0 && mine > 0)
+        __hip_atomic_fetch_add(a.sync, (int32_t) mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (u0 >= a.nunits) return;
+
+    // phase B: wait until every pair is published
+    if (threadIdx.x == 0) {
+        uint32_t polls = 0;
+        while (__hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (int32_t) a.npairs) {
+            if (++polls > a.spin) {
+                __hip_atomic_store(a.sync + MD_SYNC_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    uint16_t * abw = ab + wave * al;
+    float * abgw = abg + wave * DB * GPB;
+    for (int64_t u = u0; u < a.nunits; u += G) {
+        if (u != u0) load_unit(u);
+        const int64_t t = u / a.dNT, h = u % a.dNT;
+        float part = 0.f;
+        if (wave < k) {
+            // act row of slot t k + wave (agent-scope loads: written by other workgroups in this launch)
+            // into this wave's LDS row, 8 bytes per lane per step, zero past I; group sums by shuffles
+            const int64_t s = t * k + wave;
+            const uint64_t * src = (const uint64_t *) (a.act + s * a.I);
+            for (int64_t e0 = 0; e0 < al; e0 += 256) {
+                const int64_t e = e0 + 4 * lane;
+                uint64_t v = 0;
+                if (e < a.I) v = __hip_atomic_load(GLB(const uint64_t, src + e / 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *(__attribute__((address_space(3))) uint64_t *) (abw + e) = v;
+                float sum = 0.f;
+                for (int d = 0; d < 2; d++) {
+                    const uint32_t wd = (uint32_t) (v >> (32 * d));
+                    sum += __uint_as_float(wd << 16) + __uint_as_float(wd & 0xffff0000u);
+                }
+                for (int o = GS / 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+                if ((e % GS) == 0) abgw[e / GS] = sum;
+            }
+            f32x4 acc[1][1] = {{{0.f, 0.f, 0.f, 0.f}}};
+            md_accum<FMT, 1, DB>(dw, dp, (int) a.dKB, abw, abgw, 0, acc);
+            part = sw[s] * acc[0][0][0];
+        }
+        red[wave * 64 + lane] = part;
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            float ys = 0.f;
+            for (int j = 0; j < k; j++) ys += red[j * 64 + r];
+            const int64_t n = 16 * h + r;
+            if (n < a.Nd) store_out(a.y, a.yf32, t * a.Nd + n, ys);
+        }
+        __syncthreads();
+    }
+    // the last workgroup with units clears the counters for the next launch
+    if (threadIdx.x == 0) {
+        const int32_t consumers = (int32_t) (a.nunits < G ? a.nunits : G);
+        if (__hip_atomic_fetch_add(a.sync + MD_SYNC_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == consumers - 1) {
+            __hip_atomic_store(a.sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.sync + MD_SYNC_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
 
 // ------------------------------------------------------------------ chained decode GEMVs
 // One launch runs a.n GEMVs in order (M <= 16 rows, x staged in LDS), one workgroup per CU of

@@ -2,86 +2,17 @@
 // conversion, the host-API MoE helpers) and the launchers that dispatch the per-format ones.
 #include "onpu_kern.h"
 
-// ------------------------------------------------------------------ router
-// Wave-wide reductions with DPP inside each 16-lane row and readlane across the four rows (no LDS
-// round trips): every lane gets the result.
-template <int CTRL>
-DEV uint32_t dpp_u(uint32_t v) { return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xf, 0xf, false); }
-DEV float readlane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
-
-DEV uint32_t wave_umax(uint32_t v) {
-    v = max(v, dpp_u<0x111>(v));                      // row_shr:1 (lanes without a source see 0)
-    v = max(v, dpp_u<0x112>(v));                      // row_shr:2
-    v = max(v, dpp_u<0x114>(v));                      // row_shr:4
-    v = max(v, dpp_u<0x118>(v));                      // row_shr:8: lane 15 of each row has the row's max
-    const uint32_t a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
-    const uint32_t c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
-    return max(max(a, b), max(c, d));
-}
-
-DEV float wave_fsum(float v) {
-    v += __uint_as_float(dpp_u<0xB1>(__float_as_uint(v)));   // quad_perm [1,0,3,2]
-    v += __uint_as_float(dpp_u<0x4E>(__float_as_uint(v)));   // quad_perm [2,3,0,1]
-    v += __uint_as_float(dpp_u<0x124>(__float_as_uint(v)));  // row_ror:4
-    v += __uint_as_float(dpp_u<0x128>(__float_as_uint(v)));  // row_ror:8: every lane has its row's sum
-    return (readlane_f(v, 0) + readlane_f(v, 16)) +
-           (readlane_f(v, 32) + readlane_f(v, 48));
-}
-
-// float <-> unsigned key with the same order
-DEV uint32_t ord_key(float f) {
-    const uint32_t b = __float_as_uint(f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-DEV float ord_val(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k); }
-
 // one wave per token: softmax over E <= 256 logits, top-k by probability (ties to the lower id),
-// renormalised (moe_runtime.py:333-341). Lane l holds experts 4 l .. 4 l + 3, so the lowest lane
-// holding the maximum also holds its lowest id.
+// renormalised (moe_runtime.py:333-341).
 __global__ __launch_bounds__(64) void k_route(const float * __restrict__ logits, int64_t T, int E, int k, int renorm,
                                               int32_t * __restrict__ ids, float * __restrict__ w) {
     const int64_t t = blockIdx.x;
-    const int lane = threadIdx.x;
-    const float * l = logits + t * E;
-    float v[4];
-    uint32_t mk = 0;
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * lane + i;
-        v[i] = e < E ? l[e] : -INFINITY;
-        mk = max(mk, ord_key(v[i]));
-    }
-    const float mx = ord_val(wave_umax(mk));
-    float p[4], sum = 0.f;
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * lane + i;
-        p[i] = e < E ? expf(v[i] - mx) : 0.f;
-        sum += p[i];
-    }
-    sum = wave_fsum(sum);
-    // selection keys: probability bits + 1 (p >= 0, so the bits order like the values); 0 = taken
-    uint32_t key[4];
-    for (int i = 0; i < 4; i++) key[i] = 4 * lane + i < E ? __float_as_uint(p[i]) + 1u : 0u;
-    // lane j keeps the j-th pick; one coalesced store per output at the end
-    float ws = 0.f, my_p = 0.f;
-    int my_id = 0;
-    for (int j = 0; j < k; j++) {
-        uint32_t lb = 0;
-        int li = 0;
-        for (int i = 0; i < 4; i++)
-            if (key[i] > lb) { lb = key[i]; li = i; }
-        const uint32_t best = wave_umax(lb);
-        const uint64_t hold = __ballot(lb == best);
-        const int first = __builtin_ctzll(hold);
-        const int bi = 4 * first + __builtin_amdgcn_readlane(li, first);
-        for (int i = 0; i < 4; i++)
-            if (lane == first && i == li) key[i] = 0u;
-        const float pj = __uint_as_float(best - 1u) / sum;
-        ws += pj;
-        if (lane == j) { my_id = bi; my_p = pj; }
-    }
-    if (lane < k) {
-        ids[t * k + lane] = my_id;
-        w[t * k + lane] = renorm ? my_p / ws : my_p;
+    int my_id;
+    float my_w;
+    route_token(logits + t * E, E, k, renorm, my_id, my_w);
+    if ((int) threadIdx.x < k) {
+        ids[t * k + threadIdx.x] = my_id;
+        w[t * k + threadIdx.x] = my_w;
     }
 }
 
@@ -313,6 +244,33 @@ hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStrea
         case 1: return qgemm_sk_f1(a, cfg, grid, s);
         case 2: return qgemm_sk_f2(a, cfg, grid, s);
         case 3: return qgemm_sk_f3(a, cfg, grid, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+bool moe_decode_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int64_t dKB, int T, int k, int E) {
+    return T >= 1 && T <= MD_MAX_T && k >= 1 && k <= MD_MAX_K && E >= k && E <= 256 && I % 16 == 0 && I >= 16 &&
+           Nd >= 1 && gKB >= 1 && (gKB + MD_WAVES - 1) / MD_WAVES <= MD_MAX_GB && dKB >= 1 && dKB <= MD_MAX_DB &&
+           (H * 2) % 16 == 0;
+}
+
+hipError_t launch_moe_decode(int fmt, const MDArgs & a, int grid, hipStream_t s) {
+    if (!moe_decode_fits(a.H, a.I, a.Nd, a.gKB, a.dKB, a.T, a.k, a.E) || grid <= 0 || !a.act || !a.sync)
+        return hipErrorInvalidValue;
+    if (a.gNT * 16 != 2 * a.I || a.npairs != (int64_t) a.T * a.k * (a.I / 16) || a.nunits != a.T * a.dNT)
+        return hipErrorInvalidValue;
+    const int gb = (int) ((a.gKB + MD_WAVES - 1) / MD_WAVES);
+    const int GPB = fmt == ONPU_G128S ? 1 : 4;
+    const int db = (gb == 2 && a.dKB <= 6) ? 6 : MD_MAX_DB;
+    const size_t lds = (size_t) 2 * MD_MAX_T * MD_MAX_K * 4 + (size_t) a.T * a.gKB * 128 * 2 +
+                       (size_t) ((a.T * a.gKB * GPB + 3) / 4 * 4) * 4 + (size_t) MD_WAVES * 2 * 64 * 4 +
+                       (size_t) MD_WAVES * db * 128 * 2 + (size_t) MD_WAVES * db * GPB * 4;
+    if (lds > 163840) return hipErrorInvalidValue;
+    switch (fmt) {
+        case 0: return moe_decode_f0(a, gb, grid, lds, s);
+        case 1: return moe_decode_f1(a, gb, grid, lds, s);
+        case 2: return moe_decode_f2(a, gb, grid, lds, s);
+        case 3: return moe_decode_f3(a, gb, grid, lds, s);
     }
     return hipErrorInvalidValue;
 }

@@ -61,6 +61,31 @@ struct MArgs {
     int64_t xbytes;           // k_moe_gemm: bytes of x (buffer range of the gathered rows, < 2^31)
 };
 
+// MoE decode in one launch (k_moe_decode): router (optional), gate_up + SiLU * up per routed slot,
+// down + routing-weighted slot sum per token. T <= MD_MAX_T tokens, k <= MD_MAX_K slots each.
+struct MDArgs {
+    const uint8_t * Wg;       // gate_up bank: expert e at Wg + e * gstride, [2 I][H] tiled
+    int64_t gstride, gNT, gKB;
+    const uint8_t * Wd;       // down bank: [Nd][I] tiled
+    int64_t dstride, dNT, dKB;
+    int64_t H, I, Nd;
+    const uint16_t * x;       // [T][H] bf16
+    const float * logits;     // [T][E] fp32 -> route in the kernel; nullptr: ids / w are inputs
+    int E, k, renorm, T;
+    int32_t * ids;            // [T][k]
+    float * w;                // [T][k]
+    uint16_t * act;           // [T k][I] bf16 scratch (written and read with agent-scope accesses)
+    void * y;                 // [T][Nd]
+    int yf32;
+    int32_t * sync;           // [0] act tiles published, [MD_SYNC_DONE] consumers done, [MD_SYNC_ERR]
+                              // timed-out wait flag; zero between launches
+    int64_t npairs, nunits;   // T k (I / 16) gate/up tile pairs; T * dNT down tile rows
+    uint32_t spin;            // poll limit of the wait for the act tiles
+};
+constexpr int MD_MAX_T = 4, MD_MAX_K = 8, MD_WAVES = 8, MD_SYNC_DONE = 16, MD_SYNC_ERR = 32, MD_SYNC_INTS = 48;
+constexpr int MD_MAX_GB = 4;      // gate_up K blocks per wave (H <= 8 * 4 * 128)
+constexpr int MD_MAX_DB = 8;      // down K blocks (I <= 1024)
+
 // chained decode GEMVs (k_qgemv_chain): entry i = y_i [M][N] = x_i [M][K] . W_i^T, in order, each
 // entry may read what earlier ones wrote
 struct ChainEntry {
@@ -104,6 +129,10 @@ hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_pe
                               int32_t * items, int32_t * nitems, hipStream_t s);
 // grouped GEMM over the work items (k_moe_gemm): grid.x column groups (gate_up: NT / 8, down: NT / 8)
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s);
+// one-launch MoE decode on `grid` workgroups (one per CU); hipErrorInvalidValue when the shapes are
+// outside what k_moe_decode handles (moe_decode_fits; the caller then uses the multi-launch path)
+hipError_t launch_moe_decode(int fmt, const MDArgs & a, int grid, hipStream_t s);
+bool moe_decode_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int64_t dKB, int T, int k, int E);
 // zero the chain's counters, then the chained kernel on `grid` workgroups (all resident at once)
 // (ring: CHAIN_RING_SLOTS[ring] weight blocks per compute wave)
 hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,
@@ -144,6 +173,7 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
     hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
     hipError_t qgemm_sk_f##id(const GArgs & a, int cfg, int grid, hipStream_t s);                          \
     hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
+    hipError_t moe_decode_f##id(const MDArgs & a, int gb, int grid, size_t lds, hipStream_t s);       \
     hipError_t chain_f##id(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,  \
                            hipStream_t s);                                                                \
     int chain_occ_f##id(int ring, size_t lds);

@@ -125,6 +125,24 @@ class QFfn:
                                       int(out.dtype == torch.float32), _stream()), "onpu_moe_ffn_dev")
         return out
 
+    def decode(self, logits, x, k, renorm=True, out=None, f32=False):
+        """router + FFN from logits fp32 [T][E] and x bf16 [T][H] (one launch for T <= 4, k <= 8):
+        returns (y [T][Nd], ids int32 [T][k], w fp32 [T][k])."""
+        import torch
+        T, E = logits.shape
+        ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+        w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+        if out is None:
+            out = torch.empty((T, self.Nd), dtype=torch.float32 if f32 else torch.bfloat16, device=x.device)
+        check(self.L.onpu_moe_decode_dev(self.h, _ptr(logits), _ptr(x), T, E, k, int(renorm), _ptr(ids), _ptr(w),
+                                         _ptr(out), int(out.dtype == torch.float32), _stream()),
+              "onpu_moe_decode_dev")
+        return out, ids, w
+
+    def status(self):
+        """1 if a one-launch decode gave up waiting since the last call (then cleared), else 0"""
+        return self.L.onpu_moe_status(self.h)
+
     def free(self):
         if self.h:
             self.L.onpu_ffn_free(self.h)
