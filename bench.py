@@ -328,6 +328,22 @@ def profile_target(torch, QMatrix, syn, reps=3):
                       "calibration_copy_bytes": 512 << 20}), flush=True)
 
 
+def profile_gemm(torch, QMatrix, syn, reps=3):
+    """The prefill GEMMs alone (Llama-3.1-8B FFN at M=2048: up 14336x4096, down 4096x14336, g128s),
+    `reps` launches each, for hardware-counter runs (MFMA busy cycles)."""
+    M = 2048
+    for name, N, K in [("up", 14336, 4096), ("down", 4096, 14336)]:
+        q = QMatrix(N, K, G128S, syn.weights(G128S, N, K, 7))
+        x = bf16_tensor(torch, syn.activations(M, K, 8)).reshape(M, K)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        for _ in range(reps):
+            q.mv(x, out=y)
+        torch.cuda.synchronize()
+        q.free()
+    print(json.dumps({"profile_target": "prefill GEMM up 14336x4096 and down 4096x14336, M=2048",
+                      "launches_each": reps, "flop_per_launch": 2 * M * 14336 * 4096}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -337,6 +353,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile", action="store_true",
                     help="only the roofline kernel plus a calibration copy, for rocprofv3 --pmc runs")
+    ap.add_argument("--profile-gemm", action="store_true",
+                    help="only the prefill GEMMs, for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the int4 path on a single MI355X; --gpus {args.gpus} "
@@ -349,6 +367,9 @@ def main():
     torch.cuda.set_device(0)
     if args.profile:
         profile_target(torch, QMatrix, syn)
+        return
+    if args.profile_gemm:
+        profile_gemm(torch, QMatrix, syn)
         return
     t_all = time.perf_counter()
     log("decode layers ...")
