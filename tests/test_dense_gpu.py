@@ -199,6 +199,56 @@ def test_lm_head_q4_0(gpu, M):
             assert idx[m] == int(np.argmax(ref[m])), f"row {m}"
 
 
+@pytest.mark.parametrize("fmt,N,K,M", [(orc.FMT_Q4_0, 9000, 1024, 1), (orc.FMT_Q4_0, 9000, 1024, 8),
+                                       (orc.FMT_G128S, 4100, 2048, 3)])
+def test_argmax_ties_and_replays(gpu, fmt, N, K, M):
+    """LM-head argmax: equal to the oracle argmax of the returned logits, with a planted tie at the
+    top of row 0 (the last weight row repeats the row holding the maximum: the first column must
+    win); repeated calls and graph replays give the same result."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    st = syn.weights(fmt, N, K, 31).copy()
+    xb = syn.activations(M, K, 32)
+    if fmt == orc.FMT_Q4_0:
+        # GGUF rows are contiguous in the staging bytes: the last row repeats the row holding row 0's
+        # maximum, so that row 0 has a tie at its top and the first column must win
+        rb = st.size // N
+        r0 = int(np.argmax(orc.qmm(fmt, st, N, K, xb[:1])[0]))
+        assert r0 < N - 1
+        st[(N - 1) * rb:] = st[r0 * rb:(r0 + 1) * rb]
+    q = QMatrix(N, K, fmt, st)
+    try:
+        x = to_torch_bf16(xb).reshape(M, K)
+        lg1, i1 = q.argmax(x)
+        lg2, i2 = q.argmax(x)
+        lgg = torch.empty_like(lg1)
+        ig = torch.empty_like(i1)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            q.argmax(x, lgg, ig)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            q.argmax(x, lgg, ig)
+        for _ in range(3):
+            ig.fill_(-1)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(ig, i1), "graph replay argmax differs"
+            q.argmax(x)
+        torch.cuda.synchronize()
+        assert torch.equal(lg1, lg2) and torch.equal(i1, i2)
+        lg, idx = from_torch(lg1), i1.cpu().numpy()
+    finally:
+        q.free()
+    assert np.array_equal(idx, orc.argmax(lg)), "argmax of the returned logits"
+    if fmt == orc.FMT_Q4_0:
+        assert lg[0, r0] == lg[0, N - 1] and idx[0] == r0, "tie at the top of row 0: the first column"
+    check_f32_out(lg, orc.qmm(fmt, st, N, K, xb), what="LM-head logits")
+
+
 def test_rows_zero_and_reuse(gpu):
     """M = 0 is a no-op; one handle serves several calls with different M."""
     import torch
