@@ -102,6 +102,7 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     int64_t sstride = 0;
     DBuf ws[6];                            // workspace of the calls on this handle
     DBuf gsk_ws, gsk_sync;                 // k_qgemm_sk partial tiles and slot counters (zeroed once)
+    DBuf am_cnt;                           // argmax row counters (zeroed once; each call leaves them zero)
 };
 
 struct Ffn {
@@ -138,6 +139,7 @@ void free_mat(Mat4 * m) {
     for (auto & b : m->ws) b.release();
     m->gsk_ws.release();
     m->gsk_sync.release();
+    m->am_cnt.release();
     delete m;
 }
 
@@ -614,11 +616,15 @@ int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, 
 int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream) {
     auto * m = (Mat4 *) h;
     if (M <= 0) return 0;
-    // per-part maxima of the two-pass argmax: workspace of the handle (allocated on the first call
-    // with this many rows; calls that overlap on one handle must not share it)
-    HIPR(m->ws[5].ensure((size_t) (M * ARGMAX_PARTS * 8)));
+    // per-workgroup keys and per-row counters of the argmax: workspace of the handle (allocated on
+    // the first call with this many rows; calls that overlap on one handle must not share it)
+    HIPR(m->ws[5].ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
+    if (m->am_cnt.n < (size_t) M * ARGMAX_PAD) {
+        HIPR(m->am_cnt.ensure((size_t) M * ARGMAX_PAD));
+        HIPR(hipMemset(m->am_cnt.p, 0, m->am_cnt.n));
+    }
     HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
-    HIPR(launch_argmax(logits, M, m->N, argmax, m->ws[5].as<float>(), m->ws[5].as<int32_t>((size_t) M * ARGMAX_PARTS * 4),
+    HIPR(launch_argmax(logits, M, m->N, argmax, m->ws[5].as<uint64_t>(), m->am_cnt.as<uint32_t>(),
                        (hipStream_t) stream));
     return 0;
 }

@@ -86,46 +86,80 @@ __global__ void k_invert(const int32_t * __restrict__ perm, int64_t n, int32_t *
 }
 
 // ------------------------------------------------------------------ argmax
-// first maximum of logits[row][0..N): pass 1 splits each row over gridDim.x workgroups, each leaving
-// its (value, index) in pv / pi [row][part]; pass 2 reduces a row's parts with one wave. Ties go to
-// the lower index in both passes.
-DEV void argmax_merge(float & bv, int & bi, float ov, int oi) {
-    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+// first maximum of v[row][0..N) in one launch. Each of a row's gridDim.x workgroups reduces
+// ARGMAX_CHUNK values (a thread issues all of its loads before its first compare) to one key: the
+// value's order-preserving bits above the complement of the index, so the larger key is the larger
+// value and, among equal values, the lower index. A NaN key has zero value bits, so NaN never wins
+// and a row of NaNs gives index 0. The workgroup publishes its key and counts in on the row's
+// counter; the one that arrives last reduces the row's keys, writes the index and puts the counter
+// back to zero, so the counters are zero between calls with no clearing step (graph replays too).
+// Keys and counters sit ARGMAX_PAD bytes apart: atomics of different workgroups on one cache line
+// queue behind each other.
+DEV uint64_t argmax_key(float v, int64_t n) {
+    return ((uint64_t) (v != v ? 0u : ord_key(v)) << 32) | (uint32_t) (0xffffffffu - (uint32_t) n);
 }
 
-DEV void argmax_wave(float & bv, int & bi) {
-    for (int o = 32; o > 0; o >>= 1) argmax_merge(bv, bi, __shfl_xor(bv, o), __shfl_xor(bi, o));
-}
-
-__global__ __launch_bounds__(256) void k_argmax_part(const float * __restrict__ v, int64_t N, float * __restrict__ pv,
-                                                     int32_t * __restrict__ pi) {
-    const int64_t row = blockIdx.y, parts = gridDim.x;
-    const int64_t per = (N + parts - 1) / parts, n0 = blockIdx.x * per, n1 = n0 + per < N ? n0 + per : N;
-    const float * x = v + row * N;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int64_t n = n0 + threadIdx.x; n < n1; n += blockDim.x) argmax_merge(bv, bi, x[n], (int) n);
-    argmax_wave(bv, bi);
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) argmax_merge(bv, bi, sv[w], si[w]);
-        pv[row * parts + blockIdx.x] = bv;
-        pi[row * parts + blockIdx.x] = bi;
+DEV uint64_t wave_umax64(uint64_t v) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t u = __shfl_xor(v, o);
+        v = u > v ? u : v;
     }
+    return v;
 }
 
-__global__ __launch_bounds__(64) void k_argmax_final(const float * __restrict__ pv, const int32_t * __restrict__ pi,
-                                                     int parts, int64_t N, int32_t * __restrict__ out) {
-    const int64_t row = blockIdx.x;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int p = threadIdx.x; p < parts; p += 64) argmax_merge(bv, bi, pv[row * parts + p], pi[row * parts + p]);
-    argmax_wave(bv, bi);
-    if (threadIdx.x == 0) out[row] = bi < N ? bi : 0;       // a row of NaNs: 0
+// workgroup maximum of the threads' keys; the result is valid in thread 0
+DEV uint64_t block_umax64(uint64_t k, uint64_t * wk) {
+    k = wave_umax64(k);
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < ARGMAX_THREADS / 64; w++) k = wk[w] > k ? wk[w] : k;
+    return k;
+}
+
+__global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float * __restrict__ v, int64_t N,
+                                                           uint64_t * __restrict__ keys, uint32_t * __restrict__ cnt,
+                                                           int32_t * __restrict__ out) {
+    constexpr int PT = ARGMAX_CHUNK / ARGMAX_THREADS, KS = ARGMAX_PAD / 8, CS = ARGMAX_PAD / 4;
+    const int64_t row = blockIdx.y;
+    const uint32_t P = gridDim.x;
+    const float * x = v + row * N;
+    const int64_t n0 = (int64_t) blockIdx.x * ARGMAX_CHUNK + threadIdx.x;
+    float val[PT];
+#pragma unroll
+    for (int j = 0; j < PT; j++) {
+        const int64_t n = n0 + (int64_t) j * ARGMAX_THREADS;
+        val[j] = n < N ? x[n] : 0.f;
+    }
+    uint64_t k = 0;                                     // below every key of a value in range
+#pragma unroll
+    for (int j = 0; j < PT; j++) {
+        const int64_t n = n0 + (int64_t) j * ARGMAX_THREADS;
+        const uint64_t kj = n < N ? argmax_key(val[j], n) : 0;
+        k = kj > k ? kj : k;
+    }
+    __shared__ uint64_t wk[ARGMAX_THREADS / 64];
+    __shared__ uint32_t last;
+    k = block_umax64(k, wk);
+    if (threadIdx.x == 0) {
+        // the release orders the key before the count; the acquire of the last arrival orders the
+        // other workgroups' keys before its reads
+        __hip_atomic_store(keys + (row * P + blockIdx.x) * KS, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = __hip_atomic_fetch_add(cnt + row * CS, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == P - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    uint64_t r = 0;
+    for (uint32_t p = threadIdx.x; p < P; p += ARGMAX_THREADS) {
+        const uint64_t kp = __hip_atomic_load(keys + (row * P + p) * KS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        r = kp > r ? kp : r;
+    }
+    __syncthreads();                                    // wk is reused
+    r = block_umax64(r, wk);
+    if (threadIdx.x == 0) {
+        out[row] = (int32_t) (0xffffffffu - (uint32_t) r);
+        __hip_atomic_store(cnt + row * CS, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ------------------------------------------------------------------ small helpers
@@ -348,11 +382,13 @@ hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float 
     return hipSuccess;
 }
 
-hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, float * pv, int32_t * pi,
+int64_t argmax_parts(int64_t N) { return (N + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
+
+hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, uint64_t * keys, uint32_t * cnt,
                          hipStream_t s) {
-    k_argmax_part<<<dim3(ARGMAX_PARTS, (unsigned) rows), 256, 0, s>>>(v, N, pv, pi);
-    CHECK_LAUNCH();
-    k_argmax_final<<<dim3((unsigned) rows), 64, 0, s>>>(pv, pi, ARGMAX_PARTS, N, out);
+    if (rows <= 0 || N <= 0) return hipSuccess;
+    if (rows > 65535 || N >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
+    k_argmax<<<dim3((unsigned) argmax_parts(N), (unsigned) rows), ARGMAX_THREADS, 0, s>>>(v, N, keys, cnt, out);
     CHECK_LAUNCH();
     return hipSuccess;
 }

@@ -142,9 +142,12 @@ int chain_occupancy(int fmt, int ring, size_t lds);
 hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
 hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
-// pv / pi: workspace of rows * ARGMAX_PARTS floats / ints
-constexpr int ARGMAX_PARTS = 64;
-hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, float * pv, int32_t * pi,
+// one launch of argmax_parts(N) workgroups per row, each over ARGMAX_CHUNK values; keys: workspace
+// of rows * argmax_parts(N) * ARGMAX_PAD bytes; cnt: rows * ARGMAX_PAD bytes of counters, zero before
+// the first call (each call leaves them at zero). Calls that overlap must not share keys / cnt.
+constexpr int ARGMAX_THREADS = 256, ARGMAX_CHUNK = 16 * ARGMAX_THREADS, ARGMAX_PAD = 128;
+int64_t argmax_parts(int64_t N);
+hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, uint64_t * keys, uint32_t * cnt,
                          hipStream_t s);
 hipError_t launch_f32_to_bf16(const float * in, int64_t n, uint16_t * out, hipStream_t s);
 hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * bias, int act,
