@@ -158,27 +158,33 @@ DEV Par<FMT> load_par(const uint8_t * blk, int r) {
     return p;
 }
 
-// scale and additive offset per MFMA step such that w = s * (128 + u) + boff
-// (sym: boff = -136 s; q4nx: boff = m - 128 s)
+// Symmetric formats (w = s (u - 8)): the scale of each MFMA step (G128S: one for the block).
 template <int FMT>
-DEV void decode_par(const Par<FMT> & p, float (&s)[4], float (&bo)[4]) {
+DEV void decode_scale(const Par<FMT> & p, float (&s)[4]) {
     if (FMT == ONPU_G128S) {
         const float v = bf16_to_f32((uint16_t) p.v[0]);
-        for (int j = 0; j < 4; j++) { s[j] = v; bo[j] = -136.0f * v; }
-    } else if (FMT == ONPU_Q4NX) {
-        for (int j = 0; j < 4; j++) {
-            const uint32_t pj = p.v[j % (sizeof(p.v) / 4)];
-            s[j] = bf16_to_f32((uint16_t) (pj & 0xffff));
-            bo[j] = bf16_to_f32((uint16_t) (pj >> 16)) - 128.0f * s[j];
-        }
+        for (int j = 0; j < 4; j++) s[j] = v;
     } else {
-        for (int j = 0; j < 4; j++) {
-            const uint32_t bits = (p.v[(j >> 1) % (sizeof(p.v) / 4)] >> (16 * (j & 1))) & 0xffff;
-            s[j] = scale_f32(FMT, bits);
-            bo[j] = -136.0f * s[j];
-        }
+        for (int j = 0; j < 4; j++)
+            s[j] = scale_f32(FMT, (p.v[(j >> 1) % (sizeof(p.v) / 4)] >> (16 * (j & 1))) & 0xffff);
     }
 }
+
+// q4nx (w = s u + m): scale and additive offset per MFMA step with w = s (128 + u) + boff,
+// boff = m - 128 s
+template <int FMT>
+DEV void decode_par(const Par<FMT> & p, float (&s)[4], float (&bo)[4]) {
+    for (int j = 0; j < 4; j++) {
+        const uint32_t pj = p.v[j % (sizeof(p.v) / 4)];
+        s[j] = bf16_to_f32((uint16_t) (pj & 0xffff));
+        bo[j] = bf16_to_f32((uint16_t) (pj >> 16)) - 128.0f * s[j];
+    }
+}
+
+// The factor on x's group sums as the decode kernels carry them: the symmetric formats start each
+// MFMA from -136 * (sum of x over the group), so that it ends at x . (u - 8) (128 + u codes less
+// the 8 of the symmetric zero point); q4nx keeps the plain sums for its offset term.
+template <int FMT> constexpr float xsum_mul() { return FMT == ONPU_Q4NX ? 1.0f : -136.0f; }
 
 // raw parameters for dequant (s, m) per step
 template <int FMT>
@@ -304,17 +310,25 @@ DEV void route_token(const float * __restrict__ l, int E, int k, int renorm, int
 
 // ------------------------------------------------------------------ decode GEMV family
 // Per wave: RT row tiles x a run of K blocks. A operand = x rows (16 per MFMA block, MB blocks),
-// B operand = unpacked biased codes. For each MFMA step j (32 k, one 32-group):
-//   cg = x . (128 + u)^T,  cs = x . 1  (column sums of x, shared by all row tiles)
-//   acc += s_j * cg + boff_j * cs
-// cs[mb][j] comes from the caller (G128S: cs[mb][0] is the sum over the whole block), in the MFMA
-// C layout: lane (q, r) holds the sums of rows 16 mb + 4 q + v.
+// B operand = unpacked biased codes 128 + u. For each MFMA step j (32 k, one 32-group), with cs the
+// group sums of x times xsum_mul (shared by all row tiles):
+//   symmetric formats:  cg = x . (128 + u)^T + cs = x . (u - 8)^T,   acc += s_j * cg
+//                       (G128S: the four steps chain into one cg, one scale per block)
+//   q4nx:               cg = x . (128 + u)^T,   acc += s_j * cg + boff_j * cs
+// cs[mb][j] comes from the caller (G128S: cs[mb][0] is over the whole block), in the MFMA C layout:
+// lane (q, r) holds the sums of rows 16 mb + 4 q + v.
 // mrows: rows of x (uniform); with one A block only rows v < mrows of lanes q = 0 can be stored,
 // so for mrows == 1 the accumulate touches row 0 alone.
 DEV void acc4(f32x4 & acc, float s, float bo, const f32x4 & cg, const f32x4 & cs, int rows) {
     acc[0] = fmaf(s, cg[0], fmaf(bo, cs[0], acc[0]));
     if (rows > 1)
         for (int v = 1; v < 4; v++) acc[v] = fmaf(s, cg[v], fmaf(bo, cs[v], acc[v]));
+}
+
+DEV void acc1(f32x4 & acc, float s, const f32x4 & cg, int rows) {
+    acc[0] = fmaf(s, cg[0], acc[0]);
+    if (rows > 1)
+        for (int v = 1; v < 4; v++) acc[v] = fmaf(s, cg[v], acc[v]);
 }
 
 template <int FMT, int MB, int RT>
@@ -327,16 +341,16 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
         for (int rt = 0; rt < RT; rt++) {
             if (!valid[rt]) continue;
             f32x4 cg[MB];
-            for (int mb = 0; mb < MB; mb++) cg[mb] = z;
+            for (int mb = 0; mb < MB; mb++) cg[mb] = cs[mb][0];
             for (int j = 0; j < 4; j++) {
                 const u32x4 bw = unpack_biased(wv[rt][j], mag);
                 for (int mb = 0; mb < MB; mb++) cg[mb] = mfma(xa[mb][j], bw, cg[mb]);
             }
-            float s[4], bo[4];
-            decode_par<FMT>(par[rt], s, bo);
-            for (int mb = 0; mb < MB; mb++) acc4(acc[rt][mb], s[0], bo[0], cg[mb], cs[mb][0], rows);
+            float s[4];
+            decode_scale<FMT>(par[rt], s);
+            for (int mb = 0; mb < MB; mb++) acc1(acc[rt][mb], s[0], cg[mb], rows);
         }
-    } else {
+    } else if (FMT == ONPU_Q4NX) {
         for (int rt = 0; rt < RT; rt++) {
             if (!valid[rt]) continue;
             float s[4], bo[4];
@@ -349,13 +363,25 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
                 }
             }
         }
+    } else {
+        for (int rt = 0; rt < RT; rt++) {
+            if (!valid[rt]) continue;
+            float s[4];
+            decode_scale<FMT>(par[rt], s);
+            for (int j = 0; j < 4; j++) {
+                const u32x4 bw = unpack_biased(wv[rt][j], mag);
+                for (int mb = 0; mb < MB; mb++) acc1(acc[rt][mb], s[j], mfma(xa[mb][j], bw, cs[mb][j]), rows);
+            }
+        }
     }
 }
 
-// column sums of x for one block from an MFMA against ones (x from global memory)
+// column sums of x for one block times xsum_mul, from an MFMA against a constant B of bf16 1 (q4nx)
+// or -136 (exact in bf16, so each product is exact) (x from global memory)
 template <int FMT, int MB>
 DEV void xsum_mfma(const u32x4 (&xa)[MB][4], f32x4 (&cs)[MB][4]) {
-    const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const uint32_t c = FMT == ONPU_Q4NX ? 0x3f803f80u : 0xc308c308u;
+    const u32x4 ones = {c, c, c, c};
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     for (int mb = 0; mb < MB; mb++) {
         if (FMT == ONPU_G128S) {
@@ -578,7 +604,8 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     const int64_t b0 = (int64_t) kpart * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
     constexpr int PER = RT * MB * 256;
     uint16_t * xs = (uint16_t *) (red + nw * PER);
-    // XL: column sums of x per 32-group (G128S: per 128) after the x rows: xsum[group][16 rows]
+    // XL: column sums of x per 32-group (G128S: per 128) times xsum_mul after the x rows:
+    // xsum[group][16 rows]
     constexpr int GS = FMT == ONPU_G128S ? 128 : 32, UPG = GS / 8;       // 16 B units per group
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
     const XSrc X{x, a.ldx, nullptr, XL ? xs : nullptr, a.xls, XL ? xsum : nullptr};
@@ -613,7 +640,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         for (int o = UPG / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
         if (u < nunits && u % UPG == 0) {
             const uint32_t m = u / kp8, g = (u - m * kp8) / UPG;
-            xsum[g * 16 + m] = t;
+            xsum[g * 16 + m] = t * xsum_mul<FMT>();
         }
     };
     auto post = [&]() {
@@ -1255,8 +1282,9 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
 // loads and finishes its units. The last workgroup with units clears sync[0] and sync[MD_SYNC_DONE]
 // again, so the counters are zero between launches (and a captured graph replays without resets).
 
-// x rows [T][H] -> LDS xs[T][xl] (bf16, zero past H) and their group sums xg[T][KB * GPB], by the
-// whole workgroup: thread u takes 8 elements, a group's threads are consecutive lanes of one wave
+// x rows [T][H] -> LDS xs[T][xl] (bf16, zero past H) and their group sums times xsum_mul,
+// xg[T][KB * GPB], by the whole workgroup: thread u takes 8 elements, a group's threads are
+// consecutive lanes of one wave
 template <int FMT>
 DEV void md_stage_x(const uint16_t * __restrict__ x, int T, int64_t H, int64_t KB, int64_t xl, uint16_t * xs,
                     float * xg) {
@@ -1270,7 +1298,7 @@ DEV void md_stage_x(const uint16_t * __restrict__ x, int T, int64_t H, int64_t K
         float sum = 0.f;
         for (int d = 0; d < 4; d++) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
         for (int o = UPG / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-        if (u < nunits && (k / 8) % UPG == 0) xg[(int64_t) t * KB * GPB + k / GS] = sum;
+        if (u < nunits && (k / 8) % UPG == 0) xg[(int64_t) t * KB * GPB + k / GS] = sum * xsum_mul<FMT>();
     }
 }
 
@@ -1449,7 +1477,8 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
         float part = 0.f;
         if (wave < k) {
             // act row of slot t k + wave (agent-scope loads: written by other workgroups in this launch)
-            // into this wave's LDS row, 8 bytes per lane per step, zero past I; group sums by shuffles
+            // into this wave's LDS row, 8 bytes per lane per step, zero past I; group sums (times
+            // xsum_mul) by shuffles
             const int64_t s = t * k + wave;
             const uint64_t * src = (const uint64_t *) (a.act + s * a.I);
             for (int64_t e0 = 0; e0 < al; e0 += 256) {
@@ -1463,7 +1492,7 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
                     sum += __uint_as_float(wd << 16) + __uint_as_float(wd & 0xffff0000u);
                 }
                 for (int o = GS / 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-                if ((e % GS) == 0) abgw[e / GS] = sum;
+                if ((e % GS) == 0) abgw[e / GS] = sum * xsum_mul<FMT>();
             }
             f32x4 acc[1][1] = {{{0.f, 0.f, 0.f, 0.f}}};
             md_accum<FMT, 1, DB>(dw, dp, (int) a.dKB, abw, abgw, 0, acc);
@@ -1505,12 +1534,12 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
 //     no wave can wait forever)
 //   all waves: stage x_{i+1} (agent-scope loads) and its column sums in LDS.
 // Every workgroup must be resident at once (the host sizes the grid from the occupancy).
-// x rows [M][K] (bf16) into the LDS copy xs[M][xls] and the column sums of each group of gs, by the
-// whole workgroup: consecutive threads take consecutive 8-element units (coalesced loads, two per
+// x rows [M][K] (bf16) into the LDS copy xs[M][xls] and the column sums of each group of gs times
+// xmul, by the whole workgroup: consecutive threads take consecutive 8-element units (coalesced loads, two per
 // thread in flight at once); a group's units sit in consecutive lanes of one wave and are summed
 // across them.
-DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, uint16_t * xs,
-                       float * xsum) {
+DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, float xmul,
+                       uint16_t * xs, float * xsum) {
     const uint32_t T = blockDim.x, tid = threadIdx.x, upg = gs / 8;
     const uint32_t kp8 = (uint32_t) KB * 16, nunits = (uint32_t) M * kp8;
     for (uint32_t u0 = 0; u0 < nunits; u0 += 2 * T) {            // same trip count for the whole workgroup
@@ -1537,7 +1566,7 @@ DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t
             float t = 0.f;
             for (int d = 0; d < 4; d++) t += __uint_as_float(w[d] << 16) + __uint_as_float(w[d] & 0xffff0000u);
             for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
-            if (u < nunits && u % upg == 0) xsum[(kk[j] / gs) * 16 + m[j]] = t;
+            if (u < nunits && u % upg == 0) xsum[(kk[j] / gs) * 16 + m[j]] = t * xmul;
         }
     }
 }
@@ -1678,7 +1707,7 @@ __global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArg
         chain_settle<FMT>(ic, ents, a.n, w, P, wave);
         for (int s = 0; s < S; s++) chain_issue<FMT>(ic, ents, a.n, w, P, wave, ring + s * BLK, lane);
     }
-    chain_stage_x(ents[0].x, a.M, ents[0].K, ents[0].KB, a.xls, GS, xs, xsum);
+    chain_stage_x(ents[0].x, a.M, ents[0].K, ents[0].KB, a.xls, GS, xsum_mul<FMT>(), xs, xsum);
     chain_sync();
     const uint32_t mag = 0x43004300u;
     uint32_t k = 0;                     // blocks consumed: the next one sits in slot k % S
@@ -1732,7 +1761,7 @@ __global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArg
         }
         chain_sync();
         const ChainEntry & F = ents[i + 1];
-        chain_stage_x(F.x, a.M, F.K, F.KB, a.xls, GS, xs, xsum);
+        chain_stage_x(F.x, a.M, F.K, F.KB, a.xls, GS, xsum_mul<FMT>(), xs, xsum);
         chain_sync();
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));      // the ring's last (out-of-range) loads have landed
