@@ -94,6 +94,17 @@ def time_it(torch, step, iters, warmup):
     return a.elapsed_time(b) / 1e3 / iters
 
 
+# Each timed graph of a config repeats its calls this often, so that the gap between two graph
+# launches (several microseconds) is spread over many calls, as inside a longer decode step
+GRAPH_REPS = 4
+
+
+def time_med(torch, step, iters, warmup, windows=5):
+    """median over `windows` back-to-back timed windows of `iters` calls each (the first after
+    `warmup` calls) of the mean seconds per call: one slow window (a clock change) does not move it"""
+    return float(np.median([time_it(torch, step, iters, warmup if w == 0 else 0) for w in range(windows)]))
+
+
 def bf16_tensor(torch, bits):
     return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
 
@@ -146,7 +157,7 @@ def decode_layers(torch, QMatrix, QChain, syn, Ms, steps, warmup):
                 for layer in range(LAYERS):
                     mats[name][layer].mv(xs[K], out=ys[name])
             gm = GraphStep(one, torch)
-            tm = time_it(torch, gm, max(20, steps // 2), 3) / LAYERS
+            tm = time_med(torch, gm, max(20, steps // 2), 3) / LAYERS
             b1 = wbytes(G128S, N, K) + M * K * 2 + M * N * 2
             per[name] = {"us": tm * 1e6, "GBps": b1 / tm / 1e9, "hbm_frac": b1 / tm / HBM_PEAK, "bytes": b1}
         res[M]["per_matrix"] = per
@@ -184,7 +195,7 @@ def config0(torch, QMatrix, syn, iters):
         for q in copies:
             q.mv(x, out=y)
     g = GraphStep(step, torch)
-    t = time_it(torch, g, iters, 3) / len(copies)
+    t = time_med(torch, g, iters, 3) / len(copies)
     b = wbytes(G128S, N, K) + K * 2 + N * 2
     for q in copies:
         q.free()
@@ -198,8 +209,11 @@ def prefill(torch, QMatrix, syn, iters):
         q = QMatrix(N, K, G128S, syn.weights(G128S, N, K, 7))
         x = bf16_tensor(torch, syn.activations(M, K, 8)).reshape(M, K)
         y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-        g = GraphStep(lambda: q.mv(x, out=y), torch)
-        t = time_it(torch, g, iters, 3)
+        def step(q=q, x=x, y=y):
+            for _ in range(GRAPH_REPS):
+                q.mv(x, out=y)
+        g = GraphStep(step, torch)
+        t = time_med(torch, g, iters, 3) / GRAPH_REPS
         fl = 2.0 * M * N * K
         out[name] = {"us_per_call": t * 1e6, "TFLOPS": fl / t / 1e12, "mfma_frac": fl / t / BF16_PEAK}
         q.free()
@@ -226,11 +240,12 @@ def moe(torch, QFfn, syn, iters):
         hit = len(np.unique(ids.cpu().numpy()))
 
         def step(lg=lg, x=x, y=y):
-            for f in ffns:
-                i, w = f.route(lg, k)
-                f.ffn(x, i, w, out=y)
+            for _ in range(GRAPH_REPS):
+                for f in ffns:
+                    i, w = f.route(lg, k)
+                    f.ffn(x, i, w, out=y)
         g = GraphStep(step, torch)
-        t = time_it(torch, g, iters, 3) / nl
+        t = time_med(torch, g, iters, 3) / (nl * GRAPH_REPS)
         byts = hit * per_expert + T * H * 2 * 2 + T * E * 4
         fl = 2.0 * T * k * (2 * I * H + H * I)
         out[f"M{T}"] = {"us_per_layer": t * 1e6, "GBps": byts / t / 1e9, "hbm_frac": byts / t / HBM_PEAK,
@@ -252,10 +267,11 @@ def lm_head(torch, QMatrix, syn, iters):
         idx = torch.empty((M,), dtype=torch.int32, device="cuda")
 
         def step(x=x, lg=lg, idx=idx):
-            for q in copies:
-                q.argmax(x, lg, idx)
+            for _ in range(GRAPH_REPS):
+                for q in copies:
+                    q.argmax(x, lg, idx)
         g = GraphStep(step, torch)
-        t = time_it(torch, g, iters, 3) / len(copies)
+        t = time_med(torch, g, iters, 3) / (len(copies) * GRAPH_REPS)
         b = wbytes(Q4_0, N, K) + M * K * 2 + M * N * 4
         out[f"M{M}"] = {"us_per_call": t * 1e6, "GBps": b / t / 1e9, "hbm_frac": b / t / HBM_PEAK}
     for q in copies:

@@ -317,8 +317,9 @@ DEV void route_token(const float * __restrict__ l, int E, int k, int renorm, int
 //   q4nx:               cg = x . (128 + u)^T,   acc += s_j * cg + boff_j * cs
 // cs[mb][j] comes from the caller (G128S: cs[mb][0] is over the whole block), in the MFMA C layout:
 // lane (q, r) holds the sums of rows 16 mb + 4 q + v.
-// mrows: rows of x (uniform); with one A block only rows v < mrows of lanes q = 0 can be stored,
-// so for mrows == 1 the accumulate touches row 0 alone.
+// With one A block (MB = 1) x row m sits in MFMA row perm16(m), so C element v of lane quarter q
+// holds x row 4 v + q: RV (compile time) = the elements that hold rows below M (1 for M <= 4, 2 for
+// M <= 8, else 4), and the accumulate touches those alone. MB > 1 keeps rows in order and all four.
 DEV void acc4(f32x4 & acc, float s, float bo, const f32x4 & cg, const f32x4 & cs, int rows) {
     acc[0] = fmaf(s, cg[0], fmaf(bo, cs[0], acc[0]));
     if (rows > 1)
@@ -331,11 +332,14 @@ DEV void acc1(f32x4 & acc, float s, const f32x4 & cg, int rows) {
         for (int v = 1; v < 4; v++) acc[v] = fmaf(s, cg[v], acc[v]);
 }
 
-template <int FMT, int MB, int RT>
+// MFMA row of x row m (0..15) in a single A block: rows 0..3 go to MFMA rows 0, 4, 8, 12 (element 0
+// of the four lane quarters of C), rows 4..7 to 1, 5, 9, 13, ...; the map is its own inverse.
+DEV int perm16(int m) { return 4 * (m & 3) + (m >> 2); }
+
+template <int FMT, int MB, int RT, int RV>
 DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FMT> (&par)[RT],
-                    const u32x4 (&xa)[MB][4], const f32x4 (&cs)[MB][4], uint32_t mag, int mrows,
-                    f32x4 (&acc)[RT][MB]) {
-    const int rows = MB > 1 ? 4 : mrows;
+                    const u32x4 (&xa)[MB][4], const f32x4 (&cs)[MB][4], uint32_t mag, f32x4 (&acc)[RT][MB]) {
+    constexpr int rows = MB == 1 ? RV : 4;
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     if (FMT == ONPU_G128S) {
         for (int rt = 0; rt < RT; rt++) {
@@ -368,9 +372,12 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
             if (!valid[rt]) continue;
             float s[4];
             decode_scale<FMT>(par[rt], s);
-            for (int j = 0; j < 4; j++) {
-                const u32x4 bw = unpack_biased(wv[rt][j], mag);
-                for (int mb = 0; mb < MB; mb++) acc1(acc[rt][mb], s[j], mfma(xa[mb][j], bw, cs[mb][j]), rows);
+            u32x4 bw[4];
+            for (int j = 0; j < 4; j++) bw[j] = unpack_biased(wv[rt][j], mag);
+            for (int mb = 0; mb < MB; mb++) {
+                f32x4 cg[4];                              // four independent MFMAs, then their scales
+                for (int j = 0; j < 4; j++) cg[j] = mfma(xa[mb][j], bw[j], cs[mb][j]);
+                for (int j = 0; j < 4; j++) acc1(acc[rt][mb], s[j], cg[j], rows);
             }
         }
     }
@@ -413,14 +420,14 @@ DEV void load_x(const XSrc & X, int M, int64_t K, int64_t b, int r, int q, u32x4
         // LDS rows are zero-padded to 128 KB columns; rows >= M read row M - 1 (their MFMA rows are
         // never stored), so the reads need no masks
         for (int mb = 0; mb < MB; mb++) {
-            const int m = 16 * mb + r < M ? 16 * mb + r : M - 1;
+            const int i = MB == 1 ? perm16(r) : 16 * mb + r, m = i < M ? i : M - 1;
             const uint16_t * base = X.xs + (uint32_t) m * (uint32_t) X.xls + (uint32_t) b * 128u + 8u * q;
             for (int j = 0; j < 4; j++) xa[mb][j] = *LDS_U32X4(base + 32 * j);
         }
         return;
     }
     for (int mb = 0; mb < MB; mb++) {
-        const int m = 16 * mb + r;
+        const int m = MB == 1 ? perm16(r) : 16 * mb + r;
         int64_t row = m;
         bool ok = m < M;
         if (!XL && X.xrows && ok) { row = X.xrows[m]; ok = row >= 0; }
@@ -467,7 +474,7 @@ DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], co
 }
 
 // The MFMAs of one chunk (blocks c0 .. c0 + NB - 1, those below b1)
-template <int FMT, int MB, int RT, int NB, bool XL>
+template <int FMT, int MB, int RT, int NB, bool XL, int RV>
 DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, const XSrc & X, int M, int64_t K,
                        int r, int q, uint32_t mag, f32x4 (&acc)[RT][MB]) {
     if (XL) {                             // x from LDS, one block at a time (short latency)
@@ -481,7 +488,7 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
                 for (int j = 0; j < GPB; j++)
                     cs[mb][j] = *(const __attribute__((address_space(3))) f32x4 *) (X.xsum + ((c0 + i) * GPB + j) * 16 +
                                                                                    16 * mb + 4 * q);
-            qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, M, acc);
+            qacc_block<FMT, MB, RT, RV>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, acc);
         }
     } else {                              // x from global memory: the chunk's x loads first
         u32x4 xa[NB][MB][4];
@@ -490,7 +497,7 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
             if (c0 + i < b1) {
                 f32x4 cs[MB][4];
                 xsum_mfma<FMT, MB>(xa[i], cs);
-                qacc_block<FMT, MB, RT>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], cs, mag, M, acc);
+                qacc_block<FMT, MB, RT, RV>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], cs, mag, acc);
             }
     }
 }
@@ -509,7 +516,7 @@ DEV const uint8_t * qacc_start(WChunk<FMT, RT, NB> & ca, const uint8_t * const (
 
 // the chunk loop after qacc_start (acc accumulates; the caller zeroes it); b1 and last as
 // qacc_start left them
-template <int FMT, int MB, int RT, int NB, bool XL>
+template <int FMT, int MB, int RT, int NB, bool XL, int RV>
 DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], const uint8_t * last, int64_t b0,
                    int64_t b1, const XSrc & X, int M, int64_t K, f32x4 (&acc)[RT][MB]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
@@ -520,16 +527,16 @@ DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], co
     int64_t i = 0;
     for (; i + 2 < nc; i += 2) {                     // chunks i + 1 and i + 2 exist
         load_chunk<FMT, RT, NB>(cb, tb, last, b0 + (i + 1) * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
         load_chunk<FMT, RT, NB>(ca, tb, last, b0 + (i + 2) * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
     }
     if (i + 1 < nc) {                                // two chunks left: ca (loaded) and one more
         load_chunk<FMT, RT, NB>(cb, tb, last, b0 + (i + 1) * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
-        compute_chunk<FMT, MB, RT, NB, XL>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
     } else {
-        compute_chunk<FMT, MB, RT, NB, XL>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
     }
 }
 
@@ -541,7 +548,7 @@ DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], co
 // before the first loads are issued and post() right after (the workgroup's LDS staging of x: its
 // loads first, then the LDS writes and the barrier while the weights stream); every wave calls
 // both, also one with no blocks. (Issuing both chunks before the barrier measured slower.)
-template <int FMT, int MB, int RT, int NB, bool XL, class Pre, class Post>
+template <int FMT, int MB, int RT, int NB, bool XL, int RV, class Pre, class Post>
 DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const XSrc & X, int M, int64_t K, Pre pre,
                   Post post, f32x4 (&acc)[RT][MB]) {
     for (int rt = 0; rt < RT; rt++)
@@ -550,7 +557,7 @@ DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const
     pre();
     const uint8_t * last = qacc_start<FMT, RT, NB>(ca, tb, b0, b1);
     post();
-    qacc_rest<FMT, MB, RT, NB, XL>(ca, tb, last, b0, b1, X, M, K, acc);
+    qacc_rest<FMT, MB, RT, NB, XL, RV>(ca, tb, last, b0, b1, X, M, K, acc);
 }
 
 // Epilogues
@@ -605,7 +612,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     constexpr int PER = RT * MB * 256;
     uint16_t * xs = (uint16_t *) (red + nw * PER);
     // XL: column sums of x per 32-group (G128S: per 128) times xsum_mul after the x rows:
-    // xsum[group][16 rows]
+    // xsum[group][16 MFMA rows] (x row m at perm16(m))
     constexpr int GS = FMT == ONPU_G128S ? 128 : 32, UPG = GS / 8;       // 16 B units per group
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
     const XSrc X{x, a.ldx, nullptr, XL ? xs : nullptr, a.xls, XL ? xsum : nullptr};
@@ -640,7 +647,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         for (int o = UPG / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
         if (u < nunits && u % UPG == 0) {
             const uint32_t m = u / kp8, g = (u - m * kp8) / UPG;
-            xsum[g * 16 + m] = t * xsum_mul<FMT>();
+            xsum[g * 16 + (MB == 1 ? perm16(m) : m)] = t * xsum_mul<FMT>();
         }
     };
     auto post = [&]() {
@@ -653,7 +660,9 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         __syncthreads();
     };
     f32x4 acc[RT][MB];
-    qacc_run<FMT, MB, RT, NB, XL != 0>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
+    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
+    else if (MB == 1 && a.M <= 8) qacc_run<FMT, MB, RT, NB, XL != 0, 2>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
+    else qacc_run<FMT, MB, RT, NB, XL != 0, 4>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
 
     // cross-wave reduction through LDS: red[wave][((rt * MB + mb) * 4 + v) * 64 + lane]
     for (int rt = 0; rt < RT; rt++)
@@ -664,7 +673,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     for (int oo = threadIdx.x; oo < ntw * nout; oo += blockDim.x) {
         const int tw = oo / nout, o = oo % nout;
         const int rt = o / (MB * 256), mb = (o / 256) % MB, v = (o / 64) % 4, l = o % 64;
-        const int m = 16 * mb + 4 * (l >> 4) + v;
+        const int m = MB == 1 ? 4 * v + (l >> 4) : 16 * mb + 4 * (l >> 4) + v;     // see perm16
         const int64_t n = 16 * (tg0 + tw + rt * stride) + (l & 15);
         if (m >= a.M) continue;
         const float * rp = red + (int64_t) tw * KW * PER + o;
@@ -1326,7 +1335,7 @@ DEV void md_accum(const u32x4 (&wv)[NB][RT], const Par<FMT> (&par)[NB][RT], int 
             const float v = *(const __attribute__((address_space(3))) float *) (xg + b * GPB + (j < GPB ? j : 0));
             cs[0][j] = (f32x4){v, v, v, v};
         }
-        qacc_block<FMT, 1, RT>(valid, wv[i], par[i], xa, cs, 0x43004300u, 1, acc);
+        qacc_block<FMT, 1, RT, 1>(valid, wv[i], par[i], xa, cs, 0x43004300u, acc);
     }
 }
 
@@ -1535,7 +1544,7 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
 //   all waves: stage x_{i+1} (agent-scope loads) and its column sums in LDS.
 // Every workgroup must be resident at once (the host sizes the grid from the occupancy).
 // x rows [M][K] (bf16) into the LDS copy xs[M][xls] and the column sums of each group of gs times
-// xmul, by the whole workgroup: consecutive threads take consecutive 8-element units (coalesced loads, two per
+// xmul (xsum[group][perm16(row)]: the chained GEMVs run one A block), by the whole workgroup: consecutive threads take consecutive 8-element units (coalesced loads, two per
 // thread in flight at once); a group's units sit in consecutive lanes of one wave and are summed
 // across them.
 DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, float xmul,
@@ -1566,7 +1575,7 @@ DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t
             float t = 0.f;
             for (int d = 0; d < 4; d++) t += __uint_as_float(w[d] << 16) + __uint_as_float(w[d] & 0xffff0000u);
             for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
-            if (u < nunits && u % upg == 0) xsum[(kk[j] / gs) * 16 + m[j]] = t * xmul;
+            if (u < nunits && u % upg == 0) xsum[(kk[j] / gs) * 16 + perm16((int) m[j])] = t * xmul;
         }
     }
 }
@@ -1731,7 +1740,7 @@ __global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArg
                     ch.ok[0][0] = true;
                     ch.wv[0][0] = *LDS_U32X4(sl + 16 * lane);
                     ch.par[0][0] = load_par_lds<FMT>(sl, r);
-                    compute_chunk<FMT, 1, 1, 1, true>(ch, b, b1, X, a.M, E.K, r, q, mag, acc);
+                    compute_chunk<FMT, 1, 1, 1, true, 4>(ch, b, b1, X, a.M, E.K, r, q, mag, acc);
                     __builtin_amdgcn_s_waitcnt(LGKM0_IMM);            // the slot's reads are done
                     chain_issue<FMT>(ic, ents, a.n, w, P, wave, sl, lane);     // refill it
                     k++;
@@ -1743,8 +1752,9 @@ __global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArg
                 for (int o = lane; o < nout; o += 64) {
                     const int ti = o / (16 * a.M), m = (o / 16) % a.M, c = o % 16;
                     const int64_t n = 16 * (g * etw + ti) + c;
-                    // the accumulator of row m, column c sits at lane c + 16 (m / 4), element m % 4
-                    const float * src = rp + ti * ekw * 256 + (m & 3) * 64 + c + 16 * (m >> 2);
+                    // the accumulator of row m, column c sits at lane c + 16 (m % 4), element m / 4
+                    // (x row m in MFMA row perm16(m))
+                    const float * src = rp + ti * ekw * 256 + (m >> 2) * 64 + c + 16 * (m & 3);
                     float sum = src[0];
 #pragma unroll
                     for (int k2 = 1; k2 < CHAIN_WAVES; k2++)
