@@ -145,6 +145,24 @@ int onpu_moe_decode_dev(void * h, const float * logits, const void * x, int64_t 
  * invalid; the flag is cleared), 0 otherwise, -1 on error. Synchronises the device. */
 int onpu_moe_status(void * h);
 
+/* ---- weight codecs on the GPU (load time). The reference quantizes on the host (onpu_pack,
+ * onpu_api.cpp:499-504, with the search quantizers of opennpu_core.hpp:103-169) and transcodes GGUF
+ * Q4_K for its ggml backend on the host (ggml-opennpu.cpp:103-138); these run the same codecs on
+ * weights already in HBM and write the handle's tiled layout directly. They allocate a temporary
+ * staging buffer (at most 256 MiB, or one expert) and return after their launches on `stream`
+ * completed; calls on one handle are serialised by the library mutex. 0 ok, -1 error
+ * (onpu_last_error). */
+/* experts [e0, e0 + n) of a dense (E = 1) or bank handle from W [n][N][ldw] (row stride ldw >= K
+ * elements), fp32 (w_bf16 = 0) or bf16 (1), with the handle's format: the bytes onpu_pack writes */
+int onpu_quantize_dev(void * h, int64_t e0, int64_t n, const void * W, int64_t ldw, int w_bf16, void * stream);
+/* q4nx handle, K a multiple of 256: experts [e0, e0 + n) from GGUF Q4_K rows of K / 256 super-blocks
+ * (144 bytes each), rows ld bytes apart, experts N * ld bytes apart */
+int onpu_transcode_q4k_dev(void * h, int64_t e0, int64_t n, const void * blocks, int64_t ld, void * stream);
+/* the same transcode on the host (replaces ggml-opennpu.cpp:103-138's QuantFn for Q4_K groups):
+ * rows of K / 256 super-blocks -> q4nx staging bytes; returns onpu_stage_bytes(q4nx, N, K), 0 when
+ * K is not a multiple of 256 */
+int64_t onpu_pack_q4k(const uint8_t * blocks, int64_t N, int64_t K, uint8_t * out, int threads);
+
 /* ---- chained decode GEMVs (no counterpart in the reference's ABI; the reference's fused decode
  * engine likewise runs a token's products in one NPU dispatch). A chain is n dense GEMVs
  * y_i [M][N_i] = x_i [M][K_i] . W_i^T fixed at creation (handles, x and y device pointers; one

@@ -77,6 +77,9 @@ def _declare(lib):
         "onpu_moe_ffn_dev": (I32, [P, P, I64, P, I32, P, P, I32, P]),
         "onpu_moe_decode_dev": (I32, [P, P, P, I64, I32, I32, I32, P, P, P, I32, P]),
         "onpu_moe_status": (I32, [P]),
+        "onpu_quantize_dev": (I32, [P, I64, I64, P, I64, I32, P]),
+        "onpu_transcode_q4k_dev": (I32, [P, I64, I64, P, I64, P]),
+        "onpu_pack_q4k": (I64, [U8P, I64, I64, U8P, I32]),
         "onpu_chain_new": (P, [C.POINTER(P), C.POINTER(P), C.POINTER(P), I32, I64, I32]),
         "onpu_chain_run": (I32, [P, P]),
         "onpu_chain_status": (I32, [P]),

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "onpu.h"
+#include "onpu_codec.h"
 #include "onpu_common.h"
 #include "onpu_host.h"
 #include "onpu_launch.h"
@@ -975,6 +976,70 @@ void onpu_quant_dequant(const float * W, int64_t N, int64_t K, int sym, float * 
     std::vector<uint8_t> st((size_t) stage_bytes(sym, N, K));
     pack_staging(sym, W, N, K, st.data(), threads);
     dequant_staging(sym, st.data(), N, K, out, threads);
+}
+
+int64_t onpu_pack_q4k(const uint8_t * blocks, int64_t N, int64_t K, uint8_t * out, int threads) {
+    if (!blocks || !out || !pack_q4k_staging(blocks, K / 256 * Q4K_BLOCK, N, K, out, threads)) return 0;
+    return stage_bytes(ONPU_Q4NX, N, K);
+}
+}  // extern "C"
+
+// ---------------------------------------------------------------- GPU weight codecs
+// Experts [e0, e0 + n) of m from a device source: fill(e, k, staging, stride) writes the staging of
+// experts e .. e + k - 1 (stride bytes apart) on stream s, which is then repacked into the tiled
+// layout. The staging is a temporary of at most 256 MiB (or one expert), freed before returning,
+// so the call waits for its launches.
+template <class Fill>
+static int codec_load(Mat4 * m, int64_t e0, int64_t n, hipStream_t s, Fill fill) {
+    const int64_t sb = round_up(stage_bytes(m->fmt, m->N, m->K), 256);
+    const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(n, ((int64_t) 256 << 20) / sb));
+    if (n == 0) return 0;
+    void * tmp = nullptr;
+    HIPR(hipMalloc(&tmp, (size_t) (chunk * sb)));
+    hipError_t e = hipSuccess;
+    for (int64_t c = 0; c < n && e == hipSuccess; c += chunk) {
+        const int64_t k = std::min(chunk, n - c);
+        e = fill(e0 + c, k, (uint8_t *) tmp, sb);
+        if (e == hipSuccess)
+            e = launch_repack(m->fmt, (const uint8_t *) tmp, sb, m->N, m->K, m->dev + (e0 + c) * m->dstride, m->dstride,
+                              k, s);
+    }
+    const hipError_t es = hipStreamSynchronize(s);
+    (void) hipFree(tmp);
+    if (e == hipSuccess) e = es;
+    if (e != hipSuccess) { set_err("weight codec", e); return -1; }
+    return 0;
+}
+
+extern "C" {
+
+int onpu_quantize_dev(void * h, int64_t e0, int64_t n, const void * W, int64_t ldw, int w_bf16, void * stream) {
+    auto * m = (Mat4 *) h;
+    if (!m || !W || e0 < 0 || n < 0 || e0 + n > m->E || ldw < m->K || (w_bf16 != 0 && w_bf16 != 1)) {
+        set_err("onpu_quantize_dev: bad arguments");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    const hipStream_t s = (hipStream_t) stream;
+    const int64_t es = m->N * ldw * (w_bf16 ? 2 : 4);           // bytes per expert of W
+    return codec_load(m, e0, n, s, [&](int64_t e, int64_t k, uint8_t * st, int64_t sb) {
+        return launch_quant_stage(m->fmt, (const char *) W + (e - e0) * es, ldw, w_bf16, m->N, m->K, k, st, sb, s);
+    });
+}
+
+int onpu_transcode_q4k_dev(void * h, int64_t e0, int64_t n, const void * blocks, int64_t ld, void * stream) {
+    auto * m = (Mat4 *) h;
+    if (!m || !blocks || m->fmt != ONPU_Q4NX || m->K % 256 != 0 || e0 < 0 || n < 0 || e0 + n > m->E ||
+        ld < m->K / 256 * Q4K_BLOCK) {
+        set_err("onpu_transcode_q4k_dev: bad arguments (a q4nx handle, K a multiple of 256, rows of K / 256 blocks)");
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    const hipStream_t s = (hipStream_t) stream;
+    const int64_t es = m->N * ld;                                 // bytes per expert of the blocks
+    return codec_load(m, e0, n, s, [&](int64_t e, int64_t k, uint8_t * st, int64_t sb) {
+        return launch_q4k_stage((const uint8_t *) blocks + (e - e0) * es, ld, es, m->N, m->K, k, st, sb, s);
+    });
 }
 
 }  // extern "C"

@@ -12,6 +12,8 @@ struct RefGeom {                  // the reference Mat: R, S, tiles, kc, ks, row
 
 RefGeom ref_geometry(int64_t N, int64_t K, int ncols, bool sym);
 bool pack_staging(int fmt, const float * W, int64_t N, int64_t K, uint8_t * out, int threads);
+// GGUF Q4_K rows (K / 256 super-blocks of 144 bytes each, rows ld bytes apart) -> q4nx staging
+bool pack_q4k_staging(const uint8_t * blocks, int64_t ld, int64_t N, int64_t K, uint8_t * out, int threads);
 void dequant_staging(int fmt, const uint8_t * st, int64_t N, int64_t K, float * out, int threads);
 
 }  // namespace onpu

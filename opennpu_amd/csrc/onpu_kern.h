@@ -60,10 +60,11 @@ DEV float scale_f32(int fmt, uint32_t bits) {
     return fmt == ONPU_Q4_0 ? f16_to_f32((uint16_t) bits) : bf16_to_f32((uint16_t) bits);
 }
 
-// dequantized weight (fp32) as the reference defines it: (u - 8) * s, or u * s + m for q4nx.
-// u * s is exact in fp32 (4-bit times 8/11-bit), so fmaf rounds exactly once, like mul-then-add.
+// dequantized weight (fp32) as the reference defines it: (u - 8) * s (exact; a negative scale
+// gives -0 for u = 8, as the reference's expression does), or u * s + m for q4nx (u * s is exact
+// in fp32, 4-bit times 8-bit, so fmaf rounds once, like the reference's multiply-then-add).
 DEV float dq_val(int fmt, uint32_t u, float s, float m) {
-    return fmt_has_min(fmt) ? fmaf((float) u, s, m) : fmaf((float) u, s, -8.0f * s);
+    return fmt_has_min(fmt) ? fmaf((float) u, s, m) : ((float) u - 8.0f) * s;
 }
 
 // two fp32 -> packed bf16 (round to nearest even: v_cvt_pk_bf16_f32), low half = lo

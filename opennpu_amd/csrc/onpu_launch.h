@@ -149,6 +149,13 @@ constexpr int ARGMAX_THREADS = 256, ARGMAX_CHUNK = 16 * ARGMAX_THREADS, ARGMAX_P
 int64_t argmax_parts(int64_t N);
 hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, uint64_t * keys, uint32_t * cnt,
                          hipStream_t s);
+// GPU weight codecs (onpu_codec.hip): W [ne][N][ldw] fp32 (wbf16 = 0) or bf16 -> ne staging buffers of
+// format fmt, ostride bytes apart (a multiple of 16); Q4_K rows (ld bytes apart, experts bstride
+// bytes apart) -> q4nx staging
+hipError_t launch_quant_stage(int fmt, const void * W, int64_t ldw, int wbf16, int64_t N, int64_t K, int64_t ne,
+                              uint8_t * out, int64_t ostride, hipStream_t s);
+hipError_t launch_q4k_stage(const uint8_t * blocks, int64_t ld, int64_t bstride, int64_t N, int64_t K, int64_t ne,
+                            uint8_t * out, int64_t ostride, hipStream_t s);
 hipError_t launch_f32_to_bf16(const float * in, int64_t n, uint16_t * out, hipStream_t s);
 hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * bias, int act,
                           float alpha, float limit, float * o, hipStream_t s);

@@ -7,6 +7,7 @@
 #include <thread>
 #include <vector>
 
+#include "onpu_codec.h"
 #include "onpu_common.h"
 #include "onpu_host.h"
 
@@ -43,124 +44,25 @@ RefGeom ref_geometry(int64_t N, int64_t K, int ncols, bool sym) {
     return g;
 }
 
-static float bfr(float f) { return bf16_to_f32(f32_to_bf16(f)); }
-
-// fp32 -> IEEE binary16, round to nearest even (finite inputs; overflow -> inf)
-static uint16_t f32_to_f16(float f) {
-    union { float f; uint32_t u; } v;
-    v.f = f;
-    const uint32_t s = (v.u >> 16) & 0x8000u;
-    const uint32_t a = v.u & 0x7fffffffu;
-    if (a >= 0x7f800000u) return (uint16_t) (s | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0u));
-    if (a >= 0x477ff000u) return (uint16_t) (s | 0x7c00u);               // rounds past 65504
-    if (a < 0x38800000u) {                                               // subnormal or zero in fp16
-        const float m = std::fabs(f) * 16777216.0f;                      // in units of 2^-24
-        return (uint16_t) (s | (uint32_t) std::nearbyint(m));            // exact scaling, RNE rounding
-    }
-    uint32_t r = a - 0x38000000u;                                        // rebias 127 -> 15 (<< 13)
-    r += 0xfffu + ((r >> 13) & 1u);
-    return (uint16_t) (s | (r >> 13));
-}
-
-// q4s-style search over n weights (the reference's quant_sym32, opennpu_core.hpp:142-169, with the
-// group length as a parameter): 16 candidate scales around absmax, each refit by least squares and
-// rounded to bf16; the least squared error wins. codes u = clamp(rint(x/d), -8, 7) + 8.
-static void quant_sym(const float * x, int n, uint8_t * q, uint16_t & d_bf) {
-    float mx = 0;
-    for (int i = 0; i < n; i++) if (std::fabs(x[i]) > std::fabs(mx)) mx = x[i];
-    if (mx == 0) { d_bf = f32_to_bf16(1.0f); std::memset(q, 8, (size_t) n); return; }
-    float best_e = INFINITY, best_d = mx / -8.0f;
-    for (int c = 0; c < 16; c++) {
-        const float dv = c < 8 ? -9.0f + 2.5f * c / 7 : 6.5f + 1.5f * (c - 8) / 7;
-        const float d0 = mx / dv;
-        float sqq = 0, sqx = 0;
-        for (int i = 0; i < n; i++) {
-            const float v = std::min(7.0f, std::max(-8.0f, std::nearbyint(x[i] / d0)));
-            sqq += v * v;
-            sqx += v * x[i];
-        }
-        float d = sqq > 0 ? sqx / sqq : d0;
-        d = bfr(d);
-        if (d == 0) continue;
-        float e = 0;
-        for (int i = 0; i < n; i++) {
-            const float v = std::min(7.0f, std::max(-8.0f, std::nearbyint(x[i] / d)));
-            const float r = v * d - x[i];
-            e += r * r;
-        }
-        if (e < best_e) { best_e = e; best_d = d; }
-    }
-    for (int i = 0; i < n; i++)
-        q[i] = (uint8_t) (std::min(7.0f, std::max(-8.0f, std::nearbyint(x[i] / best_d))) + 8);
-    d_bf = f32_to_bf16(best_d);
-}
-
-// q4nx per 32 (the reference's quant_asym32, opennpu_core.hpp:103-138): 21 stretched grids over
-// [min, max], (s, m) refit by least squares, bf16-rounded, least squared error wins
-static void quant_asym32(const float * x, uint8_t * q, uint16_t & s_bf, uint16_t & m_bf) {
-    float lo = x[0], hi = x[0];
-    for (int i = 1; i < 32; i++) { lo = std::min(lo, x[i]); hi = std::max(hi, x[i]); }
-    const float range = hi - lo;
-    if (!(range > 0)) {
-        s_bf = f32_to_bf16(1.0f);
-        m_bf = f32_to_bf16(lo);
-        std::memset(q, 0, 32);
-        return;
-    }
-    float best_e = INFINITY, best_s = range / 15, best_m = lo;
-    for (int st = 0; st <= 20; st++) {
-        const float isc = (-1.0f + 0.1f * st + 15.0f) / range;
-        float sl = 0, sll = 0, sx = 0, slx = 0;
-        for (int i = 0; i < 32; i++) {
-            const float l = std::min(15.0f, std::max(0.0f, std::nearbyint(isc * (x[i] - lo))));
-            sl += l; sll += l * l; sx += x[i]; slx += l * x[i];
-        }
-        const float D = 32 * sll - sl * sl;
-        float sc = range / 15, mn = lo;
-        if (D > 0) { sc = (32 * slx - sl * sx) / D; mn = (sll * sx - sl * slx) / D; }
-        sc = bfr(sc);
-        mn = bfr(mn);
-        if (!(sc > 0)) continue;
-        float e = 0;
-        for (int i = 0; i < 32; i++) {
-            const float l = std::min(15.0f, std::max(0.0f, std::nearbyint((x[i] - mn) / sc)));
-            const float d = l * sc + mn - x[i];
-            e += d * d;
-        }
-        if (e < best_e) { best_e = e; best_s = sc; best_m = mn; }
-    }
-    best_s = bfr(best_s);
-    best_m = bfr(best_m);
-    for (int i = 0; i < 32; i++)
-        q[i] = (uint8_t) std::min(15.0f, std::max(0.0f, std::nearbyint((x[i] - best_m) / best_s)));
-    s_bf = f32_to_bf16(best_s);
-    m_bf = f32_to_bf16(best_m);
-}
-
-// GGUF Q4_0 block quantizer (ggml's published quantize_row_q4_0 rule): d = v / -8 for the value v of
-// largest magnitude, u = min(15, trunc(x / d + 8.5)); d stored as fp16
-static void quant_q4_0(const float * x, uint8_t * blk) {
-    float amax = 0, vmax = 0;
-    for (int j = 0; j < 32; j++)
-        if (amax < std::fabs(x[j])) { amax = std::fabs(x[j]); vmax = x[j]; }
-    const float d = vmax / -8.0f, id = d != 0 ? 1.0f / d : 0.0f;
-    const uint16_t dh = f32_to_f16(d);
-    blk[0] = (uint8_t) (dh & 0xff);
-    blk[1] = (uint8_t) (dh >> 8);
-    for (int j = 0; j < 16; j++) {
-        const int a = std::min(15, (int) (int8_t) (x[j] * id + 8.5f));
-        const int b = std::min(15, (int) (int8_t) (x[16 + j] * id + 8.5f));
-        blk[2 + j] = (uint8_t) (a | (b << 4));
-    }
-}
-
-// rows [r0, r1) of W [N][K] -> staging layout of format fmt (out holds the whole matrix)
+// rows [r0, r1) of W [N][K] -> staging layout of format fmt (out holds the whole matrix), with the
+// quantizers of onpu_codec.h
 static void pack_rows(int fmt, const float * W, int64_t N, int64_t K, int64_t r0, int64_t r1, uint8_t * out) {
     const int64_t G = fmt_group(fmt);
+    float x[128];
     uint8_t q[128];
+    auto & x32 = *reinterpret_cast<float (*)[32]>(x);
+    auto & q32 = *reinterpret_cast<uint8_t (*)[32]>(q);
     if (fmt == ONPU_Q4_0) {
         for (int64_t r = r0; r < r1; r++)
-            for (int64_t g = 0; g < K / 32; g++) quant_q4_0(W + r * K + 32 * g, out + (r * (K / 32) + g) * 18);
+            for (int64_t g = 0; g < K / 32; g++) {
+                std::memcpy(x, W + r * K + 32 * g, 32 * sizeof(float));
+                uint16_t dh = 0;
+                quant_q4_0(x32, q32, dh);
+                uint8_t * blk = out + (r * (K / 32) + g) * 18;
+                blk[0] = (uint8_t) (dh & 0xff);
+                blk[1] = (uint8_t) (dh >> 8);
+                for (int j = 0; j < 16; j++) blk[2 + j] = (uint8_t) (q[j] | (q[16 + j] << 4));
+            }
         return;
     }
     uint8_t * codes = out;
@@ -168,14 +70,30 @@ static void pack_rows(int fmt, const float * W, int64_t N, int64_t K, int64_t r0
     uint16_t * mn = sc + N * (K / G);
     for (int64_t r = r0; r < r1; r++)
         for (int64_t g = 0; g < K / G; g++) {
-            const float * x = W + r * K + G * g;
+            std::memcpy(x, W + r * K + G * g, (size_t) G * sizeof(float));
             uint16_t s = 0, m = 0;
-            if (fmt == ONPU_Q4NX) quant_asym32(x, q, s, m);
-            else quant_sym(x, (int) G, q, s);
+            if (fmt == ONPU_Q4NX) quant_asym32(x32, q32, s, m);
+            else if (G == 128) quant_sym<128>(x, q, s);
+            else quant_sym<32>(x32, q32, s);
             for (int64_t i = 0; i < G; i += 2)
                 codes[r * (K / 2) + (G * g + i) / 2] = (uint8_t) (q[i] | (q[i + 1] << 4));
             sc[r * (K / G) + g] = s;
             if (fmt == ONPU_Q4NX) mn[r * (K / G) + g] = m;
+        }
+}
+
+// GGUF Q4_K rows [r0, r1) (K / 256 super-blocks per row, ld bytes apart) -> q4nx staging
+static void q4k_rows(const uint8_t * blocks, int64_t ld, int64_t N, int64_t K, int64_t r0, int64_t r1, uint8_t * out) {
+    uint8_t q[32];
+    uint16_t * sc = (uint16_t *) (out + N * K / 2);
+    uint16_t * mn = sc + N * (K / 32);
+    for (int64_t r = r0; r < r1; r++)
+        for (int64_t g = 0; g < K / 32; g++) {
+            uint16_t s = 0, m = 0;
+            q4k_sub(blocks + r * ld + (g / 8) * Q4K_BLOCK, (int) (g % 8), q, s, m);
+            for (int i = 0; i < 32; i += 2) out[r * (K / 2) + (32 * g + i) / 2] = (uint8_t) (q[i] | (q[i + 1] << 4));
+            sc[r * (K / 32) + g] = s;
+            mn[r * (K / 32) + g] = m;
         }
 }
 
@@ -190,6 +108,12 @@ static void parallel_rows(int64_t N, int threads, const std::function<void(int64
 bool pack_staging(int fmt, const float * W, int64_t N, int64_t K, uint8_t * out, int threads) {
     if (!fmt_valid(fmt) || K % fmt_group(fmt) != 0 || N <= 0) return false;
     parallel_rows(N, threads, [&](int64_t a, int64_t b) { pack_rows(fmt, W, N, K, a, b, out); });
+    return true;
+}
+
+bool pack_q4k_staging(const uint8_t * blocks, int64_t ld, int64_t N, int64_t K, uint8_t * out, int threads) {
+    if (N <= 0 || K <= 0 || K % 256 != 0 || ld < K / 256 * Q4K_BLOCK) return false;
+    parallel_rows(N, threads, [&](int64_t a, int64_t b) { q4k_rows(blocks, ld, N, K, a, b, out); });
     return true;
 }
 

@@ -43,6 +43,23 @@ class QMatrix:
         assert stage.size == self.L.onpu_stage_bytes(self.fmt, self.N, self.K)
         check(self.L.onpu_dense_load(self.h, _np_ptr(stage)), "onpu_dense_load")
 
+    def quantize(self, W):
+        """Quantize W (fp32 or bf16 cuda tensor [N][>=K], rows contiguous) on the GPU into this
+        matrix, with the format's quantizer (the bytes onpu_pack writes)."""
+        import torch
+        assert W.is_cuda and W.dtype in (torch.float32, torch.bfloat16) and W.dim() == 2 and W.stride(1) == 1
+        assert W.shape[0] == self.N and W.shape[1] >= self.K
+        check(self.L.onpu_quantize_dev(self.h, 0, 1, _ptr(W), W.stride(0), int(W.dtype == torch.bfloat16),
+                                       _stream()), "onpu_quantize_dev")
+
+    def transcode_q4k(self, blocks):
+        """Load GGUF Q4_K rows (uint8 cuda tensor [N][K / 256 * 144]) into this q4nx matrix."""
+        import torch
+        assert blocks.is_cuda and blocks.dtype == torch.uint8 and blocks.dim() == 2 and blocks.stride(1) == 1
+        assert blocks.shape[0] == self.N and blocks.shape[1] >= self.K // 256 * 144
+        check(self.L.onpu_transcode_q4k_dev(self.h, 0, 1, _ptr(blocks), blocks.stride(0), _stream()),
+              "onpu_transcode_q4k_dev")
+
     def mv(self, x, out=None, f32=False):
         """x: bf16 cuda tensor [M][K] -> y [M][N] (bf16, or fp32 when f32)."""
         import torch
@@ -104,6 +121,16 @@ class QFfn:
         n = gu_stage.size // sg
         check(self.L.onpu_bank_load(self.gu, e0, n, _np_ptr(gu_stage)), "onpu_bank_load")
         check(self.L.onpu_bank_load(self.dn, e0, n, _np_ptr(dn_stage)), "onpu_bank_load")
+
+    def quantize(self, gu_w, dn_w, e0=0):
+        """Quantize n experts on the GPU into experts [e0, e0 + n): gu_w [n][2I][H] and dn_w
+        [n][Nd][I], fp32 or bf16 contiguous cuda tensors."""
+        import torch
+        for w, h, N, K in ((gu_w, self.gu, 2 * self.I, self.H), (dn_w, self.dn, self.Nd, self.I)):
+            assert w.is_cuda and w.dtype in (torch.float32, torch.bfloat16) and w.is_contiguous()
+            assert w.dim() == 3 and tuple(w.shape[1:]) == (N, K)
+            check(self.L.onpu_quantize_dev(h, e0, w.shape[0], _ptr(w), K, int(w.dtype == torch.bfloat16),
+                                           _stream()), "onpu_quantize_dev")
 
     def route(self, logits, k, renorm=True):
         """logits fp32 cuda [T][E] -> ids int32 [T][k], w fp32 [T][k]."""

@@ -11,8 +11,10 @@
  *   - router: torch softmax/topk + the invariants sum(w) = 1, ids = top-k of the logits;
  *   - silu-mul / weighted sum / argmax: torch.nn.functional.silu, numpy, first-max rule;
  *   - geometry: the values the reference formula gives at the benchmark shapes.
- * The search quantizers (orc_quant_sym32 / orc_quant_asym32) are off the measured path and are
- * only checked by invariants: parity unpinned.
+ * The search quantizers (orc_quant_sym / orc_quant_asym32) are off the measured path and are
+ * only checked by invariants (exact grids come back exactly): parity unpinned. The GGUF codecs
+ * (orc_quant_q4_0, orc_transcode_q4k) are checked on hand-built blocks whose results are exact,
+ * by the closed forms of the formats, and the transcode's choice by a brute-force neighbourhood.
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, so no fused multiply-adds change rounding).
  */
@@ -274,18 +276,18 @@ void orc_geometry(int64_t N, int64_t K, int ncols, int sym, int64_t * out) {
 }
 
 /* ---------------------------------------------------------------- search quantizers (load time)
- * q4s per 32: 16 candidate scales around absmax, least-squares refit, bf16, least SSE wins
- * (opennpu_core.hpp:142-169). Parity unpinned: checked by invariants only. */
-void orc_quant_sym32(const float * x, uint8_t * q, uint16_t * d_bf) {
+ * q4s over n weights (n = 32: q4s, 128: g128s): 16 candidate scales around absmax, least-squares
+ * refit, bf16, least SSE wins (opennpu_core.hpp:142-169, written there for n = 32). */
+void orc_quant_sym(const float * x, int n, uint8_t * q, uint16_t * d_bf) {
     float mx = 0;
-    for (int i = 0; i < 32; i++) if (fabsf(x[i]) > fabsf(mx)) mx = x[i];
-    if (mx == 0) { *d_bf = orc_f2bf(1.0f); memset(q, 8, 32); return; }
+    for (int i = 0; i < n; i++) if (fabsf(x[i]) > fabsf(mx)) mx = x[i];
+    if (mx == 0) { *d_bf = orc_f2bf(1.0f); memset(q, 8, (size_t) n); return; }
     float best_e = INFINITY, best_d = mx / -8.0f;
     for (int c = 0; c < 16; c++) {
         const float dv = c < 8 ? -9.0f + 2.5f * c / 7 : 6.5f + 1.5f * (c - 8) / 7;
         const float d0 = mx / dv;
         float sqq = 0, sqx = 0;
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < n; i++) {
             float v = nearbyintf(x[i] / d0);
             v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
             sqq += v * v;
@@ -295,7 +297,7 @@ void orc_quant_sym32(const float * x, uint8_t * q, uint16_t * d_bf) {
         d = orc_bf2f(orc_f2bf(d));
         if (d == 0) continue;
         float e = 0;
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < n; i++) {
             float v = nearbyintf(x[i] / d);
             v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
             const float r = v * d - x[i];
@@ -303,13 +305,15 @@ void orc_quant_sym32(const float * x, uint8_t * q, uint16_t * d_bf) {
         }
         if (e < best_e) { best_e = e; best_d = d; }
     }
-    for (int i = 0; i < 32; i++) {
+    for (int i = 0; i < n; i++) {
         float v = nearbyintf(x[i] / best_d);
         v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
         q[i] = (uint8_t) (v + 8);
     }
     *d_bf = orc_f2bf(best_d);
 }
+
+void orc_quant_sym32(const float * x, uint8_t * q, uint16_t * d_bf) { orc_quant_sym(x, 32, q, d_bf); }
 
 /* q4nx per 32: 21 stretched grids over [min, max], (s, m) refit by least squares, bf16
  * (opennpu_core.hpp:103-138). Parity unpinned: invariants only. */
@@ -351,4 +355,115 @@ void orc_quant_asym32(const float * x, uint8_t * q, uint16_t * s_bf, uint16_t * 
     }
     *s_bf = orc_f2bf(best_s);
     *m_bf = orc_f2bf(best_m);
+}
+
+/* ---------------------------------------------------------------- GGUF codecs (load time)
+ * fp32 -> IEEE binary16, round to nearest even (what ggml's GGML_FP32_TO_FP16 computes). */
+uint16_t orc_f2h(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    const uint32_t sgn = (u >> 16) & 0x8000u;
+    const float a = fabsf(f);
+    if (a != a) return (uint16_t) (sgn | 0x7e00u);
+    if (a >= 65520.0f) return (uint16_t) (sgn | 0x7c00u);       /* rounds to infinity */
+    if (a < 6.103515625e-05f) {                                  /* fp16 subnormal: multiples of 2^-24 */
+        return (uint16_t) (sgn | (uint32_t) nearbyintf(a * 16777216.0f));
+    }
+    int e;
+    const float m = frexpf(a, &e);                               /* a = m 2^e, m in [0.5, 1) */
+    uint32_t mant = (uint32_t) nearbyintf(ldexpf(m, 11));        /* 11 significant bits, RNE */
+    if (mant == 2048u) { mant = 1024u; e++; }
+    return (uint16_t) (sgn | ((uint32_t) (e + 14) << 10) | (mant - 1024u));
+}
+
+/* ggml's quantize_row_q4_0 rule (llama.cpp 4413a19, the GGUF Q4_0 the reference reads,
+ * ggml-opennpu.cpp:78-98): d = vmax / -8 for the first value of largest magnitude, id = 1/d (0 when
+ * d = 0), u = min(15, (int8) (x id + 8.5)); codes in element order, d as fp16. */
+void orc_quant_q4_0(const float * x, uint8_t * q, uint16_t * d_h) {
+    float amax = 0, vmax = 0;
+    for (int j = 0; j < 32; j++)
+        if (amax < fabsf(x[j])) { amax = fabsf(x[j]); vmax = x[j]; }
+    const float d = vmax / -8.0f, id = d != 0 ? 1.0f / d : 0.0f;
+    *d_h = orc_f2h(d);
+    for (int j = 0; j < 32; j++) {
+        const int u = (int) (int8_t) (x[j] * id + 8.5f);
+        q[j] = (uint8_t) (u < 15 ? u : 15);
+    }
+}
+
+/* neighbouring bf16 value (ggml-opennpu.cpp:108-112) */
+static uint16_t orc_bf_step(uint16_t h, int dir) {
+    const float f = orc_bf2f(h);
+    if (f == 0) return dir > 0 ? (uint16_t) 0x0001 : (uint16_t) 0x8001;
+    return (uint16_t) (((f > 0) == (dir > 0)) ? h + 1 : h - 1);
+}
+
+/* GGUF Q4_K -> q4nx (ggml-opennpu.cpp:114-138). blocks: rows of K/256 super-blocks (144 bytes:
+ * fp16 d, fp16 dmin, 12 bytes of packed 6-bit scales/mins, 128 bytes of nibbles), rows ld bytes
+ * apart. Out: codes q [N][K] (u8 0..15), bf16 scale s and min m per 32 [N][K/32]. */
+void orc_transcode_q4k(const uint8_t * blocks, int64_t N, int64_t K, int64_t ld, uint8_t * q, uint16_t * s,
+                       uint16_t * m) {
+    for (int64_t r = 0; r < N; r++)
+        for (int64_t g = 0; g < K / 32; g++) {
+            const uint8_t * b = blocks + r * ld + (g / 8) * 144;
+            const int sub = (int) (g % 8);
+            const float d = orc_h2f((uint16_t) (b[0] | (b[1] << 8))), dmin = orc_h2f((uint16_t) (b[2] | (b[3] << 8)));
+            const uint8_t * sc = b + 4, * qs = b + 16;
+            unsigned sv, mv;
+            if (sub < 4) { sv = sc[sub] & 63u; mv = sc[sub + 4] & 63u; }
+            else {
+                sv = (sc[sub + 4] & 0xFu) | ((unsigned) (sc[sub - 4] >> 6) << 4);
+                mv = (unsigned) (sc[sub + 4] >> 4) | ((unsigned) (sc[sub] >> 6) << 4);
+            }
+            uint8_t * qo = q + r * K + 32 * g;
+            for (int l = 0; l < 32; l++) {
+                const uint8_t byte = qs[(sub / 2) * 32 + l];
+                qo[l] = (sub & 1) ? (uint8_t) (byte >> 4) : (uint8_t) (byte & 0xF);
+            }
+            const float S = d * (float) sv, M = -dmin * (float) mv;
+            const uint16_t s0 = orc_f2bf(S), m0 = orc_f2bf(M);
+            float best = INFINITY;
+            uint16_t bs = s0, bm = m0;
+            for (int ds = -1; ds <= 1; ds++)
+                for (int dm = -1; dm <= 1; dm++) {
+                    const uint16_t sc_ = ds ? orc_bf_step(s0, ds) : s0, mn_ = dm ? orc_bf_step(m0, dm) : m0;
+                    const float sf = orc_bf2f(sc_), mf = orc_bf2f(mn_);
+                    float e = 0;
+                    for (int l = 0; l < 32; l++) {
+                        const float t = qo[l] * sf + mf - (qo[l] * S + M);
+                        e += t * t;
+                    }
+                    if (e < best) { best = e; bs = sc_; bm = mn_; }
+                }
+            s[r * (K / 32) + g] = bs;
+            m[r * (K / 32) + g] = bm;
+        }
+}
+
+/* W [N][K] fp32 -> the staging layout of fmt (orc_stage_bytes bytes), by the quantizers above:
+ * the bytes onpu_pack writes (the staging layout is this library's; see the layout comment above). */
+void orc_quantize(int fmt, const float * W, int64_t N, int64_t K, uint8_t * out) {
+    const int G = fmt == FMT_G128S ? 128 : 32;
+    uint8_t q[128];
+    uint16_t * sc = (uint16_t *) (out + N * K / 2);
+    uint16_t * mn = sc + N * (K / G);
+    for (int64_t r = 0; r < N; r++)
+        for (int64_t g = 0; g < K / G; g++) {
+            const float * x = W + r * K + (int64_t) G * g;
+            if (fmt == FMT_Q4_0) {
+                uint16_t dh;
+                orc_quant_q4_0(x, q, &dh);
+                uint8_t * blk = out + (r * (K / 32) + g) * 18;
+                blk[0] = (uint8_t) (dh & 0xff);
+                blk[1] = (uint8_t) (dh >> 8);
+                for (int j = 0; j < 16; j++) blk[2 + j] = (uint8_t) (q[j] | (q[16 + j] << 4));
+                continue;
+            }
+            uint16_t s1 = 0, m1 = 0;
+            if (fmt == FMT_Q4NX) orc_quant_asym32(x, q, &s1, &m1);
+            else orc_quant_sym(x, G, q, &s1);
+            for (int i = 0; i < G; i += 2) out[r * (K / 2) + (G * g + i) / 2] = (uint8_t) (q[i] | (q[i + 1] << 4));
+            sc[r * (K / G) + g] = s1;
+            if (fmt == FMT_Q4NX) mn[r * (K / G) + g] = m1;
+        }
 }

@@ -51,7 +51,12 @@ def lib():
         L.orc_argmax.argtypes = [P, I64, I64, P]
         L.orc_geometry.argtypes = [I64, I64, I32, I32, P]
         L.orc_quant_sym32.argtypes = [P, P, P]
+        L.orc_quant_sym.argtypes = [P, I32, P, P]
         L.orc_quant_asym32.argtypes = [P, P, P, P]
+        L.orc_f2h.restype, L.orc_f2h.argtypes = C.c_uint16, [C.c_float]
+        L.orc_quant_q4_0.argtypes = [P, P, P]
+        L.orc_transcode_q4k.argtypes = [P, I64, I64, I64, P, P, P]
+        L.orc_quantize.argtypes = [I32, P, I64, I64, P]
         _lib = L
     return _lib
 
@@ -245,6 +250,64 @@ def quant_asym32(x):
     m = np.zeros(1, np.uint16)
     lib().orc_quant_asym32(_p(x), _p(q), _p(s), _p(m))
     return q, int(s[0]), int(m[0])
+
+
+def quant_sym(x):
+    """q4s search quantizer over len(x) weights (32: q4s, 128: g128s; opennpu_core.hpp:142-169):
+    (codes, bf16 d bits)."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(x.size, np.uint8)
+    d = np.zeros(1, np.uint16)
+    lib().orc_quant_sym(_p(x), x.size, _p(q), _p(d))
+    return q, int(d[0])
+
+
+def f2h(x):
+    """float32 -> fp16 bits, RNE (ggml's GGML_FP32_TO_FP16)."""
+    return np.array([lib().orc_f2h(float(v)) for v in np.ravel(x)], np.uint16).reshape(np.shape(x))
+
+
+def quant_q4_0(x):
+    """ggml's quantize_row_q4_0 rule on 32 weights: (codes in element order, fp16 d bits)."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(32, np.uint8)
+    d = np.zeros(1, np.uint16)
+    lib().orc_quant_q4_0(_p(x), _p(q), _p(d))
+    return q, int(d[0])
+
+
+def transcode_q4k(blocks, N, K, ld=None):
+    """GGUF Q4_K rows -> q4nx (ggml-opennpu.cpp:114-138): codes [N][K], bf16 s and m [N][K/32]."""
+    if K % 256:
+        raise ValueError("Q4_K rows hold whole 256-weight super-blocks")
+    ld = K // 256 * 144 if ld is None else ld
+    b = np.ascontiguousarray(blocks, np.uint8)
+    if b.size < (N - 1) * ld + K // 256 * 144:
+        raise ValueError("Q4_K buffer too small")
+    q = np.empty((N, K), np.uint8)
+    s = np.empty((N, K // 32), np.uint16)
+    m = np.empty((N, K // 32), np.uint16)
+    lib().orc_transcode_q4k(_p(b), N, K, ld, _p(q), _p(s), _p(m))
+    return q, s, m
+
+
+def quantize(fmt, W):
+    """W [N][K] fp32 -> staging bytes of fmt by the quantizers above (what onpu_pack writes)."""
+    W = np.ascontiguousarray(W, np.float32)
+    N, K = W.shape
+    if K % group(fmt):
+        raise ValueError(f"K = {K} is not a multiple of the format's group ({group(fmt)})")
+    out = np.zeros(stage_bytes(fmt, N, K), np.uint8)
+    lib().orc_quantize(fmt, _p(W), N, K, _p(out))
+    return out
+
+
+def stage_q4nx(q, s, m):
+    """codes [N][K] + bf16 s, m [N][K/32] -> q4nx staging bytes (low nibble = even k)."""
+    q = np.asarray(q, np.uint8)
+    codes = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return np.concatenate([codes.ravel(), np.asarray(s, np.uint16).ravel().view(np.uint8),
+                           np.asarray(m, np.uint16).ravel().view(np.uint8)])
 
 
 def max_rel_err(y, r):

@@ -136,3 +136,44 @@ def test_pack_round_trip_q4s():
             q, d = orc.quant_sym32(W[r, 32 * gi:32 * gi + 32])
             assert np.array_equal(orc.unpack(1, st, N, K)[r, 32 * gi:32 * gi + 32], q)
             assert st[N * K // 2:].view(np.uint16)[r * (K // 32) + gi] == d
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+def test_pack_equals_oracle_quantize(fmt):
+    """onpu_pack (host quantizers of onpu_codec.h) writes exactly the oracle's staging bytes, for
+    every format, Gaussian weights with a few outliers and an all-zero row"""
+    L = _lib.lib()
+    rng = np.random.default_rng(20 + fmt)
+    N, K = 19, 512
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    W[3, 17] = 0.9
+    W[5] = 0.0
+    g = (C.c_int64 * 8)()
+    L.onpu_geometry2(N, K, 8, fmt, g)
+    assert g[7] > 0
+    out = np.zeros(g[7], np.uint8)
+    n = L.onpu_pack(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 8, fmt, out.ctypes.data_as(C.POINTER(C.c_uint8)), 3)
+    assert n == g[7]
+    sb = orc.stage_bytes(fmt, N, K)
+    assert np.array_equal(out[:sb], orc.quantize(fmt, W))
+    assert not out[sb:].any()
+
+
+def test_pack_q4k_equals_oracle_transcode():
+    """onpu_pack_q4k (GGUF Q4_K -> q4nx staging on the host) writes exactly the oracle's transcode"""
+    L = _lib.lib()
+    rng = np.random.default_rng(30)
+    N, K = 7, 768
+    nb = N * (K // 256)
+    blocks = rng.integers(0, 256, (nb, 144)).astype(np.uint8)
+    d = (rng.uniform(1e-4, 3e-2, nb)).astype(np.float16)
+    dmin = (rng.uniform(0, 1e-2, nb)).astype(np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    blocks[0, 4:16] = 0                                   # zero scales and mins in one super-block
+    out = np.zeros(orc.stage_bytes(orc.FMT_Q4NX, N, K), np.uint8)
+    n = L.onpu_pack_q4k(blocks.ctypes.data_as(C.POINTER(C.c_uint8)), N, K, out.ctypes.data_as(C.POINTER(C.c_uint8)), 2)
+    assert n == out.size
+    q, s, m = orc.transcode_q4k(blocks, N, K)
+    assert np.array_equal(out, orc.stage_q4nx(q, s, m))
+    assert L.onpu_pack_q4k(blocks.ctypes.data_as(C.POINTER(C.c_uint8)), N, 384, out.ctypes.data_as(C.POINTER(C.c_uint8)), 1) == 0

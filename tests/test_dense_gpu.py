@@ -30,10 +30,17 @@ def _mv(fmt, N, K, M, seed, f32=False):
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_dequant_bit_exact(gpu, fmt):
-    """unpack + dequant in HBM layout == the reference's dequant, bit for bit (fp32 and bf16 RNE)."""
+    """unpack + dequant in HBM layout == the reference's dequant, bit for bit (fp32 and bf16 RNE),
+    with every other scale negative (the quantizers produce those): (u - 8) s is -0 for u = 8 there,
+    as the reference's expression gives."""
     from opennpu_amd.device import QMatrix
     for (N, K) in [(48, 256), (37, 384), (16, 2048)] + ([] if fmt == orc.FMT_G128S else [(21, 160)]):
-        st = syn.weights(fmt, N, K, 11 + N)
+        st = syn.weights(fmt, N, K, 11 + N).copy()
+        if fmt == orc.FMT_Q4_0:
+            st.reshape(-1, 18)[::2, 1] ^= 0x80                  # sign bit of d (fp16, little endian)
+        elif fmt != orc.FMT_Q4NX:
+            G = orc.group(fmt)
+            st[N * K // 2:N * K // 2 + N * (K // G) * 2].view(np.uint16)[::2] ^= 0x8000
         q = QMatrix(N, K, fmt, st)
         try:
             w = q.dequant()

@@ -284,3 +284,179 @@ def test_oracle_rejects_shapes_outside_the_format():
         orc.dequant(orc.FMT_G128S, np.zeros(64 * 32, np.uint8), 64, 64)      # K not a multiple of 128
     with pytest.raises(ValueError):
         orc.qmm(orc.FMT_Q4S, np.zeros(10, np.uint8), 4, 64, np.zeros((1, 64), np.uint16))   # short buffer
+
+
+# ------------------------------------------------------------------ GGUF codecs and the g128s quantizer
+def test_f2h_matches_numpy_float16():
+    """fp32 -> fp16 RNE against numpy's own conversion, over normal, subnormal, tie and overflow
+    values"""
+    rng = np.random.default_rng(11)
+    x = np.concatenate([rng.standard_normal(4000) * 10.0 ** rng.integers(-9, 5, 4000),
+                        np.float32(2.0) ** np.arange(-26, 17),
+                        [65504, 65519.99, 65520, -65520, 0.0, -0.0, 2.0 ** -25, 3 * 2.0 ** -25,
+                         1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11]]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(orc.f2h(x), want)
+
+
+def test_quant_sym_128_exact_grid_round_trip():
+    """the g128s quantizer (quant_sym over 128): exact grids v * d come back exactly"""
+    rng = np.random.default_rng(12)
+    for t in range(30):
+        d = np.float32(2.0 ** rng.integers(-12, 2))
+        v = rng.integers(-8, 8, 128)
+        v[rng.integers(0, 128)] = -8
+        q, db = orc.quant_sym((v * d).astype(np.float32))
+        assert orc.bf2f(np.array([db], np.uint16))[0] == d
+        assert np.array_equal(q.astype(int), v + 8)
+
+
+def test_quant_q4_0_closed_form():
+    """ggml's Q4_0 rule: with the largest magnitude -8 d (d a power of two) the codes are v + 8 and
+    d comes back exactly; with it +8 d the scale flips sign and (u - 8) d' still reproduces x; all
+    zeros give d = -0 and codes 8"""
+    rng = np.random.default_rng(13)
+    for t in range(40):
+        d = np.float32(2.0 ** rng.integers(-14, 3))
+        v = rng.integers(-7, 8, 32)
+        i = rng.integers(0, 32)
+        v[i] = -8 if t % 2 == 0 else 8
+        x = (v * d).astype(np.float32)
+        q, dh = orc.quant_q4_0(x)
+        dd = np.float32(np.array([dh], np.uint16).view(np.float16)[0])
+        assert abs(dd) == d
+        assert np.array_equal(((q.astype(np.float32) - 8) * dd).astype(np.float32), x)
+        if t % 2 == 0:
+            assert np.array_equal(q.astype(int), v + 8)
+    q, dh = orc.quant_q4_0(np.zeros(32, np.float32))
+    assert dh == 0x8000 and (q == 8).all()            # d = 0 / -8 = -0
+
+
+def _q4k_block(rng, d, dmin, sv, mv, nib):
+    """one GGUF Q4_K super-block (ggml's block_q4_K): fp16 d, dmin, 6-bit (scale, min) pairs of the
+    8 sub-blocks packed into 12 bytes as ggml's quantize_row_q4_K packs them, codes [8][32]"""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    sc = np.zeros(12, np.uint8)
+    for j in range(4):
+        sc[j] = sv[j] | ((sv[j + 4] >> 4) << 6)
+        sc[j + 4] = mv[j] | ((mv[j + 4] >> 4) << 6)
+        sc[j + 8] = (sv[j + 4] & 0xF) | ((mv[j + 4] & 0xF) << 4)
+    b[4:16] = sc
+    for c in range(4):                          # sub-blocks 2c (low nibbles) and 2c + 1 (high)
+        b[16 + 32 * c:48 + 32 * c] = nib[2 * c] | (nib[2 * c + 1] << 4)
+    return b
+
+
+def test_transcode_q4k_exact_blocks():
+    """d = 1, dmin = 1/2 and integer 6-bit scales: every sub-block's scale d sc and min -dmin mn
+    are exact in bf16, so the transcode keeps them, the codes are the sub-block's nibbles and the
+    q4nx weights equal the Q4_K weights d sc u - dmin mn exactly"""
+    rng = np.random.default_rng(14)
+    N, K = 3, 512
+    blocks, want_u, want_w = [], np.zeros((N, K), np.uint8), np.zeros((N, K), np.float64)
+    for r in range(N):
+        for sb in range(K // 256):
+            sv, mv = rng.integers(1, 64, 8), rng.integers(1, 64, 8)
+            nib = rng.integers(0, 16, (8, 32)).astype(np.uint8)
+            blocks.append(_q4k_block(rng, 1.0, 0.5, sv, mv, nib))
+            for sub in range(8):
+                k0 = 256 * sb + 32 * sub
+                want_u[r, k0:k0 + 32] = nib[sub]
+                want_w[r, k0:k0 + 32] = 1.0 * sv[sub] * nib[sub] - 0.5 * mv[sub]
+    q, s, m = orc.transcode_q4k(np.concatenate(blocks), N, K)
+    assert np.array_equal(q, want_u)
+    w = q.astype(np.float64) * np.repeat(orc.bf2f(s), 32, axis=1) + np.repeat(orc.bf2f(m), 32, axis=1)
+    assert np.array_equal(w, want_w)
+
+
+def test_transcode_q4k_zero_scale_takes_the_first_tie():
+    """a zero scale (sc = 0) or min (mn = 0): the neighbours +-2^-133 of bf16 zero reproduce the
+    weights equally well in fp32 (u * 2^-133 is absorbed), and the search keeps the first minimum
+    in its order (step -1 first), so the stored value is -2^-133 (0x8001); the weights it gives
+    equal the exact ones in fp32, but for an all-zero sub-block, which keeps subnormal residues"""
+    rng = np.random.default_rng(17)
+    sv = np.array([0, 9, 0, 3, 7, 0, 5, 2])
+    mv = np.array([4, 0, 0, 6, 0, 8, 1, 3])
+    nib = rng.integers(0, 16, (8, 32)).astype(np.uint8)
+    nib[:, 0] = 1                                   # not all codes zero
+    q, s, m = orc.transcode_q4k(_q4k_block(rng, 1.0, 0.5, sv, mv, nib), 1, 256)
+    for sub in range(8):
+        if sv[sub] == 0:
+            assert s[0, sub] == 0x8001
+        if mv[sub] == 0:
+            assert m[0, sub] == 0x8001
+        u = q[0, 32 * sub:32 * sub + 32].astype(np.float32)
+        w = (u * orc.bf2f(s[0, sub:sub + 1])[0]).astype(np.float32) + orc.bf2f(m[0, sub:sub + 1])[0]
+        want = (u * np.float32(sv[sub])).astype(np.float32) + np.float32(-0.5 * mv[sub])
+        if sv[sub] == 0 and mv[sub] == 0:               # all weights zero: a subnormal residue remains
+            assert np.abs(w).max() < 2.0 ** -120
+        else:
+            assert np.array_equal(w[u > 0], want[u > 0])
+
+
+def test_transcode_q4k_picks_the_best_neighbour():
+    """general fp16 d, dmin: the chosen (s, m) is one of the 3 x 3 bf16 neighbours of the rounded
+    exact scale and min, and no neighbour reproduces the exact weights better (fp64 error, with
+    fp32-accumulation slack)"""
+    rng = np.random.default_rng(15)
+    N, K = 4, 256
+    blocks, exact = [], []
+    for r in range(N):
+        sv, mv = rng.integers(1, 64, 8), rng.integers(0, 64, 8)
+        nib = rng.integers(0, 16, (8, 32)).astype(np.uint8)
+        d, dmin = np.float16(rng.uniform(1e-4, 2e-2)), np.float16(rng.uniform(0, 1e-2))
+        blocks.append(_q4k_block(rng, d, dmin, sv, mv, nib))
+        exact.append((np.float32(d) * sv.astype(np.float32), -np.float32(dmin) * mv.astype(np.float32), nib))
+    q, s, m = orc.transcode_q4k(np.concatenate(blocks), N, K)
+
+    def step(h, dirn):
+        f = orc.bf2f(np.array([h], np.uint16))[0]
+        if f == 0:
+            return 0x0001 if dirn > 0 else 0x8001
+        return h + 1 if (f > 0) == (dirn > 0) else h - 1
+
+    for r in range(N):
+        S, M, nib = exact[r]
+        for sub in range(8):
+            u = nib[sub].astype(np.float64)
+            s0, m0 = int(orc.f2bf(np.array([S[sub]]))[0]), int(orc.f2bf(np.array([M[sub]]))[0])
+            cands = [(step(s0, a) if a else s0, step(m0, b) if b else m0) for a in (-1, 0, 1) for b in (-1, 0, 1)]
+            err = lambda c: float(np.sum((u * orc.bf2f(np.array([c[0]], np.uint16))[0]
+                                          + orc.bf2f(np.array([c[1]], np.uint16))[0]
+                                          - (u * np.float64(S[sub]) + np.float64(M[sub]))) ** 2))
+            got = (int(s[r, sub]), int(m[r, sub]))
+            assert got in cands
+            best = min(err(c) for c in cands)
+            assert err(got) <= best * (1 + 1e-4) + 1e-30
+            assert np.array_equal(q[r, 32 * sub:32 * sub + 32], nib[sub])
+
+
+def test_quantize_staging_layout():
+    """orc.quantize lays the per-group quantizers' outputs out as the staging layout: codes two per
+    byte (low nibble = even k), then scales (then mins); Q4_0 as GGUF blocks"""
+    rng = np.random.default_rng(16)
+    N, K = 5, 256
+    W = (rng.standard_normal((N, K)) * 0.03).astype(np.float32)
+    for fmt in (orc.FMT_Q4NX, orc.FMT_Q4S, orc.FMT_G128S, orc.FMT_Q4_0):
+        st = orc.quantize(fmt, W)
+        u = orc.unpack(fmt, st, N, K)
+        G = orc.group(fmt)
+        for r in range(N):
+            for g in range(K // G):
+                x = W[r, G * g:G * g + G]
+                if fmt == orc.FMT_Q4NX:
+                    q, sb, mb = orc.quant_asym32(x)
+                elif fmt == orc.FMT_Q4_0:
+                    q, sb = orc.quant_q4_0(x)
+                else:
+                    q, sb = orc.quant_sym(x)
+                assert np.array_equal(u[r, G * g:G * g + G], q), (fmt, r, g)
+                if fmt == orc.FMT_Q4_0:
+                    assert st[(r * (K // 32) + g) * 18:][:2].view(np.uint16)[0] == sb
+                else:
+                    assert st[N * K // 2:].view(np.uint16)[r * (K // G) + g] == sb
+                    if fmt == orc.FMT_Q4NX:
+                        assert st[N * K // 2 + N * (K // G) * 2:].view(np.uint16)[r * (K // G) + g] == mb
