@@ -11,7 +11,8 @@ bytes per step (int4 codes + bf16 scales + x + y) / time, in GB/s.
 Also measured in the same run (the "configs" object): M=4 and M=8 decode steps, a single
 4096x4096 GEMV rotated over 64 copies, the Llama-3.1-8B prefill FFN GEMMs (M=2048, TFLOPS), the
 Qwen3-30B-A3B MoE layer (decode M=1 and prefill M=512, router included), and the 151936x4096
-Q4_0 LM head with argmax (M=1, 5). The roofline object is the dominant kernel: the gate+up GEMV,
+Q4_0 LM head with argmax (M=1, 5), and the load-time weight codecs on one layer (GPU quantization
+into each format and the GGUF Q4_K transcode, beside the host quantizer). The roofline object is the dominant kernel: the gate+up GEMV,
 timed with HIP events over a graph of back-to-back launches on its stream. The cpu_baseline leg
 times the reference's own CPU pattern (dequantize to fp32, then x @ W^T in torch fp32,
 opennpu/native/reference.py:24-28,55) on one layer of the same workload.
@@ -279,6 +280,68 @@ def lm_head(torch, QMatrix, syn, iters):
     return out
 
 
+def codecs(torch, QMatrix):
+    """Load-time weight codecs on one Qwen3-8B layer (4 matrices, 174 M weights): GPU quantization
+    of fp32 weights already in HBM into each format (onpu_quantize_dev: the search quantizers, the
+    GGUF Q4_0 rule) and the GGUF Q4_K -> q4nx transcode (onpu_transcode_q4k_dev), each call
+    synchronous (temporary staging, repack into the tiled layout included); beside it the host
+    quantizer (onpu_pack) on all host threads over the layer's o matrix (16.8 M weights)."""
+    import ctypes as C
+    from opennpu_amd import _lib
+    L = _lib.lib()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    Ws = [torch.randn((N, K), generator=g, device="cuda", dtype=torch.float32) * 0.02 for _, N, K in QWEN3_8B]
+    nw = sum(N * K for _, N, K in QWEN3_8B)
+    out = {}
+    for name, fmt in (("q4s", 1), ("q4nx", 0), ("g128s", G128S), ("q4_0", Q4_0)):
+        qs = [QMatrix(N, K, fmt) for _, N, K in QWEN3_8B]
+        ts = []
+        for rep in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for q, W in zip(qs, Ws):
+                q.quantize(W)
+            ts.append(time.perf_counter() - t0)
+        t = float(np.median(ts))
+        out[name] = {"ms_per_layer": t * 1e3, "Mweights_per_s": nw / t / 1e6}
+        for q in qs:
+            q.free()
+    # Q4_K super-blocks with random nibbles and 6-bit scales, fp16 d / dmin of typical magnitude
+    blocks = []
+    for _, N, K in QWEN3_8B:
+        b = torch.randint(0, 256, (N, K // 256, 144), generator=g, device="cuda", dtype=torch.uint8)
+        b[..., 0:2] = (torch.rand((N, K // 256, 1), generator=g, device="cuda") * 0.02 + 1e-4).half().view(torch.uint8)
+        b[..., 2:4] = (torch.rand((N, K // 256, 1), generator=g, device="cuda") * 0.01).half().view(torch.uint8)
+        blocks.append(b.reshape(N, K // 256 * 144))
+    qs = [QMatrix(N, K, 0) for _, N, K in QWEN3_8B]
+    ts = []
+    for rep in range(3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for q, b in zip(qs, blocks):
+            q.transcode_q4k(b)
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    out["q4k_to_q4nx"] = {"ms_per_layer": t * 1e3, "Mweights_per_s": nw / t / 1e6}
+    for q in qs:
+        q.free()
+    # the host quantizer over the o matrix
+    N, K = 4096, 4096
+    W = Ws[1].cpu().numpy()
+    cores = len(os.sched_getaffinity(0))
+    for name, fmt in (("q4s", 1), ("q4nx", 0), ("g128s", G128S), ("q4_0", Q4_0)):
+        geo = (C.c_int64 * 8)()
+        L.onpu_geometry2(N, K, 8, fmt, geo)
+        buf = np.zeros(geo[7], np.uint8)
+        t0 = time.perf_counter()
+        L.onpu_pack(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 8, fmt, buf.ctypes.data_as(C.POINTER(C.c_uint8)),
+                    cores)
+        t = time.perf_counter() - t0
+        out[name]["cpu_Mweights_per_s"] = N * K / t / 1e6
+        out[name]["cpu_threads"] = cores
+    return out
+
+
 def cpu_baseline(syn, seconds=12.0):
     """The reference's CPU pattern on one Qwen3-8B layer at M=1: dequantize W to fp32 (timed once),
     then x @ W^T in torch fp32 (timed, repeated for about `seconds`)."""
@@ -401,6 +464,8 @@ def main():
         configs["qwen3_30b_a3b_moe"] = moe(torch, QFfn, syn, 30)
         log("lm head ...")
         configs["lm_head_q4_0"] = lm_head(torch, QMatrix, syn, 30)
+        log("weight codecs ...")
+        configs["weight_codecs_qwen3_8b_layer"] = codecs(torch, QMatrix)
     gu = head["per_matrix"]["gate_up"]
     roof = {"kernel": "k_qgemv<g128s> gate+up 24576x4096, M=1 (768 workgroups x 8 waves, x in LDS)",
             "bound": "hbm", "achieved": gu["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
