@@ -163,6 +163,19 @@ int onpu_transcode_q4k_dev(void * h, int64_t e0, int64_t n, const void * blocks,
  * K is not a multiple of 256 */
 int64_t onpu_pack_q4k(const uint8_t * blocks, int64_t N, int64_t K, uint8_t * out, int threads);
 
+/* ---- decode attention on the GPU: the reference's host onpu_attn_step / onpu_attn_step_bf16
+ * (onpu_cpu.cpp:173-229, bound by npu4 at model.py:392-397, 612-615) with device pointers, on
+ * `stream`. q fp32 [Hq][D]; K, V: Hkv heads of S rows of D values, fp32 (kv_bf16 = 0) or bf16 (1),
+ * head stride hs and row stride rs in elements (shared by K and V, rows 16-byte aligned); mask fp32
+ * [S] additive or NULL; sinks fp32 [Hq] or NULL (an extra logit per head with no value); out fp32
+ * [Hq][D]. Hq a multiple of Hkv with Hq / Hkv <= 16, D <= 256 and a multiple of 8. ws: device
+ * workspace of onpu_attn_ws_bytes(Hq, D, Hkv, S) bytes (calls in flight together need their own).
+ * Capturable in a HIP graph. 0 ok, -1 error (onpu_last_error). */
+int64_t onpu_attn_ws_bytes(int Hq, int D, int Hkv, int64_t S);
+int onpu_attn_step_dev(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv, int64_t S,
+                       int64_t hs, int64_t rs, const float * mask, const float * sinks, float scale, float * out,
+                       void * ws, int64_t ws_bytes, void * stream);
+
 /* ---- chained decode GEMVs (no counterpart in the reference's ABI; the reference's fused decode
  * engine likewise runs a token's products in one NPU dispatch). A chain is n dense GEMVs
  * y_i [M][N_i] = x_i [M][K_i] . W_i^T fixed at creation (handles, x and y device pointers; one

@@ -19,7 +19,7 @@ BUILD = HERE / "_build"
 ARCH = os.environ.get("ONPU_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # (source, extra defines, object name): onpu_fmt.hip is built once per weight format
-SOURCES = [("onpu_kernels.hip", [], "onpu_kernels"), ("onpu_codec.hip", [], "onpu_codec"), ("onpu_api.cpp", [], "onpu_api"), ("onpu_quant.cpp", [], "onpu_quant")] + \
+SOURCES = [("onpu_kernels.hip", [], "onpu_kernels"), ("onpu_codec.hip", [], "onpu_codec"), ("onpu_attn.hip", [], "onpu_attn"), ("onpu_api.cpp", [], "onpu_api"), ("onpu_quant.cpp", [], "onpu_quant")] + \
     [("onpu_fmt.hip", [f"-DONPU_FMT_ID={i}"], f"onpu_fmt{i}") for i in range(4)]
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(CSRC), "-I", str(ROOT / "include"),
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]

@@ -1027,6 +1027,25 @@ int onpu_quantize_dev(void * h, int64_t e0, int64_t n, const void * W, int64_t l
     });
 }
 
+int64_t onpu_attn_ws_bytes(int Hq, int D, int Hkv, int64_t S) { return attn_ws_bytes(Hq, D, Hkv, S); }
+
+int onpu_attn_step_dev(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv, int64_t S,
+                       int64_t hs, int64_t rs, const float * mask, const float * sinks, float scale, float * out,
+                       void * ws, int64_t ws_bytes, void * stream) {
+    if (!q || !K || !V || !out || !ws || (kv_bf16 != 0 && kv_bf16 != 1)) {
+        set_err("onpu_attn_step_dev: bad arguments");
+        return -1;
+    }
+    const hipError_t e = launch_attn_step(q, Hq, D, K, V, kv_bf16, Hkv, S, hs, rs, mask, sinks, scale, out, ws, ws_bytes,
+                                          (hipStream_t) stream);
+    if (e != hipSuccess) {
+        set_err("onpu_attn_step_dev (Hq a multiple of Hkv with Hq / Hkv <= 16, D <= 256 and a multiple of 8, "
+                "16-byte aligned rows, workspace of onpu_attn_ws_bytes)", e);
+        return -1;
+    }
+    return 0;
+}
+
 int onpu_transcode_q4k_dev(void * h, int64_t e0, int64_t n, const void * blocks, int64_t ld, void * stream) {
     auto * m = (Mat4 *) h;
     if (!m || !blocks || m->fmt != ONPU_Q4NX || m->K % 256 != 0 || e0 < 0 || n < 0 || e0 + n > m->E ||

@@ -156,6 +156,11 @@ hipError_t launch_quant_stage(int fmt, const void * W, int64_t ldw, int wbf16, i
                               uint8_t * out, int64_t ostride, hipStream_t s);
 hipError_t launch_q4k_stage(const uint8_t * blocks, int64_t ld, int64_t bstride, int64_t N, int64_t K, int64_t ne,
                             uint8_t * out, int64_t ostride, hipStream_t s);
+// decode attention (onpu_attn.hip): workspace bytes for (Hq, D, Hkv, S), and the two launches
+int64_t attn_ws_bytes(int Hq, int D, int Hkv, int64_t S);
+hipError_t launch_attn_step(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv,
+                            int64_t S, int64_t hs, int64_t rs, const float * mask, const float * sinks, float scale,
+                            float * out, void * ws, int64_t ws_bytes, hipStream_t s);
 hipError_t launch_f32_to_bf16(const float * in, int64_t n, uint16_t * out, hipStream_t s);
 hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32_t * ids, const float * bias, int act,
                           float alpha, float limit, float * o, hipStream_t s);

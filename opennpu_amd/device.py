@@ -210,3 +210,25 @@ class QChain:
         if self.h:
             self.L.onpu_chain_free(self.h)
             self.h = None
+
+
+def attn_step(q, K, V, mask=None, sinks=None, scale=None, out=None, ws=None):
+    """One decode token of grouped-query attention on the GPU (onpu_attn_step_dev): q fp32 [Hq][D];
+    K, V [Hkv][S][D] fp32 or bf16 cuda views with unit stride in D and the same strides (a KV
+    cache slice); mask fp32 [S] or None; sinks fp32 [Hq] or None. Returns out fp32 [Hq][D]."""
+    import torch
+    L = require_gpu()
+    Hq, D = q.shape
+    Hkv, S, _ = K.shape
+    assert q.dtype == torch.float32 and q.is_contiguous() and K.dtype == V.dtype
+    assert K.stride() == V.stride() and K.stride(2) == 1 and K.shape == V.shape and K.shape[2] == D
+    if out is None:
+        out = torch.empty((Hq, D), dtype=torch.float32, device=q.device)
+    nb = L.onpu_attn_ws_bytes(Hq, D, Hkv, S)
+    if ws is None or ws.numel() < nb:
+        ws = torch.empty((max(nb, 4),), dtype=torch.uint8, device=q.device)
+    check(L.onpu_attn_step_dev(_ptr(q), Hq, D, _ptr(K), _ptr(V), int(K.dtype == torch.bfloat16), Hkv, S,
+                               K.stride(0), K.stride(1), None if mask is None else _ptr(mask),
+                               None if sinks is None else _ptr(sinks), float(D ** -0.5 if scale is None else scale),
+                               _ptr(out), _ptr(ws), ws.numel(), _stream()), "onpu_attn_step_dev")
+    return out

@@ -467,3 +467,45 @@ void orc_quantize(int fmt, const float * W, int64_t N, int64_t K, uint8_t * out)
             if (fmt == FMT_Q4NX) mn[r * (K / G) + g] = m1;
         }
 }
+
+/* ---------------------------------------------------------------- decode attention (one token)
+ * onpu_attn_step / onpu_attn_step_bf16 (onpu_cpu.cpp:180-229): q [Hq][D]; K, V: Hkv heads of S
+ * rows (head stride hs, row stride rs, elements; fp32, or bf16 bits when kv_bf16); mask [S] additive
+ * or NULL; sinks [Hq] or NULL; out [Hq][D]. fp32, sequential sums in the reference's order. */
+void orc_attn_step(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv, int64_t S,
+                   int64_t hs, int64_t rs, const float * mask, const float * sinks, float scale, float * out) {
+    const int rep = Hq / Hkv;
+    float * p = (float *) malloc((size_t) S * sizeof(float));
+    for (int h = 0; h < Hq; h++) {
+        const float * qh = q + (int64_t) h * D;
+        const int64_t base = (int64_t) (h / rep) * hs;
+        float mx = sinks ? sinks[h] : -INFINITY;
+        for (int64_t j = 0; j < S; j++) {
+            float s = 0.f;
+            for (int d = 0; d < D; d++) {
+                const int64_t i = base + j * rs + d;
+                const float k = kv_bf16 ? orc_bf2f(((const uint16_t *) K)[i]) : ((const float *) K)[i];
+                s += qh[d] * k;
+            }
+            s = s * scale + (mask ? mask[j] : 0.f);
+            p[j] = s;
+            if (s > mx) mx = s;
+        }
+        float sum = sinks ? expf(sinks[h] - mx) : 0.f;
+        for (int64_t j = 0; j < S; j++) {
+            p[j] = expf(p[j] - mx);
+            sum += p[j];
+        }
+        float * o = out + (int64_t) h * D;
+        for (int d = 0; d < D; d++) o[d] = 0.f;
+        for (int64_t j = 0; j < S; j++) {
+            const float pj = p[j] / sum;
+            for (int d = 0; d < D; d++) {
+                const int64_t i = base + j * rs + d;
+                const float v = kv_bf16 ? orc_bf2f(((const uint16_t *) V)[i]) : ((const float *) V)[i];
+                o[d] += pj * v;
+            }
+        }
+    }
+    free(p);
+}

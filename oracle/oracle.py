@@ -57,6 +57,7 @@ def lib():
         L.orc_quant_q4_0.argtypes = [P, P, P]
         L.orc_transcode_q4k.argtypes = [P, I64, I64, I64, P, P, P]
         L.orc_quantize.argtypes = [I32, P, I64, I64, P]
+        L.orc_attn_step.argtypes = [P, I32, I32, P, P, I32, I32, I64, I64, I64, P, P, C.c_float, P]
         _lib = L
     return _lib
 
@@ -308,6 +309,23 @@ def stage_q4nx(q, s, m):
     codes = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
     return np.concatenate([codes.ravel(), np.asarray(s, np.uint16).ravel().view(np.uint8),
                            np.asarray(m, np.uint16).ravel().view(np.uint8)])
+
+
+def attn_step(q, K, V, mask=None, sinks=None, scale=None):
+    """One decode token of GQA attention (onpu_cpu.cpp:180-229). q [Hq][D] fp32; K, V [Hkv][S][D]
+    fp32 or bf16 bits (uint16); mask [S]; sinks [Hq]. Returns out [Hq][D] fp32."""
+    q = np.ascontiguousarray(q, np.float32)
+    Hq, D = q.shape
+    K = np.ascontiguousarray(K)
+    V = np.ascontiguousarray(V)
+    Hkv, S, _ = K.shape
+    bf = int(K.dtype == np.uint16)
+    out = np.empty((Hq, D), np.float32)
+    m = None if mask is None else np.ascontiguousarray(mask, np.float32)
+    sk = None if sinks is None else np.ascontiguousarray(sinks, np.float32)
+    lib().orc_attn_step(_p(q), Hq, D, _p(K), _p(V), bf, Hkv, S, S * D, D, None if m is None else _p(m),
+                        None if sk is None else _p(sk), float(D ** -0.5 if scale is None else scale), _p(out))
+    return out
 
 
 def max_rel_err(y, r):

@@ -460,3 +460,32 @@ def test_quantize_staging_layout():
                     assert st[N * K // 2:].view(np.uint16)[r * (K // G) + g] == sb
                     if fmt == orc.FMT_Q4NX:
                         assert st[N * K // 2 + N * (K // G) * 2:].view(np.uint16)[r * (K // G) + g] == mb
+
+
+# ------------------------------------------------------------------ decode attention
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_attn_step_against_torch_float64(kv):
+    """GQA decode attention with an additive mask (some -inf) and per-head sinks, against a float64
+    torch softmax with the sink as an extra logit without a value"""
+    import torch
+    rng = np.random.default_rng(90)
+    Hq, Hkv, S, D = 8, 2, 300, 64
+    q = rng.standard_normal((Hq, D)).astype(np.float32)
+    Kf = rng.standard_normal((Hkv, S, D)).astype(np.float32)
+    Vf = rng.standard_normal((Hkv, S, D)).astype(np.float32)
+    mask = np.where(rng.random(S) < 0.1, -np.inf, rng.standard_normal(S) * 0.1).astype(np.float32)
+    sinks = rng.standard_normal(Hq).astype(np.float32)
+    if kv == "bf16":
+        K, V = orc.f2bf_np(Kf), orc.f2bf_np(Vf)
+        Kf, Vf = orc.bf2f(K).reshape(Kf.shape), orc.bf2f(V).reshape(Vf.shape)
+    else:
+        K, V = Kf, Vf
+    for sk in (None, sinks):
+        out = orc.attn_step(q, K, V, mask, sk)
+        qt = torch.from_numpy(q).double().reshape(Hkv, Hq // Hkv, D)
+        s = torch.einsum("grd,gsd->grs", qt, torch.from_numpy(Kf).double()) * D ** -0.5 + torch.from_numpy(mask).double()
+        if sk is not None:
+            s = torch.cat([s, torch.from_numpy(sk).double().reshape(Hkv, Hq // Hkv, 1)], -1)
+        p = torch.softmax(s, -1)[..., :S]
+        ref = torch.einsum("grs,gsd->grd", p, torch.from_numpy(Vf).double()).reshape(Hq, D).numpy()
+        assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
