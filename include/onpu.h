@@ -168,7 +168,7 @@ int64_t onpu_pack_q4k(const uint8_t * blocks, int64_t N, int64_t K, uint8_t * ou
  * `stream`. q fp32 [Hq][D]; K, V: Hkv heads of S rows of D values, fp32 (kv_bf16 = 0) or bf16 (1),
  * head stride hs and row stride rs in elements (shared by K and V, rows 16-byte aligned); mask fp32
  * [S] additive or NULL; sinks fp32 [Hq] or NULL (an extra logit per head with no value); out fp32
- * [Hq][D]. Hq a multiple of Hkv with Hq / Hkv <= 16, D <= 256 and a multiple of 8. ws: device
+ * [Hq][D] (q, K and V 16-byte aligned). Hq a multiple of Hkv with Hq / Hkv <= 16, D <= 256 and a multiple of 8. ws: device
  * workspace of onpu_attn_ws_bytes(Hq, D, Hkv, S) bytes (calls in flight together need their own).
  * Capturable in a HIP graph. 0 ok, -1 error (onpu_last_error). */
 int64_t onpu_attn_ws_bytes(int Hq, int D, int Hkv, int64_t S);

@@ -4,20 +4,26 @@
 // optional per-head sink logit that takes probability mass but has no value), out_h = sum_j p_j
 // V[g][j]. fp32 arithmetic; the KV cache is fp32 or bf16 (widened exactly).
 //
-// Split over the sequence (HBM-bound: K and V are read once). k_attn_part: workgroup (c, g) takes
-// rows [c C, c C + C) of kv head g for all rep = Hq / Hkv query heads that share it, so each K and
-// V row is read once for rep heads. Phase 1: thread t scores its rows (a row's D values streamed in
-// 16-byte loads, q from LDS), the chunk's max and exp-sum per head through LDS. Phase 2: threads
-// own pairs of d and row groups, accumulate p_j V[j][d] (a row's D values read by consecutive
-// lanes), reduce the row groups in LDS and write the chunk's (max, sum, o[rep][D]) partials.
-// k_attn_combine: one workgroup per query head rescales the chunks' partials to the global max
-// (and the sink) and divides by the total mass.
+// Split over the sequence; HBM-bound at long context (K and V are read once). k_attn_part:
+// workgroup (c, g, z) takes rows [c C, c C + C) of kv head g for HG of the query heads that share
+// it (group z), so each K and V row is read once for HG heads. A row is read by LPR = D / 8
+// consecutive lanes, 16 bytes each (one wave instruction covers 64 / LPR consecutive rows), with
+// AU rows per lane group in flight. Phase 1 scores the chunk's rows into LDS (a lane's 8 products
+// per head, summed across its LPR lanes by DPP); the chunk's max and exp-sum per head follow from
+// LDS while the first V loads fly; phase 2 accumulates p_j V[j] in registers (8 values of d per lane
+// and head), sums the row slots of a wave by shuffles and the waves in LDS, and writes the chunk's
+// (max, sum, o[HG][D]). k_attn_combine: per query head, the chunks' partials rescaled to the
+// global max (and the sink) and divided by the total mass.
 #include "onpu_launch.h"
 
 namespace {
 
-constexpr int ATT_T = 256;                   // threads per workgroup
-constexpr int ATT_RPT = 4;                   // rows per thread at most in phase 1 (C <= 1024)
+constexpr int AT = 512;                      // threads per workgroup (8 waves)
+constexpr int AW = AT / 64;
+constexpr int AU = 4;                        // rows per lane group in flight
+constexpr int AP_MAX = 16384;                // floats of P per workgroup (64 KiB)
+constexpr int TARGET_WG = 512;
+constexpr int ATT_MAX_CH = 4096;             // chunks per kv head at most (the combine's LDS)
 
 struct AttnArgs {
     const float * q;
@@ -26,7 +32,7 @@ struct AttnArgs {
     float * ws, * out;
     int64_t S, hs, rs;
     float scale;
-    int Hq, D, Hkv, rep, C, nch;
+    int Hq, D, Hkv, rep, ngrp, C, nch;
 };
 
 template <typename KV> __device__ __forceinline__ void load8(const KV * p, float (&v)[8]);
@@ -45,16 +51,19 @@ template <> __device__ __forceinline__ void load8<float>(const float * p, float 
     v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-template <typename KV> __device__ __forceinline__ void load2(const KV * p, float & v0, float & v1);
-template <> __device__ __forceinline__ void load2<uint16_t>(const uint16_t * p, float & v0, float & v1) {
-    const uint32_t w = *(const uint32_t *) p;
-    v0 = __uint_as_float(w << 16);
-    v1 = __uint_as_float(w & 0xffff0000u);
+// sum over aligned groups of L lanes (L = 8, 16, 32), every lane of a group left with the sum: DPP
+// within a row of 16 (xor 1 and 2 by quad permutes, then the half-row and row mirrors, which pair
+// lanes of equal partial sums), one cross-row shuffle for 32
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
-template <> __device__ __forceinline__ void load2<float>(const float * p, float & v0, float & v1) {
-    const float2 f = *(const float2 *) p;
-    v0 = f.x;
-    v1 = f.y;
+template <int L> __device__ __forceinline__ float group_sum(float x) {
+    x += dpp_f<0xB1>(x);                     // quad_perm [1, 0, 3, 2]
+    x += dpp_f<0x4E>(x);                     // quad_perm [2, 3, 0, 1]
+    x += dpp_f<0x141>(x);                    // row_half_mirror: lane i <-> 7 - i
+    if (L >= 16) x += dpp_f<0x140>(x);       // row_mirror: lane i <-> 15 - i
+    if (L >= 32) x += __shfl_xor(x, 16);
+    return x;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -66,161 +75,206 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// LDS: qs [RP][D], P [RP][C], red [ATT_T / (D / 2)][RP][D], small [2][4][RP]
-template <typename KV, int RP>
-__global__ __launch_bounds__(ATT_T) void k_attn_part(AttnArgs a) {
+// LDS: P [HG][C], red [AW][HG][D], wmax / wsum [AW][HG], qs [HG][D]
+template <typename KV, int LPR, int HG>
+__global__ __launch_bounds__(AT) void k_attn_part(AttnArgs a) {
+    constexpr int RPW = 64 / LPR, RIT = AW * RPW * AU;          // row slots per wave; rows per pass
     extern __shared__ float lds[];
-    const int D = a.D, C = a.C, c = blockIdx.x, g = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    float * qs = lds, * P = qs + RP * D, * red = P + RP * C;
-    float * wmax = red + (ATT_T / (D / 2)) * RP * D, * wsum = wmax + 4 * RP;
-    const int rep = a.rep;
-    for (int i = t; i < RP * D; i += ATT_T) {
-        const int h = i / D;
-        qs[i] = h < rep ? a.q[(int64_t) (g * rep + h) * D + (i - h * D)] : 0.f;
-    }
-    __syncthreads();
-    const KV * Kg = (const KV *) a.K + (int64_t) g * a.hs;
-    const KV * Vg = (const KV *) a.V + (int64_t) g * a.hs;
+    const int D = a.D, C = a.C, c = blockIdx.x, g = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, li = lane % LPR, slot = lane / LPR;
+    float * P = lds, * red = P + HG * C, * wmax = red + AW * HG * D, * wsum = wmax + AW * HG, * qs = wsum + AW * HG;
+    const bool dl = 8 * li < D;                                  // this lane's 8 values of d exist
     const int64_t j0 = (int64_t) c * C;
     const int rows = (int) (a.S - j0 < C ? a.S - j0 : C);
+    const KV * Kg = (const KV *) a.K + (int64_t) g * a.hs + j0 * a.rs + 8 * li;
+    const KV * Vg = (const KV *) a.V + (int64_t) g * a.hs + j0 * a.rs + 8 * li;
+    // q of the group's heads: coalesced 16-byte loads (0 past rep), stored to LDS after the first
+    // pass's K loads are issued; the barrier then waits for LDS only (a __syncthreads would also
+    // wait for the K loads)
+    const int nq = HG * D / 4, hq0 = z * HG, hqn = a.rep - hq0 < HG ? a.rep - hq0 : HG;
+    const float4 qv = t < nq && t * 4 < hqn * D ? *(const float4 *) (a.q + (int64_t) (g * a.rep + hq0) * D + 4 * t)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    // Row of (pass r0, step u, wave, slot): consecutive slots and waves take consecutive rows, so one
+    // wave instruction reads RPW consecutive rows.
+    float kv[AU][8];
+    auto issue = [&](const KV * base, int r0) {
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            const int row = r0 + (u * AW + wave) * RPW + slot;
+            if (row < rows && dl) load8<KV>(base + (int64_t) row * a.rs, kv[u]);
+            else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) kv[u][e] = 0.f;
+            }
+        }
+    };
+    issue(Kg, 0);
+    if (t < nq) *(float4 *) (qs + 4 * t) = qv;
+    __builtin_amdgcn_s_waitcnt(0xc07f);                                 // lgkmcnt(0): the LDS stores
+    __builtin_amdgcn_s_barrier();
+    float qr[HG][8];
+#pragma unroll
+    for (int h = 0; h < HG; h++) {
+        const float4 a0 = dl ? *(const float4 *) (qs + h * D + 8 * li) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 a1 = dl ? *(const float4 *) (qs + h * D + 8 * li + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        qr[h][0] = a0.x; qr[h][1] = a0.y; qr[h][2] = a0.z; qr[h][3] = a0.w;
+        qr[h][4] = a1.x; qr[h][5] = a1.y; qr[h][6] = a1.z; qr[h][7] = a1.w;
+    }
 
-    // phase 1: scores of this thread's rows t, t + 256, ...
-    float mloc[RP];
+    // phase 1: scores into P
+    for (int r0 = 0; r0 < rows; r0 += RIT) {
+        if (r0 > 0) issue(Kg, r0);
 #pragma unroll
-    for (int h = 0; h < RP; h++) mloc[h] = -__builtin_inff();
+        for (int u = 0; u < AU; u++) {
+            const int row = r0 + (u * AW + wave) * RPW + slot;
+            float sc[HG];
 #pragma unroll
-    for (int i = 0; i < ATT_RPT; i++) {
-        const int jl = t + i * ATT_T;
-        if (jl >= C) break;
-        float sc[RP];
+            for (int h = 0; h < HG; h++) {
+                float x = 0.f;
 #pragma unroll
-        for (int h = 0; h < RP; h++) sc[h] = 0.f;
-        if (jl < rows) {
-            const KV * kr = Kg + (j0 + jl) * a.rs;
-            for (int d0 = 0; d0 < D; d0 += 8) {
-                float kv[8];
-                load8<KV>(kr + d0, kv);
+                for (int e = 0; e < 8; e++) x += qr[h][e] * kv[u][e];
+                sc[h] = group_sum<LPR>(x);                                   // the row's lanes
+            }
+            if (li == 0 && row < rows) {
+                const float mk = a.mask ? a.mask[j0 + row] : 0.f;
 #pragma unroll
-                for (int h = 0; h < RP; h++) {
-                    const float4 qa = *(const float4 *) (qs + h * D + d0), qb = *(const float4 *) (qs + h * D + d0 + 4);
-                    sc[h] += qa.x * kv[0]; sc[h] += qa.y * kv[1]; sc[h] += qa.z * kv[2]; sc[h] += qa.w * kv[3];
-                    sc[h] += qb.x * kv[4]; sc[h] += qb.y * kv[5]; sc[h] += qb.z * kv[6]; sc[h] += qb.w * kv[7];
+                for (int h = 0; h < HG; h++) P[h * C + row] = sc[h] * a.scale + mk;
+            }
+        }
+    }
+    issue(Vg, 0);                           // phase 2's first V loads fly during the softmax
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    // chunk max and exp-sum per head (a chunk whose rows are all -inf keeps p = 0)
+#pragma unroll
+    for (int h = 0; h < HG; h++) {
+        float mx = -__builtin_inff();
+        for (int r = t; r < rows; r += AT) mx = fmaxf(mx, P[h * C + r]);
+        mx = wave_max(mx);
+        if (lane == 0) wmax[wave * HG + h] = mx;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int h = 0; h < HG; h++) {
+        float mx = wmax[h];
+#pragma unroll
+        for (int w = 1; w < AW; w++) mx = fmaxf(mx, wmax[w * HG + h]);
+        float l = 0.f;
+        for (int r = t; r < rows; r += AT) {
+            const float p = mx == -__builtin_inff() ? 0.f : expf(P[h * C + r] - mx);
+            P[h * C + r] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) wsum[wave * HG + h] = l;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+
+    // phase 2: o[h][d] = sum_j P[h][j] V[j][d]
+    float acc[HG][8];
+#pragma unroll
+    for (int h = 0; h < HG; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] = 0.f;
+    for (int r0 = 0; r0 < rows; r0 += RIT) {
+        if (r0 > 0) issue(Vg, r0);
+#pragma unroll
+        for (int u = 0; u < AU; u++) {
+            const int row = r0 + (u * AW + wave) * RPW + slot;
+            if (row < rows) {
+#pragma unroll
+                for (int h = 0; h < HG; h++) {
+                    const float p = P[h * C + row];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[h][e] += p * kv[u][e];
                 }
             }
-            const float mk = a.mask ? a.mask[j0 + jl] : 0.f;
-#pragma unroll
-            for (int h = 0; h < RP; h++) {
-                sc[h] = sc[h] * a.scale + mk;
-                mloc[h] = fmaxf(mloc[h], sc[h]);
-            }
-        } else {
-#pragma unroll
-            for (int h = 0; h < RP; h++) sc[h] = -__builtin_inff();
         }
-#pragma unroll
-        for (int h = 0; h < RP; h++) P[h * C + jl] = sc[h];
     }
+    // sum the wave's row slots (lanes LPR apart), then the waves
 #pragma unroll
-    for (int h = 0; h < RP; h++) {
-        const float m = wave_max(mloc[h]);
-        if (lane == 0) wmax[wave * RP + h] = m;
+    for (int h = 0; h < HG; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float x = acc[h][e];
+#pragma unroll
+            for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o);
+            acc[h][e] = x;
+        }
+    if (slot == 0 && dl) {
+#pragma unroll
+        for (int h = 0; h < HG; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) red[(wave * HG + h) * D + 8 * li + e] = acc[h][e];
     }
     __syncthreads();
-    float mc[RP];
+    float * wp = a.ws + (((int64_t) g * a.ngrp + z) * a.nch + c) * (HG * (2 + D));
+    for (int i = t; i < HG * D; i += AT) {
+        float sum = 0.f;
 #pragma unroll
-    for (int h = 0; h < RP; h++)
-        mc[h] = fmaxf(fmaxf(wmax[h], wmax[RP + h]), fmaxf(wmax[2 * RP + h], wmax[3 * RP + h]));
-    float lloc[RP];
-#pragma unroll
-    for (int h = 0; h < RP; h++) lloc[h] = 0.f;
-#pragma unroll
-    for (int i = 0; i < ATT_RPT; i++) {
-        const int jl = t + i * ATT_T;
-        if (jl >= C) break;
-#pragma unroll
-        for (int h = 0; h < RP; h++) {
-            // a chunk whose rows are all masked (-inf) keeps p = 0 instead of exp(-inf + inf)
-            const float p = mc[h] == -__builtin_inff() ? 0.f : expf(P[h * C + jl] - mc[h]);
-            P[h * C + jl] = p;
-            lloc[h] += p;
-        }
+        for (int w = 0; w < AW; w++) sum += red[w * HG * D + i];
+        wp[2 * HG + i] = sum;
     }
+    if (t < HG) {
+        float mx = wmax[t], l = 0.f;
 #pragma unroll
-    for (int h = 0; h < RP; h++) {
-        const float s = wave_sum(lloc[h]);
-        if (lane == 0) wsum[wave * RP + h] = s;
-    }
-    __syncthreads();
-
-    // phase 2: o[h][d] = sum_j P[h][j] V[j][d]; thread (row group rg, d pair dp)
-    const int ndp = D / 2, tpd = ATT_T / ndp, dp = t % ndp, rg = t / ndp;
-    float acc[RP][2];
+        for (int w = 1; w < AW; w++) mx = fmaxf(mx, wmax[w * HG + t]);
 #pragma unroll
-    for (int h = 0; h < RP; h++) acc[h][0] = acc[h][1] = 0.f;
-    if (rg < tpd) {
-        const KV * vb = Vg + j0 * a.rs + 2 * dp;
-        int j = rg;
-        for (; j + 3 * tpd < rows; j += 4 * tpd) {            // four rows' loads in flight
-            float v[4][2];
-#pragma unroll
-            for (int u = 0; u < 4; u++) load2<KV>(vb + (int64_t) (j + u * tpd) * a.rs, v[u][0], v[u][1]);
-#pragma unroll
-            for (int u = 0; u < 4; u++)
-#pragma unroll
-                for (int h = 0; h < RP; h++) {
-                    const float p = P[h * C + j + u * tpd];
-                    acc[h][0] += p * v[u][0];
-                    acc[h][1] += p * v[u][1];
-                }
-        }
-        for (; j < rows; j += tpd) {
-            float v0, v1;
-            load2<KV>(vb + (int64_t) j * a.rs, v0, v1);
-#pragma unroll
-            for (int h = 0; h < RP; h++) {
-                const float p = P[h * C + j];
-                acc[h][0] += p * v0;
-                acc[h][1] += p * v1;
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < RP; h++) {
-            red[(rg * RP + h) * D + 2 * dp] = acc[h][0];
-            red[(rg * RP + h) * D + 2 * dp + 1] = acc[h][1];
-        }
-    }
-    __syncthreads();
-    // partials of (g, c): m [RP], l [RP], o [RP][D]
-    float * wp = a.ws + ((int64_t) g * a.nch + c) * (RP * (2 + D));
-    for (int i = t; i < RP * D; i += ATT_T) {
-        const int h = i / D, d = i - h * D;
-        float s = 0.f;
-        for (int r = 0; r < tpd; r++) s += red[(r * RP + h) * D + d];
-        wp[2 * RP + i] = s;
-    }
-    if (t < RP) {
-        wp[t] = fmaxf(fmaxf(wmax[t], wmax[RP + t]), fmaxf(wmax[2 * RP + t], wmax[3 * RP + t]));
-        wp[RP + t] = wsum[t] + wsum[RP + t] + wsum[2 * RP + t] + wsum[3 * RP + t];
+        for (int w = 0; w < AW; w++) l += wsum[w * HG + t];
+        wp[t] = mx;
+        wp[HG + t] = l;
     }
 }
 
-// grid Hq, D threads: out[h][d] = sum_c e^(m_c - M) o_c[d] / (sum_c e^(m_c - M) l_c + e^(sink - M))
-template <int RP>
+// grid Hq, 256 threads: out[h][d] = sum_c e^(m_c - M) o_c[d] / (sum_c e^(m_c - M) l_c + e^(sink - M)).
+// Thread (group gi, d pair dp) sums chunks gi, gi + G, ... (G = 256 / (D / 2) groups), then LDS.
+template <int HG>
 __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
-    const int h = blockIdx.x, g = h / a.rep, hi = h - g * a.rep, d = threadIdx.x;
-    const float * wp = a.ws + (int64_t) g * a.nch * (RP * (2 + a.D));
-    const int64_t st = RP * (2 + a.D);
+    __shared__ float sred[256 * 2];
+    __shared__ float sm[4];
+    __shared__ float fw[ATT_MAX_CH];                 // e^(m_c - M) per chunk
+    const int h = blockIdx.x, g = h / a.rep, hr = h - g * a.rep, z = hr / HG, hh = hr - z * HG, t = threadIdx.x;
+    const int64_t st = HG * (2 + a.D);
+    const float * wp = a.ws + ((int64_t) g * a.ngrp + z) * a.nch * st;
     float M = a.sinks ? a.sinks[h] : -__builtin_inff();
-    for (int c = 0; c < a.nch; c++) M = fmaxf(M, wp[c * st + hi]);
-    float den = a.sinks ? expf(a.sinks[h] - M) : 0.f, num = 0.f;
-    for (int c = 0; c < a.nch; c++) {
-        const float mc = wp[c * st + hi];
+    for (int c = t; c < a.nch; c += 256) M = fmaxf(M, wp[c * st + hh]);
+    M = wave_max(M);
+    if ((t & 63) == 0) sm[t >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+    float den = 0.f;
+    for (int c = t; c < a.nch; c += 256) {
+        const float mc = wp[c * st + hh];
         const float f = mc == -__builtin_inff() ? 0.f : expf(mc - M);
-        den += f * wp[c * st + RP + hi];
-        if (d < a.D) num += f * wp[c * st + 2 * RP + hi * a.D + d];
+        fw[c] = f;
+        den += f * wp[c * st + HG + hh];
     }
-    if (d < a.D) a.out[(int64_t) h * a.D + d] = num / den;
+    den = wave_sum(den);
+    __syncthreads();
+    if ((t & 63) == 0) sm[t >> 6] = den;
+    __syncthreads();
+    den = sm[0] + sm[1] + sm[2] + sm[3] + (a.sinks ? expf(a.sinks[h] - M) : 0.f);
+    const int np = a.D / 2, G = 256 / np, dp = t % np, gi = t / np;
+    float n0 = 0.f, n1 = 0.f;
+    if (gi < G) {
+#pragma unroll 4
+        for (int c = gi; c < a.nch; c += G) {
+            const float2 o = *(const float2 *) (wp + c * st + 2 * HG + hh * a.D + 2 * dp);
+            n0 += fw[c] * o.x;
+            n1 += fw[c] * o.y;
+        }
+    }
+    sred[2 * t] = n0;
+    sred[2 * t + 1] = n1;
+    __syncthreads();
+    if (t < np) {
+        float s0 = 0.f, s1 = 0.f;
+        for (int i = 0; i < G; i++) { s0 += sred[2 * (i * np + t)]; s1 += sred[2 * (i * np + t) + 1]; }
+        a.out[(int64_t) h * a.D + 2 * t] = s0 / den;
+        a.out[(int64_t) h * a.D + 2 * t + 1] = s1 / den;
+    }
 }
 
 int next_pow2(int v) {
@@ -229,36 +283,56 @@ int next_pow2(int v) {
     return p;
 }
 
-// rows per chunk: a multiple of 256 up to 1024 with P [RP][C] <= 32 KiB, aiming at >= 512
-// workgroups
-int attn_chunk(int RP, int Hkv, int64_t S) {
-    int C = 256;
-    while (C < 1024 && RP * C * 2 <= 8192 && (S + 2 * C - 1) / (2 * C) * Hkv >= 512) C *= 2;
-    return C;
+struct AttnPlan { int LPR, HG, ngrp, C, nch; };
+
+// chunk rows: enough chunks for ~TARGET_WG workgroups, at least 64 rows each, P within AP_MAX
+AttnPlan attn_plan(int Hq, int D, int Hkv, int64_t S) {
+    AttnPlan p;
+    const int rep = Hq / Hkv;
+    p.LPR = next_pow2(D / 8) < 8 ? 8 : next_pow2(D / 8);
+    p.HG = next_pow2(rep) > 8 ? 8 : next_pow2(rep);
+    p.ngrp = (rep + p.HG - 1) / p.HG;
+    int64_t nch = (TARGET_WG + (int64_t) Hkv * p.ngrp - 1) / ((int64_t) Hkv * p.ngrp);
+    const int64_t nmax = (S + 63) / 64;
+    if (nch > nmax) nch = nmax;
+    if (nch < 1) nch = 1;
+    int64_t C = ((S + nch - 1) / nch + 63) / 64 * 64;
+    if (C > AP_MAX / p.HG) C = AP_MAX / p.HG;
+    p.C = (int) C;
+    p.nch = (int) ((S + C - 1) / C);
+    return p;                                 // nch <= ATT_MAX_CH is checked by the launcher
 }
 
-size_t attn_lds(int RP, int D, int C) {
-    return sizeof(float) * ((size_t) RP * D + (size_t) RP * C + (size_t) (ATT_T / (D / 2)) * RP * D + 8 * RP);
+size_t attn_lds(const AttnPlan & p, int D) {
+    return sizeof(float) * ((size_t) p.HG * p.C + (size_t) AW * p.HG * D + 2 * AW * p.HG + (size_t) p.HG * D);
 }
 
-template <typename KV, int RP>
-hipError_t run_attn(AttnArgs a, hipStream_t s) {
-    const size_t lds = attn_lds(RP, a.D, a.C);
-    k_attn_part<KV, RP><<<dim3((unsigned) a.nch, (unsigned) a.Hkv), ATT_T, lds, s>>>(a);
+template <typename KV, int LPR, int HG>
+hipError_t run_attn(const AttnArgs & a, const AttnPlan & p, hipStream_t s) {
+    k_attn_part<KV, LPR, HG><<<dim3((unsigned) a.nch, (unsigned) a.Hkv, (unsigned) a.ngrp), AT, attn_lds(p, a.D), s>>>(a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_attn_combine<RP><<<dim3((unsigned) a.Hq), 256, 0, s>>>(a);
+    k_attn_combine<HG><<<dim3((unsigned) a.Hq), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 
+template <typename KV, int LPR>
+hipError_t run_attn_hg(const AttnArgs & a, const AttnPlan & p, hipStream_t s) {
+    switch (p.HG) {
+    case 1: return run_attn<KV, LPR, 1>(a, p, s);
+    case 2: return run_attn<KV, LPR, 2>(a, p, s);
+    case 4: return run_attn<KV, LPR, 4>(a, p, s);
+    case 8: return run_attn<KV, LPR, 8>(a, p, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
 template <typename KV>
-hipError_t run_attn_rp(int RP, const AttnArgs & a, hipStream_t s) {
-    switch (RP) {
-    case 1: return run_attn<KV, 1>(a, s);
-    case 2: return run_attn<KV, 2>(a, s);
-    case 4: return run_attn<KV, 4>(a, s);
-    case 8: return run_attn<KV, 8>(a, s);
-    case 16: return run_attn<KV, 16>(a, s);
+hipError_t run_attn_lpr(const AttnArgs & a, const AttnPlan & p, hipStream_t s) {
+    switch (p.LPR) {
+    case 8: return run_attn_hg<KV, 8>(a, p, s);
+    case 16: return run_attn_hg<KV, 16>(a, p, s);
+    case 32: return run_attn_hg<KV, 32>(a, p, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -267,26 +341,23 @@ hipError_t run_attn_rp(int RP, const AttnArgs & a, hipStream_t s) {
 
 int64_t attn_ws_bytes(int Hq, int D, int Hkv, int64_t S) {
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0 || S <= 0) return 0;
-    const int RP = next_pow2(Hq / Hkv);
-    const int C = attn_chunk(RP, Hkv, S);
-    return (int64_t) Hkv * ((S + C - 1) / C) * RP * (2 + D) * (int64_t) sizeof(float);
+    const AttnPlan p = attn_plan(Hq, D, Hkv, S);
+    return (int64_t) Hkv * p.ngrp * p.nch * p.HG * (2 + D) * (int64_t) sizeof(float);
 }
 
 hipError_t launch_attn_step(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv,
                             int64_t S, int64_t hs, int64_t rs, const float * mask, const float * sinks, float scale,
                             float * out, void * ws, int64_t ws_bytes, hipStream_t s) {
     if (Hq <= 0 || Hkv <= 0 || Hq % Hkv || S <= 0 || D <= 0 || D > 256 || D % 8) return hipErrorInvalidValue;
-    const int rep = Hq / Hkv, RP = next_pow2(rep);
-    if (RP > 16) return hipErrorInvalidValue;
+    if (Hq / Hkv > 16) return hipErrorInvalidValue;
     const int64_t al = kv_bf16 ? 8 : 4;             // 16-byte row starts for the vector loads
-    if (rs % al || hs % al || ((uintptr_t) K | (uintptr_t) V) % 16) return hipErrorInvalidValue;
+    if (rs % al || hs % al || ((uintptr_t) K | (uintptr_t) V | (uintptr_t) q) % 16) return hipErrorInvalidValue;
     if (ws_bytes < attn_ws_bytes(Hq, D, Hkv, S)) return hipErrorInvalidValue;
+    const AttnPlan p = attn_plan(Hq, D, Hkv, S);
     AttnArgs a;
     a.q = q; a.K = K; a.V = V; a.mask = mask; a.sinks = sinks; a.ws = (float *) ws; a.out = out;
     a.S = S; a.hs = hs; a.rs = rs; a.scale = scale;
-    a.Hq = Hq; a.D = D; a.Hkv = Hkv; a.rep = rep;
-    a.C = attn_chunk(RP, Hkv, S);
-    a.nch = (int) ((S + a.C - 1) / a.C);
-    if ((int64_t) a.nch * a.C < S || a.nch > 0x7fffffff) return hipErrorInvalidValue;
-    return kv_bf16 ? run_attn_rp<uint16_t>(RP, a, s) : run_attn_rp<float>(RP, a, s);
+    a.Hq = Hq; a.D = D; a.Hkv = Hkv; a.rep = Hq / Hkv; a.ngrp = p.ngrp; a.C = p.C; a.nch = p.nch;
+    if (Hkv > 65535 || p.ngrp > 65535 || p.nch > ATT_MAX_CH) return hipErrorInvalidValue;
+    return kv_bf16 ? run_attn_lpr<uint16_t>(a, p, s) : run_attn_lpr<float>(a, p, s);
 }
