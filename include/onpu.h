@@ -163,6 +163,13 @@ int onpu_transcode_q4k_dev(void * h, int64_t e0, int64_t n, const void * blocks,
  * K is not a multiple of 256 */
 int64_t onpu_pack_q4k(const uint8_t * blocks, int64_t N, int64_t K, uint8_t * out, int threads);
 
+/* ---- int8 GEMV on the GPU: the reference's host onpu_gemv_i8 (onpu_cpu.cpp:276-299, a MoE's
+ * shared expert) with device pointers: y [N] = s[n] * sum_k W[n][k] x[k], W int8 [N][K] (rows of K
+ * bytes), s, x, y fp32; K a multiple of 16 and at most 32768, W and x 16-byte aligned. On `stream`;
+ * capturable. 0 ok, -1 error (onpu_last_error). */
+int onpu_gemv_i8_dev(const int8_t * W, const float * s, int64_t N, int64_t K, const float * x, float * y,
+                     void * stream);
+
 /* ---- decode attention on the GPU: the reference's host onpu_attn_step / onpu_attn_step_bf16
  * (onpu_cpu.cpp:173-229, bound by npu4 at model.py:392-397, 612-615) with device pointers, on
  * `stream`. q fp32 [Hq][D]; K, V: Hkv heads of S rows of D values, fp32 (kv_bf16 = 0) or bf16 (1),

@@ -1027,6 +1027,20 @@ int onpu_quantize_dev(void * h, int64_t e0, int64_t n, const void * W, int64_t l
     });
 }
 
+int onpu_gemv_i8_dev(const int8_t * W, const float * sc, int64_t N, int64_t K, const float * x, float * y,
+                     void * stream) {
+    if (!W || !sc || !x || !y || N < 0 || K < 0) {
+        set_err("onpu_gemv_i8_dev: bad arguments");
+        return -1;
+    }
+    const hipError_t e = launch_gemv_i8(W, sc, N, K, x, y, (hipStream_t) stream);
+    if (e != hipSuccess) {
+        set_err("onpu_gemv_i8_dev (K a multiple of 16 and at most 32768, W and x 16-byte aligned)", e);
+        return -1;
+    }
+    return 0;
+}
+
 int64_t onpu_attn_ws_bytes(int Hq, int D, int Hkv, int64_t S) { return attn_ws_bytes(Hq, D, Hkv, S); }
 
 int onpu_attn_step_dev(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv, int64_t S,

@@ -162,6 +162,71 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float * __restr
     }
 }
 
+// ------------------------------------------------------------------ int8 GEMV
+// y[n] = s[n] * sum_k W[n][k] x[k] for int8 W [N][K] (the reference's host onpu_gemv_i8,
+// onpu_cpu.cpp:276-299, for a MoE's shared expert). A row is read by 16 consecutive lanes, 16 bytes
+// each (a wave instruction covers 4 rows, 1 KiB), GI8_U loads per lane in flight; x sits in LDS
+// (lanes of the 4 rows read the same x: broadcast). The bytes are biased to u = w + 128 by one xor
+// per dword and converted by v_cvt_f32_ubyteN, so each weight costs a convert and an fma:
+// sum u x - 128 sum x = sum w x. The 16 lanes of a row sum by DPP; lane 0 stores.
+constexpr int GI8_T = 256, GI8_U = 4;
+
+template <int CTRL> DEV float dpp_fl(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__global__ __launch_bounds__(GI8_T) void k_gemv_i8(const int8_t * __restrict__ W, const float * __restrict__ s,
+                                                   int64_t N, int64_t K, const float * __restrict__ x,
+                                                   float * __restrict__ y) {
+    extern __shared__ float xs[];
+    __shared__ float wsum[GI8_T / 64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, slot = lane >> 4;
+    float part = 0.f;
+    for (int64_t k = 4 * t; k < K; k += 4 * GI8_T) {
+        const float4 v = *(const float4 *) (x + k);
+        *(float4 *) (xs + k) = v;
+        part += (v.x + v.y) + (v.z + v.w);
+    }
+    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+    if (lane == 0) wsum[wave] = part;
+    __syncthreads();
+    const float xsum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    // rows of this workgroup: 4 waves x 4 row slots per pass, passes strided over the grid
+    for (int64_t r0 = (int64_t) blockIdx.x * 16; r0 < N; r0 += (int64_t) gridDim.x * 16) {
+        const int64_t row = r0 + wave * 4 + slot;
+        const bool live = row < N;
+        const int8_t * wr = W + (live ? row : 0) * K;
+        float acc = 0.f;
+        for (int64_t k0 = 16 * li; k0 < K; k0 += 256 * GI8_U) {
+            uint4 q[GI8_U];
+#pragma unroll
+            for (int u = 0; u < GI8_U; u++) {
+                const int64_t k = k0 + 256 * u;
+                q[u] = k < K ? *(const uint4 *) (wr + k) : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+            }
+#pragma unroll
+            for (int u = 0; u < GI8_U; u++) {
+                const int64_t k = k0 + 256 * u;
+                if (k >= K) break;
+                const uint32_t d[4] = {q[u].x ^ 0x80808080u, q[u].y ^ 0x80808080u, q[u].z ^ 0x80808080u, q[u].w ^ 0x80808080u};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 xv = *(const float4 *) (xs + k + 4 * i);
+                    acc += (float) (d[i] & 0xffu) * xv.x;
+                    acc += (float) ((d[i] >> 8) & 0xffu) * xv.y;
+                    acc += (float) ((d[i] >> 16) & 0xffu) * xv.z;
+                    acc += (float) (d[i] >> 24) * xv.w;
+                }
+            }
+        }
+        acc += dpp_fl<0xB1>(acc);               // quad_perm [1, 0, 3, 2]
+        acc += dpp_fl<0x4E>(acc);               // quad_perm [2, 3, 0, 1]
+        acc += dpp_fl<0x141>(acc);              // row_half_mirror
+        acc += dpp_fl<0x140>(acc);              // row_mirror
+        if (li == 0 && live) y[row] = (acc - 128.0f * xsum) * s[row];
+    }
+}
+
 // ------------------------------------------------------------------ small helpers
 __global__ void k_f32_to_bf16(const float * __restrict__ in, int64_t n, uint16_t * __restrict__ out) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -403,6 +468,17 @@ hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32
                           float alpha, float limit, float * o, hipStream_t s) {
     const int64_t n = rows * (Ng / 2);
     k_moe_act<<<dim3((unsigned) ((n + 255) / 256)), 256, 0, s>>>(h, rows, Ng, ids, bias, act, alpha, limit, o);
+    CHECK_LAUNCH();
+    return hipSuccess;
+}
+
+hipError_t launch_gemv_i8(const int8_t * W, const float * sc, int64_t N, int64_t K, const float * x, float * y,
+                          hipStream_t s) {
+    if (N <= 0 || K <= 0) return hipSuccess;
+    if (K % 16 || K * 4 > 128 * 1024 || ((uintptr_t) W | (uintptr_t) x) % 16) return hipErrorInvalidValue;
+    const int64_t groups = (N + 15) / 16;
+    const unsigned grid = (unsigned) (groups < 4096 ? groups : 4096);
+    k_gemv_i8<<<grid, GI8_T, (size_t) K * 4, s>>>(W, sc, N, K, x, y);
     CHECK_LAUNCH();
     return hipSuccess;
 }

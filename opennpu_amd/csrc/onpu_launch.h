@@ -156,6 +156,9 @@ hipError_t launch_quant_stage(int fmt, const void * W, int64_t ldw, int wbf16, i
                               uint8_t * out, int64_t ostride, hipStream_t s);
 hipError_t launch_q4k_stage(const uint8_t * blocks, int64_t ld, int64_t bstride, int64_t N, int64_t K, int64_t ne,
                             uint8_t * out, int64_t ostride, hipStream_t s);
+// int8 GEMV y = s * (W x) for int8 W [N][K] rows (K a multiple of 16, K * 4 bytes of x in LDS)
+hipError_t launch_gemv_i8(const int8_t * W, const float * sc, int64_t N, int64_t K, const float * x, float * y,
+                          hipStream_t s);
 // decode attention (onpu_attn.hip): workspace bytes for (Hq, D, Hkv, S), and the two launches
 int64_t attn_ws_bytes(int Hq, int D, int Hkv, int64_t S);
 hipError_t launch_attn_step(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv,

@@ -509,3 +509,14 @@ void orc_attn_step(const float * q, int Hq, int D, const void * K, const void * 
     }
     free(p);
 }
+
+/* ---------------------------------------------------------------- int8 GEMV
+ * onpu_gemv_i8 (onpu_cpu.cpp:276-299): y[n] = s[n] * sum_k W[n][k] x[k], W int8; the sum in fp64
+ * here (the reference sums in fp32 lanes; the tests carry a tolerance). */
+void orc_gemv_i8(const int8_t * W, const float * s, int64_t N, int64_t K, const float * x, double * y) {
+    for (int64_t n = 0; n < N; n++) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; k++) acc += (double) W[n * K + k] * (double) x[k];
+        y[n] = acc * (double) s[n];
+    }
+}

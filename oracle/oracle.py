@@ -57,6 +57,7 @@ def lib():
         L.orc_quant_q4_0.argtypes = [P, P, P]
         L.orc_transcode_q4k.argtypes = [P, I64, I64, I64, P, P, P]
         L.orc_quantize.argtypes = [I32, P, I64, I64, P]
+        L.orc_gemv_i8.argtypes = [P, P, I64, I64, P, P]
         L.orc_attn_step.argtypes = [P, I32, I32, P, P, I32, I32, I64, I64, I64, P, P, C.c_float, P]
         _lib = L
     return _lib
@@ -309,6 +310,16 @@ def stage_q4nx(q, s, m):
     codes = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
     return np.concatenate([codes.ravel(), np.asarray(s, np.uint16).ravel().view(np.uint8),
                            np.asarray(m, np.uint16).ravel().view(np.uint8)])
+
+
+def gemv_i8(W, s, x):
+    """y[n] = s[n] * sum_k W[n][k] x[k] (onpu_cpu.cpp:276-299), fp64."""
+    W = np.ascontiguousarray(W, np.int8)
+    N, K = W.shape
+    y = np.empty(N, np.float64)
+    lib().orc_gemv_i8(_p(W), _p(np.ascontiguousarray(s, np.float32)), N, K, _p(np.ascontiguousarray(x, np.float32)),
+                      _p(y))
+    return y
 
 
 def attn_step(q, K, V, mask=None, sinks=None, scale=None):

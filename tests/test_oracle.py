@@ -489,3 +489,12 @@ def test_attn_step_against_torch_float64(kv):
         p = torch.softmax(s, -1)[..., :S]
         ref = torch.einsum("grs,gsd->grd", p, torch.from_numpy(Vf).double()).reshape(Hq, D).numpy()
         assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_gemv_i8_against_numpy():
+    rng = np.random.default_rng(95)
+    W = rng.integers(-128, 128, (37, 300)).astype(np.int8)
+    s = rng.uniform(1e-3, 2e-2, 37).astype(np.float32)
+    x = rng.standard_normal(300).astype(np.float32)
+    want = (W.astype(np.float64) @ x.astype(np.float64)) * s.astype(np.float64)
+    assert np.allclose(orc.gemv_i8(W, s, x), want, rtol=1e-12, atol=1e-12)
