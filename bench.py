@@ -11,8 +11,9 @@ bytes per step (int4 codes + bf16 scales + x + y) / time, in GB/s.
 Also measured in the same run (the "configs" object): M=4 and M=8 decode steps, a single
 4096x4096 GEMV rotated over 64 copies, the Llama-3.1-8B prefill FFN GEMMs (M=2048, TFLOPS), the
 Qwen3-30B-A3B MoE layer (decode M=1 and prefill M=512, router included), and the 151936x4096
-Q4_0 LM head with argmax (M=1, 5), and the load-time weight codecs on one layer (GPU quantization
-into each format and the GGUF Q4_K transcode, beside the host quantizer). The roofline object is the dominant kernel: the gate+up GEMV,
+Q4_0 LM head with argmax (M=1, 5), the load-time weight codecs on one layer (GPU quantization
+into each format and the GGUF Q4_K transcode, beside the host quantizer), and the per-token steps
+the reference runs on the host (decode attention, the int8 shared-expert GEMV). The roofline object is the dominant kernel: the gate+up GEMV,
 timed with HIP events over a graph of back-to-back launches on its stream. The cpu_baseline leg
 times the reference's own CPU pattern (dequantize to fp32, then x @ W^T in torch fp32,
 opennpu/native/reference.py:24-28,55) on one layer of the same workload.
@@ -342,6 +343,51 @@ def codecs(torch, QMatrix):
     return out
 
 
+def decode_glue(torch):
+    """The per-token steps the reference runs on the host beside the int4 matmuls, on the GPU:
+    decode attention at Qwen3-8B heads (Hq 32, Hkv 8, D 128, bf16 KV) for 4K and 32K positions, and
+    the int8 shared-expert GEMV (11264 x 2048 gate+up, 2048 x 5632 down); inputs rotated over
+    copies that together exceed the 256 MB Infinity Cache. GB/s = bytes read once (K and V; W)."""
+    import ctypes as C
+    from opennpu_amd import _lib
+    from opennpu_amd.device import attn_step
+    L = _lib.lib()
+    out = {}
+    Hq, Hkv, D = 32, 8, 128
+    for S in (4096, 32768):
+        nbytes = 2 * Hkv * S * D * 2
+        nc = max(2, int(np.ceil(600e6 / nbytes)))
+        caches = [(torch.randn((Hkv, S, D), device="cuda").bfloat16(), torch.randn((Hkv, S, D), device="cuda").bfloat16())
+                  for _ in range(nc)]
+        q = torch.randn((Hq, D), device="cuda")
+        ws = torch.empty((L.onpu_attn_ws_bytes(Hq, D, Hkv, S),), dtype=torch.uint8, device="cuda")
+        o = torch.empty((Hq, D), device="cuda")
+
+        def step(caches=caches, q=q, ws=ws, o=o):
+            for K, V in caches:
+                attn_step(q, K, V, out=o, ws=ws)
+        g = GraphStep(step, torch)
+        t = time_med(torch, g, 10, 3) / nc
+        out[f"attention_S{S}"] = {"us_per_call": t * 1e6, "GBps": nbytes / t / 1e9, "hbm_frac": nbytes / t / HBM_PEAK}
+        del caches
+    for name, N, K in (("gemv_i8_gate_up_11264x2048", 11264, 2048), ("gemv_i8_down_2048x5632", 2048, 5632)):
+        nc = max(2, int(np.ceil(600e6 / (N * K))))
+        Ws = [torch.randint(-128, 128, (N, K), device="cuda", dtype=torch.int8) for _ in range(nc)]
+        sc = torch.rand(N, device="cuda") * 0.01
+        x = torch.randn(K, device="cuda")
+        y = torch.empty(N, device="cuda")
+        P = lambda t: C.c_void_p(t.data_ptr())
+
+        def step(Ws=Ws, sc=sc, x=x, y=y, N=N, K=K):
+            for W in Ws:
+                L.onpu_gemv_i8_dev(P(W), P(sc), N, K, P(x), P(y), C.c_void_p(torch.cuda.current_stream().cuda_stream))
+        g = GraphStep(step, torch)
+        t = time_med(torch, g, 10, 3) / nc
+        out[name] = {"us_per_call": t * 1e6, "GBps": N * K / t / 1e9, "hbm_frac": N * K / t / HBM_PEAK}
+        del Ws
+    return out
+
+
 def cpu_baseline(syn, seconds=12.0):
     """The reference's CPU pattern on one Qwen3-8B layer at M=1: dequantize W to fp32 (timed once),
     then x @ W^T in torch fp32 (timed, repeated for about `seconds`)."""
@@ -466,6 +512,8 @@ def main():
         configs["lm_head_q4_0"] = lm_head(torch, QMatrix, syn, 30)
         log("weight codecs ...")
         configs["weight_codecs_qwen3_8b_layer"] = codecs(torch, QMatrix)
+        log("decode attention, int8 GEMV ...")
+        configs["decode_glue"] = decode_glue(torch)
     gu = head["per_matrix"]["gate_up"]
     roof = {"kernel": "k_qgemv<g128s> gate+up 24576x4096, M=1 (768 workgroups x 8 waves, x in LDS)",
             "bound": "hbm", "achieved": gu["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",

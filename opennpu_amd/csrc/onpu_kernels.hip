@@ -164,66 +164,91 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float * __restr
 
 // ------------------------------------------------------------------ int8 GEMV
 // y[n] = s[n] * sum_k W[n][k] x[k] for int8 W [N][K] (the reference's host onpu_gemv_i8,
-// onpu_cpu.cpp:276-299, for a MoE's shared expert). A row is read by 16 consecutive lanes, 16 bytes
-// each (a wave instruction covers 4 rows, 1 KiB), GI8_U loads per lane in flight; x sits in LDS
-// (lanes of the 4 rows read the same x: broadcast). The bytes are biased to u = w + 128 by one xor
-// per dword and converted by v_cvt_f32_ubyteN, so each weight costs a convert and an fma:
-// sum u x - 128 sum x = sum w x. The 16 lanes of a row sum by DPP; lane 0 stores.
-constexpr int GI8_T = 256, GI8_U = 4;
+// onpu_cpu.cpp:276-299, for a MoE's shared expert). Rows go in groups of 4; a group's K range is
+// split into ks slices (4 below 8192 groups, then 2, then 1), one wave per (group,
+// slice), 4 / ks groups per workgroup. In a wave a row is read by 16 consecutive lanes, 16 bytes
+// each (a wave instruction covers the 4 rows, 1 KiB), GI8_U loads per lane in flight per batch.
+// x sits in LDS (copied once per workgroup with its sum); the four rows' lanes read the same x (a
+// broadcast). The bytes are biased to u = w + 128 by one xor per dword and converted by
+// v_cvt_f32_ubyteN, so a weight costs a convert and an fma, and 128 sum(x) is subtracted once.
+// The 16 lanes of a row sum by DPP, the slices in LDS.
+constexpr int GI8_T = 256, GI8_U = 8;
 
 template <int CTRL> DEV float dpp_fl(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
 __global__ __launch_bounds__(GI8_T) void k_gemv_i8(const int8_t * __restrict__ W, const float * __restrict__ s,
-                                                   int64_t N, int64_t K, const float * __restrict__ x,
-                                                   float * __restrict__ y) {
+                                                   int64_t N, int64_t K, int ks, int64_t Kw,
+                                                   const float * __restrict__ x, float * __restrict__ y) {
     extern __shared__ float xs[];
-    __shared__ float wsum[GI8_T / 64];
+    __shared__ float wsx[GI8_T / 64];
+    __shared__ float red[GI8_T / 64][4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, slot = lane >> 4;
+    // x to LDS: all of a thread's loads of a batch issued before the stores (8 x 1024 floats per batch)
     float part = 0.f;
-    for (int64_t k = 4 * t; k < K; k += 4 * GI8_T) {
-        const float4 v = *(const float4 *) (x + k);
-        *(float4 *) (xs + k) = v;
-        part += (v.x + v.y) + (v.z + v.w);
+    for (int64_t k0 = 4 * t; k0 < K; k0 += 8 * 4 * GI8_T) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int64_t k = k0 + (int64_t) i * 4 * GI8_T;
+            v[i] = k < K ? *(const float4 *) (x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int64_t k = k0 + (int64_t) i * 4 * GI8_T;
+            if (k < K) *(float4 *) (xs + k) = v[i];
+            part += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
     }
     for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
-    if (lane == 0) wsum[wave] = part;
+    if (lane == 0) wsx[wave] = part;
     __syncthreads();
-    const float xsum = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-    // rows of this workgroup: 4 waves x 4 row slots per pass, passes strided over the grid
-    for (int64_t r0 = (int64_t) blockIdx.x * 16; r0 < N; r0 += (int64_t) gridDim.x * 16) {
-        const int64_t row = r0 + wave * 4 + slot;
-        const bool live = row < N;
-        const int8_t * wr = W + (live ? row : 0) * K;
-        float acc = 0.f;
-        for (int64_t k0 = 16 * li; k0 < K; k0 += 256 * GI8_U) {
-            uint4 q[GI8_U];
+    const float xsum = (wsx[0] + wsx[1]) + (wsx[2] + wsx[3]);
+    const int gpw = 4 / ks;
+    const int64_t grp = (int64_t) blockIdx.x * gpw + wave / ks, row = grp * 4 + slot;
+    const int64_t k0 = (wave % ks) * Kw, k1 = k0 + Kw < K ? k0 + Kw : K;
+    const int8_t * wr = W + (row < N ? row : 0) * K;
+    float acc = 0.f;
+    for (int64_t kb = k0 + 16 * li; kb < k1; kb += 256 * GI8_U) {
+        uint4 q[GI8_U];
 #pragma unroll
-            for (int u = 0; u < GI8_U; u++) {
-                const int64_t k = k0 + 256 * u;
-                q[u] = k < K ? *(const uint4 *) (wr + k) : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-            }
+        for (int u = 0; u < GI8_U; u++) {
+            const int64_t k = kb + 256 * u;
+            q[u] = k < k1 ? *(const uint4 *) (wr + k) : make_uint4(0u, 0u, 0u, 0u);
+        }
 #pragma unroll
-            for (int u = 0; u < GI8_U; u++) {
-                const int64_t k = k0 + 256 * u;
-                if (k >= K) break;
-                const uint32_t d[4] = {q[u].x ^ 0x80808080u, q[u].y ^ 0x80808080u, q[u].z ^ 0x80808080u, q[u].w ^ 0x80808080u};
+        for (int u = 0; u < GI8_U; u++) {
+            const int64_t k = kb + 256 * u;
+            if (k >= k1) break;
+            const uint32_t d[4] = {q[u].x ^ 0x80808080u, q[u].y ^ 0x80808080u, q[u].z ^ 0x80808080u,
+                                   q[u].w ^ 0x80808080u};
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float4 xv = *(const float4 *) (xs + k + 4 * i);
-                    acc += (float) (d[i] & 0xffu) * xv.x;
-                    acc += (float) ((d[i] >> 8) & 0xffu) * xv.y;
-                    acc += (float) ((d[i] >> 16) & 0xffu) * xv.z;
-                    acc += (float) (d[i] >> 24) * xv.w;
-                }
+            for (int i = 0; i < 4; i++) {
+                const float4 xv = *(const float4 *) (xs + k + 4 * i);
+                acc += (float) (d[i] & 0xffu) * xv.x;
+                acc += (float) ((d[i] >> 8) & 0xffu) * xv.y;
+                acc += (float) ((d[i] >> 16) & 0xffu) * xv.z;
+                acc += (float) (d[i] >> 24) * xv.w;
             }
         }
-        acc += dpp_fl<0xB1>(acc);               // quad_perm [1, 0, 3, 2]
-        acc += dpp_fl<0x4E>(acc);               // quad_perm [2, 3, 0, 1]
-        acc += dpp_fl<0x141>(acc);              // row_half_mirror
-        acc += dpp_fl<0x140>(acc);              // row_mirror
-        if (li == 0 && live) y[row] = (acc - 128.0f * xsum) * s[row];
+    }
+    acc += dpp_fl<0xB1>(acc);               // quad_perm [1, 0, 3, 2]
+    acc += dpp_fl<0x4E>(acc);               // quad_perm [2, 3, 0, 1]
+    acc += dpp_fl<0x141>(acc);              // row_half_mirror
+    acc += dpp_fl<0x140>(acc);              // row_mirror
+    if (ks == 1) {
+        if (li == 0 && row < N) y[row] = (acc - 128.0f * xsum) * s[row];
+        return;
+    }
+    if (li == 0) red[wave][slot] = acc;
+    __syncthreads();
+    if (t < 4 * gpw) {
+        const int gl = t / 4;
+        const int64_t r = ((int64_t) blockIdx.x * gpw + gl) * 4 + (t & 3);
+        float sum = 0.f;
+        for (int sl = 0; sl < ks; sl++) sum += red[gl * ks + sl][t & 3];
+        if (r < N) y[r] = (sum - 128.0f * xsum) * s[r];
     }
 }
 
@@ -476,9 +501,12 @@ hipError_t launch_gemv_i8(const int8_t * W, const float * sc, int64_t N, int64_t
                           hipStream_t s) {
     if (N <= 0 || K <= 0) return hipSuccess;
     if (K % 16 || K * 4 > 128 * 1024 || ((uintptr_t) W | (uintptr_t) x) % 16) return hipErrorInvalidValue;
-    const int64_t groups = (N + 15) / 16;
-    const unsigned grid = (unsigned) (groups < 4096 ? groups : 4096);
-    k_gemv_i8<<<grid, GI8_T, (size_t) K * 4, s>>>(W, sc, N, K, x, y);
+    const int64_t ng = (N + 3) / 4;
+    const int ks = ng >= 16384 ? 1 : (ng >= 8192 ? 2 : 4);           // measured: more, shorter waves win
+    const int64_t Kw = (K + (int64_t) ks * 256 - 1) / ((int64_t) ks * 256) * 256;
+    const int64_t grid = (ng + 4 / ks - 1) / (4 / ks);
+    if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
+    k_gemv_i8<<<(unsigned) grid, GI8_T, (size_t) K * 4, s>>>(W, sc, N, K, ks, Kw, x, y);
     CHECK_LAUNCH();
     return hipSuccess;
 }
