@@ -180,9 +180,10 @@ struct Plan {
 
 // Workgroup = tw tile groups x kw K parts; each wave streams bpw K blocks of its tile group (rt row
 // tiles) through a two-chunk pipeline of nb blocks. The plan aims at ~4096 waves with an equal
-// contiguous share of 4..8 blocks (4..8 KiB of nibbles) each (up to 16 when there are 4096 or
-// more tile groups, as for a vocabulary-sized LM head), at most 2 tile groups per workgroup (4
-// with several x rows, whose LDS staging then serves more tiles) with at least 512 workgroups,
+// contiguous share of 4..8 blocks (4..8 KiB of nibbles) each (up to 32, a whole row tile, when
+// there are 4096 or more tile groups, as for a vocabulary-sized LM head), at most 2 tile groups per
+// workgroup (4 with several x rows, whose LDS staging then serves more tiles; 8 for the vocabulary-
+// sized case, where the x copy per workgroup is the cost to share) with at least 512 workgroups,
 // and x staged in LDS (xl) when M rows of K and their column sums fit in 52 KiB (112 KiB with
 // 1024 or more tile groups).
 // ACT pairs gate tile t with up tile t + NT/2, so tw divides NT/2 there. (Sweeps of kw, tw and nb
@@ -199,8 +200,11 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
     const int64_t groups = epi == EPI_ACT_ ? NT / 2 : NT;
-    const int64_t per = std::min<int64_t>(groups * slots >= 4096 ? 16 : 8,
-                                          std::max<int64_t>(4, (groups * slots * KB + 4095) / 4096));
+    // vocabulary-sized matrices (>= 4096 tile groups) stream whole rows per wave (up to 32 blocks)
+    // in workgroups of up to 8 tile groups sharing one x copy: measured on the 151936 x 4096 LM head,
+    // M = 5: 65.7 us against 75.0 us with two K parts per tile and 4 tiles (M = 1: equal)
+    const bool vocab = groups * slots >= 4096;
+    const int64_t per = std::min<int64_t>(vocab ? 32 : 8, std::max<int64_t>(4, (groups * slots * KB + 4095) / 4096));
     int64_t kw = std::min<int64_t>(16, std::max<int64_t>(1, (KB + per - 1) / per));
     const int ekw = env_int("ONPU_GEMV_KW", 0);
     if (ekw > 0) kw = std::min<int64_t>(ekw, KB);
@@ -226,7 +230,7 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
         p.bpw = (KB + p.kw - 1) / p.kw;
         p.kw = (int) ((KB + p.bpw - 1) / p.bpw);
     }
-    int tw = std::max(1, std::min(M > 1 ? 4 : 2, maxw / p.kw));
+    int tw = std::max(1, std::min(vocab ? 8 : (M > 1 ? 4 : 2), maxw / p.kw));
     while (tw > 1 && (tw * p.kw * p.rt * p.mb > red_kib || (groups + tw - 1) / tw * slots < 512 ||
                       (epi == EPI_ACT_ && groups % tw != 0)))
         tw--;
