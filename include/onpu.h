@@ -170,6 +170,18 @@ int64_t onpu_pack_q4k(const uint8_t * blocks, int64_t N, int64_t K, uint8_t * ou
 int onpu_gemv_i8_dev(const int8_t * W, const float * s, int64_t N, int64_t K, const float * x, float * y,
                      void * stream);
 
+/* ---- Gated DeltaNet decode step on the GPU: the reference's host onpu_gdn_step (onpu_cpu.cpp:107-
+ * 171, bound by npu4 at model.py:386-391, 646-649) with device pointers and the same arguments:
+ * x [H], qkv [C = 2 Hk Dk + Hv Dv], z [Hv Dv], Wb / Wa [Hv][H], conv_w [C][Kc], conv_state [C][L]
+ * (updated), A_log / dt_bias [Hv], norm_w [Dv], S [Hv][Dk][Dv] (updated), out [Hv Dv]; plus a
+ * device workspace of onpu_gdn_ws_bytes(Hk, Hv, Dk, Dv) bytes. Hv a multiple of Hk, Dv dividing
+ * 256, Dk * Dv <= 32768. On `stream`; capturable. 0 ok, -1 error (onpu_last_error). */
+int64_t onpu_gdn_ws_bytes(int Hk, int Hv, int Dk, int Dv);
+int onpu_gdn_step_dev(const float * x, int H, const float * qkv, const float * z, const float * Wb, const float * Wa,
+                      const float * conv_w, int Kc, float * conv_state, int L, const float * A_log,
+                      const float * dt_bias, const float * norm_w, float eps, float * S, int Hk, int Hv, int Dk,
+                      int Dv, float * out, void * ws, int64_t ws_bytes, void * stream);
+
 /* ---- decode attention on the GPU: the reference's host onpu_attn_step / onpu_attn_step_bf16
  * (onpu_cpu.cpp:173-229, bound by npu4 at model.py:392-397, 612-615) with device pointers, on
  * `stream`. q fp32 [Hq][D]; K, V: Hkv heads of S rows of D values, fp32 (kv_bf16 = 0) or bf16 (1),

@@ -81,6 +81,9 @@ def _declare(lib):
         "onpu_transcode_q4k_dev": (I32, [P, I64, I64, P, I64, P]),
         "onpu_pack_q4k": (I64, [U8P, I64, I64, U8P, I32]),
         "onpu_gemv_i8_dev": (I32, [P, P, I64, I64, P, P, P]),
+        "onpu_gdn_ws_bytes": (I64, [I32, I32, I32, I32]),
+        "onpu_gdn_step_dev": (I32, [P, I32, P, P, P, P, P, I32, P, I32, P, P, P, C.c_float, P, I32, I32, I32, I32, P,
+                                    P, I64, P]),
         "onpu_attn_ws_bytes": (I64, [I32, I32, I32, I64]),
         "onpu_attn_step_dev": (I32, [P, I32, I32, P, P, I32, I32, I64, I64, I64, P, P, C.c_float, P, P, I64, P]),
         "onpu_chain_new": (P, [C.POINTER(P), C.POINTER(P), C.POINTER(P), I32, I64, I32]),

@@ -1045,6 +1045,27 @@ int onpu_gemv_i8_dev(const int8_t * W, const float * sc, int64_t N, int64_t K, c
     return 0;
 }
 
+int64_t onpu_gdn_ws_bytes(int Hk, int Hv, int Dk, int Dv) { return gdn_ws_bytes(Hk, Hv, Dk, Dv); }
+
+int onpu_gdn_step_dev(const float * x, int H, const float * qkv, const float * z, const float * Wb, const float * Wa,
+                      const float * conv_w, int Kc, float * conv_state, int L, const float * A_log,
+                      const float * dt_bias, const float * norm_w, float eps, float * S, int Hk, int Hv, int Dk,
+                      int Dv, float * out, void * ws, int64_t ws_bytes, void * stream) {
+    if (!x || !qkv || !z || !Wb || !Wa || !conv_w || !conv_state || !A_log || !dt_bias || !norm_w || !S || !out ||
+        !ws) {
+        set_err("onpu_gdn_step_dev: bad arguments");
+        return -1;
+    }
+    const hipError_t e = launch_gdn_step(x, H, qkv, z, Wb, Wa, conv_w, Kc, conv_state, L, A_log, dt_bias, norm_w, eps,
+                                         S, Hk, Hv, Dk, Dv, out, ws, ws_bytes, (hipStream_t) stream);
+    if (e != hipSuccess) {
+        set_err("onpu_gdn_step_dev (Hv a multiple of Hk, Dv dividing 256, Dk * Dv <= 32768, L >= Kc - 1, "
+                "workspace of onpu_gdn_ws_bytes)", e);
+        return -1;
+    }
+    return 0;
+}
+
 int64_t onpu_attn_ws_bytes(int Hq, int D, int Hkv, int64_t S) { return attn_ws_bytes(Hq, D, Hkv, S); }
 
 int onpu_attn_step_dev(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv, int64_t S,

@@ -361,3 +361,140 @@ hipError_t launch_attn_step(const float * q, int Hq, int D, const void * K, cons
     if (Hkv > 65535 || p.ngrp > 65535 || p.nch > ATT_MAX_CH) return hipErrorInvalidValue;
     return kv_bf16 ? run_attn_lpr<uint16_t>(a, p, s) : run_attn_lpr<float>(a, p, s);
 }
+
+// ------------------------------------------------------------------ Gated DeltaNet decode step
+// One decode token of a Gated DeltaNet layer: the reference's host onpu_gdn_step (onpu_cpu.cpp:107-
+// 171). k_gdn_conv: one thread per channel c of qkv: causal conv over the last Kc inputs (the same
+// order of products as the reference), SiLU into co, and the conv state shifts by one. k_gdn_head:
+// one workgroup per value head h: q, k of its key head L2-normalised (q also / sqrt Dk), beta =
+// sigmoid(Wb x), decay = exp(-exp(A_log) softplus(Wa x + dt_bias)); the head's state S [Dk][Dv]
+// goes to LDS scaled by decay while thread (d-column j, row group g) sums kv_j = sum_i S_ij k_i;
+// delta = beta (v - kv); S += k delta^T and o = S^T q in a second pass over LDS, S written back;
+// out = norm_w * o / sqrt(mean(o^2) + eps) * silu(z). Sums are block reductions (another order than
+// the reference's sequential loops).
+namespace {
+
+__device__ __forceinline__ float gdn_silu(float v) { return v / (1.f + expf(-v)); }
+
+__global__ __launch_bounds__(256) void k_gdn_conv(const float * __restrict__ qkv, const float * __restrict__ conv_w,
+                                                  int Kc, float * __restrict__ conv_state, int L, int C,
+                                                  float * __restrict__ co) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= C) return;
+    float * st = conv_state + (int64_t) c * L;
+    const float * w = conv_w + (int64_t) c * Kc;
+    float s = w[Kc - 1] * qkv[c];
+    for (int j = 0; j < Kc - 1; j++) s += w[j] * st[L - (Kc - 1) + j];
+    co[c] = gdn_silu(s);
+    for (int j = 0; j + 1 < L; j++) st[j] = st[j + 1];
+    st[L - 1] = qkv[c];
+}
+
+// block sum over 256 threads (every thread gets the sum); red: 8 floats of LDS
+__device__ __forceinline__ float gdn_block_sum(float v, float * red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+struct GdnArgs {
+    const float * x, * z, * Wb, * Wa, * A_log, * dt_bias, * norm_w, * co;
+    float * S, * out;
+    float eps;
+    int H, Hk, Hv, Dk, Dv;
+};
+
+// LDS: Sl [Dk][Dv], vec [4][max(Dk, Dv)] (q, k, delta / o), part [256 / Dv][Dv], red [8]
+__global__ __launch_bounds__(256) void k_gdn_head(GdnArgs a) {
+    extern __shared__ float lds[];
+    const int h = blockIdx.x, t = threadIdx.x, Dk = a.Dk, Dv = a.Dv, rep = a.Hv / a.Hk, kh = h / rep;
+    const int key_dim = a.Hk * Dk, mx = Dk > Dv ? Dk : Dv, G = 256 / Dv, j = t % Dv, g = t / Dv;
+    float * Sl = lds, * qv = Sl + Dk * Dv, * kvec = qv + mx, * dv = kvec + mx, * ov = dv + mx;
+    float * part = ov + mx, * red = part + G * Dv;
+    float qq = 0.f, kk = 0.f;
+    for (int i = t; i < Dk; i += 256) {
+        const float qi = a.co[kh * Dk + i], ki = a.co[key_dim + kh * Dk + i];
+        qv[i] = qi;
+        kvec[i] = ki;
+        qq += qi * qi;
+        kk += ki * ki;
+    }
+    float pb = 0.f, pa = 0.f;
+    for (int i = t; i < a.H; i += 256) {
+        pb += a.Wb[(int64_t) h * a.H + i] * a.x[i];
+        pa += a.Wa[(int64_t) h * a.H + i] * a.x[i];
+    }
+    qq = gdn_block_sum(qq, red);
+    kk = gdn_block_sum(kk, red);
+    const float b = gdn_block_sum(pb, red), av = gdn_block_sum(pa, red);
+    const float qn = 1.f / sqrtf(qq + 1e-6f) / sqrtf((float) Dk), kn = 1.f / sqrtf(kk + 1e-6f);
+    const float beta = 1.f / (1.f + expf(-b));
+    const float ad = av + a.dt_bias[h];
+    const float sp = ad > 20.f ? ad : log1pf(expf(ad));
+    const float decay = expf(-expf(a.A_log[h]) * sp);
+    // pass 1: S <- decay S into LDS, kv_j = sum_i S_ij k_i (row groups g, g + G, ...)
+    float * Sh = a.S + (int64_t) h * Dk * Dv;
+    float kv = 0.f;
+    if (g < G)
+        for (int i = g; i < Dk; i += G) {
+            const float r = Sh[(int64_t) i * Dv + j] * decay;
+            Sl[i * Dv + j] = r;
+            kv += r * (kvec[i] * kn);
+        }
+    if (g < G) part[g * Dv + j] = kv;
+    __syncthreads();
+    if (t < Dv) {
+        float s = 0.f;
+        for (int r = 0; r < G; r++) s += part[r * Dv + t];
+        dv[t] = (a.co[2 * key_dim + (int64_t) h * Dv + t] - s) * beta;
+    }
+    __syncthreads();
+    // pass 2: S += k delta^T, o_j = sum_i S_ij q_i; S back to HBM
+    float o = 0.f;
+    if (g < G)
+        for (int i = g; i < Dk; i += G) {
+            const float r = Sl[i * Dv + j] + (kvec[i] * kn) * dv[j];
+            Sh[(int64_t) i * Dv + j] = r;
+            o += r * (qv[i] * qn);
+        }
+    if (g < G) part[g * Dv + j] = o;
+    __syncthreads();
+    float oj = 0.f;
+    if (t < Dv) {
+        for (int r = 0; r < G; r++) oj += part[r * Dv + t];
+        ov[t] = oj;
+    }
+    const float ms = gdn_block_sum(t < Dv ? oj * oj : 0.f, red) / Dv;
+    const float rn = 1.f / sqrtf(ms + a.eps);
+    if (t < Dv) a.out[(int64_t) h * Dv + t] = a.norm_w[t] * (oj * rn) * gdn_silu(a.z[(int64_t) h * Dv + t]);
+}
+
+}  // namespace
+
+int64_t gdn_ws_bytes(int Hk, int Hv, int Dk, int Dv) {
+    return (int64_t) (2 * Hk * Dk + Hv * Dv) * (int64_t) sizeof(float);
+}
+
+hipError_t launch_gdn_step(const float * x, int H, const float * qkv, const float * z, const float * Wb,
+                           const float * Wa, const float * conv_w, int Kc, float * conv_state, int L,
+                           const float * A_log, const float * dt_bias, const float * norm_w, float eps, float * S,
+                           int Hk, int Hv, int Dk, int Dv, float * out, void * ws, int64_t ws_bytes, hipStream_t s) {
+    if (H <= 0 || Hk <= 0 || Hv <= 0 || Hv % Hk || Dk <= 0 || Dv <= 0 || 256 % Dv || Dv < 4 || Kc < 1 ||
+        L < Kc - 1 || L < 1 || (int64_t) Dk * Dv > 32768)
+        return hipErrorInvalidValue;
+    if (ws_bytes < gdn_ws_bytes(Hk, Hv, Dk, Dv)) return hipErrorInvalidValue;
+    const int C = 2 * Hk * Dk + Hv * Dv;
+    float * co = (float *) ws;
+    k_gdn_conv<<<(C + 255) / 256, 256, 0, s>>>(qkv, conv_w, Kc, conv_state, L, C, co);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GdnArgs a;
+    a.x = x; a.z = z; a.Wb = Wb; a.Wa = Wa; a.A_log = A_log; a.dt_bias = dt_bias; a.norm_w = norm_w; a.co = co;
+    a.S = S; a.out = out; a.eps = eps; a.H = H; a.Hk = Hk; a.Hv = Hv; a.Dk = Dk; a.Dv = Dv;
+    const int mx = Dk > Dv ? Dk : Dv;
+    const size_t lds = sizeof(float) * ((size_t) Dk * Dv + 4 * (size_t) mx + (size_t) (256 / Dv) * Dv + 8);
+    k_gdn_head<<<Hv, 256, lds, s>>>(a);
+    return hipGetLastError();
+}

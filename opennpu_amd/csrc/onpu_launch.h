@@ -159,6 +159,12 @@ hipError_t launch_q4k_stage(const uint8_t * blocks, int64_t ld, int64_t bstride,
 // int8 GEMV y = s * (W x) for int8 W [N][K] rows (K a multiple of 16, K * 4 bytes of x in LDS)
 hipError_t launch_gemv_i8(const int8_t * W, const float * sc, int64_t N, int64_t K, const float * x, float * y,
                           hipStream_t s);
+// Gated DeltaNet decode step (onpu_attn.hip): workspace of the conv outputs, and the two launches
+int64_t gdn_ws_bytes(int Hk, int Hv, int Dk, int Dv);
+hipError_t launch_gdn_step(const float * x, int H, const float * qkv, const float * z, const float * Wb,
+                           const float * Wa, const float * conv_w, int Kc, float * conv_state, int L,
+                           const float * A_log, const float * dt_bias, const float * norm_w, float eps, float * S,
+                           int Hk, int Hv, int Dk, int Dv, float * out, void * ws, int64_t ws_bytes, hipStream_t s);
 // decode attention (onpu_attn.hip): workspace bytes for (Hq, D, Hkv, S), and the two launches
 int64_t attn_ws_bytes(int Hq, int D, int Hkv, int64_t S);
 hipError_t launch_attn_step(const float * q, int Hq, int D, const void * K, const void * V, int kv_bf16, int Hkv,

@@ -520,3 +520,63 @@ void orc_gemv_i8(const int8_t * W, const float * s, int64_t N, int64_t K, const 
         y[n] = acc * (double) s[n];
     }
 }
+
+/* ---------------------------------------------------------------- Gated DeltaNet decode step
+ * onpu_gdn_step (onpu_cpu.cpp:107-171): one token of a Gated DeltaNet layer. Causal conv over the
+ * last Kc inputs + SiLU, then the state shifts by one; per value head: L2-normalised q (also / sqrt
+ * Dk) and k of its key head, beta = sigmoid(Wb x), decay = exp(-exp(A_log) softplus(Wa x + dt_bias)),
+ * S <- decay S; delta = beta (v - S^T k); S <- S + k delta^T; o = S^T q; out = norm_w * o / rms(o)
+ * * silu(z). fp32, sequential sums as written there. */
+static float orc_silu(float x) { return x / (1.f + expf(-x)); }
+static float orc_dot(const float * a, const float * b, int n) {
+    float s = 0.f;
+    for (int i = 0; i < n; i++) s += a[i] * b[i];
+    return s;
+}
+
+void orc_gdn_step(const float * x, int H, const float * qkv, const float * z, const float * Wb, const float * Wa,
+                  const float * conv_w, int Kc, float * conv_state, int L, const float * A_log, const float * dt_bias,
+                  const float * norm_w, float eps, float * S, int Hk, int Hv, int Dk, int Dv, float * out) {
+    const int key_dim = Hk * Dk, C = 2 * key_dim + Hv * Dv, rep = Hv / Hk;
+    float * co = (float *) malloc((size_t) C * sizeof(float));
+    for (int c = 0; c < C; c++) {
+        float * st = conv_state + (int64_t) c * L;
+        const float * w = conv_w + (int64_t) c * Kc;
+        float s = w[Kc - 1] * qkv[c];
+        for (int j = 0; j < Kc - 1; j++) s += w[j] * st[L - (Kc - 1) + j];
+        co[c] = orc_silu(s);
+        for (int j = 0; j + 1 < L; j++) st[j] = st[j + 1];
+        st[L - 1] = qkv[c];
+    }
+    float * q = (float *) malloc((size_t) Dk * sizeof(float)), * k = (float *) malloc((size_t) Dk * sizeof(float));
+    float * kv = (float *) malloc((size_t) Dv * sizeof(float)), * o = (float *) malloc((size_t) Dv * sizeof(float));
+    float * delta = (float *) malloc((size_t) Dv * sizeof(float));
+    for (int h = 0; h < Hv; h++) {
+        const int kh = h / rep;
+        for (int i = 0; i < Dk; i++) { q[i] = co[kh * Dk + i]; k[i] = co[key_dim + kh * Dk + i]; }
+        const float * v = co + 2 * key_dim + (int64_t) h * Dv;
+        const float qn = 1.f / sqrtf(orc_dot(q, q, Dk) + 1e-6f) / sqrtf((float) Dk);
+        const float kn = 1.f / sqrtf(orc_dot(k, k, Dk) + 1e-6f);
+        for (int i = 0; i < Dk; i++) { q[i] *= qn; k[i] *= kn; }
+        const float b = orc_dot(Wb + (int64_t) h * H, x, H), a = orc_dot(Wa + (int64_t) h * H, x, H);
+        const float beta = 1.f / (1.f + expf(-b));
+        const float ad = a + dt_bias[h];
+        const float sp = ad > 20.f ? ad : log1pf(expf(ad));
+        const float decay = expf(-expf(A_log[h]) * sp);
+        float * Sh = S + (int64_t) h * Dk * Dv;
+        for (int j = 0; j < Dv; j++) { kv[j] = 0.f; o[j] = 0.f; }
+        for (int i = 0; i < Dk; i++) {
+            float * r = Sh + (int64_t) i * Dv;
+            for (int j = 0; j < Dv; j++) { r[j] *= decay; kv[j] += r[j] * k[i]; }
+        }
+        for (int j = 0; j < Dv; j++) delta[j] = (v[j] - kv[j]) * beta;
+        for (int i = 0; i < Dk; i++) {
+            float * r = Sh + (int64_t) i * Dv;
+            for (int j = 0; j < Dv; j++) { r[j] += k[i] * delta[j]; o[j] += r[j] * q[i]; }
+        }
+        const float ms = orc_dot(o, o, Dv) / Dv;
+        const float rn = 1.f / sqrtf(ms + eps);
+        for (int j = 0; j < Dv; j++) out[(int64_t) h * Dv + j] = norm_w[j] * (o[j] * rn) * orc_silu(z[(int64_t) h * Dv + j]);
+    }
+    free(co); free(q); free(k); free(kv); free(o); free(delta);
+}

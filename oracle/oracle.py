@@ -58,6 +58,7 @@ def lib():
         L.orc_transcode_q4k.argtypes = [P, I64, I64, I64, P, P, P]
         L.orc_quantize.argtypes = [I32, P, I64, I64, P]
         L.orc_gemv_i8.argtypes = [P, P, I64, I64, P, P]
+        L.orc_gdn_step.argtypes = [P, I32, P, P, P, P, P, I32, P, I32, P, P, P, C.c_float, P, I32, I32, I32, I32, P]
         L.orc_attn_step.argtypes = [P, I32, I32, P, P, I32, I32, I64, I64, I64, P, P, C.c_float, P]
         _lib = L
     return _lib
@@ -320,6 +321,20 @@ def gemv_i8(W, s, x):
     lib().orc_gemv_i8(_p(W), _p(np.ascontiguousarray(s, np.float32)), N, K, _p(np.ascontiguousarray(x, np.float32)),
                       _p(y))
     return y
+
+
+def gdn_step(x, qkv, z, Wb, Wa, conv_w, conv_state, A_log, dt_bias, norm_w, eps, S, Hk, Hv, Dk, Dv):
+    """One Gated DeltaNet decode token (onpu_cpu.cpp:107-171). conv_state [C][L] and S [Hv][Dk][Dv]
+    are updated copies (returned with out [Hv*Dv])."""
+    f = lambda a: np.ascontiguousarray(a, np.float32)
+    x, qkv, z, Wb, Wa, conv_w = f(x), f(qkv), f(z), f(Wb), f(Wa), f(conv_w)
+    A_log, dt_bias, norm_w = f(A_log), f(dt_bias), f(norm_w)
+    cs, S = f(conv_state).copy(), f(S).copy()
+    C_, L = cs.shape
+    out = np.empty(Hv * Dv, np.float32)
+    lib().orc_gdn_step(_p(x), x.size, _p(qkv), _p(z), _p(Wb), _p(Wa), _p(conv_w), conv_w.shape[1], _p(cs), L,
+                       _p(A_log), _p(dt_bias), _p(norm_w), float(eps), _p(S), Hk, Hv, Dk, Dv, _p(out))
+    return out, cs, S
 
 
 def attn_step(q, K, V, mask=None, sinks=None, scale=None):

@@ -498,3 +498,86 @@ def test_gemv_i8_against_numpy():
     x = rng.standard_normal(300).astype(np.float32)
     want = (W.astype(np.float64) @ x.astype(np.float64)) * s.astype(np.float64)
     assert np.allclose(orc.gemv_i8(W, s, x), want, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------ Gated DeltaNet decode step
+def _gdn_inputs(rng, Hk=2, Hv=4, Dk=16, Dv=8, H=24, Kc=4, L=3):
+    C = 2 * Hk * Dk + Hv * Dv
+    return dict(x=rng.standard_normal(H), qkv=rng.standard_normal(C), z=rng.standard_normal(Hv * Dv),
+                Wb=rng.standard_normal((Hv, H)) * 0.1, Wa=rng.standard_normal((Hv, H)) * 0.1,
+                conv_w=rng.standard_normal((C, Kc)) * 0.5, conv_state=rng.standard_normal((C, L)),
+                A_log=rng.standard_normal(Hv) * 0.5, dt_bias=rng.standard_normal(Hv) * 0.5,
+                norm_w=rng.uniform(0.5, 1.5, Dv), eps=1e-6, S=rng.standard_normal((Hv, Dk, Dv)) * 0.1,
+                Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv)
+
+
+def _silu(v):
+    return v / (1 + np.exp(-v))
+
+
+def test_gdn_conv_state_shifts_and_delta_kernel():
+    """the conv state shifts by one and takes qkv; with a unit last tap and zero others, the conv
+    output is silu(qkv), which the delta-rule checks below rely on"""
+    rng = np.random.default_rng(100)
+    a = _gdn_inputs(rng)
+    out, cs, S = orc.gdn_step(**a)
+    assert np.array_equal(cs[:, :-1], a["conv_state"][:, 1:].astype(np.float32))
+    assert np.array_equal(cs[:, -1], a["qkv"].astype(np.float32))
+
+
+def _unit_conv(a):
+    w = np.zeros_like(a["conv_w"])
+    w[:, -1] = 1.0
+    a["conv_w"] = w
+
+
+def test_gdn_delta_rule_stores_v_for_k():
+    """decay 1 (A_log -> -inf) and beta 1 (Wb x = +60): the delta rule S' = S + k (v - S^T k)^T with
+    a unit-norm k leaves S'^T k = v for every value head, whatever S was"""
+    rng = np.random.default_rng(101)
+    a = _gdn_inputs(rng)
+    _unit_conv(a)
+    a["A_log"][:] = -1e30
+    a["Wb"] = np.outer(np.full(a["Hv"], 1.0), a["x"]) * (60.0 / np.dot(a["x"], a["x"]))
+    out, cs, S = orc.gdn_step(**a)
+    Hk, Hv, Dk, Dv = a["Hk"], a["Hv"], a["Dk"], a["Dv"]
+    co = _silu(a["qkv"].astype(np.float64))
+    for h in range(Hv):
+        kh = h // (Hv // Hk)
+        k = co[Hk * Dk + kh * Dk:Hk * Dk + (kh + 1) * Dk]
+        k = k / np.sqrt(np.dot(k, k) + 1e-6)
+        v = co[2 * Hk * Dk + h * Dv:2 * Hk * Dk + (h + 1) * Dv]
+        assert np.allclose(S[h].astype(np.float64).T @ k, v, rtol=1e-4, atol=1e-5)
+
+
+def test_gdn_zero_state_output_is_normalised_v():
+    """zero state, decay 1, beta 1 and q = k: S' = k v^T, o = (q . k) v with q . k = |k|^2 / (|k|^2 +
+    1e-6) / sqrt(Dk), so the gated RMSNorm output is norm_w * o / sqrt(mean(o^2) + eps) * silu(z)"""
+    rng = np.random.default_rng(102)
+    a = _gdn_inputs(rng)
+    _unit_conv(a)
+    Hk, Hv, Dk, Dv = a["Hk"], a["Hv"], a["Dk"], a["Dv"]
+    a["qkv"][:Hk * Dk] = a["qkv"][Hk * Dk:2 * Hk * Dk]          # q = k
+    a["S"][:] = 0
+    a["A_log"][:] = -1e30
+    a["Wb"] = np.outer(np.full(Hv, 1.0), a["x"]) * (60.0 / np.dot(a["x"], a["x"]))
+    out, cs, S = orc.gdn_step(**a)
+    co = _silu(a["qkv"].astype(np.float64))
+    for h in range(Hv):
+        kh = h // (Hv // Hk)
+        k = co[Hk * Dk + kh * Dk:Hk * Dk + (kh + 1) * Dk]
+        c = np.dot(k, k) / (np.dot(k, k) + 1e-6) / np.sqrt(Dk)
+        o = c * co[2 * Hk * Dk + h * Dv:2 * Hk * Dk + (h + 1) * Dv]
+        want = a["norm_w"] * o / np.sqrt(np.mean(o * o) + a["eps"]) * _silu(a["z"][h * Dv:(h + 1) * Dv])
+        assert np.allclose(out[h * Dv:(h + 1) * Dv], want, rtol=1e-4, atol=1e-5)
+
+
+def test_gdn_beta_zero_is_pure_decay():
+    """beta 0 (Wb x = -60): S' = decay S with decay = exp(-exp(A_log) softplus(Wa x + dt_bias))"""
+    rng = np.random.default_rng(103)
+    a = _gdn_inputs(rng)
+    a["Wb"] = -np.outer(np.full(a["Hv"], 1.0), a["x"]) * (60.0 / np.dot(a["x"], a["x"]))
+    out, cs, S = orc.gdn_step(**a)
+    ad = a["Wa"] @ a["x"] + a["dt_bias"]
+    decay = np.exp(-np.exp(a["A_log"]) * np.log1p(np.exp(ad)))
+    assert np.allclose(S, a["S"] * decay[:, None, None], rtol=1e-5, atol=1e-7)
