@@ -1172,18 +1172,19 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 
 // ------------------------------------------------------------------ MoE prefill: grouped GEMM
 // Work item = (expert e, first permuted position, rows <= 64) from k_moe_permute; blockIdx.y =
-// item, blockIdx.x = a group of output columns. Workgroup: 4 waves x 2 weight tiles, 64 rows of X
+// item, blockIdx.x = a group of output columns. Workgroup: WV waves x 2 weight tiles, 64 rows of X
 // (the item's rows, gathered) as 4 A blocks; per 128-wide K block the X tile (16 KiB of A
-// fragments) is filled by buffer loads straight to LDS, each lane from its own row (rows past the
-// item land as zeros), and each wave dequantizes its two weight tiles in registers (the k_qgemm
-// scheme over one expert's weights).
-//   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = 4 blockIdx.x + w and up tile
+// fragments, 16 / WV of them loaded by each wave) is filled by buffer loads straight to LDS, each
+// lane from its own row (rows past the item land as zeros), and each wave dequantizes its two
+// weight tiles in registers (the k_qgemm scheme over one expert's weights). Every column group
+// re-reads the item's X, so wider groups (WV = 8) halve that traffic.
+//   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = WV blockIdx.x + w and up tile
 //           g + NT / 2; act[position][16 g + r] = bf16(silu(gate) * up)
-//   WHICH 1 (down): wave w holds tiles 8 blockIdx.x + 2 w + {0, 1}; o[position][n] = fp32
+//   WHICH 1 (down): wave w holds tiles 2 WV blockIdx.x + 2 w + {0, 1}; o[position][n] = fp32
 // X rows: WHICH 0 token perm[position] / k of x [T][K]; WHICH 1 position of act [T k][K].
-template <int FMT, int WHICH>
-__global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
-    constexpr int MBG = 4;
+template <int FMT, int WHICH, int WV>
+__global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) {
+    constexpr int MBG = 4, FPW = 16 / WV;                        // X fragments loaded per wave
     __shared__ u32x4 xs0[MBG * 4 * 64], xs1[MBG * 4 * 64];     // 2 x 16 KiB
     const int item = blockIdx.y;
     if (item >= *a.nitems) return;
@@ -1193,8 +1194,8 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
     const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
     const uint8_t * W = a.W + (int64_t) e * a.estride;
     int64_t t[2];
-    if (WHICH == 0) { t[0] = (int64_t) blockIdx.x * 4 + wave; t[1] = t[0] + a.NT / 2; }
-    else { t[0] = (int64_t) blockIdx.x * 8 + 2 * wave; t[1] = t[0] + 1; }
+    if (WHICH == 0) { t[0] = (int64_t) blockIdx.x * WV + wave; t[1] = t[0] + a.NT / 2; }
+    else { t[0] = (int64_t) blockIdx.x * 2 * WV + 2 * wave; t[1] = t[0] + 1; }
     const bool ok0 = WHICH == 0 ? t[0] < a.NT / 2 : t[0] < a.NT;
     const bool ok1 = WHICH == 0 ? ok0 : t[1] < a.NT;
     __amdgpu_buffer_rsrc_t wrs[2];
@@ -1203,10 +1204,11 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
         wrs[i] = __builtin_amdgcn_make_buffer_rsrc((void *) (W + tt * a.KB * BLK), (short) 0,
                                                    (int) (uint32_t) (a.KB * BLK), 0x00020000);
     }
-    // this wave's 4 X fragments f = 4 wave + i: (mb, j) = (f / 4, f % 4) = (wave, i)
+    // this wave's FPW X fragments f = FPW wave + i: (mb, j) = (f / 4, f % 4), one A block mb
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) a.xbytes, 0x00020000);
-    const int row = 16 * wave + r;
+    const int xmb = FPW * wave / 4, xj0 = FPW * wave % 4;
+    const int row = 16 * xmb + r;
     uint32_t xrow = 0x80000000u;
     if (row < rows) {
         const int64_t src = WHICH == 0 ? (int64_t) (a.perm[first + row] / a.k) : (int64_t) (first + row);
@@ -1215,10 +1217,11 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(MArgs a) {
     const bool ktail = a.K % 128 != 0;
     auto load_xt = [&](int64_t b, u32x4 * buf) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t off = xrow == 0x80000000u ? xrow : xrow + (uint32_t) (32 * i + 8 * q) * 2;
-            if (ktail && 128 * b + 32 * i + 8 * q >= a.K) off = 0x80000000u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + (4 * wave + i) * 64), 16, off,
+        for (int i = 0; i < FPW; i++) {
+            const int j = xj0 + i;
+            uint32_t off = xrow == 0x80000000u ? xrow : xrow + (uint32_t) (32 * j + 8 * q) * 2;
+            if (ktail && 128 * b + 32 * j + 8 * q >= a.K) off = 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + (FPW * wave + i) * 64), 16, off,
                                                      (uint32_t) (256 * b), 0, 0);
         }
     };
