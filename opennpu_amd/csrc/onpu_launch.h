@@ -119,7 +119,9 @@ int qgemv_max_waves(int mb, int rt, int nb, int xl);
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
 // k_qgemm_sk configuration: {weight tiles per wave, 16-row A blocks, waves}; rows and columns of the
 // workgroup tile are 16 * MBG and 16 * NTW * WV. (Measured on MI355X against 256 x 64 per wave with
-// one wave per SIMD and 256 x 32 with four waves: both slower, the first by ~30 %.)
+// one wave per SIMD and 256 x 32 with four waves: both slower, the first by ~30 %; and against
+// 128 x 64 per wave with eight waves, which halves the LDS reads of X but doubles the dequantization
+// per MFMA and spills: 40 % slower.)
 struct GskCfg { int ntw, mbg, wv; };
 constexpr GskCfg GSK_CFGS[1] = {{2, 16, 8}};
 hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s);
