@@ -36,6 +36,10 @@ DEV f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                    0, 0, 0);
 }
 
+// s_waitcnt immediates (gfx9 encoding): vmcnt(n) with the other counters free, and lgkmcnt(0)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
+
 // D_j -> 8 bf16 holding 128 + u (bf16 0x43XX = 128 + XX for XX < 128), in B-operand order:
 // r.x = (d & M) | mag, r.y = ((d >> 4) & M) | mag, r.z = ((d >> 8) & M) | mag, r.w = ((d >> 12) & M) | mag.
 // Seven VALU ops: with the mask in an SGPR and mag in a VGPR, both opaque (gfx9 VOP3 takes no
@@ -147,7 +151,8 @@ DEV Par<FMT> par_zero() {
 template <int FMT>
 DEV Par<FMT> load_par(const uint8_t * blk, int r) {
     Par<FMT> p;
-    if (FMT == ONPU_G128S) p.v[0] = *GLB(const uint16_t, blk + 1024 + 2 * r);
+    // G128S: the dword holding rows r & ~1 and r | 1 (decode_scale picks the half)
+    if (FMT == ONPU_G128S) p.v[0] = *GLB(const uint32_t, blk + 1024 + 4 * (r >> 1));
     else if (FMT == ONPU_Q4NX) {
         const u32x4 q = __builtin_nontemporal_load(GLB(const u32x4, blk + 1024 + 16 * r));
         for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];
@@ -163,7 +168,12 @@ DEV Par<FMT> load_par(const uint8_t * blk, int r) {
 template <int FMT>
 DEV void decode_scale(const Par<FMT> & p, float (&s)[4]) {
     if (FMT == ONPU_G128S) {
-        const float v = bf16_to_f32((uint16_t) p.v[0]);
+        // p.v[0] holds the scales of rows r & ~1 (low half) and r | 1 (high half); one byte
+        // permute moves this lane's half to the top (r & 1 = lane & 1). A 16-bit load instead
+        // lets the compiler narrow the loop's phi of loaded values to 16 bits and widen it again
+        // at the loop's entry, a use that waits for the first chunk before the next one is issued.
+        const uint32_t sel = (threadIdx.x & 1) ? 0x03020c0cu : 0x01000c0cu;
+        const float v = __uint_as_float(__builtin_amdgcn_perm(p.v[0], p.v[0], sel));
         for (int j = 0; j < 4; j++) s[j] = v;
     } else {
         for (int j = 0; j < 4; j++)
@@ -401,44 +411,40 @@ DEV void xsum_mfma(const u32x4 (&xa)[MB][4], f32x4 (&cs)[MB][4]) {
     }
 }
 
-// Where the A operand (x rows) comes from: global rows (optionally gathered through xrows) or the
-// workgroup's LDS copy xs[M][xls] (bf16, zero past K).
+// Where the A operand (x rows) comes from: global rows or the workgroup's LDS copy xs[M][xls]
+// (bf16, zero past K).
 struct XSrc {
     const uint16_t * x;
     int64_t ldx;
-    const int32_t * xrows;
     const uint16_t * xs;
     int64_t xls;
     const float * xsum;       // XL: LDS column sums [group][16] of x's 32- (G128S: 128-) groups
 };
 
-// x fragments of block b: lane (r, q) of A-block mb holds x[row(16 mb + r)][128 b + 32 j + 8 q .. +7]
-// (XL: from the LDS copy, else from global rows; a compile-time choice so that the LDS path has
-// no global load the waits would have to cover)
-template <int MB, bool XL>
-DEV void load_x(const XSrc & X, int M, int64_t K, int64_t b, int r, int q, u32x4 (&xa)[MB][4]) {
-    if (XL) {
-        // LDS rows are zero-padded to 128 KB columns; rows >= M read row M - 1 (their MFMA rows are
-        // never stored), so the reads need no masks
-        for (int mb = 0; mb < MB; mb++) {
-            const int i = MB == 1 ? perm16(r) : 16 * mb + r, m = i < M ? i : M - 1;
-            const uint16_t * base = X.xs + (uint32_t) m * (uint32_t) X.xls + (uint32_t) b * 128u + 8u * q;
-            for (int j = 0; j < 4; j++) xa[mb][j] = *LDS_U32X4(base + 32 * j);
-        }
-        return;
+// x fragments of block b from the LDS copy: lane (r, q) of A-block mb holds
+// x[row(16 mb + r)][128 b + 32 j + 8 q .. +7]. LDS rows are zero-padded to 128 KB columns; rows
+// >= M read row M - 1 (their MFMA rows are never stored), so the reads need no masks.
+template <int MB>
+DEV void load_x_lds(const XSrc & X, int M, int64_t b, int r, int q, u32x4 (&xa)[MB][4]) {
+    for (int mb = 0; mb < MB; mb++) {
+        const int i = MB == 1 ? perm16(r) : 16 * mb + r, m = i < M ? i : M - 1;
+        const uint16_t * base = X.xs + (uint32_t) m * (uint32_t) X.xls + (uint32_t) b * 128u + 8u * q;
+        for (int j = 0; j < 4; j++) xa[mb][j] = *LDS_U32X4(base + 32 * j);
     }
+}
+
+// x fragments of block b from global rows (zero for rows >= M and columns past K), loaded just
+// before the block's MFMAs, after the next chunk's weights were issued: measured faster (M = 4..8,
+// K = 4096..12288) than loading a whole chunk's x first or loading it ahead with the chunk's
+// weights (clamped, branch-free), which holds registers across the whole pipeline.
+template <int MB>
+DEV void load_x_glb(const XSrc & X, int M, int64_t K, int64_t b, int r, int q, u32x4 (&xa)[MB][4]) {
     for (int mb = 0; mb < MB; mb++) {
         const int m = MB == 1 ? perm16(r) : 16 * mb + r;
-        int64_t row = m;
-        bool ok = m < M;
-        if (!XL && X.xrows && ok) { row = X.xrows[m]; ok = row >= 0; }
         for (int j = 0; j < 4; j++) {
             const int64_t k = 128 * b + 32 * j + 8 * q;
             u32x4 v = {0u, 0u, 0u, 0u};
-            if (ok && k < K) {
-                if (XL) v = *LDS_U32X4(X.xs + m * X.xls + k);
-                else v = *(const u32x4 *) (X.x + row * X.ldx + k);
-            }
+            if (m < M && k < K) v = *(const u32x4 *) (X.x + m * X.ldx + k);
             xa[mb][j] = v;
         }
     }
@@ -464,7 +470,7 @@ DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], co
         for (int rt = 0; rt < RT; rt++) {
             // a block past b1 (or of a missing tile) re-reads `last`, the wave's own last block of
             // tile 0: an address the wave fetches anyway, never one that every wave shares
-            c.ok[i][rt] = tb[rt] != nullptr && c0 + i < b1;
+            c.ok[i][rt] = tb[rt] != nullptr && (int) c0 + i < (int) b1;      // 32-bit: scalar compares
             p[i][rt] = c.ok[i][rt] ? tb[rt] + (c0 + i) * BLK : last;
         }
     for (int i = 0; i < NB; i++)
@@ -480,9 +486,9 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
                        int r, int q, uint32_t mag, f32x4 (&acc)[RT][MB]) {
     if (XL) {                             // x from LDS, one block at a time (short latency)
         for (int i = 0; i < NB; i++) {
-            if (c0 + i >= b1) break;
+            if ((int) c0 + i >= (int) b1) break;
             u32x4 xa[MB][4];
-            load_x<MB, true>(X, M, K, c0 + i, r, q, xa);
+            load_x_lds<MB>(X, M, c0 + i, r, q, xa);
             f32x4 cs[MB][4];
             constexpr int GPB = FMT == ONPU_G128S ? 1 : 4;
             for (int mb = 0; mb < MB; mb++)
@@ -491,27 +497,31 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
                                                                                    16 * mb + 4 * q);
             qacc_block<FMT, MB, RT, RV>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, acc);
         }
-    } else {                              // x from global memory: the chunk's x loads first
-        u32x4 xa[NB][MB][4];
-        for (int i = 0; i < NB; i++) load_x<MB, false>(X, M, c0 + i < b1 ? K : 0, c0 + i, r, q, xa[i]);
+    } else {                              // x from global memory, each block's just before its MFMAs
         for (int i = 0; i < NB; i++)
-            if (c0 + i < b1) {
+            if ((int) c0 + i < (int) b1) {
+                u32x4 xa[MB][4];
+                load_x_glb<MB>(X, M, K, c0 + i, r, q, xa);
                 f32x4 cs[MB][4];
-                xsum_mfma<FMT, MB>(xa[i], cs);
-                qacc_block<FMT, MB, RT, RV>(ch.ok[i], ch.wv[i], ch.par[i], xa[i], cs, mag, acc);
+                xsum_mfma<FMT, MB>(xa, cs);
+                qacc_block<FMT, MB, RT, RV>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, acc);
             }
     }
 }
 
-// the first chunk's loads (qacc_run's prologue; a chained launch issues them before a barrier).
-// Returns the wave's last block (the target of out-of-range slots); b1 drops to b0 without a tile.
+// the first chunk's loads (qacc_run's prologue). Returns the wave's last block (the target of
+// out-of-range slots); b1 drops to b0 without a tile. The loads are issued also by a wave without
+// blocks (from `safe`, a block every launch has): a load under a branch would make the compiler's
+// wait counts at the join assume the branch not taken, and the first wait for x would then also
+// wait for the weights just issued.
 template <int FMT, int RT, int NB>
-DEV const uint8_t * qacc_start(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], int64_t b0, int64_t & b1) {
+DEV const uint8_t * qacc_start(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], int64_t b0, int64_t & b1,
+                               const uint8_t * safe) {
     const int lane = threadIdx.x & 63, r = lane & 15;
     if (tb[0] == nullptr) b1 = b0;
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
-    const uint8_t * last = b0 < b1 ? tb[0] + (b1 - 1) * BLK : nullptr;
-    if (b0 < b1) load_chunk<FMT, RT, NB>(ca, tb, last, b0, b1, lane, r);
+    const uint8_t * last = b0 < b1 ? tb[0] + (b1 - 1) * BLK : safe;
+    load_chunk<FMT, RT, NB>(ca, tb, last, b0, b1, lane, r);
     return last;
 }
 
@@ -550,16 +560,96 @@ DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], co
 // loads first, then the LDS writes and the barrier while the weights stream); every wave calls
 // both, also one with no blocks. (Issuing both chunks before the barrier measured slower.)
 template <int FMT, int MB, int RT, int NB, bool XL, int RV, class Pre, class Post>
-DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const XSrc & X, int M, int64_t K, Pre pre,
-                  Post post, f32x4 (&acc)[RT][MB]) {
+DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const uint8_t * safe, const XSrc & X, int M,
+                  int64_t K, Pre pre, Post post, f32x4 (&acc)[RT][MB]) {
     for (int rt = 0; rt < RT; rt++)
         for (int mb = 0; mb < MB; mb++) acc[rt][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
     WChunk<FMT, RT, NB> ca;
     pre();
-    const uint8_t * last = qacc_start<FMT, RT, NB>(ca, tb, b0, b1);
+    const uint8_t * last = qacc_start<FMT, RT, NB>(ca, tb, b0, b1, safe);
     post();
     qacc_rest<FMT, MB, RT, NB, XL, RV>(ca, tb, last, b0, b1, X, M, K, acc);
 }
+
+// The workgroup's LDS copy of x [M][K] (bf16) for the XL variants, in 16 B units u = tid + i *
+// blockDim; rows are zero-padded from K to Kpad = 128 * KB and followed by the column sums of x per
+// 32-group (G128S: per 128) times xsum_mul, xsum[group][16 MFMA rows] (MB = 1: x row m at
+// perm16(m)). pre() loads the first 4 units per thread and is called before the weight loads are
+// issued; post() stores them, copies any further units and ends with a barrier, while the weights
+// stream. The first 4 units are buffer loads over x's M rows (the host keeps M * ldx * 2 < 2^31):
+// units past the rows or past K get an offset out of the buffer's range, which returns zeros
+// without a memory access, so the loads need no branch (a load under a branch gets a wait for
+// every outstanding load at the branch's end, which would hold the weight loads back by a full
+// memory round trip) and no clamped address (which would send every wave to one L2 line).
+template <int FMT, int MB>
+struct XStage {
+    const uint16_t * x;
+    int64_t ldx, K;
+    uint16_t * xs;
+    int64_t xls;
+    float * xsum;
+    uint32_t kp8, nunits, bd, xbytes;
+    u32x4 xv[4];
+    static constexpr int UPG = (FMT == ONPU_G128S ? 128 : 32) / 8;     // 16 B units per group
+
+    __device__ __forceinline__ XStage(const uint16_t * x_, int64_t ldx_, int64_t K_, int64_t KB, int M, uint16_t * xs_,
+                                      int64_t xls_, float * xsum_)
+        : x(x_), ldx(ldx_), K(K_), xs(xs_), xls(xls_), xsum(xsum_), kp8((uint32_t) KB * 16),
+          nunits((uint32_t) M * (uint32_t) KB * 16), bd(blockDim.x), xbytes((uint32_t) (M * ldx_ * 2)) {}
+
+    __device__ __forceinline__ u32x4 unit(uint32_t u) const {
+        const uint32_t m = u / kp8, k = (u - m * kp8) * 8;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (k < K) v = *(const u32x4 *) (x + (int64_t) m * ldx + k);
+        return v;
+    }
+    // row m = u / kp8 from a float reciprocal (u < 2^24, so the estimate is off by at most one).
+    // Iterations past the last unit are skipped as a whole (measured 0.2-0.3 us faster per launch
+    // at M = 1 than issuing all four).
+    __device__ __forceinline__ void pre() {
+        const float inv = 1.0f / (float) kp8;
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *) x, (short) 0, (int) xbytes, 0x00020000);
+        for (int i = 0; i < 4; i++) {
+            if ((uint32_t) i * bd >= nunits) break;
+            const uint32_t u = threadIdx.x + i * bd;
+            uint32_t m = (uint32_t) ((float) u * inv);
+            m = m * kp8 > u ? m - 1 : ((m + 1) * kp8 <= u ? m + 1 : m);
+            const uint32_t k = (u - m * kp8) * 8;
+            const uint32_t off = u < nunits && k < K ? (m * (uint32_t) ldx + k) * 2u : 0x80000000u;
+            xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        }
+    }
+    // unit u's 8 values summed in fp32, then over the UPG consecutive lanes holding one group (the
+    // units of a group are consecutive in u, and u = tid + i * blockDim keeps them in one wave)
+    __device__ __forceinline__ void stage(uint32_t u, u32x4 v) {
+        if (u < nunits) {
+            const uint32_t m = u / kp8;
+            *LDS_U32X4(xs + (int64_t) m * xls + (u - m * kp8) * 8) = v;
+        }
+        float t = 0.f;
+        for (int d = 0; d < 4; d++) t += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+        for (int o = UPG / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+        if (u < nunits && u % UPG == 0) {
+            const uint32_t m = u / kp8, g = (u - m * kp8) / UPG;
+            xsum[g * 16 + (MB == 1 ? perm16(m) : m)] = t * xsum_mul<FMT>();
+        }
+    }
+    // REST: copy units past the first 4 per thread (a kernel that never has them leaves the loop
+    // out: its loads would make the compiler's wait counts after it assume a pending load)
+    template <bool REST = true>
+    __device__ __forceinline__ void post() {
+        for (int i = 0; i < 4; i++) {
+            if ((uint32_t) i * bd >= nunits) break;
+            stage(threadIdx.x + i * bd, xv[i]);
+        }
+        if (REST)
+            for (uint32_t u0 = 4 * bd; u0 < nunits; u0 += bd) {      // same trip count for every lane
+                const uint32_t u = u0 + threadIdx.x;
+                stage(u, u < nunits ? unit(u) : (u32x4){0u, 0u, 0u, 0u});
+            }
+        __syncthreads();
+    }
+};
 
 // Epilogues
 enum { EPI_STORE = 0, EPI_ACT = 1, EPI_SLOTSUM = 2 };
@@ -614,56 +704,19 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     uint16_t * xs = (uint16_t *) (red + nw * PER);
     // XL: column sums of x per 32-group (G128S: per 128) times xsum_mul after the x rows:
     // xsum[group][16 MFMA rows] (x row m at perm16(m))
-    constexpr int GS = FMT == ONPU_G128S ? 128 : 32, UPG = GS / 8;       // 16 B units per group
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
-    const XSrc X{x, a.ldx, nullptr, XL ? xs : nullptr, a.xls, XL ? xsum : nullptr};
-    // XL: the workgroup copies x [M][K] into LDS in 16 B units u = tid + i * blockDim; rows are
-    // zero-padded from K to Kpad = 128 * KB. The first 4 units per thread are loaded before the
-    // weight loads are issued (pre) and stored after (post); any further ones are copied in post.
-    const uint32_t kp8 = (uint32_t) a.KB * 16, nunits = (uint32_t) a.M * kp8, bd = blockDim.x;
-    u32x4 xv[4];
-    auto xunit = [&](uint32_t u) {
-        const uint32_t m = u / kp8, k = (u - m * kp8) * 8;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (k < a.K) v = *(const u32x4 *) (x + (int64_t) m * a.ldx + k);
-        return v;
-    };
-    auto xslot = [&](uint32_t u) {
-        const uint32_t m = u / kp8;
-        return LDS_U32X4(xs + (int64_t) m * a.xls + (u - m * kp8) * 8);
-    };
+    const XSrc X{x, a.ldx, XL ? xs : nullptr, a.xls, XL ? xsum : nullptr};
+    XStage<FMT, MB> xst(x, a.ldx, a.K, a.KB, a.M, xs, a.xls, xsum);
     auto pre = [&]() {
-        if (!XL) return;
-        for (int i = 0; i < 4; i++) {
-            const uint32_t u = threadIdx.x + i * bd;
-            xv[i] = u < nunits ? xunit(u) : (u32x4){0u, 0u, 0u, 0u};
-        }
-    };
-    // unit u's 8 values summed in fp32, then over the UPG consecutive lanes holding one group (the
-    // units of a group are consecutive in u, and u = tid + i * blockDim keeps them in one wave)
-    auto stage = [&](uint32_t u, u32x4 v) {
-        if (u < nunits) *xslot(u) = v;
-        float t = 0.f;
-        for (int d = 0; d < 4; d++) t += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
-        for (int o = UPG / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
-        if (u < nunits && u % UPG == 0) {
-            const uint32_t m = u / kp8, g = (u - m * kp8) / UPG;
-            xsum[g * 16 + (MB == 1 ? perm16(m) : m)] = t * xsum_mul<FMT>();
-        }
+        if (XL) xst.pre();
     };
     auto post = [&]() {
-        if (!XL) return;
-        for (int i = 0; i < 4; i++) stage(threadIdx.x + i * bd, xv[i]);
-        for (uint32_t u0 = 4 * bd; u0 < nunits; u0 += bd) {          // same trip count for every lane
-            const uint32_t u = u0 + threadIdx.x;
-            stage(u, u < nunits ? xunit(u) : (u32x4){0u, 0u, 0u, 0u});
-        }
-        __syncthreads();
+        if (XL) xst.post();
     };
     f32x4 acc[RT][MB];
-    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
-    else if (MB == 1 && a.M <= 8) qacc_run<FMT, MB, RT, NB, XL != 0, 2>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
-    else qacc_run<FMT, MB, RT, NB, XL != 0, 4>(tb, b0, b1, X, a.M, a.K, pre, post, acc);
+    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
+    else if (MB == 1 && a.M <= 8) qacc_run<FMT, MB, RT, NB, XL != 0, 2>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
+    else qacc_run<FMT, MB, RT, NB, XL != 0, 4>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
 
     // cross-wave reduction through LDS: red[wave][((rt * MB + mb) * 4 + v) * 64 + lane]
     for (int rt = 0; rt < RT; rt++)
@@ -1614,9 +1667,6 @@ DEV void chain_barrier(int32_t * bar, int64_t w, int64_t P, int epoch, uint32_t 
     }
 }
 
-// s_waitcnt immediates (gfx9 encoding): vmcnt(n) with the other counters free, and lgkmcnt(0)
-constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
 
 // position in a wave's block sequence over the chain: block b (< b1) of tile t of entry e, tile
 // group g; e == a.n: past the end
@@ -1687,9 +1737,9 @@ DEV void chain_sync() {
 template <int FMT>
 DEV Par<FMT> load_par_lds(const uint8_t * blk, int r) {
     Par<FMT> p;
-    typedef __attribute__((address_space(3))) const uint16_t lds_u16;
+    typedef __attribute__((address_space(3))) const uint32_t lds_u32;
     typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
-    if (FMT == ONPU_G128S) p.v[0] = *(lds_u16 *) (blk + 1024 + 2 * r);
+    if (FMT == ONPU_G128S) p.v[0] = *(lds_u32 *) (blk + 1024 + 4 * (r >> 1));     // as load_par
     else if (FMT == ONPU_Q4NX) {
         const u32x4 q = *LDS_U32X4(blk + 1024 + 16 * r);
         for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];
@@ -1714,7 +1764,7 @@ __global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArg
     uint16_t * xs = (uint16_t *) (red + 2 * CHAIN_WAVES * 256);
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
     uint8_t * ring = (uint8_t *) red + a.ring + (ctrl ? 0 : wave * S * BLK);
-    const XSrc X{nullptr, 0, nullptr, xs, a.xls, xsum};
+    const XSrc X{nullptr, 0, xs, a.xls, xsum};
     ChainCur ic{0, w - P, 0, 0, 0, ents[0].W, 1, 0u};   // past the end, refills read entry 0 out of range
     if (!ctrl) {
         chain_settle<FMT>(ic, ents, a.n, w, P, wave);

@@ -336,7 +336,7 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
     const size_t red = (size_t) waves * rt * mb * 1024;
     // x rows, then the column sums [KB * groups per block][16] floats
     const size_t xb = xl ? (size_t) a.M * a.xls * 2 + (size_t) a.KB * (fmt == 2 ? 1 : 4) * 64 : 0;
-    if (xl && a.M > 16) return hipErrorInvalidValue;
+    if (xl && (a.M > 16 || (int64_t) a.M * a.ldx * 2 >= ((int64_t) 1 << 31))) return hipErrorInvalidValue;
     if (red > 32768 || red + xb > 163840) return hipErrorInvalidValue;      // gfx950: 160 KiB per workgroup
     if (xl && a.xls < a.KB * 128) return hipErrorInvalidValue;
     switch (fmt) {

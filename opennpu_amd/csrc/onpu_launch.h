@@ -115,6 +115,7 @@ hipError_t launch_dequant(int fmt, const uint8_t * W, int64_t N, int64_t K, void
 hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,
                         hipStream_t s);
 int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl);
+
 int qgemv_max_waves(int mb, int rt, int nb, int xl);
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
 // k_qgemm_sk configuration: {weight tiles per wave, 16-row A blocks, waves}; rows and columns of the
