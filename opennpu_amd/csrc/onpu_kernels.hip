@@ -185,14 +185,18 @@ __global__ __launch_bounds__(GI8_T) void k_gemv_i8(const int8_t * __restrict__ W
     __shared__ float wsx[GI8_T / 64];
     __shared__ float red[GI8_T / 64][4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, slot = lane >> 4;
-    // x to LDS: all of a thread's loads of a batch issued before the stores (8 x 1024 floats per batch)
+    // x to LDS: all of a thread's loads of a batch issued before the stores (8 x 1024 floats per
+    // batch). Buffer loads over x's K floats (the host keeps K * 4 < 2^31): past K they return
+    // zeros, so the loads need no branch (a load under a branch is waited for where the branch
+    // rejoins, which would serialize the batch).
     float part = 0.f;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *) x, (short) 0, (int) (K * 4), 0x00020000);
     for (int64_t k0 = 4 * t; k0 < K; k0 += 8 * 4 * GI8_T) {
         float4 v[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int64_t k = k0 + (int64_t) i * 4 * GI8_T;
-            v[i] = k < K ? *(const float4 *) (x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t) (k * 4), 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -210,12 +214,14 @@ __global__ __launch_bounds__(GI8_T) void k_gemv_i8(const int8_t * __restrict__ W
     const int64_t k0 = (wave % ks) * Kw, k1 = k0 + Kw < K ? k0 + Kw : K;
     const int8_t * wr = W + (row < N ? row : 0) * K;
     float acc = 0.f;
+    // all GI8_U loads of a step unconditional: past k1 a lane re-reads its own first 16 bytes of
+    // the step (never used: the products below stop at k1)
     for (int64_t kb = k0 + 16 * li; kb < k1; kb += 256 * GI8_U) {
         uint4 q[GI8_U];
 #pragma unroll
         for (int u = 0; u < GI8_U; u++) {
             const int64_t k = kb + 256 * u;
-            q[u] = k < k1 ? *(const uint4 *) (wr + k) : make_uint4(0u, 0u, 0u, 0u);
+            q[u] = *(const uint4 *) (wr + (k < k1 ? k : kb));
         }
 #pragma unroll
         for (int u = 0; u < GI8_U; u++) {
@@ -504,10 +510,13 @@ hipError_t launch_gemv_i8(const int8_t * W, const float * sc, int64_t N, int64_t
     if (N <= 0 || K <= 0) return hipSuccess;
     if (K % 16 || K * 4 > 128 * 1024 || ((uintptr_t) W | (uintptr_t) x) % 16) return hipErrorInvalidValue;
     const int64_t ng = (N + 3) / 4;
-    const int ks = ng >= 16384 ? 1 : (ng >= 8192 ? 2 : 4);           // measured: more, shorter waves win
+    // K parts per row: more, shorter waves win, except that a row of one full step (256 GI8_U
+    // bytes) stays whole (11264 x 2048: 15.1 us against 15.9 with 4 parts; 2048 x 5632 keeps 4
+    // parts: 8.8 us against 9.4 with 2)
+    const int ks = K <= 256 * GI8_U ? 1 : (ng >= 16384 ? 1 : (ng >= 8192 ? 2 : 4));
     const int64_t Kw = (K + (int64_t) ks * 256 - 1) / ((int64_t) ks * 256) * 256;
     const int64_t grid = (ng + 4 / ks - 1) / (4 / ks);
-    if (grid >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
+    if (grid >= ((int64_t) 1 << 31) || K * 4 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     k_gemv_i8<<<(unsigned) grid, GI8_T, (size_t) K * 4, s>>>(W, sc, N, K, ks, Kw, x, y);
     CHECK_LAUNCH();
     return hipSuccess;
