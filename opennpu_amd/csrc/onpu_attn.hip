@@ -86,30 +86,31 @@ __global__ __launch_bounds__(AT) void k_attn_part(AttnArgs a) {
     const bool dl = 8 * li < D;                                  // this lane's 8 values of d exist
     const int64_t j0 = (int64_t) c * C;
     const int rows = (int) (a.S - j0 < C ? a.S - j0 : C);
-    const KV * Kg = (const KV *) a.K + (int64_t) g * a.hs + j0 * a.rs + 8 * li;
-    const KV * Vg = (const KV *) a.V + (int64_t) g * a.hs + j0 * a.rs + 8 * li;
+    // lanes past D read column 0 (their values meet zero q and are never stored)
+    const KV * Kg = (const KV *) a.K + (int64_t) g * a.hs + j0 * a.rs + 8 * (dl ? li : 0);
+    const KV * Vg = (const KV *) a.V + (int64_t) g * a.hs + j0 * a.rs + 8 * (dl ? li : 0);
     // q of the group's heads: coalesced 16-byte loads (0 past rep), stored to LDS after the first
     // pass's K loads are issued; the barrier then waits for LDS only (a __syncthreads would also
     // wait for the K loads)
     const int nq = HG * D / 4, hq0 = z * HG, hqn = a.rep - hq0 < HG ? a.rep - hq0 : HG;
-    const float4 qv = t < nq && t * 4 < hqn * D ? *(const float4 *) (a.q + (int64_t) (g * a.rep + hq0) * D + 4 * t)
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    // (loads unconditional, from clamped addresses, and masked where used: a load under a branch is
+    // waited for where the branch rejoins, which would serialize the loads)
+    const bool qok = t < nq && t * 4 < hqn * D;
+    const float4 qv = *(const float4 *) (a.q + (int64_t) (g * a.rep + hq0) * D + (qok ? 4 * t : 0));
     // Row of (pass r0, step u, wave, slot): consecutive slots and waves take consecutive rows, so one
     // wave instruction reads RPW consecutive rows.
     float kv[AU][8];
     auto issue = [&](const KV * base, int r0) {
 #pragma unroll
         for (int u = 0; u < AU; u++) {
+            // rows past the chunk re-read its last row: their scores are not stored, their V rows
+            // not accumulated
             const int row = r0 + (u * AW + wave) * RPW + slot;
-            if (row < rows && dl) load8<KV>(base + (int64_t) row * a.rs, kv[u]);
-            else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) kv[u][e] = 0.f;
-            }
+            load8<KV>(base + (int64_t) (row < rows ? row : rows - 1) * a.rs, kv[u]);
         }
     };
     issue(Kg, 0);
-    if (t < nq) *(float4 *) (qs + 4 * t) = qv;
+    if (t < nq) *(float4 *) (qs + 4 * t) = qok ? qv : make_float4(0.f, 0.f, 0.f, 0.f);
     __builtin_amdgcn_s_waitcnt(0xc07f);                                 // lgkmcnt(0): the LDS stores
     __builtin_amdgcn_s_barrier();
     float qr[HG][8];
