@@ -3,7 +3,6 @@
 The product is libonpu_hip.so (opennpu_amd/csrc, C ABI in include/onpu.h): hand-written HIP
 kernels for gfx950 behind the reference's libonpu entry points. Python modules:
   _lib       loads the library and declares its ABI
-  npu4       the reference's Python operator surface (Mat, NPULinearGroup, NPUExperts, ...)
   device     torch-tensor wrappers over the device-pointer entry points
   synthetic  seeded inputs with the benchmark distributions
   build      hipcc build of the library

@@ -116,8 +116,12 @@ struct Ffn {
 int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
 
 Mat4 * make_mat(int64_t N, int64_t K, int64_t E, int fmt, int64_t sstride) {
-    if (!device().ok || !fmt_valid(fmt) || N <= 0 || K <= 0 || E <= 0 || K % fmt_group(fmt) != 0) return nullptr;
-    if (sstride < stage_bytes(fmt, N, K)) return nullptr;
+    if (!device().ok) { set_err("no usable gfx950 GPU"); return nullptr; }
+    if (!fmt_valid(fmt) || N <= 0 || K <= 0 || E <= 0 || K % fmt_group(fmt) != 0) {
+        set_err("matrix shape or weight format not supported");
+        return nullptr;
+    }
+    if (sstride < stage_bytes(fmt, N, K)) { set_err("staging buffer smaller than the staging layout"); return nullptr; }
     auto * m = new Mat4;
     m->fmt = fmt;
     m->N = N;
@@ -126,7 +130,8 @@ Mat4 * make_mat(int64_t N, int64_t K, int64_t E, int fmt, int64_t sstride) {
     m->g = tiled_geom(fmt, N, K);
     m->dstride = round_up(m->g.bytes, 256);
     m->sstride = sstride;
-    if (hipMalloc((void **) &m->dev, (size_t) (m->dstride * E)) != hipSuccess) {
+    if (const hipError_t e = hipMalloc((void **) &m->dev, (size_t) (m->dstride * E)); e != hipSuccess) {
+        set_err("hipMalloc of the weights", e);
         delete m;
         return nullptr;
     }
@@ -554,7 +559,7 @@ int64_t onpu_stage_bytes(int fmt, int64_t N, int64_t K) {
 // ---------------------------------------------------------------- dense
 void * onpu_dense_new2(int64_t N, int64_t K, int sym) {
     const RefGeom g = ref_geometry(N, K, 8, sym != 0);
-    if (!g.ok) return nullptr;
+    if (!g.ok) { set_err("onpu_dense_new2: the shape has no reference geometry"); return nullptr; }
     return make_mat(N, K, 1, sym, g.nbytes);
 }
 void * onpu_dense_new(int64_t N, int64_t K) { return onpu_dense_new2(N, K, 0); }
@@ -640,7 +645,7 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
 // ---------------------------------------------------------------- banks
 void * onpu_bank_new2(int64_t N, int64_t K, int64_t E, int ncols, int sym) {
     const RefGeom g = ref_geometry(N, K, ncols, sym != 0);
-    if (!g.ok) return nullptr;
+    if (!g.ok) { set_err("onpu_bank_new2: the shape has no reference geometry"); return nullptr; }
     return make_mat(N, K, E, sym, g.nbytes);
 }
 void * onpu_bank_new(int64_t N, int64_t K, int64_t E, int ncols) { return onpu_bank_new2(N, K, E, ncols, 0); }
@@ -785,7 +790,7 @@ static void * ffn_make(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E
 
 void * onpu_ffn_new(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int sym) {
     const RefGeom gg = ref_geometry(Ng, Kg, 1, sym != 0), gd = ref_geometry(Nd, Kd, 1, sym != 0);
-    if (!gg.ok || !gd.ok) return nullptr;
+    if (!gg.ok || !gd.ok) { set_err("onpu_ffn_new: a shape has no reference geometry"); return nullptr; }
     return ffn_make(Ng, Kg, Nd, Kd, E, sym, gg.nbytes, gd.nbytes);
 }
 void * onpu_ffn_new3(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int fmt) {

@@ -251,7 +251,7 @@ def test_geometry_known_values(N, K, ncols, want):
             assert g == w, (got, want)
 
 
-# ------------------------------------------------------------------ search quantizers (invariants only)
+# ------------------------------------------------------------------ search quantizers
 def test_quant_sym32_exact_grid_round_trip():
     """groups that are exactly v * d (d a power of two, v spanning -8..7) come back exactly;
     the exact scale choice on general inputs stays parity unpinned"""
@@ -277,6 +277,103 @@ def test_quant_asym32_exact_grid_round_trip():
         q, sb, mb = orc.quant_asym32((u * s + m).astype(np.float32))
         sf, mf = orc.bf2f(np.array([sb, mb], np.uint16))
         assert np.array_equal((q * sf + mf).astype(np.float32), (u * s + m).astype(np.float32))
+
+
+def _groups(rng, n, g):
+    """groups of g weights with the shapes a quantizer meets: Gaussian, heavy-tailed, one outlier,
+    repeated magnitudes of both signs (ties for the largest |x|), a few exact zeros"""
+    out = []
+    for t in range(n):
+        kind = t % 5
+        if kind == 0:
+            x = rng.standard_normal(g) * 0.02
+        elif kind == 1:
+            x = rng.standard_t(2, g) * 0.01
+        elif kind == 2:
+            x = rng.standard_normal(g) * 0.01
+            x[rng.integers(0, g)] = rng.choice([-1, 1]) * 0.3
+        elif kind == 3:
+            x = rng.choice([-3, -1, 0, 2, 3], g) * 0.004
+        else:
+            x = rng.standard_normal(g) * 0.05
+            x[rng.integers(0, g, 3)] = 0.0
+        out.append(x.astype(np.float32))
+    return out
+
+
+def _bf_times(b, j):
+    """bf16 bits of 2^j times the bf16 value b (exact away from under- and overflow)"""
+    return int(orc.f2bf(np.array([orc.bf2f(np.array([b], np.uint16))[0] * np.float32(2.0 ** j)], np.float32))[0])
+
+
+@pytest.mark.parametrize("g", [32, 128])
+def test_quant_sym_sign_symmetry(g):
+    """q4s / g128s: quantizing -x gives the same codes and the negated scale, bit for bit (every
+    step of the search is odd in x: the signed absmax, x / d, the refit sum(v x) / sum(v v) and bf16
+    rounding; the squared errors are even). A quantizer that took |max|, clamped asymmetrically in
+    the wrong direction or biased a refit would break it."""
+    rng = np.random.default_rng(60 + g)
+    fn = orc.quant_sym32 if g == 32 else orc.quant_sym
+    for x in _groups(rng, 400, g):
+        q, d = fn(x)
+        qn, dn = fn(-x)
+        assert np.array_equal(q, qn) and dn == d ^ 0x8000, (x, q, qn, hex(d), hex(dn))
+
+
+@pytest.mark.parametrize("g", [32, 128])
+@pytest.mark.parametrize("j", [-5, -1, 1, 3])
+def test_quant_sym_power_of_two_equivariance(g, j):
+    """q4s / g128s: quant(2^j x) = (codes, 2^j d) exactly: each step scales exactly by a power of two
+    away from under- and overflow, so an absolute epsilon, a constant added to a refit or a scale
+    rounded before scaling would break it"""
+    rng = np.random.default_rng(70 + g + j)
+    fn = orc.quant_sym32 if g == 32 else orc.quant_sym
+    for x in _groups(rng, 300, g):
+        q, d = fn(x)
+        q2, d2 = fn((x * np.float32(2.0 ** j)).astype(np.float32))
+        assert np.array_equal(q, q2) and d2 == _bf_times(d, j), (j, hex(d), hex(d2))
+
+
+@pytest.mark.parametrize("j", [-4, -1, 2, 5])
+def test_quant_asym32_power_of_two_equivariance(j):
+    """q4nx: quant(2^j x) = (codes, 2^j s, 2^j m) exactly (the stretched grids divide by the range,
+    the least-squares refit is homogeneous of degree one in x)"""
+    rng = np.random.default_rng(80 + j)
+    for x in _groups(rng, 300, 32):
+        q, s, m = orc.quant_asym32(x)
+        q2, s2, m2 = orc.quant_asym32((x * np.float32(2.0 ** j)).astype(np.float32))
+        assert np.array_equal(q, q2), j
+        assert s2 == _bf_times(s, j) and m2 == _bf_times(m, j), (j, hex(s), hex(s2), hex(m), hex(m2))
+
+
+def test_quant_q4_0_sign_and_scale_symmetry():
+    """ggml's Q4_0 rule: -x gives the same codes and -d; 2^j x gives the same codes and 2^j d"""
+    rng = np.random.default_rng(90)
+    for x in _groups(rng, 300, 32):
+        q, d = orc.quant_q4_0(x)
+        qn, dn = orc.quant_q4_0(-x)
+        assert np.array_equal(q, qn) and dn == d ^ 0x8000
+        for j in (-2, 3):
+            q2, d2 = orc.quant_q4_0((x * np.float32(2.0 ** j)).astype(np.float32))
+            want = np.array([np.array([d], np.uint16).view(np.float16)[0] * np.float16(2.0 ** j)], np.float16)
+            assert np.array_equal(q, q2) and d2 == int(want.view(np.uint16)[0])
+
+
+def test_quant_q4_0_half_way_inputs_truncate():
+    """ggml computes a code as (int8_t)(x / d + 8.5) with d = max / -8: a truncation, so an input
+    exactly half-way between two grid points rounds up (x / d = k + 1/2 -> k + 9), where a
+    round-to-nearest-even quantizer gives k + 8 for even k. With max = -8 (d = 1) the products are
+    exact: x = 0.5 -> 9, 2.5 -> 11, -1.5 -> 7, -7.5 -> 1, 6.5 -> 15 (rint: 8, 10, 6, 0, 14)"""
+    x = np.zeros(32, np.float32)
+    x[0] = -8.0
+    halves = [0.5, 1.5, 2.5, 3.5, -0.5, -1.5, -2.5, -7.5, 6.5, 4.5]
+    x[1:1 + len(halves)] = halves
+    q, dh = orc.quant_q4_0(x)
+    assert np.array([dh], np.uint16).view(np.float16)[0] == 1.0
+    want = [min(15, int(np.floor(h + 8.5))) for h in halves]
+    assert list(q[1:1 + len(halves)]) == want
+    assert (q[1], q[3], q[6], q[8], q[9]) == (9, 11, 7, 1, 15)     # round-half-even: 8, 10, 6, 0, 14
+    assert q[0] == 0 and (q[1 + len(halves):] == 8).all()
 
 
 def test_oracle_rejects_shapes_outside_the_format():
