@@ -124,6 +124,14 @@ int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
 /* logits fp32 [M][N] and argmax [M] (first maximum) */
 int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream);
+/* onpu_dense_argmax_dev for callers that cannot allocate (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc); no counterpart in the reference. It allocates nothing:
+ * the argmax's counters and keys live in a 1 MiB device array of the library, one per GPU, set up
+ * when the library initialises. Limits: M <= 64 (the GEMV path) and M * ceil(N / 4096) <= 8064;
+ * beyond them it returns -1 with the reason in onpu_last_error. Calls that overlap on one GPU
+ * share the array and race: order them on one stream. */
+int onpu_dense_argmax_dev_noalloc(void * h, const void * x, int64_t M, float * logits, int32_t * argmax,
+                                  void * stream);
 /* router: logits fp32 [T][E] -> ids [T][k], w [T][k] (softmax, top-k by probability, ties to the
  * lower id, renormalised when renorm != 0) */
 int onpu_moe_route_dev(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,

@@ -50,6 +50,7 @@ struct Device {
     int ok = 0;
     int cus = 0;
     hipStream_t stream = nullptr;
+    hipError_t scratch = hipErrorNotInitialized;   // set-up of the argmax scratch array on device 0
 };
 
 Device & device() {
@@ -68,6 +69,8 @@ Device & device() {
         if (hipSetDevice(0) != hipSuccess) return;
         d.cus = p.multiProcessorCount;
         if (hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking) != hipSuccess) return;
+        // the no-allocation argmax's scratch array on device 0: its address and zeroed counters
+        d.scratch = argmax_scratch_init();
         d.ok = 1;
     });
     return d;
@@ -327,19 +330,22 @@ hipError_t gsk_workspace(Mat4 * m) {
     return hipSuccess;
 }
 
+// the decode GEMV (M <= 64 rows): no workspace
+hipError_t gemv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
+    const Plan p = plan_gemv(m->fmt, m->g.NT, m->g.KB, (int) M, 1, EPI_STORE_);
+    QArgs a{};
+    a.W = m->dev + e * m->dstride; a.estride = 0; a.ids = nullptr;
+    a.N = m->N; a.K = m->K; a.NT = m->g.NT; a.KB = m->g.KB;
+    a.x = x; a.ldx = m->K; a.xslot = 0; a.xdiv = 1; a.M = (int) M;
+    a.y = y; a.ldy = m->N; a.yslot = 0; a.yf32 = yf32;
+    a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
+    return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
+}
+
 hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
     if (M <= 0) return hipSuccess;
     const uint8_t * W = m->dev + e * m->dstride;
-    if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0) {
-        const Plan p = plan_gemv(m->fmt, m->g.NT, m->g.KB, (int) M, 1, EPI_STORE_);
-        QArgs a{};
-        a.W = W; a.estride = 0; a.ids = nullptr;
-        a.N = m->N; a.K = m->K; a.NT = m->g.NT; a.KB = m->g.KB;
-        a.x = x; a.ldx = m->K; a.xslot = 0; a.xdiv = 1; a.M = (int) M;
-        a.y = y; a.ldy = m->N; a.yslot = 0; a.yf32 = yf32;
-        a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
-        return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
-    }
+    if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0) return gemv_core(m, e, x, M, y, yf32, s);
     int cfg = 0;
     int64_t grid = 0;
     GArgs ga{};
@@ -639,6 +645,30 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
     HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
     HIPR(launch_argmax(logits, M, m->N, argmax, m->ws[5].as<uint64_t>(), m->am_cnt.as<uint32_t>(),
                        (hipStream_t) stream));
+    return 0;
+}
+
+int onpu_dense_argmax_dev_noalloc(void * h, const void * x, int64_t M, float * logits, int32_t * argmax,
+                                  void * stream) {
+    auto * m = (Mat4 *) h;
+    if (M <= 0) return 0;
+    if (M > 64) {
+        set_err("onpu_dense_argmax_dev_noalloc: at most 64 rows (more would run the prefill GEMM, whose "
+                "workspace is allocated)");
+        return -1;
+    }
+    uint64_t * keys = nullptr;
+    uint32_t * cnt = nullptr;
+    if (const hipError_t e = argmax_scratch_get(M, m->N, &keys, &cnt); e != hipSuccess) {
+        if (e == hipErrorInvalidValue)
+            set_err("onpu_dense_argmax_dev_noalloc: M x ceil(N / 4096) exceeds the 8064 keys of the 1 MiB "
+                    "scratch array");
+        else
+            set_err("onpu_dense_argmax_dev_noalloc: scratch array", e);
+        return -1;
+    }
+    HIPR(gemv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
+    HIPR(launch_argmax(logits, M, m->N, argmax, keys, cnt, (hipStream_t) stream));
     return 0;
 }
 

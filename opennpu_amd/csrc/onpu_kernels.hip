@@ -1,5 +1,7 @@
 // Format-independent kernels of libonpu_hip (router, MoE permutation and combine, argmax, input
 // conversion, the host-API MoE helpers) and the launchers that dispatch the per-format ones.
+#include <mutex>
+
 #include "onpu_kern.h"
 
 // one wave per token: softmax over E <= 256 logits, top-k by probability (ties to the lower id),
@@ -481,6 +483,55 @@ hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float 
 }
 
 int64_t argmax_parts(int64_t N) { return (N + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
+
+// ------------------------------------------------------------------ argmax scratch without allocation
+// For callers that cannot allocate (graph capture, serving loops): the argmax's row counters and
+// per-workgroup keys live in this file-scope array, ARGMAX_SCRATCH_BYTES per GPU, held until the
+// process ends. Counters first (ARGMAX_SCRATCH_CNT bytes, zeroed once per device at set-up; every
+// call leaves them at zero), then the keys. In host code `scratch` is only a stand-in for the
+// device array: kernels get the address that hipGetSymbolAddress returns for the current device.
+// Calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) uint8_t scratch[ARGMAX_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void * g_scratch_dev[ARGMAX_SCRATCH_MAX_DEVICES];      // the array's address on each device
+}
+
+hipError_t argmax_scratch_init() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= ARGMAX_SCRATCH_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_dev[dev]) return hipSuccess;
+    void * p = nullptr;
+    if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+    if ((e = hipMemset(p, 0, ARGMAX_SCRATCH_CNT)) != hipSuccess) return e;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    g_scratch_dev[dev] = p;
+    return hipSuccess;
+}
+
+hipError_t argmax_scratch_get(int64_t rows, int64_t N, uint64_t ** keys, uint32_t ** cnt) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= ARGMAX_SCRATCH_MAX_DEVICES) return hipErrorInvalidDevice;
+    void * p = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch_dev[dev];
+    }
+    if (!p) return hipErrorNotInitialized;      // set-up (argmax_scratch_init) not run on this device
+    if (rows * ARGMAX_PAD > ARGMAX_SCRATCH_CNT ||
+        rows * argmax_parts(N) * ARGMAX_PAD > (int64_t) (ARGMAX_SCRATCH_BYTES - ARGMAX_SCRATCH_CNT))
+        return hipErrorInvalidValue;
+    *cnt = (uint32_t *) p;
+    *keys = (uint64_t *) ((uint8_t *) p + ARGMAX_SCRATCH_CNT);
+    return hipSuccess;
+}
+
 
 hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, uint64_t * keys, uint32_t * cnt,
                          hipStream_t s) {

@@ -150,6 +150,15 @@ hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float 
 // the first call (each call leaves them at zero). Calls that overlap must not share keys / cnt.
 constexpr int ARGMAX_THREADS = 256, ARGMAX_CHUNK = 16 * ARGMAX_THREADS, ARGMAX_PAD = 128;
 int64_t argmax_parts(int64_t N);
+// the argmax's counters and keys in a static device array (no allocation): ARGMAX_SCRATCH_BYTES
+// per GPU, counters (zero between calls) in the first ARGMAX_SCRATCH_CNT bytes. init: once per
+// device with that device current (hipGetSymbolAddress, counters zeroed); get: the current device's
+// counters and keys for `rows` rows of N values, hipErrorInvalidValue past the array's size,
+// hipErrorNotInitialized before init on this device.
+constexpr int64_t ARGMAX_SCRATCH_BYTES = 1 << 20, ARGMAX_SCRATCH_CNT = 16384;
+constexpr int ARGMAX_SCRATCH_MAX_DEVICES = 64;
+hipError_t argmax_scratch_init();
+hipError_t argmax_scratch_get(int64_t rows, int64_t N, uint64_t ** keys, uint32_t ** cnt);
 hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, uint64_t * keys, uint32_t * cnt,
                          hipStream_t s);
 // GPU weight codecs (onpu_codec.hip): W [ne][N][ldw] fp32 (wbf16 = 0) or bf16 -> ne staging buffers of
