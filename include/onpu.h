@@ -207,18 +207,24 @@ int onpu_attn_step_dev(const float * q, int Hq, int D, const void * K, const voi
  * engine likewise runs a token's products in one NPU dispatch). A chain is n dense GEMVs
  * y_i [M][N_i] = x_i [M][K_i] . W_i^T fixed at creation (handles, x and y device pointers; one
  * weight format; 1 <= M <= 16; y bf16 or fp32); onpu_chain_run executes them in order in ONE launch
- * on `stream`, with a grid-wide barrier between entries, so x_i may be the y_j of an earlier entry.
- * Weights stream ahead through each workgroup's LDS, across the barriers. All workgroups must be
- * resident together: do not run other kernels concurrently with a chain on the same GPU. A barrier
+ * on `stream`. An x_j that lies in an earlier entry's bf16 output y_i (the whole of y_i with
+ * K_j == N_i, or at M = 1 a range of it starting on an 8-element boundary) is read once entry i has
+ * written that part of y_i in this run: workgroups wait on the data itself, not on a grid barrier. Every
+ * other x is read as it was when the launch started; onpu_chain_new refuses (NULL) an x that
+ * overlaps an output in any other way and outputs that overlap. Weights stream ahead through each
+ * workgroup's LDS while it waits. All workgroups must be resident together: do not run other kernels
+ * concurrently with a chain on the same GPU, and keep runs of one chain ordered on one stream. A
  * wait that exceeds its poll limit (about 0.1 s) gives up rather than hanging; onpu_chain_status
  * then reports 1 (results invalid). The launch is capturable in a HIP graph. */
 void * onpu_chain_new(void * const * handles, const void * const * xs, void * const * ys, int n, int64_t M,
                       int y_f32);
 int onpu_chain_run(void * chain, void * stream);
-int onpu_chain_status(void * chain);   /* synchronises the device; 0 ok, 1 a barrier timed out, -1 error */
+/* synchronises the device; 0 ok, 1 a wait timed out since the last call (the flag is then cleared),
+ * -1 error */
+int onpu_chain_status(void * chain);
 void onpu_chain_info(void * chain, int64_t * out /* [6]: n, workgroups, LDS bytes, x row stride,
-                                                   weight-ring blocks per wave, barrier arrivals of the
-                                                   last run, (n - 1) x workgroups when whole (synchronises) */);
+                                                   weight-ring blocks per wave, runs completed
+                                                   (synchronises) */);
 void onpu_chain_free(void * chain);
 
 #ifdef __cplusplus

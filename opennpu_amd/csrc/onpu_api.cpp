@@ -914,8 +914,13 @@ struct Chain {
     int fmt = 0, n = 0, M = 0, yf32 = 0, grid = 0, ring = 0;
     size_t lds = 0;
     int64_t xls = 0, ring_off = 0;
-    DBuf entries, bar;
+    DBuf entries, ep, links;
 };
+
+namespace {
+struct Span { uintptr_t a, b; };          // byte range [a, b)
+bool overlap(Span u, Span v) { return u.a < v.b && v.a < u.b; }
+}
 
 void * onpu_chain_new(void * const * handles, const void * const * xs, void * const * ys, int n, int64_t M,
                       int y_f32) {
@@ -923,6 +928,7 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
     const int fmt = ((Mat4 *) handles[0])->fmt;
     int64_t kbmax = 0;
     std::vector<ChainEntry> es((size_t) n);
+    std::vector<Span> xr((size_t) n), yr((size_t) n);
     for (int i = 0; i < n; i++) {
         const Mat4 * m = (const Mat4 *) handles[i];
         if (m->fmt != fmt || m->E != 1) { set_err("onpu_chain_new: entries need one format and dense handles"); return nullptr; }
@@ -931,6 +937,7 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
             return nullptr;
         }
         ChainEntry & e = es[(size_t) i];
+        e = ChainEntry{};
         e.W = m->dev; e.x = (const uint16_t *) xs[i]; e.y = ys[i];
         e.NT = m->g.NT; e.KB = m->g.KB; e.N = m->N; e.K = m->K;
         // K split across 8 waves for up to 512 row tiles, else 4 (2 tiles per workgroup), else 2
@@ -940,7 +947,53 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
         e.bpw = (e.KB + e.kw - 1) / e.kw;
         e.groups = (e.NT + e.tw - 1) / e.tw;
         kbmax = std::max(kbmax, e.KB);
+        xr[(size_t) i] = {(uintptr_t) xs[i], (uintptr_t) xs[i] + (uintptr_t) (M * m->K * 2)};
+        yr[(size_t) i] = {(uintptr_t) ys[i], (uintptr_t) ys[i] + (uintptr_t) (M * m->N * (y_f32 ? 4 : 2))};
     }
+    // x_j that lies in an earlier y_i reads it through y_i's link words: the whole row (x_j == y_i,
+    // K_j == N_i) or, at M = 1, a range of it starting on an 8-element boundary. Any other overlap of
+    // an x with a y, or of two ys, would be read while written and is refused.
+    std::vector<int> src((size_t) n, -1);
+    std::vector<int64_t> xoff((size_t) n, 0);
+    for (int j = 0; j < n; j++) {
+        for (int i = 0; i < n; i++) {
+            if (i != j && overlap(yr[(size_t) i], yr[(size_t) j])) {
+                set_err("onpu_chain_new: two entries' outputs overlap");
+                return nullptr;
+            }
+            if (!overlap(xr[(size_t) j], yr[(size_t) i])) continue;
+            const ChainEntry & P = es[(size_t) i];
+            const ChainEntry & C = es[(size_t) j];
+            const uintptr_t d = xr[(size_t) j].a - yr[(size_t) i].a;
+            const bool inside = xr[(size_t) j].a >= yr[(size_t) i].a && xr[(size_t) j].b <= yr[(size_t) i].b;
+            const bool whole = d == 0 && C.K == P.N;
+            const bool range = M == 1 && inside && d % 16 == 0 && (int64_t) (d / 2) + C.K <= P.N;
+            if (i >= j || y_f32 || !(whole || range) || src[(size_t) j] >= 0) {
+                set_err(i >= j ? "onpu_chain_new: an entry reads memory that it or a later entry writes"
+                               : "onpu_chain_new: an entry reads part of an earlier output in a layout the chain "
+                                 "cannot link (bf16 outputs; the whole output, or at M = 1 a range of it starting "
+                                 "on an 8-element boundary)");
+                return nullptr;
+            }
+            src[(size_t) j] = i;
+            xoff[(size_t) j] = (int64_t) (d / 2);
+        }
+    }
+    if (src[0] >= 0) { set_err("onpu_chain_new: the first entry cannot read a chained output"); return nullptr; }
+    for (int j = 0; j < n; j++)
+        if (src[(size_t) j] < 0 && xr[(size_t) j].a % 16 != 0) {
+            set_err("onpu_chain_new: an input x must start on a 16-byte boundary");
+            return nullptr;
+        }
+    // link words for every output that a later entry reads: rows of whole tiles
+    std::vector<int64_t> loff((size_t) n, -1);
+    int64_t lbytes = 0;
+    for (int j = 0; j < n; j++)
+        if (src[(size_t) j] >= 0 && loff[(size_t) src[(size_t) j]] < 0) {
+            const int i = src[(size_t) j];
+            loff[(size_t) i] = lbytes;
+            lbytes += M * es[(size_t) i].NT * 16 * 4;
+        }
     auto * c = new Chain;
     c->fmt = fmt; c->n = n; c->M = (int) M; c->yf32 = y_f32;
     c->xls = kbmax * 128 + 8;
@@ -948,17 +1001,36 @@ void * onpu_chain_new(void * const * handles, const void * const * xs, void * co
     c->ring_off = (int64_t) 2 * CHAIN_WAVES * 256 * 4 + M * c->xls * 2 + kbmax * (fmt == ONPU_G128S ? 1 : 4) * 64;
     const int64_t blk = fmt_blk(fmt);
     c->ring = -1;
-    for (int ri = 0; ri < 3 && c->ring < 0; ri++) {
+    for (int ri = 0; ri < 4 && c->ring < 0; ri++) {
         const size_t lds = (size_t) (c->ring_off + (int64_t) CHAIN_WAVES * CHAIN_RING_SLOTS[ri] * blk);
         if (lds <= 163840 && chain_occupancy(fmt, ri, lds) >= 1) { c->ring = ri; c->lds = lds; }
     }
     if (c->ring < 0) { set_err("onpu_chain_new: x rows do not fit in LDS"); delete c; return nullptr; }
     c->grid = device().cus;                // one workgroup per CU: the ring takes most of its LDS
-    hipError_t e = c->entries.ensure(sizeof(ChainEntry) * (size_t) n);
-    if (e == hipSuccess) e = c->bar.ensure(sizeof(int32_t) * (size_t) CHAIN_BAR_INTS);
+    hipError_t e = c->ep.ensure(sizeof(int32_t) * (size_t) CHAIN_EP_INTS);
+    if (e == hipSuccess) e = hipMemset(c->ep.p, 0, sizeof(int32_t) * (size_t) CHAIN_EP_INTS);
+    if (e == hipSuccess && lbytes > 0) e = c->links.ensure((size_t) lbytes);
+    if (e == hipSuccess && lbytes > 0) e = hipMemset(c->links.p, 0, (size_t) lbytes);   // epoch 0: no run's tag
+    if (e == hipSuccess) {
+        for (int i = 0; i < n; i++)
+            if (loff[(size_t) i] >= 0) es[(size_t) i].ly = c->links.as<uint32_t>((size_t) loff[(size_t) i]);
+        for (int j = 0; j < n; j++) {
+            const int i = src[(size_t) j];
+            if (i < 0) continue;
+            ChainEntry & C = es[(size_t) j];
+            C.ldl = es[(size_t) i].NT * 16;
+            C.lx = es[(size_t) i].ly + xoff[(size_t) j];
+            C.x = nullptr;
+        }
+        e = c->entries.ensure(sizeof(ChainEntry) * (size_t) n);
+    }
     if (e == hipSuccess) e = hipMemcpy(c->entries.p, es.data(), sizeof(ChainEntry) * (size_t) n, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(c->bar.p, 0, sizeof(int32_t) * (size_t) CHAIN_BAR_INTS);
-    if (e != hipSuccess) { set_err(hipGetErrorString(e)); delete c; return nullptr; }
+    if (e != hipSuccess) {
+        set_err(hipGetErrorString(e));
+        c->entries.release(); c->ep.release(); c->links.release();
+        delete c;
+        return nullptr;
+    }
     return c;
 }
 
@@ -966,7 +1038,8 @@ int onpu_chain_run(void * h, void * stream) {
     auto * c = (Chain *) h;
     ChainArgs a{};
     a.n = c->n; a.M = c->M; a.yf32 = c->yf32;
-    a.bar = c->bar.as<int32_t>(); a.xls = c->xls; a.ring = c->ring_off; a.spin = 4u << 20;
+    a.ep = c->ep.as<int32_t>(); a.xls = c->xls; a.ring = c->ring_off;
+    a.spin = 1u << 17;                     // polls of one wait: ~0.1-0.3 s, then the error flag
     HIPR(launch_chain(c->fmt, c->ring, a, c->entries.as<ChainEntry>(), c->grid, c->lds, (hipStream_t) stream));
     return 0;
 }
@@ -974,9 +1047,9 @@ int onpu_chain_run(void * h, void * stream) {
 int onpu_chain_status(void * h) {
     auto * c = (Chain *) h;
     int32_t flag = 0;
-    if (hipDeviceSynchronize() != hipSuccess ||
-        hipMemcpy(&flag, c->bar.as<int32_t>(sizeof(int32_t) * (size_t) (CHAIN_BAR_INTS - 1)), 4, hipMemcpyDeviceToHost) != hipSuccess)
-        return -1;
+    int32_t * fp = c->ep.as<int32_t>(sizeof(int32_t) * CHAIN_EP_ERR);
+    if (hipDeviceSynchronize() != hipSuccess || hipMemcpy(&flag, fp, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (flag && hipMemset(fp, 0, 4) != hipSuccess) return -1;
     return flag ? 1 : 0;
 }
 
@@ -984,21 +1057,19 @@ void onpu_chain_info(void * h, int64_t * out) {
     auto * c = (Chain *) h;
     out[0] = c->n; out[1] = c->grid; out[2] = (int64_t) c->lds; out[3] = c->xls;
     out[4] = CHAIN_RING_SLOTS[c->ring];
-    std::vector<int32_t> ctr((size_t) CHAIN_BAR_INTS, 0);
-    int64_t arrivals = -1;
-    if (hipDeviceSynchronize() == hipSuccess &&
-        hipMemcpy(ctr.data(), c->bar.p, sizeof(int32_t) * ctr.size(), hipMemcpyDeviceToHost) == hipSuccess) {
-        arrivals = 0;
-        for (int j = 0; j < CHAIN_CTRS; j++) arrivals += ctr[(size_t) j * CHAIN_CTR_STRIDE];
-    }
-    out[5] = arrivals;                     // barrier arrivals of the last run: (n - 1) * grid when whole
+    uint32_t epoch = 0;
+    out[5] = hipDeviceSynchronize() == hipSuccess &&
+                     hipMemcpy(&epoch, c->ep.p, 4, hipMemcpyDeviceToHost) == hipSuccess
+                 ? (int64_t) epoch
+                 : -1;                     // runs completed (mod 2^32)
 }
 
 void onpu_chain_free(void * h) {
     auto * c = (Chain *) h;
     if (!c) return;
     c->entries.release();
-    c->bar.release();
+    c->ep.release();
+    c->links.release();
     delete c;
 }
 

@@ -71,7 +71,7 @@ hipError_t FN(moe_gemm)(int which, int wv, const MArgs & a, dim3 grid, hipStream
 
 template <int S>
 static hipError_t chain_s(const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds, hipStream_t s) {
-    k_qgemv_chain<F, S><<<grid, (CHAIN_WAVES + 1) * 64, lds, s>>>(a, ents);
+    k_qgemv_chain<F, S><<<grid, (CHAIN_WAVES + CHAIN_CTRL) * 64, lds, s>>>(a, ents);
     return hipGetLastError();
 }
 
@@ -80,6 +80,7 @@ hipError_t FN(chain)(int ring, const ChainArgs & a, const ChainEntry * ents, int
         case 0: return chain_s<CHAIN_RING_SLOTS[0]>(a, ents, grid, lds, s);
         case 1: return chain_s<CHAIN_RING_SLOTS[1]>(a, ents, grid, lds, s);
         case 2: return chain_s<CHAIN_RING_SLOTS[2]>(a, ents, grid, lds, s);
+        case 3: return chain_s<CHAIN_RING_SLOTS[3]>(a, ents, grid, lds, s);
     }
     return hipErrorInvalidValue;
 }
@@ -87,7 +88,8 @@ hipError_t FN(chain)(int ring, const ChainArgs & a, const ChainEntry * ents, int
 template <int S>
 static int chain_occ_s(size_t lds) {
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qgemv_chain<F, S>, (CHAIN_WAVES + 1) * 64, lds) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_qgemv_chain<F, S>, (CHAIN_WAVES + CHAIN_CTRL) * 64, lds) !=
+        hipSuccess)
         return 0;
     return nb;
 }
@@ -97,6 +99,7 @@ int FN(chain_occ)(int ring, size_t lds) {
         case 0: return chain_occ_s<CHAIN_RING_SLOTS[0]>(lds);
         case 1: return chain_occ_s<CHAIN_RING_SLOTS[1]>(lds);
         case 2: return chain_occ_s<CHAIN_RING_SLOTS[2]>(lds);
+        case 3: return chain_occ_s<CHAIN_RING_SLOTS[3]>(lds);
     }
     return 0;
 }

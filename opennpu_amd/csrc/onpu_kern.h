@@ -1586,142 +1586,184 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
 
 // ------------------------------------------------------------------ chained decode GEMVs
 // One launch runs a.n GEMVs in order (M <= 16 rows, x staged in LDS), one workgroup per CU of
-// CHAIN_WAVES compute waves + one control wave. Entry i's tile groups (tw tiles x kw K parts,
-// tw kw = CHAIN_WAVES) go to workgroups g = blockIdx.x, + gridDim.x, ...
-// Weights stream through a ring of S block slots per compute wave, filled by buffer-to-LDS loads.
-// A wave's sequence of blocks over the whole chain is known up front (weights do not depend on x),
-// so the ring is refilled with the next block of the sequence as each block is consumed and keeps
-// S blocks in flight across entry boundaries and grid barriers: HBM streams while the grid waits.
-// Between entries every workgroup meets at a grid barrier (entry i + 1 may read entry i's output):
-//   compute waves: leave their partial sums in LDS; besides the ring's loads they only load x in
-//     the staging and wait for those loads completely, so the ring's wait count stays exact
-//   control wave: sums the K parts, stores y (agent-scope stores), waits for its stores, arrives
-//     and polls (chain_barrier; bounded: past a.spin polls it sets the error flag and proceeds, so
-//     no wave can wait forever)
-//   all waves: stage x_{i+1} (agent-scope loads) and its column sums in LDS.
+// CHAIN_WAVES compute waves and CHAIN_CTRL control waves. Entry i's tile groups (tw tiles x kw K
+// parts, tw kw = CHAIN_WAVES) go to workgroups g = blockIdx.x, + gridDim.x, ...
+// Compute waves: weights stream through a ring of S block slots per wave, filled by buffer-to-LDS
+//   loads. A wave's sequence of blocks over the whole chain is known up front (weights do not depend
+//   on x), so the ring is refilled with the next block of the sequence as each block is consumed and
+//   keeps S blocks in flight across entry boundaries: HBM streams while a workgroup waits for x. The
+//   compute waves issue no other memory loads, so their wait counts stay exact and nothing drains
+//   the ring.
+// Control waves: sum the K parts of each tile group and store y; for an entry that a later entry
+//   reads, also publish y as link words (bf16 value << 16 | the run's 16-bit tag) with agent-scope
+//   stores. Then they stage the next entry's x into LDS: an external x with plain loads, a linked x
+//   by polling the producer's link words that it reads with agent-scope loads until every one
+//   carries this run's tag. Each 32-bit word is written and read whole, so a word with the tag holds
+//   this run's value. This is the dependency itself, seen one memory round trip after the data
+//   lands, instead of a grid barrier (store acknowledgement, arrival, poll, re-read). A poll past
+//   a.spin attempts sets the error flag and proceeds (results then wrong, the kernel still ends).
+// The run's tag is (epoch + 1) mod 2^16, epoch read from a.ep at the start; the last workgroup to
+// finish advances the epoch and resets the done counter, so a captured launch replays with fresh
+// tags and the link words never need clearing (they start at zero, epoch 0).
 // Every workgroup must be resident at once (the host sizes the grid from the occupancy).
-// x rows [M][K] (bf16) into the LDS copy xs[M][xls] and the column sums of each group of gs times
-// xmul (xsum[group][perm16(row)]: the chained GEMVs run one A block), by the whole workgroup: consecutive threads take consecutive 8-element units (coalesced loads, two per
-// thread in flight at once); a group's units sit in consecutive lanes of one wave and are summed
-// across them.
-DEV void chain_stage_x(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, float xmul,
-                       uint16_t * xs, float * xsum) {
-    const uint32_t T = blockDim.x, tid = threadIdx.x, upg = gs / 8;
-    const uint32_t kp8 = (uint32_t) KB * 16, nunits = (uint32_t) M * kp8;
-    for (uint32_t u0 = 0; u0 < nunits; u0 += 2 * T) {            // same trip count for the whole workgroup
-        uint64_t v[2][2];
+
+// x rows [M][K] (bf16, row stride K) of an external input into the LDS copy xs[M][xls] (zero past
+// K up to 128 KB) and the column sums of each group of gs times xmul (xsum[group][perm16(row)]), by
+// the T control threads (index ct): consecutive threads take consecutive 8-element units, a
+// group's units in consecutive lanes of one wave, summed across them.
+DEV void chain_stage_ext(const uint16_t * x, int M, int64_t K, int64_t KB, int64_t xls, int gs, float xmul,
+                         uint16_t * xs, float * xsum, uint32_t ct, uint32_t T) {
+    const uint32_t upg = gs / 8, kp8 = (uint32_t) KB * 16, nunits = (uint32_t) M * kp8;
+    for (uint32_t u0 = 0; u0 < nunits; u0 += 2 * T) {            // same trip count for every control lane
+        u32x4 v[2];
         uint32_t m[2], kk[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {                             // both loads first: one round trip
-            const uint32_t u = u0 + j * T + tid;
-            v[j][0] = v[j][1] = 0;
+            const uint32_t u = u0 + j * T + ct;
+            v[j] = (u32x4){0u, 0u, 0u, 0u};
             m[j] = u / kp8;
             kk[j] = (u - m[j] * kp8) * 8;
-            if (u < nunits && kk[j] < K) {
-                const auto * p = GLB(uint64_t, x + (int64_t) m[j] * K + kk[j]);
-                v[j][0] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                v[j][1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            if (u < nunits && kk[j] < K) v[j] = *GLB(const u32x4, x + (int64_t) m[j] * K + kk[j]);
         }
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const uint32_t u = u0 + j * T + tid;
-            const u32x4 w = {(uint32_t) v[j][0], (uint32_t) (v[j][0] >> 32), (uint32_t) v[j][1],
-                             (uint32_t) (v[j][1] >> 32)};
-            if (u < nunits) *LDS_U32X4(xs + (int64_t) m[j] * xls + kk[j]) = w;
+            const uint32_t u = u0 + j * T + ct;
+            if (u < nunits) *LDS_U32X4(xs + (int64_t) m[j] * xls + kk[j]) = v[j];
             float t = 0.f;
-            for (int d = 0; d < 4; d++) t += __uint_as_float(w[d] << 16) + __uint_as_float(w[d] & 0xffff0000u);
+            for (int d = 0; d < 4; d++) t += __uint_as_float(v[j][d] << 16) + __uint_as_float(v[j][d] & 0xffff0000u);
             for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
             if (u < nunits && u % upg == 0) xsum[(kk[j] / gs) * 16 + perm16((int) m[j])] = t * xmul;
         }
     }
 }
 
-// y of a chain entry is read by other workgroups after the barrier: agent-scope stores, which are
-// coherent across the XCDs' L2 caches once complete (no L2 write-back needed before arriving).
-DEV void chain_store(void * y, int yf32, int64_t idx, float v) {
-    if (yf32) __hip_atomic_store(GLB(uint32_t, y) + idx, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else __hip_atomic_store(GLB(uint16_t, y) + idx, f32_to_bf16(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// one 8-word unit of link words (agent-scope loads: coherent across the XCDs' L2 caches)
+DEV void chain_link_load(const uint32_t * p, uint64_t (&v)[4]) {
+    const auto * q = GLB(uint64_t, p);
+    for (int d = 0; d < 4; d++) v[d] = __hip_atomic_load(q + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Grid barrier of the control wave. Every wave of the workgroup has waited for its own stores to
-// complete and met at a workgroup barrier before this. Lane 0 arrives on counter w % CHAIN_CTRS;
-// lane j polls counter j until it holds epoch * (workgroups arriving on j). Both sides use
-// agent-scope atomics, and the x reads after the barrier are agent-scope loads, so no cache
-// write-back or invalidate is needed. A wait longer than spin polls sets the error flag and ends
-// the wait (the results are then wrong but the kernel still exits).
-DEV void chain_barrier(int32_t * bar, int64_t w, int64_t P, int epoch, uint32_t spin) {
-    const int lane = threadIdx.x & 63;
-    if (lane == 0) __hip_atomic_fetch_add(bar + (w % CHAIN_CTRS) * CHAIN_CTR_STRIDE, 1, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t cnt = lane < P ? (P - lane + CHAIN_CTRS - 1) / CHAIN_CTRS : 0;
-    const int32_t want = (int32_t) (cnt * epoch);
+DEV bool chain_link_ok(const uint64_t (&v)[4], uint32_t tag) {
+    const uint64_t t2 = (uint64_t) tag | ((uint64_t) tag << 32), m2 = 0x0000ffff0000ffffull;
+    return ((v[0] & m2) == t2) & ((v[1] & m2) == t2) & ((v[2] & m2) == t2) & ((v[3] & m2) == t2);
+}
+
+// poll until every lane's units (need[] false for those that need no wait) carry `tag`: the units
+// are (re)loaded until the whole wave sees them. Returns false when `spin` polls ran out or, checked
+// every 256 polls, another wave has already set the error flag (so one lost wait ends them all).
+template <int B, class Addr>
+DEV bool chain_poll(Addr addr, const bool (&need)[B], uint64_t (&v)[B][4], uint32_t tag, uint32_t spin,
+                    const int32_t * err) {
     for (uint32_t polls = 0;; polls++) {
-        const int32_t got = __hip_atomic_load(bar + lane * CHAIN_CTR_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__builtin_amdgcn_ballot_w64(got < want) == 0) break;
-        if (polls >= spin) {
-            if (lane == 0) __hip_atomic_store(bar + CHAIN_BAR_INTS - 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int b = 0; b < B; b++)
+            if (need[b]) chain_link_load(addr(b), v[b]);
+        bool ok = true;
+#pragma unroll
+        for (int b = 0; b < B; b++) ok &= !need[b] || chain_link_ok(v[b], tag);
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+        if (polls >= spin) return false;
+        if ((polls & 255u) == 255u &&
+            __hip_atomic_load(GLB(const int32_t, err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+            return false;
+        __builtin_amdgcn_s_sleep(2);
     }
 }
 
+// x of a linked entry from its producer's link words (row m of x = lx[m * ldl + 0 .. K)), staged
+// as chain_stage_ext does, each unit once all its words carry this run's tag
+DEV void chain_stage_link(const ChainEntry & E, int M, int64_t xls, int gs, float xmul, uint16_t * xs, float * xsum,
+                          uint32_t tag, uint32_t spin, int32_t * err, uint32_t ct, uint32_t T) {
+    constexpr int B = 4;
+    const uint32_t upg = gs / 8, kp8 = (uint32_t) E.KB * 16, nunits = (uint32_t) M * kp8;
+    const uint32_t K = (uint32_t) E.K, ldl = (uint32_t) E.ldl;
+    bool fine = true;
+    for (uint32_t u0 = 0; u0 < nunits; u0 += B * T) {            // same trip count for every control lane
+        bool need[B];
+        uint32_t m[B], kk[B];
+        uint64_t v[B][4];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const uint32_t u = u0 + b * T + ct;
+            m[b] = u / kp8;
+            kk[b] = (u - m[b] * kp8) * 8;
+            need[b] = u < nunits && kk[b] < K;
+            for (int d = 0; d < 4; d++) v[b][d] = 0;
+        }
+        if (!chain_poll<B>([&](int b) { return E.lx + m[b] * ldl + kk[b]; }, need, v, tag, spin, err)) {
+            fine = false;
+            spin = 0;                                 // the rest of this wait gives up at once
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const uint32_t u = u0 + b * T + ct;
+            u32x4 w = {0u, 0u, 0u, 0u};              // bf16 values: the high halves of the words
+            if (need[b])
+                for (int d = 0; d < 4; d++)
+                    w[d] = (uint32_t) (v[b][d] >> 16 & 0xffffu) | (uint32_t) (v[b][d] >> 32 & 0xffff0000u);
+            if (u < nunits) *LDS_U32X4(xs + (int64_t) m[b] * xls + kk[b]) = w;
+            float t = 0.f;
+            for (int d = 0; d < 4; d++) t += __uint_as_float(w[d] << 16) + __uint_as_float(w[d] & 0xffff0000u);
+            for (int o = upg / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
+            if (u < nunits && u % upg == 0) xsum[(kk[b] / gs) * 16 + perm16((int) m[b])] = t * xmul;
+        }
+    }
+    if (!fine) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // position in a wave's block sequence over the chain: block b (< b1) of tile t of entry e, tile
-// group g; e == a.n: past the end
+// group g; e == a.n: past the end. 32-bit throughout, so that the bookkeeping stays in scalar
+// registers (a 64-bit compare goes through vector registers, and a vector write on a path that
+// merges with outstanding loads makes the compiler wait for all of them)
 struct ChainCur {
-    int e;
-    int64_t g, t, b, b1;
-    const uint8_t * W;        // entry e's weights, its K blocks and bytes (kept so that refills
-    int64_t KB;               // load nothing but the block)
-    uint32_t bytes;
+    int e, g, t, b, b1;
+    uint32_t so;                      // byte offset of block b of tile t in entry e's weights
+    __amdgpu_buffer_rsrc_t rs;        // entry e's weights (bounds: the whole matrix)
 };
 
 // the wave's tile and K blocks [b0, b1) in tile group g of entry E (empty past the last tile)
-DEV void chain_range(const ChainEntry & E, int64_t g, int wave, int64_t & t, int64_t & b0, int64_t & b1) {
-    const int twi = wave / E.kw, kp = wave % E.kw;
+DEV void chain_range(const ChainEntry & E, int g, int wave, int & t, int & b0, int & b1) {
+    const int twi = wave / E.kw, kp = wave % E.kw, KB = (int) E.KB, bpw = (int) E.bpw;
     t = g * E.tw + twi;
-    b0 = (int64_t) kp * E.bpw;
-    b1 = b0 + E.bpw < E.KB ? b0 + E.bpw : E.KB;
-    if (t >= E.NT) b1 = b0;
+    b0 = kp * bpw;
+    b1 = b0 + bpw < KB ? b0 + bpw : KB;
+    if (t >= (int) E.NT) b1 = b0;
 }
 
 // moves c forward to the next position that holds a block, or past the end
 template <int FMT>
-DEV void chain_settle(ChainCur & c, const ChainEntry * __restrict__ ents, int n, int64_t w, int64_t P, int wave) {
+DEV void chain_settle(ChainCur & c, const ChainEntry * __restrict__ ents, int n, int w, int P, int wave) {
     while (c.e < n && c.b >= c.b1) {
         c.g += P;
-        if (c.g >= ents[c.e].groups) { c.e++; c.g = w; }
+        if (c.g >= (int) ents[c.e].groups) { c.e++; c.g = w; }
         c.b = c.b1 = 0;
-        if (c.e < n && c.g < ents[c.e].groups) {
+        if (c.e < n && c.g < (int) ents[c.e].groups) {
             const ChainEntry & E = ents[c.e];
             chain_range(E, c.g, wave, c.t, c.b, c.b1);
-            c.W = E.W;
-            c.KB = E.KB;
-            c.bytes = (uint32_t) (E.NT * E.KB * fmt_blk(FMT));
+            c.so = (uint32_t) (c.t * (int) E.KB + c.b) * (uint32_t) fmt_blk(FMT);
+            c.rs = __builtin_amdgcn_make_buffer_rsrc((void *) E.W, (short) 0, (int) (E.NT * E.KB * fmt_blk(FMT)),
+                                                     0x00020000);
         }
     }
 }
 
 // two buffer-to-LDS loads of c's block into `slot`: 1 KiB of nibbles (16 bytes per lane) and the
 // parameters (4 bytes per lane, the lanes they need); past the end both read out of range (zeros,
-// no memory traffic), so every refill counts two loads
+// no memory traffic), so every refill counts two loads. Within a tile's K range the next block is
+// the next BLK bytes; the cursor is settled only at the range's end.
 template <int FMT>
-DEV void chain_issue(ChainCur & c, const ChainEntry * __restrict__ ents, int n, int64_t w, int64_t P, int wave,
+DEV void chain_issue(ChainCur & c, const ChainEntry * __restrict__ ents, int n, int w, int P, int wave,
                      uint8_t * slot, int lane) {
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     constexpr int PW = (BLK - 1024) / 4;
     const bool live = c.e < n;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *) c.W, (short) 0, (int) c.bytes,
-                                                                         0x00020000);
-    const uint32_t so = live ? (uint32_t) ((c.t * c.KB + c.b) * BLK) : 0u;
     const uint32_t vo = live ? 16u * lane : 0x80000000u, vp = live ? 1024u + 4u * lane : 0x80000000u;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *) slot, 16, vo, so, 0, 0);
-    if (lane < PW) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *) (slot + 1024), 4, vp, so, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *) slot, 16, vo, c.so, 0, 0);
+    if (lane < PW) __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rs, (lds_void *) (slot + 1024), 4, vp, c.so, 0, 0);
     if (live) {
         c.b++;
-        chain_settle<FMT>(c, ents, n, w, P, wave);
+        c.so += BLK;
+        if (c.b >= c.b1) chain_settle<FMT>(c, ents, n, w, P, wave);
     }
 }
 
@@ -1751,43 +1793,46 @@ DEV Par<FMT> load_par_lds(const uint8_t * blk, int r) {
     return p;
 }
 
+// The two roles run separate loops with the same sequence of workgroup barriers (one after the
+// first x, one per tile group, one per entry boundary), so the compiler's wait counts on the compute
+// path never see the control waves' loads (a merged path makes it wait for every outstanding load,
+// which would drain the ring).
 template <int FMT, int S>
-__global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArgs a, const ChainEntry * __restrict__ ents) {
+__global__ __launch_bounds__((CHAIN_WAVES + CHAIN_CTRL) * 64) void k_qgemv_chain(ChainArgs a,
+                                                                                 const ChainEntry * __restrict__ ents) {
     constexpr int GS = FMT == ONPU_G128S ? 128 : 32;
     constexpr int BLK = 1024 + 16 * (128 / GS) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    constexpr uint32_t CT = CHAIN_CTRL * 64;            // control threads
     static_assert(2 * (S - 1) <= 63, "ring deeper than the load counter");
     extern __shared__ float red[];      // [2][CHAIN_WAVES][256] partial sums, x rows, column sums, ring
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = lane & 15, q = lane >> 4;
-    const bool ctrl = wave == CHAIN_WAVES;
-    const int64_t P = gridDim.x, w = blockIdx.x;
+    const int P = (int) gridDim.x, w = (int) blockIdx.x;
     uint16_t * xs = (uint16_t *) (red + 2 * CHAIN_WAVES * 256);
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
-    uint8_t * ring = (uint8_t *) red + a.ring + (ctrl ? 0 : wave * S * BLK);
-    const XSrc X{nullptr, 0, xs, a.xls, xsum};
-    ChainCur ic{0, w - P, 0, 0, 0, ents[0].W, 1, 0u};   // past the end, refills read entry 0 out of range
-    if (!ctrl) {
+    if (wave < CHAIN_WAVES) {
+        // ---------------- compute waves
+        const int r = lane & 15, q = lane >> 4;
+        uint8_t * ring = (uint8_t *) red + a.ring + wave * S * BLK;
+        const XSrc X{nullptr, 0, xs, a.xls, xsum};
+        ChainCur ic;                        // refills past the end read entry 0 out of range
+        ic.e = 0; ic.g = w - P; ic.t = ic.b = ic.b1 = 0; ic.so = 0;
+        ic.rs = __builtin_amdgcn_make_buffer_rsrc((void *) ents[0].W, (short) 0, 0, 0x00020000);
         chain_settle<FMT>(ic, ents, a.n, w, P, wave);
         for (int s = 0; s < S; s++) chain_issue<FMT>(ic, ents, a.n, w, P, wave, ring + s * BLK, lane);
-    }
-    chain_stage_x(ents[0].x, a.M, ents[0].K, ents[0].KB, a.xls, GS, xsum_mul<FMT>(), xs, xsum);
-    chain_sync();
-    const uint32_t mag = 0x43004300u;
-    uint32_t k = 0;                     // blocks consumed: the next one sits in slot k % S
-    int rb = 0;                         // partial-sum buffer of the current tile group
-    for (int i = 0; i < a.n; i++) {
-        const ChainEntry & E = ents[i];
-        const int etw = E.tw, ekw = E.kw, nout = etw * 16 * a.M;
-        const int64_t eN = E.N;
-        void * const ey = E.y;
-        for (int64_t g = w; g < E.groups; g += P) {          // same trip count for the whole workgroup
-            float * rp = red + rb * CHAIN_WAVES * 256;
-            if (!ctrl) {
+        chain_sync();                                           // x of entry 0 staged
+        const uint32_t mag = 0x43004300u;
+        uint32_t k = 0;                     // blocks consumed: the next one sits in slot k % S
+        int rb = 0;                         // partial-sum buffer of the current tile group
+        for (int i = 0; i < a.n; i++) {
+            const ChainEntry & E = ents[i];
+            const int groups = (int) E.groups;
+            for (int g = w; g < groups; g += P) {
+                float * rp = red + rb * CHAIN_WAVES * 256;
                 f32x4 acc[1][1];
                 acc[0][0] = (f32x4){0.f, 0.f, 0.f, 0.f};
-                int64_t t, b0, b1;
+                int t, b0, b1;
                 chain_range(E, g, wave, t, b0, b1);
-                for (int64_t b = b0; b < b1; b++) {
+                for (int b = b0; b < b1; b++) {
                     __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (S - 1)));     // block k has landed
                     uint8_t * sl = ring + (k % S) * BLK;
                     WChunk<FMT, 1, 1> ch;
@@ -1800,33 +1845,70 @@ __global__ __launch_bounds__((CHAIN_WAVES + 1) * 64) void k_qgemv_chain(ChainArg
                     k++;
                 }
                 for (int v = 0; v < 4; v++) rp[wave * 256 + v * 64 + lane] = acc[0][0][v];
+                chain_sync();                                   // partial sums of the group
+                rb ^= 1;
             }
-            chain_sync();
-            if (ctrl) {                 // outputs (tile g tw + ti, row m, column c), summed over the kw K parts
-                for (int o = lane; o < nout; o += 64) {
-                    const int ti = o / (16 * a.M), m = (o / 16) % a.M, c = o % 16;
-                    const int64_t n = 16 * (g * etw + ti) + c;
-                    // the accumulator of row m, column c sits at lane c + 16 (m % 4), element m / 4
-                    // (x row m in MFMA row perm16(m))
-                    const float * src = rp + ti * ekw * 256 + (m >> 2) * 64 + c + 16 * (m & 3);
-                    float sum = src[0];
+            if (i + 1 == a.n) break;
+            chain_sync();                                       // x of entry i + 1 staged
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));   // the ring's last (out-of-range) loads have landed
+        return;
+    }
+    // ---------------- control waves
+    const uint32_t ct = threadIdx.x - CHAIN_WAVES * 64;
+    const uint32_t epoch = __hip_atomic_load(GLB(uint32_t, a.ep) + CHAIN_EP_EPOCH, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t tag = (epoch + 1u) & 0xffffu;
+    chain_stage_ext(ents[0].x, a.M, ents[0].K, ents[0].KB, a.xls, GS, xsum_mul<FMT>(), xs, xsum, ct, CT);
+    chain_sync();
+    int rb = 0;
+    for (int i = 0; i < a.n; i++) {
+        const ChainEntry & E = ents[i];
+        const int groups = (int) E.groups, etw = E.tw, ekw = E.kw, nout = etw * 16 * a.M;
+        const int64_t eN = E.N, nl = E.NT * 16;          // link rows: whole tiles
+        void * const ey = E.y;
+        uint32_t * const ely = E.ly;
+        for (int g = w; g < groups; g += P) {
+            chain_sync();                                       // partial sums of the group
+            const float * rp = red + rb * CHAIN_WAVES * 256;
+            // outputs (tile g tw + ti, row m, column c), summed over the kw K parts
+            for (int o = (int) ct; o < nout; o += (int) CT) {
+                const int ti = o / (16 * a.M), m = (o / 16) % a.M, c = o % 16;
+                const int64_t n = 16 * ((int64_t) g * etw + ti) + c;
+                // the accumulator of row m, column c sits at lane c + 16 (m % 4), element m / 4
+                // (x row m in MFMA row perm16(m))
+                const float * src = rp + ti * ekw * 256 + (m >> 2) * 64 + c + 16 * (m & 3);
+                float sum = src[0];
 #pragma unroll
-                    for (int k2 = 1; k2 < CHAIN_WAVES; k2++)
-                        if (k2 < ekw) sum += src[k2 * 256];
-                    if (n < eN) chain_store(ey, a.yf32, (int64_t) m * eN + n, sum);
+                for (int k2 = 1; k2 < CHAIN_WAVES; k2++)
+                    if (k2 < ekw) sum += src[k2 * 256];
+                if (n < eN) store_out(ey, a.yf32, (int64_t) m * eN + n, sum);
+                if (ely != nullptr && n < nl) {             // zeros past N
+                    const uint32_t word = ((uint32_t) (n < eN ? f32_to_bf16(sum) : 0) << 16) | tag;
+                    __hip_atomic_store(GLB(uint32_t, ely) + m * nl + n, word, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
             rb ^= 1;
         }
         if (i + 1 == a.n) break;
-        if (ctrl) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));              // the y stores are complete
-            chain_barrier(a.bar, w, P, i + 1, a.spin);
-        }
-        chain_sync();
         const ChainEntry & F = ents[i + 1];
-        chain_stage_x(F.x, a.M, F.K, F.KB, a.xls, GS, xsum_mul<FMT>(), xs, xsum);
-        chain_sync();
+        if (F.lx != nullptr)
+            chain_stage_link(F, a.M, a.xls, GS, xsum_mul<FMT>(), xs, xsum, tag, a.spin, a.ep + CHAIN_EP_ERR, ct, CT);
+        else
+            chain_stage_ext(F.x, a.M, F.K, F.KB, a.xls, GS, xsum_mul<FMT>(), xs, xsum, ct, CT);
+        chain_sync();                                           // x of entry i + 1 staged
     }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));      // the ring's last (out-of-range) loads have landed
+    if (ct == 0) {
+        // the last workgroup to finish advances the epoch (the next launch's tags) and resets the
+        // count; every workgroup read the epoch before it could finish, and the next launch starts
+        // after this one has ended
+        const uint32_t done = __hip_atomic_fetch_add(GLB(uint32_t, a.ep) + CHAIN_EP_DONE, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (done == (uint32_t) P - 1) {
+            __hip_atomic_store(GLB(uint32_t, a.ep) + CHAIN_EP_DONE, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(GLB(uint32_t, a.ep) + CHAIN_EP_EPOCH, epoch + 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }

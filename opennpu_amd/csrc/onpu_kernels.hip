@@ -423,16 +423,10 @@ hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems
     return hipErrorInvalidValue;
 }
 
-__global__ void k_chain_reset(int32_t * bar) {
-    for (int i = threadIdx.x; i < CHAIN_BAR_INTS; i += blockDim.x) bar[i] = 0;
-}
-
 hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,
                         hipStream_t s) {
-    if (a.n <= 0 || a.M < 1 || a.M > 16 || grid < 1 || lds > 163840 || ring < 0 || ring > 2)
+    if (a.n <= 0 || a.M < 1 || a.M > 16 || grid < 1 || lds > 163840 || ring < 0 || ring > 3)
         return hipErrorInvalidValue;
-    k_chain_reset<<<1, 256, 0, s>>>(a.bar);
-    CHECK_LAUNCH();
     switch (fmt) {
         case 0: return chain_f0(ring, a, ents, grid, lds, s);
         case 1: return chain_f1(ring, a, ents, grid, lds, s);
@@ -531,7 +525,6 @@ hipError_t argmax_scratch_get(int64_t rows, int64_t N, uint64_t ** keys, uint32_
     *keys = (uint64_t *) ((uint8_t *) p + ARGMAX_SCRATCH_CNT);
     return hipSuccess;
 }
-
 
 hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out, uint64_t * keys, uint32_t * cnt,
                          hipStream_t s) {

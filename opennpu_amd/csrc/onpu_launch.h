@@ -86,28 +86,31 @@ constexpr int MD_MAX_T = 4, MD_MAX_K = 8, MD_WAVES = 8, MD_SYNC_DONE = 16, MD_SY
 constexpr int MD_MAX_GB = 4;      // gate_up K blocks per wave (H <= 8 * 4 * 128)
 constexpr int MD_MAX_DB = 8;      // down K blocks (I <= 1024)
 
-// chained decode GEMVs (k_qgemv_chain): entry i = y_i [M][N] = x_i [M][K] . W_i^T, in order, each
-// entry may read what earlier ones wrote
+// chained decode GEMVs (k_qgemv_chain): entry i = y_i [M][N] = x_i [M][K] . W_i^T, in order. An
+// entry reads an external x (bf16 rows, written before the launch) or a link: words
+// (bf16 << 16 | run tag) that an earlier entry publishes for its output, rows ldl words apart
 struct ChainEntry {
     const uint8_t * W;
-    const uint16_t * x;
+    const uint16_t * x;       // external x [M][K] (nullptr when linked)
     void * y;
     int64_t NT, KB, N, K, bpw, groups;
     int tw, kw;               // tw * kw = CHAIN_WAVES
+    uint32_t * ly;            // this entry's link words [M][NT * 16] (nullptr: no later entry reads y)
+    const uint32_t * lx;      // linked x: row m at lx + m * ldl, in the producer's link words
+    int64_t ldl;
 };
 struct ChainArgs {              // (the entries array is a kernel argument of its own)
     int n, M, yf32;
-    int32_t * bar;            // CHAIN_CTRS arrival counters CHAIN_CTR_STRIDE ints apart, zero at launch, then
-                              // the flag set when a wait timed out (CHAIN_BAR_INTS ints)
+    int32_t * ep;             // CHAIN_EP_INTS ints: epoch, done counter, error flag (CHAIN_EP_* apart)
     int64_t xls;              // LDS row stride of x (elements) >= 128 KB of every entry
     int64_t ring;             // LDS byte offset of the weight ring
-    uint32_t spin;            // poll limit of one barrier wait
+    uint32_t spin;            // poll limit of one wait for a link word
 };
-constexpr int CHAIN_WAVES = 8;    // compute waves per workgroup (plus one control wave)
-constexpr int CHAIN_RING_SLOTS[3] = {12, 8, 4};   // ring depths built, deepest first
-// Workgroup w arrives on counter w % CHAIN_CTRS (one counter per lane of the polling wave); the
-// counters sit 256 bytes apart so that arrivals on different counters do not queue on one line.
-constexpr int CHAIN_CTRS = 64, CHAIN_CTR_STRIDE = 64, CHAIN_BAR_INTS = CHAIN_CTRS * CHAIN_CTR_STRIDE + 1;
+constexpr int CHAIN_WAVES = 8;    // compute waves per workgroup
+constexpr int CHAIN_CTRL = 4;     // control waves per workgroup (sums, stores, x staging)
+constexpr int CHAIN_RING_SLOTS[4] = {13, 10, 5, 3};   // ring depths built, deepest first
+// the epoch, the count of finished workgroups and the error flag, on separate cache lines
+constexpr int CHAIN_EP_EPOCH = 0, CHAIN_EP_DONE = 64, CHAIN_EP_ERR = 128, CHAIN_EP_INTS = 192;
 
 hipError_t launch_repack(int fmt, const uint8_t * st, int64_t sstride, int64_t N, int64_t K, uint8_t * out,
                          int64_t ostride, int64_t E, hipStream_t s);
@@ -136,7 +139,7 @@ hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems
 // outside what k_moe_decode handles (moe_decode_fits; the caller then uses the multi-launch path)
 hipError_t launch_moe_decode(int fmt, const MDArgs & a, int grid, hipStream_t s);
 bool moe_decode_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int64_t dKB, int T, int k, int E);
-// zero the chain's counters, then the chained kernel on `grid` workgroups (all resident at once)
+// the chained kernel on `grid` workgroups (all resident at once)
 // (ring: CHAIN_RING_SLOTS[ring] weight blocks per compute wave)
 hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,
                         hipStream_t s);
