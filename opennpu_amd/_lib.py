@@ -74,6 +74,8 @@ def _declare(lib):
         "onpu_dense_mv_dev": (I32, [P, P, I64, P, I32, P]),
         "onpu_dense_argmax_dev": (I32, [P, P, I64, P, P, P]),
         "onpu_dense_argmax_dev_noalloc": (I32, [P, P, I64, P, P, P]),
+        "onpu_gemm_status": (I32, []),
+        "onpu_release_scratch": (None, []),
         "onpu_moe_route_dev": (I32, [P, I64, I32, I32, I32, P, P, P]),
         "onpu_moe_ffn_dev": (I32, [P, P, I64, P, I32, P, P, I32, P]),
         "onpu_moe_decode_dev": (I32, [P, P, P, I64, I32, I32, I32, P, P, P, I32, P]),

@@ -96,6 +96,11 @@ struct DBuf {                              // grow-only device buffer (freed wit
     template <class T> T * as(size_t byte_off = 0) const { return (T *) ((char *) p + byte_off); }
 };
 
+// staging of the host-pointer calls (x, ids, w, biases, outputs on the device): one set for the
+// library, since those calls hold g_mu and run one at a time on the library's stream; it grows to
+// the largest call and is released by onpu_release_scratch
+DBuf g_hws[12];
+
 struct Mat4 {                              // one [N][K] matrix (E = 1) or a bank of E experts
     int fmt = 0;
     int64_t N = 0, K = 0, E = 1;
@@ -104,15 +109,14 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     uint8_t * dev = nullptr;
     uint8_t * stage = nullptr;             // host staging, E * sstride bytes (lazy)
     int64_t sstride = 0;
-    DBuf ws[6];                            // workspace of the calls on this handle
-    DBuf gsk_ws, gsk_sync;                 // k_qgemm_sk partial tiles and slot counters (zeroed once)
+    DBuf am_keys;                          // argmax: per-workgroup keys of the _dev calls on this handle
     DBuf am_cnt;                           // argmax row counters (zeroed once; each call leaves them zero)
 };
 
 struct Ffn {
     Mat4 * gu = nullptr, * dn = nullptr;
     bool fused = false;
-    DBuf ws[12];
+    DBuf ws[7];                            // ffn_core: decode act; prompt permutation, items, act, o
     DBuf md_act, md_sync;                  // k_moe_decode: act rows, counters (zeroed once)
 };
 
@@ -145,9 +149,7 @@ void free_mat(Mat4 * m) {
     if (!m) return;
     if (m->dev) (void) hipFree(m->dev);
     std::free(m->stage);
-    for (auto & b : m->ws) b.release();
-    m->gsk_ws.release();
-    m->gsk_sync.release();
+    m->am_keys.release();
     m->am_cnt.release();
     delete m;
 }
@@ -314,20 +316,57 @@ bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & g
     return true;
 }
 
-// partial tiles for one workgroup per CU (the largest k_qgemm_sk slot) and the slot counters,
-// zeroed once here; the kernel leaves them zero
-hipError_t gsk_workspace(Mat4 * m) {
-    const int cus = device().cus;
+// k_qgemm_sk workspace, one per stream (not per matrix): partial tiles for the cut tiles of the
+// largest split used on that stream (at most one per CU), the slot words and the control words,
+// zeroed when allocated. Launches on one stream run in order, so they share it safely; launches on
+// different streams get different workspaces. Growing it waits for the stream (the old partials may
+// still be in use), so the first prompt-sized call on a stream belongs outside graph capture.
+struct GskWs { DBuf part, sync; };
+std::mutex g_gsk_mu;
+std::vector<std::pair<hipStream_t, GskWs *>> g_gsk;      // a few streams: a linear search
+
+hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** sync, int32_t ** ctl) {
     size_t slot = 0;
     for (const GskCfg & c : GSK_CFGS) slot = std::max(slot, (size_t) c.wv * c.mbg * c.ntw * 1024);
-    if (m->gsk_sync.n == 0) {
-        hipError_t e = m->gsk_ws.ensure(slot * (size_t) cus);
-        if (e != hipSuccess) return e;
-        const size_t sb = ((size_t) cus + 1) * GSK_SYNC_STRIDE * 4;
-        if ((e = m->gsk_sync.ensure(sb)) != hipSuccess) return e;
-        if ((e = hipMemset(m->gsk_sync.p, 0, sb)) != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(g_gsk_mu);
+    GskWs * w = nullptr;
+    for (auto & p : g_gsk)
+        if (p.first == s) w = p.second;
+    hipError_t e = hipSuccess;
+    if (!w) {
+        w = new GskWs;
+        const size_t sb = ((size_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_INTS) * 4;
+        if ((e = w->sync.ensure(sb)) != hipSuccess || (e = hipMemset(w->sync.p, 0, sb)) != hipSuccess) {
+            w->sync.release();
+            delete w;
+            return e;
+        }
+        g_gsk.emplace_back(s, w);
     }
+    const size_t need = slot * (size_t) std::max<int64_t>(cut, 1);
+    if (w->part.n < need) {
+        if (w->part.p && (e = hipStreamSynchronize(s)) != hipSuccess) return e;
+        if ((e = w->part.ensure(need)) != hipSuccess) return e;
+    }
+    *part = w->part.as<float>();
+    *sync = w->sync.as<int32_t>();
+    *ctl = w->sync.as<int32_t>((size_t) device().cus * GSK_SYNC_STRIDE * 4);
     return hipSuccess;
+}
+
+// the timed-out-wait flags of every split-K workspace: 1 if any was set (then cleared)
+int gsk_status() {
+    std::lock_guard<std::mutex> lk(g_gsk_mu);
+    if (hipDeviceSynchronize() != hipSuccess) return -1;
+    int any = 0;
+    for (auto & p : g_gsk) {
+        int32_t * f = p.second->sync.as<int32_t>(((size_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_ERR) * 4);
+        int32_t flag = 0;
+        if (hipMemcpy(&flag, f, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+        if (flag && hipMemset(f, 0, 4) != hipSuccess) return -1;
+        any |= flag != 0;
+    }
+    return any;
 }
 
 // the decode GEMV (M <= 64 rows): no workspace
@@ -351,11 +390,13 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
     GArgs ga{};
     if (env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ga) &&
         M * m->K * 2 < ((int64_t) 1 << 31)) {
-        hipError_t e = gsk_workspace(m);
+        // cut tiles: the R tail tiles (two-phase split) or the workgroup boundaries (stream-K)
+        const int64_t cut = ga.sched == 1 ? ga.R : grid;
+        hipError_t e = gsk_workspace(s, cut, &ga.ws, &ga.sync, &ga.ctl);
         if (e != hipSuccess) return e;
         ga.W = W; ga.NT = m->g.NT; ga.KB = m->g.KB; ga.N = m->N; ga.K = m->K; ga.M = M;
         ga.x = x; ga.ldx = m->K; ga.y = y; ga.ldy = m->N; ga.yf32 = yf32;
-        ga.ws = m->gsk_ws.as<float>(); ga.sync = m->gsk_sync.as<int32_t>(); ga.spin = 1u << 22;
+        ga.spin = 1u << 22;
         return launch_qgemm_sk(m->fmt, ga, cfg, (int) grid, s);
     }
     // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
@@ -539,6 +580,15 @@ void onpu_geometry2(int64_t N, int64_t K, int ncols, int sym, int64_t * out) {
 }
 void onpu_geometry(int64_t N, int64_t K, int ncols, int64_t * out) { onpu_geometry2(N, K, ncols, 0, out); }
 
+int onpu_gemm_status(void) { return gsk_status(); }
+
+void onpu_release_scratch(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!device().ok) return;
+    (void) hipStreamSynchronize(device().stream);
+    for (auto & b : g_hws) b.release();
+}
+
 void onpu_stats(int64_t * calls, double * wait_s) {
     std::lock_guard<std::mutex> lk(g_mu);
     *calls = g_calls.load();
@@ -606,9 +656,9 @@ int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16) {
     std::lock_guard<std::mutex> lk(g_mu);
     const hipStream_t s = device().stream;
     const size_t bytes = (size_t) (m->N * m->K * (bf16 ? 2 : 4));
-    HIPR(m->ws[0].ensure(bytes));
-    HIPR(launch_dequant(m->fmt, m->dev + e * m->dstride, m->N, m->K, m->ws[0].p, bf16, s));
-    HIPR(hipMemcpyAsync(out_host, m->ws[0].p, bytes, hipMemcpyDeviceToHost, s));
+    HIPR(g_hws[0].ensure(bytes));
+    HIPR(launch_dequant(m->fmt, m->dev + e * m->dstride, m->N, m->K, g_hws[0].p, bf16, s));
+    HIPR(hipMemcpyAsync(out_host, g_hws[0].p, bytes, hipMemcpyDeviceToHost, s));
     HIPR(hipStreamSynchronize(s));
     return 0;
 }
@@ -619,10 +669,10 @@ void onpu_dense_mv(void * h, const float * x, int64_t rows, float * y) {
     std::lock_guard<std::mutex> lk(g_mu);
     Timer tm;
     const hipStream_t s = device().stream;
-    HIPX(x_to_dev(m->ws[0], m->ws[1], x, rows * m->K, s));
-    HIPX(m->ws[2].ensure((size_t) (rows * m->N * 4)));
-    HIPX(mv_core(m, 0, m->ws[1].as<uint16_t>(), rows, m->ws[2].p, 1, s));
-    HIPX(hipMemcpyAsync(y, m->ws[2].p, (size_t) (rows * m->N * 4), hipMemcpyDeviceToHost, s));
+    HIPX(x_to_dev(g_hws[0], g_hws[1], x, rows * m->K, s));
+    HIPX(g_hws[2].ensure((size_t) (rows * m->N * 4)));
+    HIPX(mv_core(m, 0, g_hws[1].as<uint16_t>(), rows, g_hws[2].p, 1, s));
+    HIPX(hipMemcpyAsync(y, g_hws[2].p, (size_t) (rows * m->N * 4), hipMemcpyDeviceToHost, s));
     HIPX(hipStreamSynchronize(s));
 }
 
@@ -637,13 +687,13 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
     if (M <= 0) return 0;
     // per-workgroup keys and per-row counters of the argmax: workspace of the handle (allocated on
     // the first call with this many rows; calls that overlap on one handle must not share it)
-    HIPR(m->ws[5].ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
+    HIPR(m->am_keys.ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
     if (m->am_cnt.n < (size_t) M * ARGMAX_PAD) {
         HIPR(m->am_cnt.ensure((size_t) M * ARGMAX_PAD));
         HIPR(hipMemset(m->am_cnt.p, 0, m->am_cnt.n));
     }
     HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
-    HIPR(launch_argmax(logits, M, m->N, argmax, m->ws[5].as<uint64_t>(), m->am_cnt.as<uint32_t>(),
+    HIPR(launch_argmax(logits, M, m->N, argmax, m->am_keys.as<uint64_t>(), m->am_cnt.as<uint32_t>(),
                        (hipStream_t) stream));
     return 0;
 }
@@ -704,12 +754,12 @@ void onpu_bank_run(void * h, const float * x, int x_per_slot, int64_t T, const i
     Timer tm;
     const hipStream_t s = device().stream;
     const int64_t xrows = x_per_slot ? T * k : T;
-    HIPX(x_to_dev(m->ws[0], m->ws[1], x, xrows * m->K, s));
-    HIPX(m->ws[2].ensure((size_t) (T * k * 4)));
-    HIPX(hipMemcpyAsync(m->ws[2].p, ids, (size_t) (T * k * 4), hipMemcpyHostToDevice, s));
-    HIPX(m->ws[3].ensure((size_t) (T * k * m->N * 4)));
-    HIPX(bank_core(m, m->ws[1].as<uint16_t>(), x_per_slot, T, m->ws[2].as<int32_t>(), k, m->ws[3].p, 1, s));
-    HIPX(hipMemcpyAsync(y, m->ws[3].p, (size_t) (T * k * m->N * 4), hipMemcpyDeviceToHost, s));
+    HIPX(x_to_dev(g_hws[0], g_hws[1], x, xrows * m->K, s));
+    HIPX(g_hws[2].ensure((size_t) (T * k * 4)));
+    HIPX(hipMemcpyAsync(g_hws[2].p, ids, (size_t) (T * k * 4), hipMemcpyHostToDevice, s));
+    HIPX(g_hws[3].ensure((size_t) (T * k * m->N * 4)));
+    HIPX(bank_core(m, g_hws[1].as<uint16_t>(), x_per_slot, T, g_hws[2].as<int32_t>(), k, g_hws[3].p, 1, s));
+    HIPX(hipMemcpyAsync(y, g_hws[3].p, (size_t) (T * k * m->N * 4), hipMemcpyDeviceToHost, s));
     HIPX(hipStreamSynchronize(s));
 }
 
@@ -722,8 +772,8 @@ void onpu_moe_ffn(void * gu_h, void * dn_h, const float * x, int64_t T, const in
     Timer tm;
     const hipStream_t s = device().stream;
     const int64_t n = T * k, Ng = gu->N, I = Ng / 2, Nd = dn->N, E = gu->E;
-    DBuf * b = gu->ws;                     // gu's workspace: x f32/bf16, ids, h, a (f32, bf16)
-    DBuf * c = dn->ws;                     // dn's workspace: w, o, y, biases
+    DBuf * b = g_hws;                      // x f32/bf16, ids, h, a (f32, bf16)
+    DBuf * c = g_hws + 6;                  // w, o, y, biases
     HIPX(x_to_dev(b[0], b[1], x, T * gu->K, s));
     HIPX(b[2].ensure((size_t) n * 4));
     HIPX(hipMemcpyAsync(b[2].p, ids, (size_t) n * 4, hipMemcpyHostToDevice, s));
@@ -848,7 +898,7 @@ static int ffn_host(Ffn * f, const float * x, int64_t T, const int32_t * ids, in
     std::lock_guard<std::mutex> lk(g_mu);
     Timer tm;
     const hipStream_t s = device().stream;
-    DBuf * b = f->ws + 7;
+    DBuf * b = g_hws;
     const int64_t n = T * k, Nd = f->dn->N;
     HIPX(x_to_dev(b[0], b[1], x, T * f->gu->K, s));
     HIPX(b[2].ensure((size_t) n * 8));

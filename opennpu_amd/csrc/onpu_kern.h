@@ -1061,7 +1061,7 @@ DEV void gemm_block_sk(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT>
 template <int FMT, int NTW, int MBG, int WV>
 __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
     extern __shared__ u32x4 gsk_lds[];                   // two X buffers of 4 MBG fragments
-    __shared__ int s_old;
+    __shared__ int s_old, s_tag;
     constexpr int MT = 16 * MBG, NF = 4 * MBG, FPW = NF / WV, TPW = NTW * WV;
     static_assert(FPW % 4 == 0 && MBG % 8 == 0, "fragment split");
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
@@ -1079,6 +1079,10 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
     const bool ktail = a.K % 128 != 0;
+    if (tid == 0) {                                       // this launch's tag: the last one's + 1, never 0
+        const int32_t prev = __hip_atomic_load(a.ctl + GSK_CTL_TAG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_tag = prev == 0x7fffffff ? 1 : prev + 1;
+    }                                                     // (visible after the first __syncthreads below)
     int64_t it = itb;                                     // stream-K cursor
     for (int64_t qs = 0;; qs++) {
         int64_t t, kb0, kb1, slot;                        // this segment: tile, K blocks, partial slot
@@ -1184,13 +1188,18 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
             store_tile(false, xr);
             continue;
         }
+        // a cut tile's two segments meet at its slot: every launch adds two arrivals to the slot's
+        // counter, so an even count on arrival means first. The first publishes its partial and
+        // sets the slot's ready word to this launch's tag; the second waits for that tag, so a
+        // ready word left by any earlier launch (also by a publisher that came after a timed-out
+        // wait) never matches, and nothing has to be cleared between launches.
         int32_t * sc = a.sync + slot * GSK_SYNC_STRIDE;
         if (tid == 0) s_old = __hip_atomic_fetch_add(sc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         const int old = s_old;
         const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
             (void *) ((char *) a.ws + (int64_t) slot * SLOT), (short) 0, (int) SLOT, 0x00020000);
-        if (old == 0) {                                   // first segment: publish the partial
+        if ((old & 1) == 0) {                             // first segment: publish the partial
 #pragma unroll
             for (int mb = 0; mb < MBG; mb++)
 #pragma unroll
@@ -1200,14 +1209,13 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
                                                            0, 16 /* sc1: agent scope */);
             __builtin_amdgcn_s_waitcnt(0x0f70);           // the stores have completed
             __syncthreads();
-            if (tid == 0) __hip_atomic_store(sc + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid == 0) __hip_atomic_store(sc + 1, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {                                          // second: wait for the partial, add, store
             if (tid == 0) {
                 uint32_t polls = 0;
-                while (__hip_atomic_load(sc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+                while (__hip_atomic_load(sc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != s_tag) {
                     if (++polls > a.spin) {
-                        __hip_atomic_store(a.sync + (int64_t) G * GSK_SYNC_STRIDE, 1, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(a.ctl + GSK_CTL_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);
@@ -1215,10 +1223,14 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
             }
             __syncthreads();
             store_tile(true, wsr);
-            if (tid == 0) {
-                __hip_atomic_store(sc, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(sc + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+        }
+    }
+    if (tid == 0) {
+        // the last workgroup to finish advances the tag for the next launch (every workgroup read
+        // it before it could finish; the next launch on this workspace starts after this one ends)
+        if (__hip_atomic_fetch_add(a.ctl + GSK_CTL_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int32_t) G - 1) {
+            __hip_atomic_store(a.ctl + GSK_CTL_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.ctl + GSK_CTL_TAG, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

@@ -367,7 +367,7 @@ hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s) {
 }
 
 hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s) {
-    if (cfg != 0 || grid <= 0 || a.ipw <= 0 || !a.ws || !a.sync) return hipErrorInvalidValue;
+    if (cfg != 0 || grid <= 0 || a.ipw <= 0 || !a.ws || !a.sync || !a.ctl) return hipErrorInvalidValue;
     if (a.sched == 1 && (a.R < 0 || a.R > grid || (a.R > 0 && (a.c <= 0 || a.s <= 0 || a.s >= a.KB))))
         return hipErrorInvalidValue;
     if (a.M * a.ldx * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;     // 32-bit X offsets

@@ -32,11 +32,14 @@ struct GArgs {
     int64_t ldy;
     int yf32;
     // k_qgemm_sk only: K-block iterations per workgroup over the tile-major sequence of
-    // tiles * KB; fp32 partial tiles, one slot per workgroup boundary; per slot an arrival counter
-    // and a ready flag (GSK_SYNC_STRIDE ints apart, zero between launches), then one error flag
+    // tiles * KB; fp32 partial tiles, one slot per cut tile; per slot an arrival counter (two per
+    // launch) and a ready word holding the tag of the launch that published (GSK_SYNC_STRIDE ints
+    // apart, zero when allocated); ctl: the last launch's tag, the count of finished workgroups and
+    // the timed-out-wait flag (GSK_CTL_* ints apart)
     int64_t ipw;
     float * ws;
     int32_t * sync;
+    int32_t * ctl;
     uint32_t spin;
     // sched 1 (two-phase): rounds F of one whole tile per workgroup, then the R remaining tiles
     // cut at K block s: workgroup g < R takes blocks [0, s) of tile F G + g, workgroup g >= R the
@@ -45,6 +48,7 @@ struct GArgs {
     int64_t F, R, s, c;
 };
 constexpr int GSK_SYNC_STRIDE = 16;
+constexpr int GSK_CTL_TAG = 0, GSK_CTL_DONE = 16, GSK_CTL_ERR = 32, GSK_CTL_INTS = 48;
 
 // grouped MoE products (k_moe_gemm) over a device work list (expert, first position, rows)
 struct MArgs {

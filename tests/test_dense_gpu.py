@@ -128,8 +128,9 @@ def test_gemm_stream_k(gpu, fmt, M, N, K, monkeypatch):
     """256-row GEMM with a split of K (k_qgemm_sk) on ragged shapes with more tiles than CUs:
     2100 x 7400 has one round of whole tiles and 5 tiles cut in two; 1000 x 14300 has 224 tiles, each
     cut into a head piece and a tail piece, seven tail pieces per workgroup. A 400-column slice over
-    all rows and 32 full rows against the oracle; a second call gives the same bits (the slot
-    counters were left at zero, and a cut tile's sum does not depend on which piece finished first);
+    all rows and 32 full rows against the oracle; a second call gives the same bits (the slot words
+    need no clearing between launches, and a cut tile's sum does not depend on which piece finished
+    first); no wait timed out;
     the plain stream-K split and the 128-row kernel agree to fp32 summation order."""
     import torch
     from opennpu_amd.device import QMatrix
@@ -150,6 +151,7 @@ def test_gemm_stream_k(gpu, fmt, M, N, K, monkeypatch):
         monkeypatch.delenv("ONPU_GSK_SCHED")
         yb = q.mv(x)
         torch.cuda.synchronize()
+        assert q.L.onpu_gemm_status() == 0, "a split-K wait timed out"
         assert torch.equal(y1, y2), "split-K GEMM is not deterministic"
         for other, what in ((y0, "128-row GEMM"), (ys, "stream-K split")):
             d = ((y1 - other).abs().max() / other.abs().max()).item()
@@ -165,23 +167,97 @@ def test_gemm_stream_k(gpu, fmt, M, N, K, monkeypatch):
 
 @pytest.mark.parametrize("name,N,K", [("up", 14336, 4096), ("down", 4096, 14336)])
 def test_gemm_llama_ffn(gpu, name, N, K):
-    """Llama-3.1-8B FFN prefill at M=2048: all rows of a 128-column slice plus 48 full rows."""
+    """Llama-3.1-8B FFN prefill at M=2048 (the split-K GEMM: up cuts 192 of its 448 tiles at a K
+    block, down cuts all 128 in two): one full row in every 256-row tile and one full column in
+    every 256-column tile, so every tile, cut or whole, has a row and a column checked, plus all rows
+    of a 128-column slice"""
     import torch
     from opennpu_amd.device import QMatrix
     M = 2048
     st = syn.weights(orc.FMT_G128S, N, K, 17)
     xb = syn.activations(M, K, 18)
     q = QMatrix(N, K, orc.FMT_G128S, st)
+    rng = np.random.default_rng(0)
+    rows = np.array([256 * t + rng.integers(0, 256) for t in range(M // 256)])
+    cols = np.array([256 * t + rng.integers(0, 256) for t in range(N // 256)])
     try:
         y = q.mv(to_torch_bf16(xb).reshape(M, K))
         torch.cuda.synchronize()
+        assert q.L.onpu_gemm_status() == 0, "a split-K wait timed out"
         yc = from_torch(y[:, 1000:1128])
-        rows = np.random.default_rng(0).choice(M, 48, replace=False)
         yr = from_torch(y[torch.as_tensor(rows, device=y.device)])
+        ycols = from_torch(y[:, torch.as_tensor(cols, device=y.device)])
     finally:
         q.free()
     check_gemm(yc, orc.FMT_G128S, st, N, K, xb, 1000, 1128, what=f"{name} column slice")
-    check_gemm(yr, orc.FMT_G128S, st, N, K, xb[rows], what=f"{name} rows")
+    check_gemm(yr, orc.FMT_G128S, st, N, K, xb[rows], what=f"{name} one row per row tile")
+    for j, n in enumerate(cols):
+        check_gemm(ycols[:, j:j + 1], orc.FMT_G128S, st, N, K, xb, int(n), int(n) + 1,
+                   what=f"{name} column {n} (column tile {j})")
+
+
+def test_gemm_two_streams(gpu):
+    """split-K GEMMs on two streams at once: each stream has its own partials and slot words, so
+    both results equal the one-stream results bit for bit"""
+    import torch
+    from opennpu_amd.device import QMatrix
+    M, N, K = 1024, 7168, 4096
+    qa = QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 31))
+    qb = QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 32))
+    try:
+        xa = to_torch_bf16(syn.activations(M, K, 33)).reshape(M, K)
+        xb = to_torch_bf16(syn.activations(M, K, 34)).reshape(M, K)
+        ra, rb = qa.mv(xa, f32=True), qb.mv(xb, f32=True)
+        torch.cuda.synchronize()
+        sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+        outs = []
+        for rep in range(3):
+            with torch.cuda.stream(sa):
+                ya = qa.mv(xa, f32=True)
+            with torch.cuda.stream(sb):
+                yb = qb.mv(xb, f32=True)
+            outs.append((ya, yb))
+        torch.cuda.synchronize()
+        assert qa.L.onpu_gemm_status() == 0
+        for ya, yb in outs:
+            assert torch.equal(ya, ra) and torch.equal(yb, rb)
+    finally:
+        qa.free()
+        qb.free()
+
+
+def test_scratch_over_a_model_of_handles(gpu):
+    """36 layers x 4 Qwen3-8B-shaped matrices, an M = 2048 GEMM through each on one stream, then
+    host-pointer calls at 2048 rows through several of them: the workspaces do not grow with the
+    number of handles (< 1 GiB of device memory beyond weights, inputs and outputs)"""
+    import ctypes as C
+    import torch
+    from opennpu_amd.device import QMatrix
+    shapes = [(6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)]
+    st = {s: syn.weights(orc.FMT_G128S, s[0], s[1], 40 + i) for i, s in enumerate(shapes)}
+    mats = [QMatrix(N, K, orc.FMT_G128S, st[(N, K)]) for _ in range(36) for N, K in shapes]
+    M = 2048
+    xs = {K: to_torch_bf16(syn.activations(M, K, K)).reshape(M, K) for K in (4096, 12288)}
+    ys = {N: torch.empty((M, N), dtype=torch.bfloat16, device="cuda") for N in (4096, 6144, 24576)}
+    xh = np.random.default_rng(5).standard_normal((M, 4096)).astype(np.float32)
+    yh = np.empty((M, 24576), np.float32)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    try:
+        for q in mats:
+            q.mv(xs[q.K], out=ys[q.N])
+        torch.cuda.synchronize()
+        assert mats[0].L.onpu_gemm_status() == 0
+        fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+        for q in mats[:8]:
+            if q.K == 4096:
+                mats[0].L.onpu_dense_mv(C.c_void_p(q.h), fp(xh), M, fp(yh))
+        used = free0 - torch.cuda.mem_get_info()[0]
+        assert used < (1 << 30), f"{used / 2**20:.0f} MiB of workspace for 144 handles"
+    finally:
+        for q in mats:
+            q.free()
+        mats[0].L.onpu_release_scratch()
 
 
 @pytest.mark.parametrize("M", [1, 5])
