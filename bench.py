@@ -503,6 +503,30 @@ def profile_gemm(torch, QMatrix, syn, reps=3):
                       "launches_each": reps, "flop_per_launch": 2 * M * 14336 * 4096}), flush=True)
 
 
+def profile_moe(torch, QFfn, syn, reps=3):
+    """The Qwen3-30B-A3B MoE layer alone (E 128, H 2048, I 768, top-8, g128s) at T = 512 and T = 1,
+    `reps` calls each (router, permutation, grouped GEMMs, combine / the decode GEMVs), for
+    hardware-counter and trace runs."""
+    E, H, I, k = 128, 2048, 768, 8
+    gu = np.concatenate([syn.weights(G128S, 2 * I, H, 300 + e) for e in range(E)])
+    dn = np.concatenate([syn.weights(G128S, H, I, 600 + e) for e in range(E)])
+    f = QFfn(E, H, I, G128S)
+    f.load(gu, dn)
+    for T in (512, 1):
+        lg = torch.from_numpy(syn.logits(T, E, 9)).cuda()
+        x = bf16_tensor(torch, syn.activations(T, H, 10)).reshape(T, H)
+        y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        for _ in range(reps):
+            i, w = f.route(lg, k)
+            f.ffn(x, i, w, out=y)
+        torch.cuda.synchronize()
+    f.free()
+    per_expert = wbytes(G128S, 2 * I, H) + wbytes(G128S, H, I)
+    print(json.dumps({"profile_target": "Qwen3-30B-A3B MoE layer, T = 512 then T = 1", "calls_each": reps,
+                      "gate_up_bytes_per_expert": wbytes(G128S, 2 * I, H), "down_bytes_per_expert": wbytes(G128S, H, I),
+                      "algorithmic_bytes_T512_all_experts": E * per_expert}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -515,6 +539,8 @@ def main():
                          "gate_up) plus a calibration copy, for rocprofv3 --pmc runs")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only the prefill GEMMs, for rocprofv3 --pmc runs")
+    ap.add_argument("--profile-moe", action="store_true",
+                    help="only the MoE layer (T = 512 and T = 1), for rocprofv3 runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the int4 path on a single MI355X; --gpus {args.gpus} "
@@ -530,6 +556,9 @@ def main():
         return
     if args.profile_gemm:
         profile_gemm(torch, QMatrix, syn)
+        return
+    if args.profile_moe:
+        profile_moe(torch, QFfn, syn)
         return
     t_all = time.perf_counter()
     log("decode layers ...")

@@ -201,15 +201,16 @@ struct Plan {
 Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     Plan p;
     p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-    p.rt = epi == EPI_ACT_ ? 2 : 1;
+    const bool act = epi == EPI_ACT_;
+    p.rt = act ? 2 : 1;
     const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2 + KB * (fmt == ONPU_G128S ? 1 : 4) * 64;
     // gfx950 gives a workgroup up to 160 KiB of LDS. x in LDS up to 52 KiB keeps several workgroups
     // per CU; up to 112 KiB (one workgroup per CU) only pays off with many tile groups to share it
-    const int64_t groups0 = epi == EPI_ACT_ ? NT / 2 : NT;
+    const int64_t groups0 = act ? NT / 2 : NT;
     p.xl = (p.mb == 1 && (xbytes <= 52 * 1024 || (xbytes <= 112 * 1024 && groups0 * slots >= 1024))) ? 1 : 0;
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
-    const int64_t groups = epi == EPI_ACT_ ? NT / 2 : NT;
+    const int64_t groups = act ? NT / 2 : NT;
     // vocabulary-sized matrices (>= 4096 tile groups) stream whole rows per wave (up to 32 blocks)
     // in workgroups of up to 8 tile groups sharing one x copy: measured on the 151936 x 4096 LM head,
     // M = 5: 65.7 us against 75.0 us with two K parts per tile and 4 tiles (M = 1: equal)
@@ -245,10 +246,10 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     }
     int tw = std::max(1, std::min(vocab ? 8 : (M > 1 ? 4 : 2), maxw / p.kw));
     while (tw > 1 && (tw * p.kw * p.rt * p.mb > red_kib || (groups + tw - 1) / tw * slots < 512 ||
-                      (epi == EPI_ACT_ && groups % tw != 0)))
+                      (act && groups % tw != 0)))
         tw--;
     const int etw = env_int("ONPU_GEMV_TW", 0);
-    if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= red_kib && !(epi == EPI_ACT_ && groups % etw))
+    if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= red_kib && !(act && groups % etw))
         tw = etw;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
@@ -470,6 +471,36 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
     return launch_moe_decode(gu->fmt, a, device().cus, s);
 }
 
+// MoE decode (T <= 4 tokens) in two launches: gate_up with SiLU(gate) * up per slot, then down with
+// the routing-weighted slot sum per token. act: bf16 [T k][I] in the FFN's workspace.
+hipError_t moe_decode_two(Ffn * f, const uint16_t * x, int64_t T, int k, const int32_t * ids, const float * w,
+                          void * y, int yf32, hipStream_t s) {
+    Mat4 * gu = f->gu, * dn = f->dn;
+    const int64_t I = gu->N / 2, Nd = dn->N, n = T * k;
+    hipError_t e = f->ws[0].ensure((size_t) (n * I * 2));
+    if (e != hipSuccess) return e;
+    uint16_t * act = f->ws[0].as<uint16_t>();
+    const Plan pg = plan_gemv(gu->fmt, gu->g.NT, gu->g.KB, 1, n, EPI_ACT_);
+    QArgs a{};
+    a.W = gu->dev; a.estride = gu->dstride; a.ids = ids;
+    a.N = gu->N; a.K = gu->K; a.NT = gu->g.NT; a.KB = gu->g.KB;
+    a.x = x; a.ldx = gu->K; a.xslot = gu->K; a.xdiv = k; a.M = 1;
+    a.y = act; a.ldy = I; a.yslot = I; a.yf32 = 0; a.bpw = pg.bpw; a.tw = pg.tw;
+    a.xls = gu->g.KB * 128 + 8;
+    e = launch_qgemv(gu->fmt, EPI_ACT_, a, 1, 2, pg.nb, pg.xl, dim3((unsigned) pg.gx, (unsigned) n), pg.waves(), s);
+    if (e != hipSuccess) return e;
+    const Plan pd = plan_slotsum(dn->g.KB, k);
+    if (!pd.kw) return hipErrorInvalidValue;
+    QArgs b{};
+    b.W = dn->dev; b.estride = dn->dstride; b.ids = ids;
+    b.N = Nd; b.K = dn->K; b.NT = dn->g.NT; b.KB = dn->g.KB;
+    b.x = act; b.ldx = I; b.xslot = I; b.xdiv = 1; b.M = 1;
+    b.y = y; b.ldy = Nd; b.yslot = Nd; b.yf32 = yf32;
+    b.wslot = w; b.nslot = k; b.ksplit = pd.kw / k; b.tw = 1;
+    b.bpw = pd.bpw;
+    return launch_qgemv(dn->fmt, EPI_SLOTSUM_, b, 1, 1, pd.nb, 0, dim3((unsigned) dn->g.NT, (unsigned) T), pd.kw, s);
+}
+
 // routed-expert FFN on device data (act 0, no biases): x bf16 [T][H], ids/w [T][k] -> y [T][Nd]
 hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids, int k, const float * w, void * y,
                     int yf32, hipStream_t s) {
@@ -482,31 +513,7 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
         e = moe_decode_core(f, nullptr, x, T, k, 1, (int) gu->E, const_cast<int32_t *>(ids),
                             const_cast<float *>(w), y, yf32, s);
         if (e != hipErrorNotSupported) return e;
-        // gate_up with SiLU(gate) * up per slot, then down with the weighted slot sum per token
-        e = f->ws[0].ensure((size_t) (n * I * 2));
-        if (e != hipSuccess) return e;
-        uint16_t * act = f->ws[0].as<uint16_t>();
-        const Plan pg = plan_gemv(gu->fmt, gu->g.NT, gu->g.KB, 1, n, EPI_ACT_);
-        QArgs a{};
-        a.W = gu->dev; a.estride = gu->dstride; a.ids = ids;
-        a.N = gu->N; a.K = gu->K; a.NT = gu->g.NT; a.KB = gu->g.KB;
-        a.x = x; a.ldx = gu->K; a.xslot = gu->K; a.xdiv = k; a.M = 1;
-        a.y = act; a.ldy = I; a.yslot = I; a.yf32 = 0; a.bpw = pg.bpw; a.tw = pg.tw;
-        a.xls = gu->g.KB * 128 + 8;
-        e = launch_qgemv(gu->fmt, EPI_ACT_, a, 1, 2, pg.nb, pg.xl, dim3((unsigned) pg.gx, (unsigned) n), pg.waves(), s);
-        if (e != hipSuccess) return e;
-        const Plan pd = plan_slotsum(dn->g.KB, k);
-        if (!pd.kw) return hipErrorInvalidValue;
-        const int ksplit = pd.kw / k;
-        QArgs b{};
-        b.W = dn->dev; b.estride = dn->dstride; b.ids = ids;
-        b.N = Nd; b.K = dn->K; b.NT = dn->g.NT; b.KB = dn->g.KB;
-        b.x = act; b.ldx = I; b.xslot = I; b.xdiv = 1; b.M = 1;
-        b.y = y; b.ldy = Nd; b.yslot = Nd; b.yf32 = yf32;
-        b.wslot = w; b.nslot = k; b.ksplit = ksplit; b.tw = 1;
-        b.bpw = pd.bpw;
-        return launch_qgemv(dn->fmt, EPI_SLOTSUM_, b, 1, 1, pd.nb, 0, dim3((unsigned) dn->g.NT, (unsigned) T), pd.kw,
-                            s);
+        return moe_decode_two(f, x, T, k, ids, w, y, yf32, s);
     }
     // prompts: tokens grouped per expert (one pass over each routed expert's weights per 64 rows)
     const int rows_per_item = 64;                 // the grouped GEMM's 4 A blocks of 16 rows
@@ -516,13 +523,13 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
     if ((e = f->ws[3].ensure((size_t) n * 4)) != hipSuccess) return e;
     if ((e = f->ws[4].ensure((size_t) (maxitems * 3 + 1) * 4)) != hipSuccess) return e;
     if ((e = f->ws[5].ensure((size_t) (n * I * 2))) != hipSuccess) return e;
-    if ((e = f->ws[6].ensure((size_t) (n * Nd * 4))) != hipSuccess) return e;
+    if ((e = f->ws[6].ensure((size_t) (n * Nd * 2))) != hipSuccess) return e;
     int32_t * off = f->ws[1].as<int32_t>(), * perm = f->ws[2].as<int32_t>(), * inv = f->ws[3].as<int32_t>();
     int32_t * items = f->ws[4].as<int32_t>(), * nitems = items + maxitems * 3;
     uint16_t * act = f->ws[5].as<uint16_t>();
-    float * o = f->ws[6].as<float>();
-    if ((e = launch_moe_permute(ids, n, (int) E, rows_per_item, off, perm, items, nitems, s)) != hipSuccess) return e;
-    if ((e = launch_invert(perm, n, inv, s)) != hipSuccess) return e;
+    uint16_t * o = f->ws[6].as<uint16_t>();
+    if ((e = launch_moe_permute(ids, n, (int) E, rows_per_item, off, perm, inv, items, nitems, s)) != hipSuccess)
+        return e;
     MArgs a{};
     a.W = gu->dev; a.estride = gu->dstride; a.NT = gu->g.NT; a.KB = gu->g.KB; a.N = gu->N; a.K = gu->K;
     a.x = x; a.ldx = gu->K; a.y = act; a.ldy = I; a.perm = perm; a.items = items; a.nitems = nitems; a.k = k;

@@ -137,9 +137,17 @@ __global__ __launch_bounds__(64) void k_repack(const uint8_t * __restrict__ st, 
     }
 }
 
-// Raw group parameters of lane row r in one block (loaded early, decoded at compute time):
-// G128S one u16 scale, Q4S / Q4_0 four u16 scales, Q4NX four {u16 scale, u16 min} pairs.
-template <int FMT> struct Par { uint32_t v[FMT == ONPU_Q4NX ? 4 : (FMT == ONPU_G128S ? 1 : 2)]; };
+// Raw group parameters of lane row r in one block for the decode kernels (loaded early, decoded at
+// compute time): G128S the dword holding the u16 scales of rows r & ~1 and r | 1 plus the byte
+// selector of row r's half (set from r when loaded), Q4S / Q4_0 four u16 scales, Q4NX four
+// {u16 scale, u16 min} pairs.
+template <int FMT> struct Par { uint32_t v[FMT == ONPU_Q4NX ? 4 : 2]; };
+// The prefill GEMMs' parameters of row r: G128S the u16 scale alone (a 16-bit load), else as Par.
+// A type of its own, so that the two G128S encodings cannot be mixed up.
+template <int FMT> struct GPar { uint32_t v[FMT == ONPU_Q4NX ? 4 : (FMT == ONPU_G128S ? 1 : 2)]; };
+
+// perm selector that moves the u16 of row r (the low half for even r) to the top of a dword
+DEV uint32_t g128s_sel(int r) { return (r & 1) ? 0x03020c0cu : 0x01000c0cu; }
 
 template <int FMT>
 DEV Par<FMT> par_zero() {
@@ -151,8 +159,11 @@ DEV Par<FMT> par_zero() {
 template <int FMT>
 DEV Par<FMT> load_par(const uint8_t * blk, int r) {
     Par<FMT> p;
-    // G128S: the dword holding rows r & ~1 and r | 1 (decode_scale picks the half)
-    if (FMT == ONPU_G128S) p.v[0] = *GLB(const uint32_t, blk + 1024 + 4 * (r >> 1));
+    // G128S: the dword holding rows r & ~1 and r | 1, and the selector of row r's half
+    if (FMT == ONPU_G128S) {
+        p.v[0] = *GLB(const uint32_t, blk + 1024 + 4 * (r >> 1));
+        p.v[1] = g128s_sel(r);
+    }
     else if (FMT == ONPU_Q4NX) {
         const u32x4 q = __builtin_nontemporal_load(GLB(const u32x4, blk + 1024 + 16 * r));
         for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];
@@ -169,11 +180,11 @@ template <int FMT>
 DEV void decode_scale(const Par<FMT> & p, float (&s)[4]) {
     if (FMT == ONPU_G128S) {
         // p.v[0] holds the scales of rows r & ~1 (low half) and r | 1 (high half); one byte
-        // permute moves this lane's half to the top (r & 1 = lane & 1). A 16-bit load instead
-        // lets the compiler narrow the loop's phi of loaded values to 16 bits and widen it again
-        // at the loop's entry, a use that waits for the first chunk before the next one is issued.
-        const uint32_t sel = (threadIdx.x & 1) ? 0x03020c0cu : 0x01000c0cu;
-        const float v = __uint_as_float(__builtin_amdgcn_perm(p.v[0], p.v[0], sel));
+        // permute with the selector set at load (p.v[1]) moves row r's half to the top. A 16-bit
+        // load instead lets the compiler narrow the loop's phi of loaded values to 16 bits and
+        // widen it again at the loop's entry, a use that waits for the first chunk before the next
+        // one is issued.
+        const float v = __uint_as_float(__builtin_amdgcn_perm(p.v[0], p.v[0], p.v[1]));
         for (int j = 0; j < 4; j++) s[j] = v;
     } else {
         for (int j = 0; j < 4; j++)
@@ -772,7 +783,7 @@ DEV u32x4 dequant8(uint32_t d, float s, float c) {
 
 // scale s and additive constant c of MFMA step j such that w = u * s + c
 template <int FMT>
-DEV void par_sc(const Par<FMT> & p, int j, float & s, float & c) {
+DEV void par_sc(const GPar<FMT> & p, int j, float & s, float & c) {
     if (FMT == ONPU_G128S) {
         s = bf16_to_f32((uint16_t) p.v[0]);
         c = -8.0f * s;
@@ -805,7 +816,7 @@ typedef __attribute__((address_space(3))) void lds_void;
 // step j's dequant runs while step j's reads are in flight. NTW = 4 has no registers to spare for
 // that and reads each step's fragments at the step's start.
 template <int FMT, int NTW, int MBG>
-DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int lane,
+DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW], int lane,
                     f32x4 (&acc)[MBG][NTW]) {
     constexpr bool PIPE = NTW <= 3;
     u32x4 xa[PIPE ? 2 : 1][MBG];
@@ -872,7 +883,7 @@ DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xo)[8],
 // weight block b of the wave's NTW tiles (buffer loads: one lane offset, the block in the scalar offset)
 template <int FMT, int NTW>
 DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int lane, int r, u32x4 (&w)[NTW],
-                     Par<FMT> (&p)[NTW]) {
+                     GPar<FMT> (&p)[NTW]) {
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     const uint32_t sb = (uint32_t) (b * BLK);
 #pragma unroll
@@ -937,7 +948,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
     // two register sets for the weights, alternating with the two LDS buffers (no copies)
     u32x4 wa[NTW], wb[NTW];
-    Par<FMT> pa[NTW], pb[NTW];
+    GPar<FMT> pa[NTW], pb[NTW];
     gemm_load_x(xr, xo, 0, ktail && a.KB == 1, a.K, wave, q, xs0);
     gemm_load_w<FMT, NTW>(wrs, 0, lane, r, wa, pa);
     __builtin_amdgcn_s_waitcnt(0x0f70);                  // vmcnt(0): the DMA into xs0 is done
@@ -1019,7 +1030,7 @@ DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow
 // j + 1 are dequantized during step j (tile i in half-step i % H), so neither LDS latency nor the
 // dequant sits in front of an MFMA except at the block's start.
 template <int FMT, int NTW, int MBG>
-DEV void gemm_block_sk(const u32x4 * xsb, const u32x4 (&wr)[NTW], const Par<FMT> (&pr)[NTW], int lane,
+DEV void gemm_block_sk(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW], int lane,
                        f32x4 (&acc)[MBG][NTW]) {
     constexpr int HB = 8, H = MBG / HB, S = 4 * H;
     u32x4 xa[2][HB], bw[2][NTW];
@@ -1137,7 +1148,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 #pragma unroll
             for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
         u32x4 wc[NTW], wn[NTW];
-        Par<FMT> pc[NTW], pn[NTW];
+        GPar<FMT> pc[NTW], pn[NTW];
         __syncthreads();                                  // the previous segment is done with xs0 / xs1
         gemm_load_x_sk<FPW>(xr, xrow, kb0, ktail && kb0 + 1 == a.KB, a.K, wave, q, xs0);
         gemm_load_w<FMT, NTW>(wrs, kb0, lane, r, wc, pc);
@@ -1245,7 +1256,9 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 // re-reads the item's X, so wider groups (WV = 8) halve that traffic.
 //   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = WV blockIdx.x + w and up tile
 //           g + NT / 2; act[position][16 g + r] = bf16(silu(gate) * up)
-//   WHICH 1 (down): wave w holds tiles 2 WV blockIdx.x + 2 w + {0, 1}; o[position][n] = fp32
+//   WHICH 1 (down): wave w holds tiles 2 WV blockIdx.x + 2 w + {0, 1}; o[position][n] = bf16 (the
+//           reference device's output precision per expert: its GEMV flushes each row to bf16,
+//           gemv_any.cc:120-130, and the host sums the weighted rows in fp32, onpu_cpu.cpp:259-274)
 // X rows: WHICH 0 token perm[position] / k of x [T][K]; WHICH 1 position of act [T k][K].
 template <int FMT, int WHICH, int WV>
 __global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) {
@@ -1294,27 +1307,30 @@ __global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) 
 #pragma unroll
     for (int mb = 0; mb < MBG; mb++) acc[mb][0] = acc[mb][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
     u32x4 wa[2], wb[2];
-    Par<FMT> pa[2], pb[2];
+    GPar<FMT> pa[2], pb[2];
     load_xt(0, xs0);
     gemm_load_w<FMT, 2>(wrs, 0, lane, r, wa, pa);
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
+    auto block = [&](const u32x4 * xsb, const u32x4 (&wr)[2], const GPar<FMT> (&pr)[2]) {
+        gemm_block<FMT, 2, MBG>(xsb, wr, pr, lane, acc);
+    };
     int64_t b = 0;
     for (; b + 2 <= a.KB; b += 2) {
         load_xt(b + 1, xs1);
         gemm_load_w<FMT, 2>(wrs, b + 1, lane, r, wb, pb);
-        gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
+        block(xs0, wa, pa);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
         if (b + 2 < a.KB) {
             load_xt(b + 2, xs0);
             gemm_load_w<FMT, 2>(wrs, b + 2, lane, r, wa, pa);
         }
-        gemm_block<FMT, 2, MBG>(xs1, wb, pb, lane, acc);
+        block(xs1, wb, pb);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
-    if (b < a.KB) gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
+    if (b < a.KB) block(xs0, wa, pa);
     // lane (q, r) holds rows 4 q + v of A block mb, column r of its tiles
 #pragma unroll
     for (int mb = 0; mb < MBG; mb++)
@@ -1328,8 +1344,10 @@ __global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) 
                     ((uint16_t *) a.y)[pos * a.ldy + 16 * t[0] + r] =
                         f32_to_bf16(silu_f(acc[mb][0][v]) * acc[mb][1][v]);
             } else {
-                if (ok0 && 16 * t[0] + r < a.N) ((float *) a.y)[pos * a.ldy + 16 * t[0] + r] = acc[mb][0][v];
-                if (ok1 && 16 * t[1] + r < a.N) ((float *) a.y)[pos * a.ldy + 16 * t[1] + r] = acc[mb][1][v];
+                if (ok0 && 16 * t[0] + r < a.N)
+                    ((uint16_t *) a.y)[pos * a.ldy + 16 * t[0] + r] = f32_to_bf16(acc[mb][0][v]);
+                if (ok1 && 16 * t[1] + r < a.N)
+                    ((uint16_t *) a.y)[pos * a.ldy + 16 * t[1] + r] = f32_to_bf16(acc[mb][1][v]);
             }
         }
 }
@@ -1793,7 +1811,10 @@ DEV Par<FMT> load_par_lds(const uint8_t * blk, int r) {
     Par<FMT> p;
     typedef __attribute__((address_space(3))) const uint32_t lds_u32;
     typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
-    if (FMT == ONPU_G128S) p.v[0] = *(lds_u32 *) (blk + 1024 + 4 * (r >> 1));     // as load_par
+    if (FMT == ONPU_G128S) {                                                     // as load_par
+        p.v[0] = *(lds_u32 *) (blk + 1024 + 4 * (r >> 1));
+        p.v[1] = g128s_sel(r);
+    }
     else if (FMT == ONPU_Q4NX) {
         const u32x4 q = *LDS_U32X4(blk + 1024 + 16 * r);
         for (int j = 0; j < 4; j++) p.v[j % (sizeof(p.v) / 4)] = q[j];

@@ -20,12 +20,12 @@ __global__ __launch_bounds__(64) void k_route(const float * __restrict__ logits,
 
 // ------------------------------------------------------------------ MoE permutation
 // One workgroup. entries i = t * k + j (T * k of them) sorted by expert:
-//   cnt[e], off[e] (exclusive scan, off[E] = total), perm[off[e] + rank] = i,
+//   cnt[e], off[e] (exclusive scan, off[E] = total), perm[off[e] + rank] = i and inv[i] = its position,
 //   work list of (expert, first position, rows <= rows_per_item) items -> items[], nitems
 __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict__ ids, int64_t n, int E,
                                                       int rows_per_item, int32_t * __restrict__ off,
-                                                      int32_t * __restrict__ perm, int32_t * __restrict__ items,
-                                                      int32_t * __restrict__ nitems) {
+                                                      int32_t * __restrict__ perm, int32_t * __restrict__ inv,
+                                                      int32_t * __restrict__ items, int32_t * __restrict__ nitems) {
     extern __shared__ int32_t sh[];
     int32_t * cnt = sh;              // [E]
     int32_t * pos = sh + E;          // [E + 1]
@@ -67,24 +67,37 @@ __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
         const int32_t p = atomicAdd(&pos[ids[i]], 1);
         perm[p] = (int32_t) i;
+        inv[i] = p;
     }
 }
 
 // combine: y[t][n] = sum_j w[t][j] * o[inv[t * k + j]][n]; inv = inverse permutation (position of entry)
-__global__ __launch_bounds__(256) void k_moe_combine(const float * __restrict__ o, const int32_t * __restrict__ inv,
+__global__ __launch_bounds__(256) void k_moe_combine(const uint16_t * __restrict__ o, const int32_t * __restrict__ inv,
                                                      const float * __restrict__ w, int64_t T, int k, int64_t N,
                                                      void * __restrict__ y, int yf32) {
+    // token blockIdx.y, 8 consecutive outputs per thread: a 16-byte load of each of the k rows
     const int64_t t = blockIdx.y;
-    for (int64_t n = blockIdx.x * blockDim.x + threadIdx.x; n < N; n += (int64_t) gridDim.x * blockDim.x) {
-        float s = 0.f;
-        for (int j = 0; j < k; j++) s += w[t * k + j] * o[(int64_t) inv[t * k + j] * N + n];
-        store_out(y, yf32, t * N + n, s);
+    const int64_t n0 = 8 * ((int64_t) blockIdx.x * blockDim.x + threadIdx.x);
+    if (n0 >= N) return;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (N % 8 == 0) {
+        for (int j = 0; j < k; j++) {
+            const float wj = w[t * k + j];
+            const uint4 v = *(const uint4 *) (o + (int64_t) inv[t * k + j] * N + n0);
+            const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+            for (int i = 0; i < 4; i++) {
+                s[2 * i] += wj * __uint_as_float(d[i] << 16);
+                s[2 * i + 1] += wj * __uint_as_float(d[i] & 0xffff0000u);
+            }
+        }
+    } else {
+        for (int j = 0; j < k; j++) {
+            const float wj = w[t * k + j];
+            const uint16_t * row = o + (int64_t) inv[t * k + j] * N;
+            for (int i = 0; i < 8 && n0 + i < N; i++) s[i] += wj * bf16_to_f32(row[n0 + i]);
+        }
     }
-}
-
-__global__ void k_invert(const int32_t * __restrict__ perm, int64_t n, int32_t * __restrict__ inv) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) inv[perm[i]] = (int32_t) i;
+    for (int i = 0; i < 8 && n0 + i < N; i++) store_out(y, yf32, t * N + n0 + i, s[i]);
 }
 
 // ------------------------------------------------------------------ argmax
@@ -455,22 +468,16 @@ hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renor
 }
 
 hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_per_item, int32_t * off, int32_t * perm,
-                              int32_t * items, int32_t * nitems, hipStream_t s) {
-    k_moe_permute<<<1, 1024, (size_t) (2 * E + 1) * sizeof(int32_t), s>>>(ids, n, E, rows_per_item, off, perm, items,
-                                                                          nitems);
+                              int32_t * inv, int32_t * items, int32_t * nitems, hipStream_t s) {
+    k_moe_permute<<<1, 1024, (size_t) (2 * E + 1) * sizeof(int32_t), s>>>(ids, n, E, rows_per_item, off, perm, inv,
+                                                                          items, nitems);
     CHECK_LAUNCH();
     return hipSuccess;
 }
 
-hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s) {
-    k_invert<<<dim3((unsigned) ((n + 255) / 256)), 256, 0, s>>>(perm, n, inv);
-    CHECK_LAUNCH();
-    return hipSuccess;
-}
-
-hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
+hipError_t launch_moe_combine(const uint16_t * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s) {
-    dim3 grid((unsigned) ((N + 255) / 256), (unsigned) T);
+    dim3 grid((unsigned) ((N + 8 * 256 - 1) / (8 * 256)), (unsigned) T);
     k_moe_combine<<<grid, 256, 0, s>>>(o, inv, w, T, k, N, y, yf32);
     CHECK_LAUNCH();
     return hipSuccess;

@@ -56,7 +56,7 @@ struct MArgs {
     int64_t estride, NT, KB, N, K;
     const uint16_t * x;       // gate_up: token rows [T][K]; down: act rows in permuted order
     int64_t ldx;
-    void * y;                 // gate_up: act bf16 [T*k][N/2]; down: fp32 [T*k][N]
+    void * y;                 // gate_up: act bf16 [T*k][N/2]; down: bf16 [T*k][N]
     int64_t ldy;
     const int32_t * perm;     // permuted position -> entry t * k + j
     const int32_t * items;    // [nitems][3]
@@ -135,8 +135,9 @@ constexpr GskCfg GSK_CFGS[1] = {{2, 16, 8}};
 hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s);
 hipError_t launch_route(const float * logits, int64_t T, int E, int k, int renorm, int32_t * ids, float * w,
                         hipStream_t s);
+// ... and inv[i] = the position of entry i (perm's inverse)
 hipError_t launch_moe_permute(const int32_t * ids, int64_t n, int E, int rows_per_item, int32_t * off, int32_t * perm,
-                              int32_t * items, int32_t * nitems, hipStream_t s);
+                              int32_t * inv, int32_t * items, int32_t * nitems, hipStream_t s);
 // grouped GEMM over the work items (k_moe_gemm): grid.x column groups (gate_up: NT / 8, down: NT / 8)
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s);
 // one-launch MoE decode on `grid` workgroups (one per CU); hipErrorInvalidValue when the shapes are
@@ -149,8 +150,8 @@ hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry
                         hipStream_t s);
 // workgroups of the chained kernel that fit one CU at this LDS size
 int chain_occupancy(int fmt, int ring, size_t lds);
-hipError_t launch_invert(const int32_t * perm, int64_t n, int32_t * inv, hipStream_t s);
-hipError_t launch_moe_combine(const float * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
+// y[t] = sum_j w[t][j] o[inv[t k + j]] (o bf16 rows, fp32 sum)
+hipError_t launch_moe_combine(const uint16_t * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
 // one launch of argmax_parts(N) workgroups per row, each over ARGMAX_CHUNK values; keys: workspace
 // of rows * argmax_parts(N) * ARGMAX_PAD bytes; cnt: rows * ARGMAX_PAD bytes of counters, zero before

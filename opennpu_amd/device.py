@@ -153,8 +153,8 @@ class QFfn:
         return out
 
     def decode(self, logits, x, k, renorm=True, out=None, f32=False):
-        """router + FFN from logits fp32 [T][E] and x bf16 [T][H] (one launch for T <= 4, k <= 8):
-        returns (y [T][Nd], ids int32 [T][k], w fp32 [T][k])."""
+        """router + FFN from logits fp32 [T][E] and x bf16 [T][H]: returns (y [T][Nd], ids int32 [T][k],
+        w fp32 [T][k])."""
         import torch
         T, E = logits.shape
         ids = torch.empty((T, k), dtype=torch.int32, device=x.device)

@@ -12,13 +12,21 @@ pytestmark = pytest.mark.gpu
 
 
 def check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped, what):
-    """Decode (T <= 4) multiplies exact dequantized weights; the grouped prompt path feeds MFMA the
-    bf16 RNE of each weight, as the reference device does, so its per-element bound is taken against
-    that oracle. Both stay within the stated 1e-2 of the exact-weight oracle."""
+    """Decode (T <= 4) multiplies exact dequantized weights and sums the slots in fp32. The grouped
+    prompt path feeds MFMA the bf16 RNE of each weight and returns each expert's rows in bf16, as the
+    reference device does, before the fp32 weighted sum. The per-element bound is taken against the
+    oracle with the same rounding points; all stay within the stated 1e-2 of the exact oracle."""
     ref = orc.moe_layer(fmt, gu, dn, E, H, I, xb, rid, rw)
     if grouped:
-        check_bf16_out(y, orc.moe_layer(fmt, gu, dn, E, H, I, xb, rid, rw, bf16w=True), what=what + " (bf16 weights)",
-                       floor=2e-4)
+        # an expert row within fp32 rounding of a bf16 rounding boundary may round the other way than
+        # the oracle's (one bf16 ulp of that row), so the bound adds 2^-8 sum_j |w_j d_j|
+        r, m = orc.moe_layer(fmt, gu, dn, E, H, I, xb, rid, rw, bf16w=True, bf16o=True, mag=True)
+        what_g = what + " (bf16 weights, bf16 expert rows)"
+        y = np.asarray(y, np.float64)
+        scale = np.abs(r).max()
+        bad = np.abs(y - r) > 2.0 ** -8 * (np.abs(r) + m) + 2e-4 * scale
+        assert not bad.any(), f"{what_g}: {bad.sum()} elements outside the bound; first at {np.argwhere(bad)[0]}"
+        assert orc.max_rel_err(y, r) <= 1e-2, what_g
         assert orc.max_rel_err(y, ref) <= 1e-2, what
     else:
         check_bf16_out(y, ref, what=what, floor=2e-4)
@@ -89,9 +97,9 @@ def test_moe_ffn_small(gpu, fmt, T):
     check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=T > 4, what=f"moe fmt {fmt} T {T}")
 
 
-@pytest.mark.parametrize("T,check_tokens", [(1, 1), (512, 24)])
+@pytest.mark.parametrize("T,check_tokens", [(1, 1), (512, 512)])
 def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
-    """128 experts, H=2048, I=768, top-8 (router on device), g128s; a subset of tokens checked."""
+    """128 experts, H=2048, I=768, top-8 (router on device), g128s; every token checked."""
     import torch
     E, H, I, k = 128, 2048, 768, 8
     fmt = orc.FMT_G128S
@@ -111,17 +119,19 @@ def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
     check_moe(y[tok], fmt, gu, dn, E, H, I, xb[tok], rid[tok], rw[tok], grouped=T > 4, what=f"qwen3-30b-a3b T {T}")
 
 
-@pytest.mark.parametrize("fmt", [orc.FMT_G128S, orc.FMT_Q4S, orc.FMT_Q4NX])
-@pytest.mark.parametrize("E,H,I,k,T", [(128, 2048, 768, 8, 1), (128, 2048, 768, 8, 4), (16, 512, 256, 4, 3),
-                                       (24, 384, 160, 6, 2)])
+# g128s needs whole 128-wide groups along the down projection's K = I: no I = 160 case for it
+_ONE_LAUNCH = [(fmt, *shape) for fmt in (orc.FMT_G128S, orc.FMT_Q4S, orc.FMT_Q4NX)
+               for shape in ((128, 2048, 768, 8, 1), (128, 2048, 768, 8, 4), (16, 512, 256, 4, 3), (24, 384, 160, 6, 2))
+               if not (fmt == orc.FMT_G128S and shape[2] % 128)]
+
+
+@pytest.mark.parametrize("fmt,E,H,I,k,T", _ONE_LAUNCH)
 def test_moe_decode_one_launch(gpu, fmt, E, H, I, k, T, monkeypatch):
     """router + gate_up / SiLU * up + down / weighted sum in one launch (k_moe_decode): ids and w
     equal the oracle router, y within the bf16 bound of the oracle layer; the multi-launch path (the
     router kernel, then the two GEMV launches) agrees; repeated calls and graph replays give the same
     bits (the act counters are left at zero), and no wait timed out."""
     import torch
-    if fmt == orc.FMT_G128S and I % 128:
-        pytest.skip("g128s needs whole 128-wide groups along the down projection's K = I")
     gu, dn = _experts(fmt, E, H, I, 300 + E + T)
     xb = syn.activations(T, H, 301 + T)
     lg = syn.logits(T, E, 302 + k)
