@@ -361,6 +361,42 @@ def attn_step(q, K, V, mask=None, sinks=None, scale=None):
     return out
 
 
+# ------------------------------------------------------------------ CPU baseline kernels
+_cpu = None
+
+
+def cpu_lib():
+    """oracle/_build/libcpuint4.so: the fused int4 CPU GEMV of the benchmark's CPU baseline
+    (oracle/cpu_int4.c)."""
+    global _cpu
+    if _cpu is None:
+        p = HERE / "_build" / "libcpuint4.so"
+        if not p.exists():
+            build()
+        L = C.CDLL(str(p))
+        P, I64, I32 = C.c_void_p, C.c_int64, C.c_int
+        for n in ("cpu_g128s_mv", "cpu_q4_0_mv"):
+            getattr(L, n).restype = I32
+            getattr(L, n).argtypes = [P, I64, I64, P, I32, P, I32, I32]
+        _cpu = L
+    return _cpu
+
+
+def cpu_mv(fmt, st, N, K, x, threads=1, isa_max=2):
+    """y [M][N] fp32 = x [M][K] (fp32) . W^T by the fused CPU kernel (g128s or Q4_0, M <= 8);
+    returns (y, instruction set used: 2 AVX-512, 1 AVX2, 0 scalar)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, K)
+    M = x.shape[0]
+    y = np.empty((M, N), np.float32)
+    fn = cpu_lib().cpu_g128s_mv if fmt == FMT_G128S else cpu_lib().cpu_q4_0_mv
+    if fmt not in (FMT_G128S, FMT_Q4_0):
+        raise ValueError("the CPU baseline kernel covers g128s and Q4_0")
+    isa = fn(_p(np.ascontiguousarray(st)), N, K, _p(x), M, _p(y), threads, isa_max)
+    if isa < 0:
+        raise ValueError("cpu_mv: K off the format's group or M outside 1..8")
+    return y, isa
+
+
 def max_rel_err(y, r):
     """max|y - r| / max|r| (the tolerance BASELINE states; offload.py:313-315 reports rel-L2)."""
     y = np.asarray(y, np.float64)

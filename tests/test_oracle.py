@@ -678,3 +678,17 @@ def test_gdn_beta_zero_is_pure_decay():
     ad = a["Wa"] @ a["x"] + a["dt_bias"]
     decay = np.exp(-np.exp(a["A_log"]) * np.log1p(np.exp(ad)))
     assert np.allclose(S, a["S"] * decay[:, None, None], rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("fmt", [orc.FMT_G128S, orc.FMT_Q4_0])
+@pytest.mark.parametrize("isa", [2, 1, 0])
+def test_cpu_baseline_kernel_against_the_oracle(fmt, isa):
+    """the benchmark's fused int4 CPU kernel (oracle/cpu_int4.c) against the fp64 oracle product,
+    each instruction-set path (AVX-512 where this CPU has it), M from 1 to 8, ragged N"""
+    N, K = 131, 1024
+    st = syn.weights(fmt, N, K, 3 + fmt)
+    for M in (1, 3, 8):
+        xb = syn.activations(M, K, 4 + M)
+        y, used = orc.cpu_mv(fmt, st, N, K, orc.bf2f(xb).reshape(M, K), threads=2, isa_max=isa)
+        assert used <= isa
+        assert orc.max_rel_err(y, orc.qmm(fmt, st, N, K, xb)) <= 1e-5, (fmt, isa, M)
