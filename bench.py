@@ -419,6 +419,84 @@ def decode_glue(torch):
     return out
 
 
+def ceilings(torch):
+    """What this GPU delivers to simple kernels (libonpu_probe.so, csrc/onpu_probe.hip) and to the
+    vendor bf16 GEMM, so the int4 kernels can be read against measured ceilings as well as the
+    published peaks: a streaming read of 4 GiB (every byte once, 16-byte loads), a torch device
+    copy of 2 GiB, the LDS read rate (ds_read_b128, conflict-free), the bf16 MFMA issue rate
+    (v_mfma_f32_16x16x32_bf16, 8 independent accumulators, 2 waves per SIMD), the effective shader
+    clock (s_memtime against the 100 MHz s_memrealtime, in the MFMA and LDS probes) and torch's
+    bf16 GEMM (hipBLASLt) at the Llama-3.1-8B prefill shapes. Medians of 5 timed windows."""
+    import ctypes as C
+    P = C.CDLL(str(ROOT / "opennpu_amd" / "libonpu_probe.so"))
+    for n in ("onpu_probe_read", "onpu_probe_lds", "onpu_probe_mfma"):
+        getattr(P, n).restype = C.c_int
+    P.onpu_probe_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    P.onpu_probe_lds.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    P.onpu_probe_mfma.argtypes = P.onpu_probe_lds.argtypes
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    clk = torch.zeros(4, dtype=torch.int64, device="cuda")
+    st = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def ok(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe launch failed: {rc}")
+
+    def clock_hz():
+        c = clk.cpu().tolist()
+        return (c[2] - c[0]) / max(c[3] - c[1], 1) * 100e6
+
+    out = {"cus": cus}
+    nb = 4 << 30
+    buf = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    rd = {}
+    for wpc in (8, 16):
+        t = time_med(torch, lambda: ok(P.onpu_probe_read(buf.data_ptr(), nb, cus * wpc, sink.data_ptr(),
+                                                         clk.data_ptr(), st())), 5, 2)
+        rd[f"{wpc}_wg_per_cu"] = nb / t / 1e9
+    out["hbm_read_GBps"] = max(rd.values())
+    out["hbm_read_by_grid"] = rd
+    del buf
+    src = torch.empty(2 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    t = time_med(torch, lambda: dst.copy_(src), 5, 2)
+    out["copy_GBps_read_plus_write"] = 2 * src.numel() / t / 1e9
+    del src, dst
+    iters = 4096
+    lds = {}
+    for waves in (8, 16):
+        t = time_med(torch, lambda: ok(P.onpu_probe_lds(cus, waves, iters, sink.data_ptr(), clk.data_ptr(), st())), 5, 2)
+        hz = clock_hz()
+        byts = cus * waves * 64 * iters * 8 * 16
+        lds[f"{waves}_waves"] = {"TBps": byts / t / 1e12, "bytes_per_clk_per_cu": byts / t / hz / cus,
+                                 "clock_GHz": hz / 1e9}
+    out["lds_read"] = lds
+    iters = 2048
+    t = time_med(torch, lambda: ok(P.onpu_probe_mfma(cus * 2, 4, iters, sink.data_ptr(), clk.data_ptr(), st())), 5, 2)
+    hz = clock_hz()
+    fl = cus * 2 * 4 * iters * 8 * 16384.0
+    out["mfma_bf16_TFLOPS"] = fl / t / 1e12
+    out["mfma_clock_GHz"] = hz / 1e9
+    out["mfma_cycles_per_16x16x32"] = (cus * 4 * hz * t) / (fl / 16384.0)
+    gm = {}
+    M = 2048
+    for name, N, K in [("up", 14336, 4096), ("down", 4096, 14336)]:
+        x = torch.randn(M, K, device="cuda").to(torch.bfloat16)
+        W = torch.randn(N, K, device="cuda").to(torch.bfloat16)
+        y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+        t = time_med(torch, lambda: torch.matmul(x, W.t(), out=y), 10, 3)
+        gm[name] = {"us_per_call": t * 1e6, "TFLOPS": 2.0 * M * N * K / t / 1e12}
+        del x, W, y
+    try:
+        lib = str(torch.backends.cuda.preferred_blas_library())
+    except Exception:  # noqa: BLE001 - older torch: the default backend
+        lib = "default"
+    out["bf16_gemm_torch"] = {**gm, "blas": lib}
+    return out
+
+
 def cpu_dequant(orc, fmt, st, N, K):
     """fp32 [N][K] dequantized with numpy as the reference's CPU path writes it (reference.py:24-28:
     unpack the codes, minus 8, times the group scale); the CPU baseline times this"""
@@ -581,11 +659,28 @@ def cpu_baseline(syn):
 
 def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3):
     """Decode GEMVs alone, for hardware-counter runs: each named Qwen3-8B matrix (g128s, M=1) over
-    its 36 HBM copies, `reps` eager launches each, in the order given, then one plain 512 MiB device
-    copy (torch copy_) whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters' unit."""
+    its 36 HBM copies (or, for "lm_head", the Q4_0 LM head with its argmax at M = 1 and 5 over 2
+    copies), `reps` eager launches each, in the order given, then one plain 512 MiB device copy
+    (torch copy_) whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters' unit."""
     shapes = {name: (N, K) for name, N, K in QWEN3_8B}
     out = []
     for name in names:
+        if name == "lm_head":
+            # the Q4_0 151936 x 4096 LM head with its argmax at M = 1 then 5, on 2 copies
+            N, K = 151936, 4096
+            st = syn.weights(Q4_0, N, K, 11)
+            mats = [QMatrix(N, K, Q4_0, st) for _ in range(2)]
+            for M in (1, 5):
+                x = bf16_tensor(torch, syn.activations(M, K, 12)).reshape(M, K)
+                for _ in range(reps):
+                    for q in mats:
+                        q.argmax(x)
+                torch.cuda.synchronize()
+                out.append({"matrix": f"lm_head {N}x{K} Q4_0 M={M} + argmax", "launches": reps * len(mats),
+                            "algorithmic_bytes_per_launch": wbytes(Q4_0, N, K) + M * K * 2 + M * N * 4})
+            for q in mats:
+                q.free()
+            continue
         N, K = shapes[name]
         st = syn.weights(G128S, N, K, 100 + N + K)
         mats = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
@@ -654,12 +749,14 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline step only (no extra configs, no CPU leg)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile", nargs="?", const="gate_up", default=None,
-                    help="only the named decode GEMVs (comma-separated: qkv, o, gate_up, down; default "
+                    help="only the named decode GEMVs (comma-separated: qkv, o, gate_up, down, lm_head; default "
                          "gate_up) plus a calibration copy, for rocprofv3 --pmc runs")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only the prefill GEMMs, for rocprofv3 --pmc runs")
     ap.add_argument("--profile-moe", action="store_true",
                     help="only the MoE layer (T = 512 and T = 1), for rocprofv3 runs")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="only the measured ceilings (HBM read, copy, LDS, MFMA, clock, vendor bf16 GEMM)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the int4 path on a single MI355X; --gpus {args.gpus} "
@@ -678,6 +775,9 @@ def main():
         return
     if args.profile_moe:
         profile_moe(torch, QFfn, syn)
+        return
+    if args.ceilings:
+        print(json.dumps({"ceilings": ceilings(torch)}), flush=True)
         return
     t_all = time.perf_counter()
     log("decode layers ...")
@@ -703,11 +803,17 @@ def main():
         configs["weight_codecs_qwen3_8b_layer"] = codecs(torch, QMatrix)
         log("decode attention, int8 GEMV ...")
         configs["decode_glue"] = decode_glue(torch)
+        log("measured ceilings ...")
+        configs["ceilings"] = ceilings(torch)
     gu = head["per_matrix"]["gate_up"]
     roof = {"kernel": "k_qgemv<g128s> gate+up 24576x4096, M=1 (768 workgroups x 8 waves, x in LDS)",
             "bound": "hbm", "achieved": gu["GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": gu["GBps"] / (HBM_PEAK / 1e9), "traffic": GATE_UP_TRAFFIC, "bytes_per_launch": gu["bytes"],
             "us_per_launch": gu["us"]}
+    if "ceilings" in configs:
+        # the same kernel against the streaming read this GPU measured in this run
+        roof["measured_read_ceiling_GBps"] = configs["ceilings"]["hbm_read_GBps"]
+        roof["frac_of_measured_ceiling"] = gu["GBps"] / configs["ceilings"]["hbm_read_GBps"]
     cpu = None
     if not (args.quick or args.no_cpu):
         log("cpu baseline ...")

@@ -123,12 +123,15 @@ int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
  * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels, larger M the MFMA GEMM. */
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
 /* Workspace of the calls above. M > 64 runs the split-K prefill GEMM, whose partial tiles and slot
- * words belong to the stream (one workspace per stream, whatever the handle): calls ordered on one
- * stream share it; calls on different streams use different ones. Its first use on a stream (or
- * growth to a larger split) allocates, and the argmax allocates its keys on a handle's first call
- * with that many rows, so make those first calls outside HIP graph capture (or use
- * onpu_dense_argmax_dev_noalloc). Argmax calls on one handle share its keys: order them on one
- * stream. */
+ * words belong to the stream (one workspace per stream, whatever the handle, about 64 MiB, kept
+ * until the process ends): calls ordered on one stream share it; calls on different streams use
+ * different ones. Its first use on a stream allocates it with hipMalloc and clears its slot words
+ * with a kernel on that stream, both legal under HIP graph capture, so a first GEMM may be captured
+ * (the clearing kernel becomes a node of the graph). A graph's GEMMs use the capturing stream's
+ * workspace: replay a graph while no other GEMM on that stream runs. The argmax allocates its keys
+ * and clears its counters on a handle's first call with that many rows: make that call outside
+ * capture (or use onpu_dense_argmax_dev_noalloc). Argmax calls on one handle share its keys: order
+ * them on one stream. */
 /* 1 if a split-K GEMM gave up waiting for its partner workgroup since the last call (the flag is then
  * cleared and that launch's Y is invalid), 0 if not, -1 on error; synchronises the device */
 int onpu_gemm_status(void);

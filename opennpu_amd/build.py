@@ -1,4 +1,5 @@
-"""Builds libonpu_hip.so in-tree (opennpu_amd/libonpu_hip.so) with hipcc for gfx950.
+"""Builds libonpu_hip.so in-tree (opennpu_amd/libonpu_hip.so) with hipcc for gfx950, and the
+benchmark's ceiling probes (opennpu_amd/libonpu_probe.so, csrc/onpu_probe.hip; no part of the ABI).
 
     python -m opennpu_amd.build          # or __graft_entry__.build()
 
@@ -15,6 +16,7 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent
 CSRC = HERE / "csrc"
 OUT = HERE / "libonpu_hip.so"
+PROBE = HERE / "libonpu_probe.so"
 BUILD = HERE / "_build"
 ARCH = os.environ.get("ONPU_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -38,16 +40,23 @@ def _compile(job):
 
 def build(verbose=True):
     BUILD.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    with ThreadPoolExecutor(min(len(SOURCES) + 1, os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(_compile, SOURCES + [("onpu_probe.hip", [], "onpu_probe")]))
+    probe = objs.pop()
     tmp = OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs), "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
+    tmp = PROBE.with_suffix(".so.tmp")
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(probe)],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"probe link failed:\n{r.stderr}")
+    os.replace(tmp, PROBE)
     if verbose:
-        print(f"built {OUT} ({OUT.stat().st_size} bytes)")
+        print(f"built {OUT} ({OUT.stat().st_size} bytes), {PROBE.name}")
     return OUT
 
 

@@ -317,37 +317,46 @@ bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & g
     return true;
 }
 
-// k_qgemm_sk workspace, one per stream (not per matrix): partial tiles for the cut tiles of the
-// largest split used on that stream (at most one per CU), the slot words and the control words,
-// zeroed when allocated. Launches on one stream run in order, so they share it safely; launches on
-// different streams get different workspaces. Growing it waits for the stream (the old partials may
-// still be in use), so the first prompt-sized call on a stream belongs outside graph capture.
+// k_qgemm_sk workspace, one per stream (not per matrix): partial tiles, the slot words and the
+// control words. Launches on one stream run in order, so they share it safely; launches on
+// different streams get different workspaces.
 struct GskWs { DBuf part, sync; };
 std::mutex g_gsk_mu;
 std::vector<std::pair<hipStream_t, GskWs *>> g_gsk;      // a few streams: a linear search
 
+// The split-K workspace of stream s, created on the stream's first split-K call at its full size
+// (a partial tile for every CU: a launch cuts at most one tile per workgroup and runs at most one
+// workgroup per CU), so it never moves: a graph that captured a GEMM keeps valid pointers. Its sync
+// words are cleared by a kernel on s (under capture, a node of the graph ahead of the GEMM), so the
+// first call may be captured.
 hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** sync, int32_t ** ctl) {
     size_t slot = 0;
     for (const GskCfg & c : GSK_CFGS) slot = std::max(slot, (size_t) c.wv * c.mbg * c.ntw * 1024);
+    if (cut > device().cus) return hipErrorInvalidValue;
     std::lock_guard<std::mutex> lk(g_gsk_mu);
     GskWs * w = nullptr;
     for (auto & p : g_gsk)
         if (p.first == s) w = p.second;
-    hipError_t e = hipSuccess;
     if (!w) {
         w = new GskWs;
-        const size_t sb = ((size_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_INTS) * 4;
-        if ((e = w->sync.ensure(sb)) != hipSuccess || (e = hipMemset(w->sync.p, 0, sb)) != hipSuccess) {
+        const int64_t ints = (int64_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_INTS;
+        // hipMalloc is not stream-ordered: relaxed mode lets it run while this thread captures
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        hipError_t e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) {
+            delete w;
+            return e;
+        }
+        e = w->part.ensure(slot * (size_t) device().cus);
+        if (e == hipSuccess) e = w->sync.ensure((size_t) ints * 4);
+        (void) hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess || (e = launch_zero_i32(w->sync.as<int32_t>(), ints, s)) != hipSuccess) {
+            w->part.release();
             w->sync.release();
             delete w;
             return e;
         }
         g_gsk.emplace_back(s, w);
-    }
-    const size_t need = slot * (size_t) std::max<int64_t>(cut, 1);
-    if (w->part.n < need) {
-        if (w->part.p && (e = hipStreamSynchronize(s)) != hipSuccess) return e;
-        if ((e = w->part.ensure(need)) != hipSuccess) return e;
     }
     *part = w->part.as<float>();
     *sync = w->sync.as<int32_t>();

@@ -781,6 +781,20 @@ DEV u32x4 dequant8(uint32_t d, float s, float c) {
                    pack_bf16x2(f(hi, 1), f(hi, 3))};
 }
 
+// dequant8 in parts, for spreading its VALU work: dequant_split separates the nibbles into bytes,
+// dequant_part(k) forms output dword k of dequant8 (the same operations, so the same bits)
+DEV void dequant_split(uint32_t d, uint32_t & lo, uint32_t & hi) {
+    const uint32_t M = opaque_s(0x0f0f0f0fu);
+    lo = d & M;
+    hi = (d >> 4) & M;
+}
+DEV uint32_t dequant_part(uint32_t lo, uint32_t hi, int k, float s, float c) {
+    auto f = [&](uint32_t w, int byte) { return fmaf((float) ((w >> (8 * byte)) & 0xffu), s, c); };
+    const uint32_t w = (k & 1) ? hi : lo;
+    const int b = k >> 1;                    // dwords: (lo 0, 2), (hi 0, 2), (lo 1, 3), (hi 1, 3)
+    return pack_bf16x2(f(w, b), f(w, b + 2));
+}
+
 // scale s and additive constant c of MFMA step j such that w = u * s + c
 template <int FMT>
 DEV void par_sc(const GPar<FMT> & p, int j, float & s, float & c) {
@@ -1025,47 +1039,50 @@ DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow
     }
 }
 
-// one 128-wide K block: 4 steps j x MBG / 8 half-steps of 8 A blocks. The A fragments of the next
-// half-step are read from LDS while the current one's MFMAs run, and the weight fragments of step
-// j + 1 are dequantized during step j (tile i in half-step i % H), so neither LDS latency nor the
-// dequant sits in front of an MFMA except at the block's start.
+// one 128-wide K block, 4 steps j x MBG row blocks, with a rolling A pipeline: fragment p = (j, mb),
+// in j-major order, is read PD fragments ahead of its MFMAs, so LDS latency hides behind the MFMAs
+// of the PD fragments in between (20 registers of read-ahead; a double buffer of a half-step's 8
+// fragments took 64, which left the compiler no room to keep the reads ahead: it issued each read
+// just before its use, 4-5 % slower). A scheduling fence closes every row block, so no read can
+// sink toward its use. The next step's weight fragments are dequantized one output dword per row
+// block (dequant8 in four parts), spread over the current step.
 template <int FMT, int NTW, int MBG>
-DEV void gemm_block_sk(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW], int lane,
+DEV void gemm_block_rp(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW], int lane,
                        f32x4 (&acc)[MBG][NTW]) {
-    constexpr int HB = 8, H = MBG / HB, S = 4 * H;
-    u32x4 xa[2][HB], bw[2][NTW];
+    constexpr int PD = 4, NP = 4 * MBG, DQ = MBG / (4 * NTW);
+    static_assert(MBG % (4 * NTW) == 0, "dequant spread: four parts per tile and step");
+    u32x4 xa[PD + 1], bw[2][NTW];
+    uint32_t lo[NTW], hi[NTW];
+    float sc[NTW], cc[NTW];
+#pragma unroll
+    for (int p = 0; p < PD; p++) xa[p] = *LDS_U32X4(&xsb[((p % MBG) * 4 + p / MBG) * 64 + lane]);
 #pragma unroll
     for (int i = 0; i < NTW; i++) {
-        float sc, cc;
-        par_sc<FMT>(pr[i], 0, sc, cc);
-        bw[0][i] = dequant8<FMT>(wr[i][0], sc, cc);
+        par_sc<FMT>(pr[i], 0, sc[i], cc[i]);
+        bw[0][i] = dequant8<FMT>(wr[i][0], sc[i], cc[i]);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int mb = 0; mb < HB; mb++) xa[0][mb] = *LDS_U32X4(&xsb[(mb * 4 + 0) * 64 + lane]);
+    for (int j = 0; j < 4; j++) {
 #pragma unroll
-    for (int s = 0; s < S; s++) {
-        const int j = s / H, h = s % H;
-        if (s + 1 < S) {
-            const int j1 = (s + 1) / H, h1 = (s + 1) % H;
-#pragma unroll
-            for (int mb = 0; mb < HB; mb++)
-                xa[(s + 1) & 1][mb] = *LDS_U32X4(&xsb[((h1 * HB + mb) * 4 + j1) * 64 + lane]);
-        }
-        if (j + 1 < 4) {
-#pragma unroll
-            for (int i = 0; i < NTW; i++) {
-                if (i % H != h) continue;
-                float sc, cc;
-                par_sc<FMT>(pr[i], j + 1, sc, cc);
-                bw[(j + 1) & 1][i] = dequant8<FMT>(wr[i][j + 1], sc, cc);
+        for (int mb = 0; mb < MBG; mb++) {
+            const int p = j * MBG + mb;
+            if (p + PD < NP) {
+                const int f = p + PD;
+                xa[f % (PD + 1)] = *LDS_U32X4(&xsb[((f % MBG) * 4 + f / MBG) * 64 + lane]);
             }
+            if (j + 1 < 4 && mb % DQ == 0) {                // part k of tile i for step j + 1
+                const int i = (mb / DQ) / 4, k = (mb / DQ) % 4;
+                if (k == 0) {
+                    par_sc<FMT>(pr[i], j + 1, sc[i], cc[i]);
+                    dequant_split(wr[i][j + 1], lo[i], hi[i]);
+                }
+                bw[(j + 1) & 1][i][k] = dequant_part(lo[i], hi[i], k, sc[i], cc[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa[p % (PD + 1)], bw[j & 1][i], acc[mb][i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int mb = 0; mb < HB; mb++)
-#pragma unroll
-            for (int i = 0; i < NTW; i++)
-                acc[h * HB + mb][i] = mfma(xa[s & 1][mb], bw[j & 1][i], acc[h * HB + mb][i]);
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -1162,7 +1179,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
                 gemm_load_x_sk<FPW>(xr, xrow, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, nxt);
                 gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wn, pn);
             }
-            gemm_block_sk<FMT, NTW, MBG>(cur, wc, pc, lane, acc);
+            gemm_block_rp<FMT, NTW, MBG>(cur, wc, pc, lane, acc);
             __builtin_amdgcn_s_waitcnt(0x0f70);
             __syncthreads();
 #pragma unroll

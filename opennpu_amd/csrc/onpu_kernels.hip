@@ -483,6 +483,18 @@ hipError_t launch_moe_combine(const uint16_t * o, const int32_t * inv, const flo
     return hipSuccess;
 }
 
+__global__ void k_zero_i32(int32_t * p, int64_t n) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t) gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    k_zero_i32<<<(unsigned) std::min<int64_t>((n + 255) / 256, 1024), 256, 0, s>>>(p, n);
+    CHECK_LAUNCH();
+    return hipSuccess;
+}
+
 int64_t argmax_parts(int64_t N) { return (N + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
 
 // ------------------------------------------------------------------ argmax scratch without allocation

@@ -130,6 +130,7 @@ hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
 // one wave per SIMD and 256 x 32 with four waves: both slower, the first by ~30 %; and against
 // 128 x 64 per wave with eight waves, which halves the LDS reads of X but doubles the dequantization
 // per MFMA and spills: 40 % slower.)
+// k_qgemm_sk configurations: weight tiles per wave, row blocks per wave, waves
 struct GskCfg { int ntw, mbg, wv; };
 constexpr GskCfg GSK_CFGS[1] = {{2, 16, 8}};
 hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s);
@@ -150,6 +151,8 @@ hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry
                         hipStream_t s);
 // workgroups of the chained kernel that fit one CU at this LDS size
 int chain_occupancy(int fmt, int ring, size_t lds);
+// p[0, n) = 0 by a kernel on stream s (a graph node under capture, unlike a memset)
+hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s);
 // y[t] = sum_j w[t][j] o[inv[t k + j]] (o bf16 rows, fp32 sum)
 hipError_t launch_moe_combine(const uint16_t * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);

@@ -226,6 +226,40 @@ def test_gemm_two_streams(gpu):
         qb.free()
 
 
+def test_gemm_first_call_under_capture(gpu):
+    """torch.cuda.graph captures on a stream of its own, so the split-K GEMMs it records are that
+    stream's first: its workspace is allocated and cleared during the capture (the clearing kernel
+    is a node of the graph). Two GEMMs with different cut counts in one graph, replays interleaved
+    with eager GEMMs on the default stream, each replay equal to the eager results bit for bit."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    shapes = [(1024, 7168, 4096), (2048, 4096, 14336)]
+    mats = [QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 60 + N)) for _, N, K in shapes]
+    try:
+        xs = [to_torch_bf16(syn.activations(M, K, 61 + K)).reshape(M, K) for M, _, K in shapes]
+        ref = [q.mv(x, f32=True) for q, x in zip(mats, xs)]
+        torch.cuda.synchronize()
+        outs = [torch.empty_like(r) for r in ref]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for q, x, o in zip(mats, xs, outs):
+                q.mv(x, out=o)
+        for rep in range(3):
+            for o in outs:
+                o.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            for o, r in zip(outs, ref):
+                assert torch.equal(o, r), f"replay {rep} differs from the eager GEMM"
+            ye = mats[1].mv(xs[1], f32=True)
+            torch.cuda.synchronize()
+            assert torch.equal(ye, ref[1]), "eager GEMM after a replay differs"
+        assert mats[0].L.onpu_gemm_status() == 0
+    finally:
+        for q in mats:
+            q.free()
+
+
 def test_scratch_over_a_model_of_handles(gpu):
     """36 layers x 4 Qwen3-8B-shaped matrices, an M = 2048 GEMM through each on one stream, then
     host-pointer calls at 2048 rows through several of them: the workspaces do not grow with the
