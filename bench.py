@@ -657,6 +657,15 @@ def cpu_baseline(syn):
             "cpu_model": cpu, "configs": out}
 
 
+def calibration_copy(torch):
+    """one plain 512 MiB device copy (torch copy_): what FETCH_SIZE and WRITE_SIZE report for it per
+    dispatch gives their unit"""
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3):
     """Decode GEMVs alone, for hardware-counter runs: each named Qwen3-8B matrix (g128s, M=1) over
     its 36 HBM copies (or, for "lm_head", the Q4_0 LM head with its argmax at M = 1 and 5 over 2
@@ -694,10 +703,7 @@ def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3):
             q.free()
         out.append({"matrix": f"{name} {N}x{K} g128s M=1", "launches": reps * LAYERS,
                     "algorithmic_bytes_per_launch": wbytes(G128S, N, K) + K * 2 + N * 2})
-    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    torch.cuda.synchronize()
+    calibration_copy(torch)
     print(json.dumps({"profile_target": out, "calibration_copy_bytes": 512 << 20}), flush=True)
 
 
@@ -719,8 +725,8 @@ def profile_gemm(torch, QMatrix, syn, reps=3):
 
 def profile_moe(torch, QFfn, syn, reps=3):
     """The Qwen3-30B-A3B MoE layer alone (E 128, H 2048, I 768, top-8, g128s) at T = 512 and T = 1,
-    `reps` calls each (router, permutation, grouped GEMMs, combine / the decode GEMVs), for
-    hardware-counter and trace runs."""
+    `reps` calls each (router, permutation, grouped GEMMs, combine / the decode GEMVs), then one plain
+    512 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE, for hardware-counter and trace runs."""
     E, H, I, k = 128, 2048, 768, 8
     gu = np.concatenate([syn.weights(G128S, 2 * I, H, 300 + e) for e in range(E)])
     dn = np.concatenate([syn.weights(G128S, H, I, 600 + e) for e in range(E)])
@@ -735,6 +741,7 @@ def profile_moe(torch, QFfn, syn, reps=3):
             f.ffn(x, i, w, out=y)
         torch.cuda.synchronize()
     f.free()
+    calibration_copy(torch)
     per_expert = wbytes(G128S, 2 * I, H) + wbytes(G128S, H, I)
     print(json.dumps({"profile_target": "Qwen3-30B-A3B MoE layer, T = 512 then T = 1", "calls_each": reps,
                       "gate_up_bytes_per_expert": wbytes(G128S, 2 * I, H), "down_bytes_per_expert": wbytes(G128S, H, I),
