@@ -11,10 +11,15 @@
  *   - router: torch softmax/topk + the invariants sum(w) = 1, ids = top-k of the logits;
  *   - silu-mul / weighted sum / argmax: torch.nn.functional.silu, numpy, first-max rule;
  *   - geometry: the values the reference formula gives at the benchmark shapes.
+ *   - act / weighted sum / attention step / int8 GEMV: also against the reference's own
+ *     onpu_cpu.cpp compiled under oracle/_ref (tests/test_oracle_ref.py).
  * The search quantizers (orc_quant_sym / orc_quant_asym32) are off the measured path and are
- * only checked by invariants (exact grids come back exactly): parity unpinned. The GGUF codecs
- * (orc_quant_q4_0, orc_transcode_q4k) are checked on hand-built blocks whose results are exact,
- * by the closed forms of the formats, and the transcode's choice by a brute-force neighbourhood.
+ * checked by invariants only: exact grids come back exactly, sign symmetry (-x gives the same
+ * codes and the negated scale), power-of-two equivariance. Their candidate tables and refit order
+ * are not fixed by those: parity unpinned. The GGUF codecs (orc_quant_q4_0, orc_transcode_q4k)
+ * are checked on hand-built blocks whose results are exact, by the closed forms of the formats
+ * (Q4_0's truncation at exact half-way inputs included), and the transcode's choice by a
+ * brute-force neighbourhood.
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, so no fused multiply-adds change rounding).
  */
