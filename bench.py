@@ -422,16 +422,18 @@ def decode_glue(torch):
 def ceilings(torch):
     """What this GPU delivers to simple kernels (libonpu_probe.so, csrc/onpu_probe.hip) and to the
     vendor bf16 GEMM, so the int4 kernels can be read against measured ceilings as well as the
-    published peaks: a streaming read of 4 GiB (every byte once, 16-byte loads), a torch device
+    published peaks: a streaming read of 4 GiB (every byte once, 16-byte loads, one contiguous
+    range per workgroup), a torch device
     copy of 2 GiB, the LDS read rate (ds_read_b128, conflict-free), the bf16 MFMA issue rate
     (v_mfma_f32_16x16x32_bf16, 8 independent accumulators, 2 waves per SIMD), the effective shader
     clock (s_memtime against the 100 MHz s_memrealtime, in the MFMA and LDS probes) and torch's
-    bf16 GEMM (hipBLASLt) at the Llama-3.1-8B prefill shapes. Medians of 5 timed windows."""
+    bf16 GEMM (hipBLASLt) at the Llama-3.1-8B prefill shapes. Medians of 5 timed windows; the read
+    ceiling is the best of 4 or 16 workgroups per CU and 4 or 16 loads in flight per lane."""
     import ctypes as C
     P = C.CDLL(str(ROOT / "opennpu_amd" / "libonpu_probe.so"))
     for n in ("onpu_probe_read", "onpu_probe_lds", "onpu_probe_mfma"):
         getattr(P, n).restype = C.c_int
-    P.onpu_probe_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    P.onpu_probe_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     P.onpu_probe_lds.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     P.onpu_probe_mfma.argtypes = P.onpu_probe_lds.argtypes
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -452,10 +454,11 @@ def ceilings(torch):
     buf = torch.empty(nb, dtype=torch.uint8, device="cuda")
     buf.fill_(1)
     rd = {}
-    for wpc in (8, 16):
-        t = time_med(torch, lambda: ok(P.onpu_probe_read(buf.data_ptr(), nb, cus * wpc, sink.data_ptr(),
-                                                         clk.data_ptr(), st())), 5, 2)
-        rd[f"{wpc}_wg_per_cu"] = nb / t / 1e9
+    for wpc in (4, 16):
+        for unroll in (4, 16):
+            t = time_med(torch, lambda: ok(P.onpu_probe_read(buf.data_ptr(), nb, cus * wpc, unroll, sink.data_ptr(),
+                                                             clk.data_ptr(), st())), 5, 2)
+            rd[f"{wpc}_wg_per_cu_{unroll}_loads"] = nb / t / 1e9
     out["hbm_read_GBps"] = max(rd.values())
     out["hbm_read_by_grid"] = rd
     del buf

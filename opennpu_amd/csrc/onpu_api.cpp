@@ -215,10 +215,9 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     // in workgroups of up to 8 tile groups sharing one x copy: measured on the 151936 x 4096 LM head,
     // M = 5: 65.7 us against 75.0 us with two K parts per tile and 4 tiles (M = 1: equal)
     const bool vocab = groups * slots >= 4096;
+    // (4096 x 12288 at M = 1: 6 blocks per wave, 8.19 us, against 8.74 us with 12, interleaved on one
+    // box; at M = 4 and 8 the two are equal)
     int64_t per = std::min<int64_t>(vocab ? 32 : 8, std::max<int64_t>(4, (groups * slots * KB + 4095) / 4096));
-    // one row of x and long rows (64 or more K blocks): 12 blocks per wave; 4096 x 12288 at M = 1,
-    // 8.32-8.36 us against 8.67 us with 6 (at M = 4 and 8 the 6-block split is faster)
-    if (!vocab && KB >= 64 && M == 1) per = std::max<int64_t>(per, 12);
     int64_t kw = std::min<int64_t>(16, std::max<int64_t>(1, (KB + per - 1) / per));
     const int ekw = env_int("ONPU_GEMV_KW", 0);
     if (ekw > 0) kw = std::min<int64_t>(ekw, KB);

@@ -130,7 +130,6 @@ hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
 // one wave per SIMD and 256 x 32 with four waves: both slower, the first by ~30 %; and against
 // 128 x 64 per wave with eight waves, which halves the LDS reads of X but doubles the dequantization
 // per MFMA and spills: 40 % slower.)
-// k_qgemm_sk configurations: weight tiles per wave, row blocks per wave, waves
 struct GskCfg { int ntw, mbg, wv; };
 constexpr GskCfg GSK_CFGS[1] = {{2, 16, 8}};
 hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStream_t s);
