@@ -895,25 +895,29 @@ DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xo)[8],
 }
 
 // weight block b of the wave's NTW tiles (buffer loads: one lane offset, the block in the scalar offset)
+// weight tile block b (16 B of codes per lane) and its group parameters for lane row r
+template <int FMT>
+DEV void gemm_load_w1(const __amdgpu_buffer_rsrc_t & wrs, int64_t b, int lane, int r, u32x4 & w, GPar<FMT> & p) {
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    const uint32_t sb = (uint32_t) (b * BLK);
+    w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, 16 * lane, sb, 0));
+    if (FMT == ONPU_G128S) {
+        p.v[0] = __builtin_amdgcn_raw_buffer_load_b16(wrs, 1024 + 2 * r, sb, 0);
+    } else if (FMT == ONPU_Q4NX) {
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, 1024 + 16 * r, sb, 0));
+        for (int jj = 0; jj < 4; jj++) p.v[jj % (sizeof(p.v) / 4)] = v[jj];
+    } else {
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs, 1024 + 8 * r, sb, 0));
+        p.v[0] = v.x;
+        p.v[1 % (sizeof(p.v) / 4)] = v.y;
+    }
+}
+
 template <int FMT, int NTW>
 DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int lane, int r, u32x4 (&w)[NTW],
                      GPar<FMT> (&p)[NTW]) {
-    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
-    const uint32_t sb = (uint32_t) (b * BLK);
 #pragma unroll
-    for (int i = 0; i < NTW; i++) {
-        w[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs[i], 16 * lane, sb, 0));
-        if (FMT == ONPU_G128S) {
-            p[i].v[0] = __builtin_amdgcn_raw_buffer_load_b16(wrs[i], 1024 + 2 * r, sb, 0);
-        } else if (FMT == ONPU_Q4NX) {
-            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs[i], 1024 + 16 * r, sb, 0));
-            for (int jj = 0; jj < 4; jj++) p[i].v[jj % (sizeof(p[i].v) / 4)] = v[jj];
-        } else {
-            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs[i], 1024 + 8 * r, sb, 0));
-            p[i].v[0] = v.x;
-            p[i].v[1 % (sizeof(p[i].v) / 4)] = v.y;
-        }
-    }
+    for (int i = 0; i < NTW; i++) gemm_load_w1<FMT>(wrs[i], b, lane, r, w[i], p[i]);
 }
 
 template <int FMT, int NTW>
@@ -1028,15 +1032,18 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
 // f = FPW w + i, (mb, j) = (f / 4, f % 4). xrow[i / 4]: the lane's byte offset of row m0 + 16 mb + r
 // at k = 8 q (0x80000000, past the buffer, for rows >= M); kfix as in gemm_load_x.
 template <int FPW>
+DEV void gemm_load_x_frag(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow)[FPW / 4], int64_t b, bool kfix,
+                          int64_t K, int wave, int q, u32x4 * buf, int i) {
+    const int f = FPW * wave + i, j = i & 3;
+    uint32_t off = xrow[i >> 2] == 0x80000000u ? 0x80000000u : xrow[i >> 2] + 64u * j;
+    if (kfix && 128 * b + 32 * j + 8 * q >= K) off = 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b), 0, 0);
+}
+template <int FPW>
 DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow)[FPW / 4], int64_t b, bool kfix,
                         int64_t K, int wave, int q, u32x4 * buf) {
 #pragma unroll
-    for (int i = 0; i < FPW; i++) {
-        const int f = FPW * wave + i, j = i & 3;
-        uint32_t off = xrow[i >> 2] == 0x80000000u ? 0x80000000u : xrow[i >> 2] + 64u * j;
-        if (kfix && 128 * b + 32 * j + 8 * q >= K) off = 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b), 0, 0);
-    }
+    for (int i = 0; i < FPW; i++) gemm_load_x_frag<FPW>(xr, xrow, b, kfix, K, wave, q, buf, i);
 }
 
 // one 128-wide K block, 4 steps j x MBG row blocks, with a rolling A pipeline: fragment p = (j, mb),
@@ -1045,12 +1052,15 @@ DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow
 // fragments took 64, which left the compiler no room to keep the reads ahead: it issued each read
 // just before its use, 4-5 % slower). A scheduling fence closes every row block, so no read can
 // sink toward its use. The next step's weight fragments are dequantized one output dword per row
-// block (dequant8 in four parts), spread over the current step.
-template <int FMT, int NTW, int MBG>
+// block (dequant8 in four parts), spread over the current step, and the loads of the next K block
+// are issued by `issue(k)`, k < NI, one per row block of step 0 (all at the block's start, 8 waves
+// x 10 loads queued at once, measured 1-4 % slower).
+template <int FMT, int NTW, int MBG, int NI, class Issue>
 DEV void gemm_block_rp(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW], int lane,
-                       f32x4 (&acc)[MBG][NTW]) {
+                       f32x4 (&acc)[MBG][NTW], Issue issue) {
     constexpr int PD = 4, NP = 4 * MBG, DQ = MBG / (4 * NTW);
     static_assert(MBG % (4 * NTW) == 0, "dequant spread: four parts per tile and step");
+    static_assert(NI <= MBG, "one load per row block of step 0");
     u32x4 xa[PD + 1], bw[2][NTW];
     uint32_t lo[NTW], hi[NTW];
     float sc[NTW], cc[NTW];
@@ -1081,6 +1091,7 @@ DEV void gemm_block_rp(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT
             }
 #pragma unroll
             for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa[p % (PD + 1)], bw[j & 1][i], acc[mb][i]);
+            if (j == 0 && mb < NI) issue(mb);             // the next block's loads, one per row block
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -1175,11 +1186,15 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
         // b + 1 streams into the other LDS buffer and the other register set while b computes
         u32x4 * cur = xs0, * nxt = xs1;
         for (int64_t b = kb0; b < kb1; b++) {
-            if (b + 1 < kb1) {
-                gemm_load_x_sk<FPW>(xr, xrow, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, nxt);
-                gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wn, pn);
-            }
-            gemm_block_rp<FMT, NTW, MBG>(cur, wc, pc, lane, acc);
+            // block b + 1's X fragments and weights; at the segment's last block they reload block b
+            // (in range, no branch around the loads), ended by the wait below before any reuse
+            const int64_t bn = b + 1 < kb1 ? b + 1 : b;
+            const bool kfn = ktail && bn + 1 == a.KB;
+            auto issue = [&](int k) {
+                if (k < FPW) gemm_load_x_frag<FPW>(xr, xrow, bn, kfn, a.K, wave, q, nxt, k);
+                else gemm_load_w1<FMT>(wrs[k - FPW], bn, lane, r, wn[k - FPW], pn[k - FPW]);
+            };
+            gemm_block_rp<FMT, NTW, MBG, FPW + NTW>(cur, wc, pc, lane, acc, issue);
             __builtin_amdgcn_s_waitcnt(0x0f70);
             __syncthreads();
 #pragma unroll
