@@ -1280,28 +1280,28 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 
 // ------------------------------------------------------------------ MoE prefill: grouped GEMM
 // Work item = (expert e, first permuted position, rows <= 64) from k_moe_permute; blockIdx.y =
-// item, blockIdx.x = a group of output columns. Workgroup: WV waves x 2 weight tiles, 64 rows of X
-// (the item's rows, gathered) as 4 A blocks; per 128-wide K block the X tile (16 KiB of A
-// fragments, 16 / WV of them loaded by each wave) is filled by buffer loads straight to LDS, each
-// lane from its own row (rows past the item land as zeros), and each wave dequantizes its two
-// weight tiles in registers (the k_qgemm scheme over one expert's weights). Every column group
-// re-reads the item's X, so wider groups (WV = 8) halve that traffic.
+// item, blockIdx.x = a group of output columns. Workgroup: WV waves x 2 weight tiles, the item's
+// rows of X (gathered) as MBG = ceil(rows / 16) A blocks of 16 rows, MBG chosen per item (the
+// matrix cores do not overlap the dequant's VALU work, so MFMAs on rows past the item cost their
+// full time: with 4096 routed rows over 128 experts an item averages ~32 rows). Per 128-wide K block
+// the X tile (MBG x 4 KiB of A fragments, spread over the waves) is filled by buffer loads straight
+// to LDS, each lane from its own row (rows past the item land as zeros), and each wave dequantizes
+// its two weight tiles in registers (the k_qgemm scheme over one expert's weights). Every column
+// group re-reads the item's X, so wider groups (WV = 8) halve that traffic.
 //   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = WV blockIdx.x + w and up tile
 //           g + NT / 2; act[position][16 g + r] = bf16(silu(gate) * up)
 //   WHICH 1 (down): wave w holds tiles 2 WV blockIdx.x + 2 w + {0, 1}; o[position][n] = bf16 (the
 //           reference device's output precision per expert: its GEMV flushes each row to bf16,
 //           gemv_any.cc:120-130, and the host sums the weighted rows in fp32, onpu_cpu.cpp:259-274)
 // X rows: WHICH 0 token perm[position] / k of x [T][K]; WHICH 1 position of act [T k][K].
-template <int FMT, int WHICH, int WV>
-__global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) {
-    constexpr int MBG = 4, FPW = 16 / WV;                        // X fragments loaded per wave
-    __shared__ u32x4 xs0[MBG * 4 * 64], xs1[MBG * 4 * 64];     // 2 x 16 KiB
-    const int item = blockIdx.y;
-    if (item >= *a.nitems) return;
+template <int FMT, int WHICH, int WV, int MBG>
+DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, u32x4 * xs0, u32x4 * xs1) {
+    // X fragments f = FPW wave + i (i < FPW, f < 4 MBG): (mb, j) = (f / 4, f % 4); FPW divides 4,
+    // so that a wave's fragments share one A block and each lane one row
+    constexpr int NF = 4 * MBG, FPW0 = (NF + WV - 1) / WV, FPW = FPW0 <= 1 ? 1 : FPW0 <= 2 ? 2 : 4;
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15;
     const int q = lane >> 4;
-    const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
     const uint8_t * W = a.W + (int64_t) e * a.estride;
     int64_t t[2];
     if (WHICH == 0) { t[0] = (int64_t) blockIdx.x * WV + wave; t[1] = t[0] + a.NT / 2; }
@@ -1314,18 +1314,19 @@ __global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) 
         wrs[i] = __builtin_amdgcn_make_buffer_rsrc((void *) (W + tt * a.KB * BLK), (short) 0,
                                                    (int) (uint32_t) (a.KB * BLK), 0x00020000);
     }
-    // this wave's FPW X fragments f = FPW wave + i: (mb, j) = (f / 4, f % 4), one A block mb
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) a.xbytes, 0x00020000);
+    const bool xload = FPW * wave < NF;                          // wave-uniform
     const int xmb = FPW * wave / 4, xj0 = FPW * wave % 4;
     const int row = 16 * xmb + r;
     uint32_t xrow = 0x80000000u;
-    if (row < rows) {
+    if (xload && row < rows) {
         const int64_t src = WHICH == 0 ? (int64_t) (a.perm[first + row] / a.k) : (int64_t) (first + row);
         xrow = (uint32_t) (src * a.ldx * 2);
     }
     const bool ktail = a.K % 128 != 0;
     auto load_xt = [&](int64_t b, u32x4 * buf) {
+        if (!xload) return;
 #pragma unroll
         for (int i = 0; i < FPW; i++) {
             const int j = xj0 + i;
@@ -1344,25 +1345,22 @@ __global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) 
     gemm_load_w<FMT, 2>(wrs, 0, lane, r, wa, pa);
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
-    auto block = [&](const u32x4 * xsb, const u32x4 (&wr)[2], const GPar<FMT> (&pr)[2]) {
-        gemm_block<FMT, 2, MBG>(xsb, wr, pr, lane, acc);
-    };
     int64_t b = 0;
     for (; b + 2 <= a.KB; b += 2) {
         load_xt(b + 1, xs1);
         gemm_load_w<FMT, 2>(wrs, b + 1, lane, r, wb, pb);
-        block(xs0, wa, pa);
+        gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
         if (b + 2 < a.KB) {
             load_xt(b + 2, xs0);
             gemm_load_w<FMT, 2>(wrs, b + 2, lane, r, wa, pa);
         }
-        block(xs1, wb, pb);
+        gemm_block<FMT, 2, MBG>(xs1, wb, pb, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
-    if (b < a.KB) block(xs0, wa, pa);
+    if (b < a.KB) gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
     // lane (q, r) holds rows 4 q + v of A block mb, column r of its tiles
 #pragma unroll
     for (int mb = 0; mb < MBG; mb++)
@@ -1382,6 +1380,18 @@ __global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) 
                     ((uint16_t *) a.y)[pos * a.ldy + 16 * t[1] + r] = f32_to_bf16(acc[mb][1][v]);
             }
         }
+}
+
+template <int FMT, int WHICH, int WV>
+__global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) {
+    __shared__ u32x4 xs0[4 * 4 * 64], xs1[4 * 4 * 64];         // 2 x 16 KiB: up to 4 A blocks
+    const int item = blockIdx.y;
+    if (item >= *a.nitems) return;
+    const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
+    if (rows <= 16) moe_gemm_item<FMT, WHICH, WV, 1>(a, e, first, rows, xs0, xs1);
+    else if (rows <= 32) moe_gemm_item<FMT, WHICH, WV, 2>(a, e, first, rows, xs0, xs1);
+    else if (rows <= 48) moe_gemm_item<FMT, WHICH, WV, 3>(a, e, first, rows, xs0, xs1);
+    else moe_gemm_item<FMT, WHICH, WV, 4>(a, e, first, rows, xs0, xs1);
 }
 
 

@@ -97,6 +97,29 @@ def test_moe_ffn_small(gpu, fmt, T):
     check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=T > 4, what=f"moe fmt {fmt} T {T}")
 
 
+@pytest.mark.parametrize("fmt", [orc.FMT_G128S, orc.FMT_Q4S])
+def test_moe_grouped_item_sizes(gpu, fmt):
+    """one expert per token with per-expert row counts on both sides of every 16-row block boundary
+    and past the 64-row work item (65 = 64 + 1, 130 = 64 + 64 + 2): the grouped GEMM runs 1 to 4 A
+    blocks per item and splits an expert's rows into several items."""
+    import torch
+    counts = [1, 16, 17, 32, 33, 48, 49, 64, 65, 130]
+    E, H, I, k = len(counts), 256, 128, 1
+    T = sum(counts)
+    rng = np.random.default_rng(5)
+    rid = rng.permutation(np.repeat(np.arange(E, dtype=np.int32), counts)).reshape(T, k)
+    rw = rng.uniform(0.5, 1.0, (T, k)).astype(np.float32)
+    gu, dn = _experts(fmt, E, H, I, 4000)
+    xb = syn.activations(T, H, 6)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        y = f.ffn(to_torch_bf16(xb).reshape(T, H), torch.from_numpy(rid).cuda(), torch.from_numpy(rw).cuda())
+        y = from_torch(y)
+    finally:
+        f.free()
+    check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=True, what=f"moe item sizes fmt {fmt}")
+
+
 @pytest.mark.parametrize("T,check_tokens", [(1, 1), (512, 512)])
 def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
     """128 experts, H=2048, I=768, top-8 (router on device), g128s; every token checked."""
