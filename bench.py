@@ -426,16 +426,18 @@ def ceilings(torch):
     range per workgroup), a torch device
     copy of 2 GiB, the LDS read rate (ds_read_b128, conflict-free), the bf16 MFMA issue rate
     (v_mfma_f32_16x16x32_bf16, 8 independent accumulators, 2 waves per SIMD), the effective shader
-    clock (s_memtime against the 100 MHz s_memrealtime, in the MFMA and LDS probes) and torch's
-    bf16 GEMM (hipBLASLt) at the Llama-3.1-8B prefill shapes. Medians of 5 timed windows; the read
+    clock (s_memtime against the 100 MHz s_memrealtime, in the MFMA and LDS probes), how many VALU
+    ops a wave issues beside another wave's MFMAs on the same SIMD, and torch's bf16 GEMM (hipBLASLt)
+    at the Llama-3.1-8B prefill shapes. Medians of 5 timed windows; the read
     ceiling is the best of 4 or 16 workgroups per CU and 4 or 16 loads in flight per lane."""
     import ctypes as C
     P = C.CDLL(str(ROOT / "opennpu_amd" / "libonpu_probe.so"))
-    for n in ("onpu_probe_read", "onpu_probe_lds", "onpu_probe_mfma"):
+    for n in ("onpu_probe_read", "onpu_probe_lds", "onpu_probe_mfma", "onpu_probe_coissue"):
         getattr(P, n).restype = C.c_int
     P.onpu_probe_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     P.onpu_probe_lds.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     P.onpu_probe_mfma.argtypes = P.onpu_probe_lds.argtypes
+    P.onpu_probe_coissue.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     clk = torch.zeros(4, dtype=torch.int64, device="cuda")
@@ -483,6 +485,24 @@ def ceilings(torch):
     out["mfma_bf16_TFLOPS"] = fl / t / 1e12
     out["mfma_clock_GHz"] = hz / 1e9
     out["mfma_cycles_per_16x16x32"] = (cus * 4 * hz * t) / (fl / 16384.0)
+    # VALU issue beside MFMAs on one SIMD (wave 0 of workgroup 0 runs 48 fma per iteration, wave 4
+    # on the same SIMD 8 MFMAs): cycles per iteration of each alone and of both together
+    cyc = torch.zeros(2, dtype=torch.int64, device="cuda")
+    co = {}
+    for mode, name in ((0, "valu_alone"), (1, "mfma_alone"), (2, "both")):
+        for _ in range(3):
+            ok(P.onpu_probe_coissue(mode, cus, iters, sink.data_ptr(), cyc.data_ptr(), st()))
+        torch.cuda.synchronize()
+        c = cyc.cpu().tolist()
+        co[name] = {"valu_wave_cycles_per_iter": c[0] / iters if mode != 1 else None,
+                    "mfma_wave_cycles_per_iter": c[1] / iters if mode != 0 else None}
+    va, mf, both = co["valu_alone"]["valu_wave_cycles_per_iter"], co["mfma_alone"]["mfma_wave_cycles_per_iter"], co["both"]
+    co["valu_cycles_per_op_alone"] = va / 48
+    co["mfma_cycles_per_op_alone"] = mf / 8
+    # VALU ops the VALU wave completes while the MFMA wave streams (the rest at its lone rate)
+    during = 48 - (both["valu_wave_cycles_per_iter"] - both["mfma_wave_cycles_per_iter"]) / (va / 48)
+    co["valu_ops_per_mfma_beside"] = during / 8
+    out["valu_mfma_coissue"] = co
     gm = {}
     M = 2048
     for name, N, K in [("up", 14336, 4096), ("down", 4096, 14336)]:

@@ -6,6 +6,8 @@
 //   onpu_probe_lds   LDS read rate: ds_read_b128 with consecutive lanes on consecutive 16 bytes
 //                    (no bank conflicts), eight reads in flight per lane
 //   onpu_probe_mfma  v_mfma_f32_16x16x32_bf16 issue rate: eight independent accumulators per wave
+//   onpu_probe_coissue  VALU issue beside MFMAs on the same SIMD: waves 0-3 of a workgroup run
+//                    independent v_fma_f32 chains, waves 4-7 (one per SIMD again) stream MFMAs
 // Each kernel's wave 0 of workgroup 0 records the shader clock counter (s_memtime) and the constant
 // 100 MHz counter (s_memrealtime) at its start and end, so the host derives the effective clock.
 #include <hip/hip_runtime.h>
@@ -96,6 +98,47 @@ __global__ __launch_bounds__(512) void k_probe_mfma(int iters, float * out, uint
     stamp(clk, 1);
 }
 
+// mode 0: waves 0-3 run iters x 48 v_fma_f32 (8 independent chains), waves 4-7 idle; mode 1: waves
+// 4-7 run iters x 8 MFMAs (8 independent accumulators), waves 0-3 idle; mode 2: both. Wave w and
+// wave w + 4 share a SIMD. cyc[0] / cyc[1]: shader-clock cycles of wave 0 / wave 4 of workgroup 0.
+template <int MODE>
+__global__ __launch_bounds__(512) void k_probe_coissue(int iters, float * out, uint64_t * cyc) {
+    const uint32_t t = threadIdx.x, wave = t >> 6;
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    float s = 0.f;
+    if (wave < 4 && MODE != 1) {
+        const float k0 = 0.999f + 1e-7f * (float) t, k1 = 1e-3f;
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = (float) (j + t);
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int u = 0; u < 6; ++u)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) r[j] = fmaf(r[j], k0, k1);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += r[j];
+    } else if (wave >= 4 && MODE != 0) {
+        u32x4 a = {0x3f803f80u ^ (t & 1u), 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+        u32x4 b = {0x3f003f00u, 0x3f003f00u ^ (t & 2u), 0x3f003f00u, 0x3f003f00u};
+        f32x4 c[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = f32x4{0.f, 0.f, 0.f, (float) j};
+        for (int it = 0; it < iters; ++it) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                c[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                               __builtin_bit_cast(bf16x8, b), c[j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += c[j].x + c[j].y + c[j].z + c[j].w;
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    if (s == -1.f) out[0] = s;           // never true: the chains stay positive
+    if (blockIdx.x == 0 && (t == 0 || t == 256)) cyc[t == 0 ? 0 : 1] = t1 - t0;
+}
+
 extern "C" {
 
 // n_bytes must be a multiple of 16; unroll 4 or 16 loads in flight per lane; returns 0 or the HIP
@@ -124,6 +167,16 @@ int onpu_probe_mfma(int grid, int waves, int iters, void * out, void * clk, void
     if (grid <= 0 || waves < 1 || waves > 8 || iters <= 0) return -1;
     hipLaunchKernelGGL(k_probe_mfma, dim3(grid), dim3(64 * waves), 0, (hipStream_t) stream, iters, (float *) out,
                        (uint64_t *) clk);
+    return (int) hipGetLastError();
+}
+
+// mode 0, 1 or 2 (k_probe_coissue); grid workgroups of 8 waves
+int onpu_probe_coissue(int mode, int grid, int iters, void * out, void * cyc, void * stream) {
+    if (grid <= 0 || iters <= 0 || mode < 0 || mode > 2) return -1;
+    hipStream_t st = (hipStream_t) stream;
+    if (mode == 0) hipLaunchKernelGGL(k_probe_coissue<0>, dim3(grid), dim3(512), 0, st, iters, (float *) out, (uint64_t *) cyc);
+    else if (mode == 1) hipLaunchKernelGGL(k_probe_coissue<1>, dim3(grid), dim3(512), 0, st, iters, (float *) out, (uint64_t *) cyc);
+    else hipLaunchKernelGGL(k_probe_coissue<2>, dim3(grid), dim3(512), 0, st, iters, (float *) out, (uint64_t *) cyc);
     return (int) hipGetLastError();
 }
 
