@@ -1203,8 +1203,18 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
         }
 
         // Y from the accumulators, plus (second segment) the other segment's partial tile, added
-        // at the store so that no updated copy of the accumulators has to be merged with them
+        // at the store so that no updated copy of the accumulators has to be merged with them.
+        // Stores go through a buffer resource over this tile's rows (offsets fit 32 bits: MT rows):
+        // the lane's part of the offset (row 4 q, column n) once per weight tile, the row step
+        // 16 mb + v in the scalar offset. A column past N, and in a tile that runs past M a row past
+        // it, gets an offset past the range, so the store is dropped.
         auto store_tile = [&](bool addp, const __amdgpu_buffer_rsrc_t & wsr) {
+            const uint32_t es = a.yf32 ? 4u : 2u, rowb = (uint32_t) a.ldy * es;
+            const int64_t rows = a.M - m0 < MT ? a.M - m0 : MT;
+            const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *) ((char *) a.y + m0 * a.ldy * es), (short) 0, (int) (uint32_t) (rows * rowb), 0x00020000);
+            const bool full = rows == MT;                     // no row past M in this tile
+            const int rows_l = (int) rows - 4 * q;            // rows left from the lane's first
             // lane (q, r) holds rows 4 q + v of A block mb, column r of weight tile t0 + i
 #pragma unroll
             for (int mb = 0; mb < MBG; mb++) {
@@ -1214,14 +1224,27 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
                     if (addp)
                         v4 += __builtin_bit_cast(
                             f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                       wsr, (uint32_t) ((((wave * MBG + mb) * NTW + i) * 64 + lane) * 16), 0, 16));
+                                       wsr, (uint32_t) lane * 16, (uint32_t) (((wave * MBG + mb) * NTW + i) * 1024), 16));
                     if (i >= nt_ok) continue;
                     const int64_t n = 16 * (t0 + i) + r;
-                    if (n >= a.N) continue;
+                    const uint32_t vo = n < a.N ? (uint32_t) (4 * q) * rowb + (uint32_t) n * es : 0x80000000u;
+                    uint32_t vov[4];
 #pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        const int64_t m = m0 + 16 * mb + 4 * q + v;
-                        if (m < a.M) store_out(a.y, a.yf32, m * a.ldy + n, v4[v]);
+                    for (int v = 0; v < 4; v++) vov[v] = full || 16 * mb + v < rows_l ? vo : 0x80000000u;
+                    if (a.yf32) {
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v4[v]), yr, vov[v],
+                                                                  (uint32_t) (16 * mb + v) * rowb, 0);
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 4; v += 2) {
+                            const uint32_t pk = pack_bf16x2(v4[v], v4[v + 1]);
+                            __builtin_amdgcn_raw_buffer_store_b16((unsigned short) pk, yr, vov[v],
+                                                                  (uint32_t) (16 * mb + v) * rowb, 0);
+                            __builtin_amdgcn_raw_buffer_store_b16((unsigned short) (pk >> 16), yr, vov[v + 1],
+                                                                  (uint32_t) (16 * mb + v + 1) * rowb, 0);
+                        }
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -1248,8 +1271,9 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 #pragma unroll
                 for (int i = 0; i < NTW; i++)
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mb][i]), wsr,
-                                                           (uint32_t) ((((wave * MBG + mb) * NTW + i) * 64 + lane) * 16),
-                                                           0, 16 /* sc1: agent scope */);
+                                                           (uint32_t) lane * 16,
+                                                           (uint32_t) (((wave * MBG + mb) * NTW + i) * 1024),
+                                                           16 /* sc1: agent scope */);
             __builtin_amdgcn_s_waitcnt(0x0f70);           // the stores have completed
             __syncthreads();
             if (tid == 0) __hip_atomic_store(sc + 1, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -384,6 +384,7 @@ hipError_t launch_qgemm_sk(int fmt, const GArgs & a, int cfg, int grid, hipStrea
     if (a.sched == 1 && (a.R < 0 || a.R > grid || (a.R > 0 && (a.c <= 0 || a.s <= 0 || a.s >= a.KB))))
         return hipErrorInvalidValue;
     if (a.M * a.ldx * 2 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;     // 32-bit X offsets
+    if (256 * a.ldy * 4 >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;     // 32-bit Y offsets per tile
     switch (fmt) {
         case 0: return qgemm_sk_f0(a, cfg, grid, s);
         case 1: return qgemm_sk_f1(a, cfg, grid, s);
