@@ -1215,16 +1215,34 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
                 (void *) ((char *) a.y + m0 * a.ldy * es), (short) 0, (int) (uint32_t) (rows * rowb), 0x00020000);
             const bool full = rows == MT;                     // no row past M in this tile
             const int rows_l = (int) rows - 4 * q;            // rows left from the lane's first
+            // the other segment's partial, PF A blocks in flight ahead of the one being added (each
+            // load otherwise waits a full memory latency)
+            constexpr int PF = 4;
+            f32x4 pl[PF][NTW];
+            auto load_part = [&](int mb, f32x4 (&d)[NTW]) {
+#pragma unroll
+                for (int i = 0; i < NTW; i++)
+                    d[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         wsr, (uint32_t) lane * 16,
+                                                         (uint32_t) (((wave * MBG + mb) * NTW + i) * 1024), 16));
+            };
+            if (addp) {
+#pragma unroll
+                for (int k = 0; k < PF; k++) load_part(k, pl[k]);
+            }
             // lane (q, r) holds rows 4 q + v of A block mb, column r of weight tile t0 + i
 #pragma unroll
             for (int mb = 0; mb < MBG; mb++) {
+                f32x4 pc[NTW];
+                if (addp) {
+#pragma unroll
+                    for (int i = 0; i < NTW; i++) pc[i] = pl[mb % PF][i];
+                    if (mb + PF < MBG) load_part(mb + PF, pl[mb % PF]);
+                }
 #pragma unroll
                 for (int i = 0; i < NTW; i++) {
                     f32x4 v4 = acc[mb][i];
-                    if (addp)
-                        v4 += __builtin_bit_cast(
-                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                       wsr, (uint32_t) lane * 16, (uint32_t) (((wave * MBG + mb) * NTW + i) * 1024), 16));
+                    if (addp) v4 += pc[i];
                     if (i >= nt_ok) continue;
                     const int64_t n = 16 * (t0 + i) + r;
                     const uint32_t vo = n < a.N ? (uint32_t) (4 * q) * rowb + (uint32_t) n * es : 0x80000000u;
