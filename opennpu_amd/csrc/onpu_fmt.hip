@@ -46,8 +46,9 @@ hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
 
 hipError_t FN(qgemm_sk)(const GArgs & a, int cfg, int grid, hipStream_t s) {
     const size_t lds = (size_t) 2 * 4 * GSK_CFGS[cfg].mbg * 1024;
-    if (cfg == 0) k_qgemm_sk<F, 2, 16, 8><<<grid, 512, lds, s>>>(a);
-    else return hipErrorInvalidValue;
+    if (cfg != 0) return hipErrorInvalidValue;
+    if (a.K % 128) k_qgemm_sk<F, 2, 16, 8, true><<<grid, 512, lds, s>>>(a);
+    else k_qgemm_sk<F, 2, 16, 8, false><<<grid, 512, lds, s>>>(a);
     return hipGetLastError();
 }
 

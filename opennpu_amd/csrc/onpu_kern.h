@@ -1034,10 +1034,13 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
 template <int FPW>
 DEV void gemm_load_x_frag(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow)[FPW / 4], int64_t b, bool kfix,
                           int64_t K, int wave, int q, u32x4 * buf, int i) {
+    // step j's 64 bytes in the scalar offset (a row past M, at 0x80000000, stays past the range);
+    // the K tail is checked only in the block that holds it (kfix is uniform)
     const int f = FPW * wave + i, j = i & 3;
-    uint32_t off = xrow[i >> 2] == 0x80000000u ? 0x80000000u : xrow[i >> 2] + 64u * j;
+    uint32_t off = xrow[i >> 2];
     if (kfix && 128 * b + 32 * j + 8 * q >= K) off = 0x80000000u;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b), 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b + 64 * j), 0,
+                                             0);
 }
 template <int FPW>
 DEV void gemm_load_x_sk(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xrow)[FPW / 4], int64_t b, bool kfix,
@@ -1097,7 +1100,9 @@ DEV void gemm_block_rp(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT
     }
 }
 
-template <int FMT, int NTW, int MBG, int WV>
+// KT: K % 128 != 0 (the last K block reads zeros past K); launched with KT = false otherwise, so
+// that no block pays for the check
+template <int FMT, int NTW, int MBG, int WV, bool KT>
 __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
     extern __shared__ u32x4 gsk_lds[];                   // two X buffers of 4 MBG fragments
     __shared__ int s_old, s_tag;
@@ -1117,7 +1122,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
     const int64_t itb = lid * a.ipw, ite = itb + a.ipw < total ? itb + a.ipw : total;
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
-    const bool ktail = a.K % 128 != 0;
+    const bool ktail = KT && a.K % 128 != 0;
     if (tid == 0) {                                       // this launch's tag: the last one's + 1, never 0
         const int32_t prev = __hip_atomic_load(a.ctl + GSK_CTL_TAG, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_tag = prev == 0x7fffffff ? 1 : prev + 1;
