@@ -59,13 +59,14 @@ hipError_t FN(moe_decode)(const MDArgs & a, int gb, int grid, size_t lds, hipStr
     return hipGetLastError();
 }
 
-hipError_t FN(moe_gemm)(int which, int wv, const MArgs & a, dim3 grid, hipStream_t s) {
-    if (wv == 8) {
-        if (which == 0) k_moe_gemm<F, 0, 8><<<grid, 512, 0, s>>>(a);
-        else k_moe_gemm<F, 1, 8><<<grid, 512, 0, s>>>(a);
+hipError_t FN(moe_gemm)(int which, const MArgs & a, dim3 grid, hipStream_t s) {
+    const bool kt = a.K % 128 != 0;
+    if (which == 0) {
+        if (kt) k_moe_gemm<F, 0, true><<<grid, 512, 0, s>>>(a);
+        else k_moe_gemm<F, 0, false><<<grid, 512, 0, s>>>(a);
     } else {
-        if (which == 0) k_moe_gemm<F, 0, 4><<<grid, 256, 0, s>>>(a);
-        else k_moe_gemm<F, 1, 4><<<grid, 256, 0, s>>>(a);
+        if (kt) k_moe_gemm<F, 1, true><<<grid, 512, 0, s>>>(a);
+        else k_moe_gemm<F, 1, false><<<grid, 512, 0, s>>>(a);
     }
     return hipGetLastError();
 }

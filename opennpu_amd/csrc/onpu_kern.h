@@ -1341,7 +1341,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 //           reference device's output precision per expert: its GEMV flushes each row to bf16,
 //           gemv_any.cc:120-130, and the host sums the weighted rows in fp32, onpu_cpu.cpp:259-274)
 // X rows: WHICH 0 token perm[position] / k of x [T][K]; WHICH 1 position of act [T k][K].
-template <int FMT, int WHICH, int WV, int MBG>
+template <int FMT, int WHICH, int WV, int MBG, bool KT>
 DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, u32x4 * xs0, u32x4 * xs1) {
     // X fragments f = FPW wave + i (i < FPW, f < 4 MBG): (mb, j) = (f / 4, f % 4); FPW divides 4,
     // so that a wave's fragments share one A block and each lane one row
@@ -1366,21 +1366,22 @@ DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, 
     const bool xload = FPW * wave < NF;                          // wave-uniform
     const int xmb = FPW * wave / 4, xj0 = FPW * wave % 4;
     const int row = 16 * xmb + r;
-    uint32_t xrow = 0x80000000u;
+    // the lane's byte offset of its row and k = 8 q (a row past the item, 0x80000000 + 16 q, stays
+    // past the buffer's range); step j's 64 bytes and block b's 256 go in the scalar offset
+    uint32_t xrow = 0x80000000u + 16u * q;
     if (xload && row < rows) {
         const int64_t src = WHICH == 0 ? (int64_t) (a.perm[first + row] / a.k) : (int64_t) (first + row);
-        xrow = (uint32_t) (src * a.ldx * 2);
+        xrow = (uint32_t) (src * a.ldx * 2) + 16u * q;
     }
-    const bool ktail = a.K % 128 != 0;
     auto load_xt = [&](int64_t b, u32x4 * buf) {
         if (!xload) return;
 #pragma unroll
         for (int i = 0; i < FPW; i++) {
             const int j = xj0 + i;
-            uint32_t off = xrow == 0x80000000u ? xrow : xrow + (uint32_t) (32 * j + 8 * q) * 2;
-            if (ktail && 128 * b + 32 * j + 8 * q >= a.K) off = 0x80000000u;
+            uint32_t off = xrow;
+            if (KT && 128 * b + 32 * j + 8 * q >= a.K) off = 0x80000000u;      // the K tail reads zeros
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + (FPW * wave + i) * 64), 16, off,
-                                                     (uint32_t) (256 * b), 0, 0);
+                                                     (uint32_t) (256 * b + 64 * j), 0, 0);
         }
     };
     f32x4 acc[MBG][2];
@@ -1408,37 +1409,55 @@ DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, 
         __syncthreads();
     }
     if (b < a.KB) gemm_block<FMT, 2, MBG>(xs0, wa, pa, lane, acc);
+    // bf16 stores through a buffer resource over the item's rows (rows <= 64: 32-bit offsets): the
+    // lane's row 4 q and column in the vector offset, the row step 16 mb + v in the scalar offset;
+    // a row past the item or a column past N gets an offset past the range, so the store is dropped
+    const uint32_t rowb = (uint32_t) a.ldy * 2;
+    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *) ((uint16_t *) a.y + (int64_t) first * a.ldy), (short) 0, (int) ((uint32_t) rows * rowb), 0x00020000);
+    const int rows_l = rows - 4 * q;                               // rows left from the lane's first
+    uint32_t vo[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const bool okc = (i == 0 ? ok0 : ok1) && 16 * t[i] + r < a.N;
+        vo[i] = okc ? (uint32_t) (4 * q) * rowb + (uint32_t) (16 * t[i] + r) * 2 : 0x80000000u;
+    }
     // lane (q, r) holds rows 4 q + v of A block mb, column r of its tiles
 #pragma unroll
     for (int mb = 0; mb < MBG; mb++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int rr = 16 * mb + 4 * q + v;
-            if (rr >= rows) continue;
-            const int64_t pos = first + rr;
+        for (int v = 0; v < 4; v += 2) {
+            const uint32_t so0 = (uint32_t) (16 * mb + v) * rowb, so1 = so0 + rowb;
+            const bool in0 = 16 * mb + v < rows_l, in1 = 16 * mb + v + 1 < rows_l;
             if (WHICH == 0) {
-                if (ok0)
-                    ((uint16_t *) a.y)[pos * a.ldy + 16 * t[0] + r] =
-                        f32_to_bf16(silu_f(acc[mb][0][v]) * acc[mb][1][v]);
+                const uint32_t pk = pack_bf16x2(silu_f(acc[mb][0][v]) * acc[mb][1][v],
+                                                silu_f(acc[mb][0][v + 1]) * acc[mb][1][v + 1]);
+                __builtin_amdgcn_raw_buffer_store_b16((unsigned short) pk, yr, in0 ? vo[0] : 0x80000000u, so0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((unsigned short) (pk >> 16), yr, in1 ? vo[0] : 0x80000000u, so1, 0);
             } else {
-                if (ok0 && 16 * t[0] + r < a.N)
-                    ((uint16_t *) a.y)[pos * a.ldy + 16 * t[0] + r] = f32_to_bf16(acc[mb][0][v]);
-                if (ok1 && 16 * t[1] + r < a.N)
-                    ((uint16_t *) a.y)[pos * a.ldy + 16 * t[1] + r] = f32_to_bf16(acc[mb][1][v]);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const uint32_t pk = pack_bf16x2(acc[mb][i][v], acc[mb][i][v + 1]);
+                    __builtin_amdgcn_raw_buffer_store_b16((unsigned short) pk, yr, in0 ? vo[i] : 0x80000000u, so0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16((unsigned short) (pk >> 16), yr, in1 ? vo[i] : 0x80000000u,
+                                                          so1, 0);
+                }
             }
         }
 }
 
-template <int FMT, int WHICH, int WV>
-__global__ __launch_bounds__(64 * WV, WV == 4 ? 2 : 1) void k_moe_gemm(MArgs a) {
+// KT: K % 128 != 0 (launched with KT = false otherwise, so that no block pays for the tail check)
+template <int FMT, int WHICH, bool KT>
+__global__ __launch_bounds__(512, 1) void k_moe_gemm(MArgs a) {
+    constexpr int WV = 8;
     __shared__ u32x4 xs0[4 * 4 * 64], xs1[4 * 4 * 64];         // 2 x 16 KiB: up to 4 A blocks
     const int item = blockIdx.y;
     if (item >= *a.nitems) return;
     const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
-    if (rows <= 16) moe_gemm_item<FMT, WHICH, WV, 1>(a, e, first, rows, xs0, xs1);
-    else if (rows <= 32) moe_gemm_item<FMT, WHICH, WV, 2>(a, e, first, rows, xs0, xs1);
-    else if (rows <= 48) moe_gemm_item<FMT, WHICH, WV, 3>(a, e, first, rows, xs0, xs1);
-    else moe_gemm_item<FMT, WHICH, WV, 4>(a, e, first, rows, xs0, xs1);
+    if (rows <= 16) moe_gemm_item<FMT, WHICH, WV, 1, KT>(a, e, first, rows, xs0, xs1);
+    else if (rows <= 32) moe_gemm_item<FMT, WHICH, WV, 2, KT>(a, e, first, rows, xs0, xs1);
+    else if (rows <= 48) moe_gemm_item<FMT, WHICH, WV, 3, KT>(a, e, first, rows, xs0, xs1);
+    else moe_gemm_item<FMT, WHICH, WV, 4, KT>(a, e, first, rows, xs0, xs1);
 }
 
 

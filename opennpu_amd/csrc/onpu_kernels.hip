@@ -424,15 +424,14 @@ hipError_t launch_moe_decode(int fmt, const MDArgs & a, int grid, hipStream_t s)
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s) {
     if (a.xbytes <= 0 || a.xbytes >= ((int64_t) 1 << 31) || maxitems <= 0 || maxitems > 65535) return hipErrorInvalidValue;
     if (which == 0 && (a.NT % 2 || a.N != 16 * a.NT)) return hipErrorInvalidValue;   // gate | up halves of whole tiles
-    const char * ev = std::getenv("ONPU_MOE_WV");
-    const int wv = ev && std::atoi(ev) == 4 ? 4 : 8;
+    constexpr int wv = 8;                                   // k_moe_gemm: 8 waves x 2 weight tiles
     const int64_t gx = which == 0 ? (a.NT / 2 + wv - 1) / wv : (a.NT + 2 * wv - 1) / (2 * wv);
     const dim3 grid((unsigned) gx, (unsigned) maxitems);
     switch (fmt) {
-        case 0: return moe_gemm_f0(which, wv, a, grid, s);
-        case 1: return moe_gemm_f1(which, wv, a, grid, s);
-        case 2: return moe_gemm_f2(which, wv, a, grid, s);
-        case 3: return moe_gemm_f3(which, wv, a, grid, s);
+        case 0: return moe_gemm_f0(which, a, grid, s);
+        case 1: return moe_gemm_f1(which, a, grid, s);
+        case 2: return moe_gemm_f2(which, a, grid, s);
+        case 3: return moe_gemm_f3(which, a, grid, s);
     }
     return hipErrorInvalidValue;
 }

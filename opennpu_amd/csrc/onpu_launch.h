@@ -218,7 +218,7 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
                            size_t lds, hipStream_t s);                                                    \
     hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
     hipError_t qgemm_sk_f##id(const GArgs & a, int cfg, int grid, hipStream_t s);                          \
-    hipError_t moe_gemm_f##id(int which, int wv, const MArgs & a, dim3 grid, hipStream_t s);                  \
+    hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
     hipError_t moe_decode_f##id(const MDArgs & a, int gb, int grid, size_t lds, hipStream_t s);       \
     hipError_t chain_f##id(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,  \
                            hipStream_t s);                                                                \
