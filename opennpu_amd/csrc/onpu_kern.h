@@ -767,10 +767,25 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
 // ------------------------------------------------------------------ prefill GEMM
 // The 8 weights of dword d (B-operand order: element e at nibble (e >> 1) + 4 (e & 1)) dequantized
 // to bf16 RNE(w), w = (u - 8) s or u s + m: the weight the reference device feeds its MAC
-// (gemv_any.cc:65,106-107). Nibbles are split into bytes (lo: even nibbles, hi: odd), converted
-// with v_cvt_f32_ubyteN, one fma each (exact: u s fits fp32) and packed by v_cvt_pk_bf16_f32.
+// (gemv_any.cc:65,106-107).
+// Symmetric formats: each pair of codes becomes two fp16 1024 + u in one and-or (as unpack_biased),
+// and v_fma_mix_f32 (an fp16 operand widened inside a fused fma) forms (1024 + u) s - 1032 s: the
+// product and the sum are exact in fp32 (at most 19 significant bits), so the result is
+// (u - 8) s exactly, and v_cvt_pk_bf16_f32 rounds it to nearest even: 7 + 8 + 4 = 19 VALU ops per 8
+// weights. c (from par_sc) is -1032 s.
+// q4nx (u s + m, one rounding): the nibbles split into bytes (lo: even nibbles, hi: odd), converted
+// with v_cvt_f32_ubyteN and one fma each (u s is exact), 23 ops per 8 weights.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+DEV uint32_t dq_pair(uint32_t w16, float s, float c) {
+    const f16x2 h = __builtin_bit_cast(f16x2, w16);
+    return pack_bf16x2(fmaf((float) h.x, s, c), fmaf((float) h.y, s, c));
+}
 template <int FMT>
 DEV u32x4 dequant8(uint32_t d, float s, float c) {
+    if (FMT != ONPU_Q4NX) {
+        const u32x4 h = unpack_biased(d, 0x64006400u);
+        return (u32x4){dq_pair(h.x, s, c), dq_pair(h.y, s, c), dq_pair(h.z, s, c), dq_pair(h.w, s, c)};
+    }
     // an opaque mask, so that the optimizer cannot fold each byte extraction into a 4-bit field
     // extract (v_bfe) plus v_cvt_f32_ubyte0 (two ops per weight instead of one); plain code rather
     // than an asm v_and_b32, so that MFMA hazards stay visible to the compiler
@@ -781,33 +796,46 @@ DEV u32x4 dequant8(uint32_t d, float s, float c) {
                    pack_bf16x2(f(hi, 1), f(hi, 3))};
 }
 
-// dequant8 in parts, for spreading its VALU work: dequant_split separates the nibbles into bytes,
-// dequant_part(k) forms output dword k of dequant8 (the same operations, so the same bits)
+// dequant8 in parts, for spreading its VALU work: dequant_split prepares the dword (q4nx: the
+// nibbles split into bytes; symmetric formats: kept whole), dequant_part(k) forms output dword k
+// of dequant8 (the same operations, so the same bits)
+template <int FMT>
 DEV void dequant_split(uint32_t d, uint32_t & lo, uint32_t & hi) {
+    if (FMT != ONPU_Q4NX) {
+        lo = d;
+        hi = 0;
+        return;
+    }
     const uint32_t M = opaque_s(0x0f0f0f0fu);
     lo = d & M;
     hi = (d >> 4) & M;
 }
+template <int FMT>
 DEV uint32_t dequant_part(uint32_t lo, uint32_t hi, int k, float s, float c) {
+    if (FMT != ONPU_Q4NX) {
+        const uint32_t M = opaque_s(0x000F000Fu), g = opaque_v(0x64006400u);
+        return dq_pair(((k ? lo >> (4 * k) : lo) & M) | g, s, c);
+    }
     auto f = [&](uint32_t w, int byte) { return fmaf((float) ((w >> (8 * byte)) & 0xffu), s, c); };
     const uint32_t w = (k & 1) ? hi : lo;
     const int b = k >> 1;                    // dwords: (lo 0, 2), (hi 0, 2), (lo 1, 3), (hi 1, 3)
     return pack_bf16x2(f(w, b), f(w, b + 2));
 }
 
-// scale s and additive constant c of MFMA step j such that w = u * s + c
+// scale s and additive constant c of MFMA step j for dequant8: symmetric formats c = -1032 s (the
+// fp16 codes carry 1024 + u), q4nx c = m (w = u s + m)
 template <int FMT>
 DEV void par_sc(const GPar<FMT> & p, int j, float & s, float & c) {
     if (FMT == ONPU_G128S) {
         s = bf16_to_f32((uint16_t) p.v[0]);
-        c = -8.0f * s;
+        c = -1032.0f * s;
     } else if (FMT == ONPU_Q4NX) {
         const uint32_t pj = p.v[j % (sizeof(p.v) / 4)];
         s = bf16_to_f32((uint16_t) (pj & 0xffff));
         c = bf16_to_f32((uint16_t) (pj >> 16));
     } else {
         s = scale_f32(FMT, (p.v[(j >> 1) % (sizeof(p.v) / 4)] >> (16 * (j & 1))) & 0xffff);
-        c = -8.0f * s;
+        c = -1032.0f * s;
     }
 }
 
@@ -1088,9 +1116,9 @@ DEV void gemm_block_rp(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT
                 const int i = (mb / DQ) / 4, k = (mb / DQ) % 4;
                 if (k == 0) {
                     par_sc<FMT>(pr[i], j + 1, sc[i], cc[i]);
-                    dequant_split(wr[i][j + 1], lo[i], hi[i]);
+                    dequant_split<FMT>(wr[i][j + 1], lo[i], hi[i]);
                 }
-                bw[(j + 1) & 1][i][k] = dequant_part(lo[i], hi[i], k, sc[i], cc[i]);
+                bw[(j + 1) & 1][i][k] = dequant_part<FMT>(lo[i], hi[i], k, sc[i], cc[i]);
             }
 #pragma unroll
             for (int i = 0; i < NTW; i++) acc[mb][i] = mfma(xa[p % (PD + 1)], bw[j & 1][i], acc[mb][i]);
