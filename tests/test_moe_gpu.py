@@ -120,6 +120,24 @@ def test_moe_grouped_item_sizes(gpu, fmt):
     check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=True, what=f"moe item sizes fmt {fmt}")
 
 
+@pytest.mark.parametrize("fmt", [orc.FMT_Q4S, orc.FMT_Q4NX])
+def test_moe_grouped_k_tail(gpu, fmt):
+    """grouped products whose K is not a multiple of 128 (H = 288 for gate+up, I = 160 for down):
+    the last K block of each reads zeros past K (the grouped GEMM's tail variant)."""
+    import torch
+    E, H, I, k, T = 8, 288, 160, 2, 40
+    gu, dn = _experts(fmt, E, H, I, 5000)
+    xb = syn.activations(T, H, 7)
+    rid, rw = orc.route(syn.logits(T, E, 8), k)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        y = f.ffn(to_torch_bf16(xb).reshape(T, H), torch.from_numpy(rid).cuda(), torch.from_numpy(rw).cuda())
+        y = from_torch(y)
+    finally:
+        f.free()
+    check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=True, what=f"moe K tail fmt {fmt}")
+
+
 @pytest.mark.parametrize("T,check_tokens", [(1, 1), (512, 512)])
 def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
     """128 experts, H=2048, I=768, top-8 (router on device), g128s; every token checked."""
