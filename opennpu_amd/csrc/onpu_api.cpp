@@ -300,10 +300,12 @@ bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & g
         a.s = R ? std::min<int64_t>(KB - 1, std::max<int64_t>(1, (a.c * KB + (a.c - 1) * E + (a.c + 1) / 2) / (a.c + 1)))
                 : KB;
         a.ipw = KB;
+        a.sym = R > 0 && a.c == 1 && env_int("ONPU_GSK_SYM", 1) ? 1 : 0;
         grid = cus;
         return true;
     }
     a.sched = 0;
+    a.sym = 0;
     int64_t & ipw = a.ipw;
     if (tiles >= cus) ipw = (total + cus - 1) / cus;
     else if (2 * tiles >= cus && KB % 2 == 0) ipw = KB / 2;

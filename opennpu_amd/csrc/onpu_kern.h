@@ -1128,6 +1128,8 @@ DEV void gemm_block_rp(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT
     }
 }
 
+template <int V> struct IC { static constexpr int value = V; };     // a compile-time int as a value
+
 // KT: K % 128 != 0 (the last K block reads zeros past K); launched with KT = false otherwise, so
 // that no block pays for the check
 template <int FMT, int NTW, int MBG, int WV, bool KT>
@@ -1241,7 +1243,10 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
         // the lane's part of the offset (row 4 q, column n) once per weight tile, the row step
         // 16 mb + v in the scalar offset. A column past N, and in a tile that runs past M a row past
         // it, gets an offset past the range, so the store is dropped.
-        auto store_tile = [&](bool addp, const __amdgpu_buffer_rsrc_t & wsr) {
+        // A blocks [MB0, MB0 + NMB); with addp the other segment's partial of exactly those blocks,
+        // laid out [wave][mb - MB0][i][lane] from byte pbase of the slot
+        auto store_tile = [&](auto mb0c, auto nmbc, bool addp, const __amdgpu_buffer_rsrc_t & wsr, uint32_t pbase) {
+            constexpr int MB0 = decltype(mb0c)::value, NMB = decltype(nmbc)::value;
             const uint32_t es = a.yf32 ? 4u : 2u, rowb = (uint32_t) a.ldy * es;
             const int64_t rows = a.M - m0 < MT ? a.M - m0 : MT;
             const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
@@ -1257,20 +1262,20 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
                 for (int i = 0; i < NTW; i++)
                     d[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                          wsr, (uint32_t) lane * 16,
-                                                         (uint32_t) (((wave * MBG + mb) * NTW + i) * 1024), 16));
+                                                         pbase + (uint32_t) (((wave * NMB + mb - MB0) * NTW + i) * 1024), 16));
             };
             if (addp) {
 #pragma unroll
-                for (int k = 0; k < PF; k++) load_part(k, pl[k]);
+                for (int k = 0; k < PF && k < NMB; k++) load_part(MB0 + k, pl[k]);
             }
             // lane (q, r) holds rows 4 q + v of A block mb, column r of weight tile t0 + i
 #pragma unroll
-            for (int mb = 0; mb < MBG; mb++) {
+            for (int mb = MB0; mb < MB0 + NMB; mb++) {
                 f32x4 pc[NTW];
                 if (addp) {
 #pragma unroll
-                    for (int i = 0; i < NTW; i++) pc[i] = pl[mb % PF][i];
-                    if (mb + PF < MBG) load_part(mb + PF, pl[mb % PF]);
+                    for (int i = 0; i < NTW; i++) pc[i] = pl[(mb - MB0) % PF][i];
+                    if (mb + PF < MB0 + NMB) load_part(mb + PF, pl[(mb - MB0) % PF]);
                 }
 #pragma unroll
                 for (int i = 0; i < NTW; i++) {
@@ -1302,7 +1307,45 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
             }
         };
         if (kb0 == 0 && kb1 == a.KB) {
-            store_tile(false, xr);
+            store_tile(IC<0>(), IC<MBG>(), false, xr, 0);
+            continue;
+        }
+        int32_t * sc = a.sync + slot * GSK_SYNC_STRIDE;
+        const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *) ((char *) a.ws + (int64_t) slot * SLOT), (short) 0, (int) SLOT, 0x00020000);
+        if (a.sym) {
+            // a tile cut into two segments that end together (sched 1, one tail piece per workgroup):
+            // each publishes the half of the rows that the other finishes (A blocks MBG/2.. for the
+            // head, ..MBG/2 for the tail: half the partial tile each, both at once), sets its ready
+            // word to the launch's tag, waits for the other's, adds the other's half to its own
+            // rows and stores them. Both publish before waiting, and every workgroup of the launch
+            // is resident (one per CU), so neither waits on a workgroup that has not run.
+            constexpr int MBH = MBG / 2;
+            const int h = kb0 == 0 ? 0 : 1;               // 0: head, keeps A blocks [0, MBH)
+            const uint32_t pub = h ? SLOT / 2 : 0u;
+#pragma unroll
+            for (int mb = 0; mb < MBH; mb++)
+#pragma unroll
+                for (int i = 0; i < NTW; i++)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, h ? acc[mb][i] : acc[MBH + mb][i]), wsr, (uint32_t) lane * 16,
+                        pub + (uint32_t) (((wave * MBH + mb) * NTW + i) * 1024), 16 /* sc1: agent scope */);
+            __builtin_amdgcn_s_waitcnt(0x0f70);           // the stores have completed
+            __syncthreads();
+            if (tid == 0) {
+                __hip_atomic_store(sc + 2 + h, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                uint32_t polls = 0;
+                while (__hip_atomic_load(sc + 3 - h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != s_tag) {
+                    if (++polls > a.spin) {
+                        __hip_atomic_store(a.ctl + GSK_CTL_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+            __syncthreads();
+            if (h == 0) store_tile(IC<0>(), IC<MBH>(), true, wsr, SLOT / 2);
+            else store_tile(IC<MBH>(), IC<MBH>(), true, wsr, 0);
             continue;
         }
         // a cut tile's two segments meet at its slot: every launch adds two arrivals to the slot's
@@ -1310,12 +1353,9 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
         // sets the slot's ready word to this launch's tag; the second waits for that tag, so a
         // ready word left by any earlier launch (also by a publisher that came after a timed-out
         // wait) never matches, and nothing has to be cleared between launches.
-        int32_t * sc = a.sync + slot * GSK_SYNC_STRIDE;
         if (tid == 0) s_old = __hip_atomic_fetch_add(sc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         const int old = s_old;
-        const __amdgpu_buffer_rsrc_t wsr = __builtin_amdgcn_make_buffer_rsrc(
-            (void *) ((char *) a.ws + (int64_t) slot * SLOT), (short) 0, (int) SLOT, 0x00020000);
         if ((old & 1) == 0) {                             // first segment: publish the partial
 #pragma unroll
             for (int mb = 0; mb < MBG; mb++)
@@ -1340,7 +1380,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
                 }
             }
             __syncthreads();
-            store_tile(true, wsr);
+            store_tile(IC<0>(), IC<MBG>(), true, wsr, 0);
         }
     }
     if (tid == 0) {

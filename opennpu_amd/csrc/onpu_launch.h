@@ -37,6 +37,8 @@ struct GArgs {
     // apart, zero when allocated); ctl: the last launch's tag, the count of finished workgroups and
     // the timed-out-wait flag (GSK_CTL_* ints apart)
     int64_t ipw;
+    int sym;                  // sched 1 with one tail piece per workgroup: the two segments of a cut
+                              // tile exchange halves (each finishes half the rows), slot words 2, 3
     float * ws;
     int32_t * sync;
     int32_t * ctl;
