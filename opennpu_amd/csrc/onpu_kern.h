@@ -342,16 +342,15 @@ DEV void route_token(const float * __restrict__ l, int E, int k, int renorm, int
 // With one A block (MB = 1) x row m sits in MFMA row perm16(m), so C element v of lane quarter q
 // holds x row 4 v + q: RV (compile time) = the elements that hold rows below M (1 for M <= 4, 2 for
 // M <= 8, else 4), and the accumulate touches those alone. MB > 1 keeps rows in order and all four.
+// rows: the C elements that hold x rows below M (compile time), the only ones accumulated
 DEV void acc4(f32x4 & acc, float s, float bo, const f32x4 & cg, const f32x4 & cs, int rows) {
-    acc[0] = fmaf(s, cg[0], fmaf(bo, cs[0], acc[0]));
-    if (rows > 1)
-        for (int v = 1; v < 4; v++) acc[v] = fmaf(s, cg[v], fmaf(bo, cs[v], acc[v]));
+#pragma unroll
+    for (int v = 0; v < rows; v++) acc[v] = fmaf(s, cg[v], fmaf(bo, cs[v], acc[v]));
 }
 
 DEV void acc1(f32x4 & acc, float s, const f32x4 & cg, int rows) {
-    acc[0] = fmaf(s, cg[0], acc[0]);
-    if (rows > 1)
-        for (int v = 1; v < 4; v++) acc[v] = fmaf(s, cg[v], acc[v]);
+#pragma unroll
+    for (int v = 0; v < rows; v++) acc[v] = fmaf(s, cg[v], acc[v]);
 }
 
 // MFMA row of x row m (0..15) in a single A block: rows 0..3 go to MFMA rows 0, 4, 8, 12 (element 0
