@@ -269,14 +269,14 @@ def moe(torch, QFfn, syn, iters):
         lg = torch.from_numpy(syn.logits(T, E, 9)).cuda()
         x = bf16_tensor(torch, syn.activations(T, H, 10)).reshape(T, H)
         y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
-        ids, _ = ffns[0].route(lg, k)
+        ids, w = ffns[0].route(lg, k)
         hit = len(np.unique(ids.cpu().numpy()))
 
-        def step(lg=lg, x=x, y=y):
+        # router + experts + weighted sum per layer (at T <= 4 the gate+up launch routes)
+        def step(lg=lg, x=x, y=y, ids=ids, w=w):
             for _ in range(GRAPH_REPS):
                 for f in ffns:
-                    i, w = f.route(lg, k)
-                    f.ffn(x, i, w, out=y)
+                    f.decode(lg, x, k, out=y, ids=ids, w=w)
         g = GraphStep(step, torch)
         t = time_med(torch, g, iters, 3) / (nl * GRAPH_REPS)
         byts = hit * per_expert + T * H * 2 * 2 + T * E * 4
@@ -748,7 +748,8 @@ def profile_gemm(torch, QMatrix, syn, reps=3):
 
 def profile_moe(torch, QFfn, syn, reps=3):
     """The Qwen3-30B-A3B MoE layer alone (E 128, H 2048, I 768, top-8, g128s) at T = 512 and T = 1,
-    `reps` calls each (router, permutation, grouped GEMMs, combine / the decode GEMVs), then one plain
+    `reps` calls each (router, permutation, grouped GEMMs, combine / the routing gate+up and down
+    GEMVs), then one plain
     512 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE, for hardware-counter and trace runs."""
     E, H, I, k = 128, 2048, 768, 8
     gu = np.concatenate([syn.weights(G128S, 2 * I, H, 300 + e) for e in range(E)])
@@ -760,8 +761,7 @@ def profile_moe(torch, QFfn, syn, reps=3):
         x = bf16_tensor(torch, syn.activations(T, H, 10)).reshape(T, H)
         y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
         for _ in range(reps):
-            i, w = f.route(lg, k)
-            f.ffn(x, i, w, out=y)
+            f.decode(lg, x, k, out=y)
         torch.cuda.synchronize()
     f.free()
     calibration_copy(torch)

@@ -158,11 +158,13 @@ int onpu_moe_ffn_dev(void * h, const void * x, int64_t T, const int32_t * ids, i
                      int y_f32, void * stream);
 /* MoE decode step from router logits: logits fp32 [T][E] and x bf16 [T][Kg] in HBM -> ids / w [T][k]
  * (written) and y [T][Nd]. Replaces the reference's host routing plus onpu_ffn_run
- * (onpu_api.cpp:292-496; moe_runtime.py:333-341 for the router) with device work only: the router
- * kernel and onpu_moe_ffn_dev's launches, or, with ONPU_MOE_FUSED=1 and T <= 4, k <= 8 and expert
- * shapes that fit, one launch doing all of it (slower on MI355X: its cross-workgroup handoff costs
- * more than the kernel boundaries it saves). Calls on one handle must be ordered on one stream (they
- * share the handle's workspace). */
+ * (onpu_api.cpp:292-496; moe_runtime.py:333-341 for the router) with device work only. T <= 4
+ * (ONPU_MOE_DECODE_MAX), k <= 16, E <= 256: two launches, the gate+up GEMV routing its own token in
+ * each workgroup (ids / w written there) and the down GEMV with the weighted slot sum; with
+ * ONPU_MOE_FUSED=1, k <= 8 and expert shapes that fit, one launch doing all of it (slower on MI355X:
+ * its cross-workgroup handoff costs more than the kernel boundary it saves); longer prompts: the
+ * router kernel, then onpu_moe_ffn_dev's launches. Calls on one handle must be ordered on one stream
+ * (they share the handle's workspace). */
 int onpu_moe_decode_dev(void * h, const float * logits, const void * x, int64_t T, int E, int k, int renorm,
                         int32_t * ids, float * w, void * y, int y_f32, void * stream);
 /* 1 when a one-launch MoE decode on h gave up waiting for its act tiles since the last call (results

@@ -486,9 +486,12 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
 }
 
 // MoE decode (T <= 4 tokens) in two launches: gate_up with SiLU(gate) * up per slot, then down with
-// the routing-weighted slot sum per token. act: bf16 [T k][I] in the FFN's workspace.
+// the routing-weighted slot sum per token. act: bf16 [T k][I] in the FFN's workspace. With logits
+// (E <= 256 experts, k <= 16), the gate_up launch also routes: each of its workgroups picks its slot's
+// expert from the token's logits, and ids / w are written there for the down launch and the caller.
 hipError_t moe_decode_two(Ffn * f, const uint16_t * x, int64_t T, int k, const int32_t * ids, const float * w,
-                          void * y, int yf32, hipStream_t s) {
+                          void * y, int yf32, hipStream_t s, const float * logits = nullptr, int E = 0,
+                          int renorm = 1) {
     Mat4 * gu = f->gu, * dn = f->dn;
     const int64_t I = gu->N / 2, Nd = dn->N, n = T * k;
     hipError_t e = f->ws[0].ensure((size_t) (n * I * 2));
@@ -501,6 +504,12 @@ hipError_t moe_decode_two(Ffn * f, const uint16_t * x, int64_t T, int k, const i
     a.x = x; a.ldx = gu->K; a.xslot = gu->K; a.xdiv = k; a.M = 1;
     a.y = act; a.ldy = I; a.yslot = I; a.yf32 = 0; a.bpw = pg.bpw; a.tw = pg.tw;
     a.xls = gu->g.KB * 128 + 8;
+    if (logits != nullptr) {
+        if (E > 256 || k > 16 || k > E) return hipErrorInvalidValue;
+        a.logits = logits; a.E = E; a.renorm = renorm;
+        a.rids = const_cast<int32_t *>(ids); a.rw = const_cast<float *>(w);
+        a.ids = nullptr;
+    }
     e = launch_qgemv(gu->fmt, EPI_ACT_, a, 1, 2, pg.nb, pg.xl, dim3((unsigned) pg.gx, (unsigned) n), pg.waves(), s);
     if (e != hipSuccess) return e;
     const Plan pd = plan_slotsum(dn->g.KB, k);
@@ -962,6 +971,10 @@ int onpu_moe_decode_dev(void * h, const float * logits, const void * x, int64_t 
                                          (hipStream_t) stream);
     if (e != hipErrorNotSupported) {
         HIPR(e);
+        return 0;
+    }
+    if (T <= env_int("ONPU_MOE_DECODE_MAX", 4) && k <= 16 && E <= 256 && k <= E && plan_slotsum(f->dn->g.KB, k).kw) {
+        HIPR(moe_decode_two(f, (const uint16_t *) x, T, k, ids, w, y, y_f32, (hipStream_t) stream, logits, E, renorm));
         return 0;
     }
     HIPR(launch_route(logits, T, E, k, renorm, ids, w, (hipStream_t) stream));

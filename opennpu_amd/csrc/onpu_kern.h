@@ -699,9 +699,38 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         twi = wave / KW;
         kpart = wave % KW;
     }
-    const int64_t e = a.ids ? (int64_t) a.ids[slot] : 0;
-    const uint8_t * W = a.W + e * a.estride;
     const uint16_t * x = a.x + (slot / a.xdiv) * a.xslot;
+    constexpr int PER = RT * MB * 256;
+    uint16_t * xs = (uint16_t *) (red + nw * PER);
+    // XL: column sums of x per 32-group (G128S: per 128) times xsum_mul after the x rows:
+    // xsum[group][16 MFMA rows] (x row m at perm16(m))
+    float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
+    XStage<FMT, MB> xst(x, a.ldx, a.K, a.KB, a.M, xs, a.xls, xsum);
+    int64_t e = 0;
+    const bool route = EPI == EPI_ACT && a.logits != nullptr;
+    if (route) {
+        // the slot's expert from the token's logits (wave 0, the router kernel's selection) while
+        // the x loads are in flight; the weights' addresses wait for it
+        __shared__ int s_expert;
+        if (XL) xst.pre();
+        if (wave == 0) {
+            const int64_t t = slot / a.xdiv;
+            const int j = (int) (slot - t * a.xdiv);
+            int my_id;
+            float my_w;
+            route_token(a.logits + t * a.E, a.E, (int) a.xdiv, a.renorm, my_id, my_w);
+            if (lane == 0) s_expert = __builtin_amdgcn_readlane(my_id, j);
+            if (blockIdx.x == 0 && j == 0 && lane < a.xdiv) {
+                a.rids[t * a.xdiv + lane] = my_id;
+                a.rw[t * a.xdiv + lane] = my_w;
+            }
+        }
+        __syncthreads();
+        e = s_expert;
+    } else if (a.ids) {
+        e = a.ids[slot];
+    }
+    const uint8_t * W = a.W + e * a.estride;
     const uint8_t * tb[RT];
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     const int64_t stride = (int64_t) gridDim.x * ntw, tg0 = (int64_t) blockIdx.x * ntw;
@@ -710,15 +739,9 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         tb[rt] = t < a.NT ? W + t * a.KB * BLK : nullptr;
     }
     const int64_t b0 = (int64_t) kpart * a.bpw, b1 = b0 + a.bpw < a.KB ? b0 + a.bpw : a.KB;
-    constexpr int PER = RT * MB * 256;
-    uint16_t * xs = (uint16_t *) (red + nw * PER);
-    // XL: column sums of x per 32-group (G128S: per 128) times xsum_mul after the x rows:
-    // xsum[group][16 MFMA rows] (x row m at perm16(m))
-    float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
     const XSrc X{x, a.ldx, XL ? xs : nullptr, a.xls, XL ? xsum : nullptr};
-    XStage<FMT, MB> xst(x, a.ldx, a.K, a.KB, a.M, xs, a.xls, xsum);
     auto pre = [&]() {
-        if (XL) xst.pre();
+        if (XL && !route) xst.pre();              // (routing workgroups issued them already)
     };
     auto post = [&]() {
         if (XL) xst.post();

@@ -20,6 +20,13 @@ struct QArgs {
     int64_t bpw;              // K blocks (128 wide) per wave
     int64_t xls;              // LDS-staged x (XL variants): row stride in elements
     int tw;                   // tile groups per workgroup (waves = tw * K parts); 1 for EPI_SLOTSUM
+    // EPI_ACT with logits: each workgroup routes its token (slot / xdiv, top xdiv of E experts) and
+    // multiplies by the expert it picks for its slot instead of reading ids; one workgroup per token
+    // writes the token's ids and weights to rids / rw (renorm as the router kernel)
+    const float * logits;
+    int E, renorm;
+    int32_t * rids;
+    float * rw;
 };
 
 // k_qgemm / k_qgemm_sk: prefill, Y[M][N] = X[M][K] . deq(W)^T

@@ -152,13 +152,15 @@ class QFfn:
                                       int(out.dtype == torch.float32), _stream()), "onpu_moe_ffn_dev")
         return out
 
-    def decode(self, logits, x, k, renorm=True, out=None, f32=False):
+    def decode(self, logits, x, k, renorm=True, out=None, f32=False, ids=None, w=None):
         """router + FFN from logits fp32 [T][E] and x bf16 [T][H]: returns (y [T][Nd], ids int32 [T][k],
-        w fp32 [T][k])."""
+        w fp32 [T][k]); out, ids and w may be given."""
         import torch
         T, E = logits.shape
-        ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
-        w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+        if ids is None:
+            ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+        if w is None:
+            w = torch.empty((T, k), dtype=torch.float32, device=x.device)
         if out is None:
             out = torch.empty((T, self.Nd), dtype=torch.float32 if f32 else torch.bfloat16, device=x.device)
         check(self.L.onpu_moe_decode_dev(self.h, _ptr(logits), _ptr(x), T, E, k, int(renorm), _ptr(ids), _ptr(w),

@@ -160,6 +160,56 @@ def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
     check_moe(y[tok], fmt, gu, dn, E, H, I, xb[tok], rid[tok], rw[tok], grouped=T > 4, what=f"qwen3-30b-a3b T {T}")
 
 
+@pytest.mark.parametrize("fmt,E,H,I,k,T", [(orc.FMT_G128S, 128, 2048, 768, 8, 1), (orc.FMT_Q4S, 64, 512, 256, 4, 3),
+                                             (orc.FMT_Q4NX, 24, 384, 160, 6, 4), (orc.FMT_G128S, 16, 256, 128, 16, 2)])
+def test_moe_decode_routed_gate_up(gpu, fmt, E, H, I, k, T, monkeypatch):
+    """decode from logits at T <= 4 (the default path): the gate+up launch routes each workgroup's
+    token and writes ids / w, equal to the oracle router; y within the bf16 bound of the oracle layer
+    and bit-equal to the router kernel followed by the FFN launches on the same ids / w; graph replays
+    give the same bits."""
+    import torch
+    monkeypatch.delenv("ONPU_MOE_FUSED", raising=False)
+    gu, dn = _experts(fmt, E, H, I, 700 + E + T)
+    xb = syn.activations(T, H, 701 + T)
+    lg = syn.logits(T, E, 702 + k)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        x = to_torch_bf16(xb).reshape(T, H)
+        lgd = torch.from_numpy(lg).cuda()
+        y, ids, w = f.decode(lgd, x, k)
+        i2, w2 = f.route(lgd, k)
+        y2 = f.ffn(x, i2, w2)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, i2) and torch.equal(w, w2), "ids / w differ from the router kernel's"
+        assert torch.equal(y, y2), "routed decode differs from router kernel + FFN"
+        yg, ig, wg = torch.empty_like(y), torch.empty_like(ids), torch.empty_like(w)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            f.decode(lgd, x, k, out=yg, ids=ig, w=wg)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            f.decode(lgd, x, k, out=yg, ids=ig, w=wg)
+        for _ in range(3):
+            yg.zero_()
+            ig.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(yg, y) and torch.equal(ig, ids) and torch.equal(wg, w), "graph replay differs"
+            ye, _, _ = f.decode(lgd, x, k)
+            torch.cuda.synchronize()
+            assert torch.equal(ye, y), "eager decode after a replay differs"
+        ids, w, y = ids.cpu().numpy(), w.cpu().numpy(), from_torch(y)
+    finally:
+        f.free()
+    rid, rw = orc.route(lg, k)
+    assert np.array_equal(ids, rid)
+    np.testing.assert_allclose(w, rw, rtol=2e-6, atol=1e-7)
+    check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=False, what=f"routed decode fmt {fmt} E {E} T {T}")
+
+
 # g128s needs whole 128-wide groups along the down projection's K = I: no I = 160 case for it
 _ONE_LAUNCH = [(fmt, *shape) for fmt in (orc.FMT_G128S, orc.FMT_Q4S, orc.FMT_Q4NX)
                for shape in ((128, 2048, 768, 8, 1), (128, 2048, 768, 8, 4), (16, 512, 256, 4, 3), (24, 384, 160, 6, 2))
