@@ -236,7 +236,8 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     }
     if (!pick) { p.nb = 1; p.xl = 0; }
     // the reduction buffer (waves x rt x mb KiB) <= 32 KiB and, with x in LDS, <= 160 KiB together
-    const int64_t red_kib = p.xl ? std::min<int64_t>(32, (163840 - xbytes) / 1024) : 32;
+    const int64_t red_kib =
+        p.xl ? std::min<int64_t>(32, (163840 - xbytes - (epi == EPI_ARGMAX_ ? 1024 : 0)) / 1024) : 32;
     const int maxw = std::max(1, std::min(qgemv_max_waves(p.mb, p.rt, p.nb, p.xl), (int) (red_kib / (p.rt * p.mb))));
     if (p.kw > maxw) {                               // more K per wave
         p.kw = maxw;
@@ -394,6 +395,25 @@ hipError_t gemv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * 
     a.y = y; a.ldy = m->N; a.yslot = 0; a.yf32 = yf32;
     a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
     return launch_qgemv(m->fmt, EPI_STORE_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
+}
+
+// LM-head GEMV whose epilogue also leaves each workgroup's key per row (EPI_ARGMAX; fp32 logits
+// [M][N]), then the small launch that reduces those keys to argmax [M]: the logits are not read
+// again. Keys: the handle's argmax workspace.
+hipError_t argmax_gemv(Mat4 * m, const uint16_t * x, int64_t M, float * logits, int32_t * argmax, hipStream_t s) {
+    const Plan p = plan_gemv(m->fmt, m->g.NT, m->g.KB, (int) M, 1, EPI_ARGMAX_);
+    hipError_t e = m->am_keys.ensure((size_t) (M * p.gx * 8));
+    if (e != hipSuccess) return e;
+    QArgs a{};
+    a.W = m->dev; a.estride = 0; a.ids = nullptr;
+    a.N = m->N; a.K = m->K; a.NT = m->g.NT; a.KB = m->g.KB;
+    a.x = x; a.ldx = m->K; a.xslot = 0; a.xdiv = 1; a.M = (int) M;
+    a.y = logits; a.ldy = m->N; a.yslot = 0; a.yf32 = 1;
+    a.bpw = p.bpw; a.tw = p.tw; a.xls = m->g.KB * 128 + 8;
+    a.akeys = m->am_keys.as<uint64_t>();
+    e = launch_qgemv(m->fmt, EPI_ARGMAX_, a, p.mb, p.rt, p.nb, p.xl, dim3((unsigned) p.gx, 1), p.waves(), s);
+    if (e != hipSuccess) return e;
+    return launch_argmax_keys(a.akeys, p.gx, M, argmax, s);
 }
 
 hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
@@ -717,11 +737,17 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
     if (M <= 0) return 0;
     // per-workgroup keys and per-row counters of the argmax: workspace of the handle (allocated on
     // the first call with this many rows; calls that overlap on one handle must not share it)
-    HIPR(m->am_keys.ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
     if (m->am_cnt.n < (size_t) M * ARGMAX_PAD) {
         HIPR(m->am_cnt.ensure((size_t) M * ARGMAX_PAD));
         HIPR(hipMemset(m->am_cnt.p, 0, m->am_cnt.n));
     }
+    // up to 64 rows: per-workgroup keys from the GEMV's epilogue (ONPU_ARGMAX_FUSED=0: the argmax
+    // launch over the logits)
+    if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0 && env_int("ONPU_ARGMAX_FUSED", 1)) {
+        HIPR(argmax_gemv(m, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
+        return 0;
+    }
+    HIPR(m->am_keys.ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
     HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
     HIPR(launch_argmax(logits, M, m->N, argmax, m->am_keys.as<uint64_t>(), m->am_cnt.as<uint32_t>(),
                        (hipStream_t) stream));

@@ -662,7 +662,22 @@ struct XStage {
 };
 
 // Epilogues
-enum { EPI_STORE = 0, EPI_ACT = 1, EPI_SLOTSUM = 2 };
+enum { EPI_STORE = 0, EPI_ACT = 1, EPI_SLOTSUM = 2, EPI_ARGMAX = 3 };
+
+// argmax key of value v at index n: the value's order-preserving bits above the complement of the
+// index, so the larger key is the larger value and, among equal values, the lower index. A NaN key
+// has zero value bits, so NaN never wins and a row of NaNs gives index 0.
+DEV uint64_t argmax_key(float v, int64_t n) {
+    return ((uint64_t) (v != v ? 0u : ord_key(v)) << 32) | (uint32_t) (0xffffffffu - (uint32_t) n);
+}
+
+DEV uint64_t wave_umax64(uint64_t v) {
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t u = __shfl_xor(v, o);
+        v = u > v ? u : v;
+    }
+    return v;
+}
 
 DEV void store_out(void * y, int yf32, int64_t idx, float v) {
     if (yf32) ((float *) y)[idx] = v;
@@ -681,6 +696,10 @@ constexpr int qgemv_lb(int MB, int RT, int NB, int XL) { return (MB == 1 && RT *
 //   ACT    : RT = 2, tiles (gate t, up t + stride); out[m][16 t + r] = silu(g) * u
 //   SLOTSUM: a.tw = 1; wave w -> slot w / ksplit (its expert and x row), K part w % ksplit;
 //            out = sum_s w_s y_s
+//   ARGMAX : as STORE (fp32 y), and each row's key over the workgroup's outputs (an LDS maximum)
+//            into a.akeys[m][blockIdx.x], for k_argmax_keys to reduce. (One counter on which the
+//            ~1000 workgroups of the LM head count in, the last reducing, measured ~5x slower: the
+//            agent-scope increments of one address queue behind each other, ~0.2 us apiece.)
 template <int FMT, int MB, int RT, int NB, int EPI, int XL>
 __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     extern __shared__ float red[];
@@ -755,6 +774,8 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     for (int rt = 0; rt < RT; rt++)
         for (int mb = 0; mb < MB; mb++)
             for (int v = 0; v < 4; v++) red[wave * PER + ((rt * MB + mb) * 4 + v) * 64 + lane] = acc[rt][mb][v];
+    __shared__ uint64_t s_key[EPI == EPI_ARGMAX ? 64 : 1];
+    if (EPI == EPI_ARGMAX && (int) threadIdx.x < a.M) s_key[threadIdx.x] = 0;    // below every key
     __syncthreads();
     const int nout = EPI == EPI_ACT ? MB * 256 : PER;
     for (int oo = threadIdx.x; oo < ntw * nout; oo += blockDim.x) {
@@ -781,8 +802,15 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         } else {
             float s = 0.f;
             for (int kp = 0; kp < KW; kp++) s += rp[kp * PER];
-            if (n < a.N) store_out(a.y, a.yf32, (int64_t) slot * a.yslot + (int64_t) m * a.ldy + n, s);
+            if (n < a.N) {
+                store_out(a.y, a.yf32, (int64_t) slot * a.yslot + (int64_t) m * a.ldy + n, s);
+                if (EPI == EPI_ARGMAX) atomicMax((unsigned long long *) &s_key[m], (unsigned long long) argmax_key(s, n));
+            }
         }
+    }
+    if (EPI == EPI_ARGMAX) {
+        __syncthreads();
+        if ((int) threadIdx.x < a.M) a.akeys[(int64_t) threadIdx.x * gridDim.x + blockIdx.x] = s_key[threadIdx.x];
     }
 }
 

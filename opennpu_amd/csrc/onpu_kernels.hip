@@ -110,18 +110,6 @@ __global__ __launch_bounds__(256) void k_moe_combine(const uint16_t * __restrict
 // back to zero, so the counters are zero between calls with no clearing step (graph replays too).
 // Keys and counters sit ARGMAX_PAD bytes apart: atomics of different workgroups on one cache line
 // queue behind each other.
-DEV uint64_t argmax_key(float v, int64_t n) {
-    return ((uint64_t) (v != v ? 0u : ord_key(v)) << 32) | (uint32_t) (0xffffffffu - (uint32_t) n);
-}
-
-DEV uint64_t wave_umax64(uint64_t v) {
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t u = __shfl_xor(v, o);
-        v = u > v ? u : v;
-    }
-    return v;
-}
-
 // workgroup maximum of the threads' keys; the result is valid in thread 0
 DEV uint64_t block_umax64(uint64_t k, uint64_t * wk) {
     k = wave_umax64(k);
@@ -175,6 +163,21 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float * __restr
         out[row] = (int32_t) (0xffffffffu - (uint32_t) r);
         __hip_atomic_store(cnt + row * CS, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// the first maximum of each row from the LM-head GEMV's keys (one per workgroup, [row][P]); the key
+// order is the value order with ties to the lower index, as in k_argmax
+__global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax_keys(const uint64_t * __restrict__ keys, int64_t P,
+                                                                int32_t * __restrict__ out) {
+    const int64_t row = blockIdx.x;
+    uint64_t k = 0;
+    for (int64_t p = threadIdx.x; p < P; p += ARGMAX_THREADS) {
+        const uint64_t kp = keys[row * P + p];
+        k = kp > k ? kp : k;
+    }
+    __shared__ uint64_t wk[ARGMAX_THREADS / 64];
+    k = block_umax64(k, wk);
+    if (threadIdx.x == 0) out[row] = (int32_t) (0xffffffffu - (uint32_t) k);
 }
 
 // ------------------------------------------------------------------ int8 GEMV
@@ -358,7 +361,8 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
     // x rows, then the column sums [KB * groups per block][16] floats
     const size_t xb = xl ? (size_t) a.M * a.xls * 2 + (size_t) a.KB * (fmt == 2 ? 1 : 4) * 64 : 0;
     if (xl && (a.M > 16 || (int64_t) a.M * a.ldx * 2 >= ((int64_t) 1 << 31))) return hipErrorInvalidValue;
-    if (red > 32768 || red + xb > 163840) return hipErrorInvalidValue;      // gfx950: 160 KiB per workgroup
+    // gfx950: 160 KiB per workgroup (the argmax epilogue's row keys take 1 KiB of static LDS)
+    if (red > 32768 || red + xb + (epi == EPI_ARGMAX_ ? 1024 : 0) > 163840) return hipErrorInvalidValue;
     if (xl && a.xls < a.KB * 128) return hipErrorInvalidValue;
     switch (fmt) {
         case 0: return qgemv_f0(epi, a, mb, rt, nb, xl, grid, waves, red + xb, s);
@@ -550,6 +554,14 @@ hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out
     if (rows <= 0 || N <= 0) return hipSuccess;
     if (rows > 65535 || N >= ((int64_t) 1 << 31)) return hipErrorInvalidValue;
     k_argmax<<<dim3((unsigned) argmax_parts(N), (unsigned) rows), ARGMAX_THREADS, 0, s>>>(v, N, keys, cnt, out);
+    CHECK_LAUNCH();
+    return hipSuccess;
+}
+
+hipError_t launch_argmax_keys(const uint64_t * keys, int64_t P, int64_t rows, int32_t * out, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    if (rows > 65535 || P <= 0) return hipErrorInvalidValue;
+    k_argmax_keys<<<dim3((unsigned) rows), ARGMAX_THREADS, 0, s>>>(keys, P, out);
     CHECK_LAUNCH();
     return hipSuccess;
 }

@@ -27,6 +27,8 @@ struct QArgs {
     int E, renorm;
     int32_t * rids;
     float * rw;
+    // EPI_ARGMAX: the workgroups' keys per row, [M][gridDim.x]
+    uint64_t * akeys;
 };
 
 // k_qgemm / k_qgemm_sk: prefill, Y[M][N] = X[M][K] . deq(W)^T
@@ -164,6 +166,8 @@ hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s);
 // y[t] = sum_j w[t][j] o[inv[t k + j]] (o bf16 rows, fp32 sum)
 hipError_t launch_moe_combine(const uint16_t * o, const int32_t * inv, const float * w, int64_t T, int k, int64_t N,
                               void * y, int yf32, hipStream_t s);
+// index of the largest of each row's P keys (k_qgemv's EPI_ARGMAX keys [rows][P]): one workgroup per row
+hipError_t launch_argmax_keys(const uint64_t * keys, int64_t P, int64_t rows, int32_t * out, hipStream_t s);
 // one launch of argmax_parts(N) workgroups per row, each over ARGMAX_CHUNK values; keys: workspace
 // of rows * argmax_parts(N) * ARGMAX_PAD bytes; cnt: rows * ARGMAX_PAD bytes of counters, zero before
 // the first call (each call leaves them at zero). Calls that overlap must not share keys / cnt.
@@ -207,7 +211,7 @@ hipError_t launch_moe_act(const float * h, int64_t rows, int64_t Ng, const int32
 hipError_t launch_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * ids, const float * w,
                           const float * bias, float * y, hipStream_t s);
 
-enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
+enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2, EPI_ARGMAX_ = 3 };
 
 // k_qgemv variants built for every format: X(epilogue, MB, RT, NB, XL). MB: 16-row x blocks;
 // RT: row tiles per workgroup; NB: K blocks each wave loads before computing; XL: x staged in LDS.
@@ -215,7 +219,8 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2 };
     X(0, 1, 1, 1, 1) X(0, 1, 1, 2, 1) X(0, 1, 1, 4, 1) X(0, 1, 2, 2, 1)                                 \
     X(0, 1, 1, 1, 0) X(0, 1, 1, 2, 0) X(0, 1, 2, 1, 0) X(0, 2, 1, 1, 0) X(0, 2, 1, 2, 0) X(0, 4, 1, 1, 0) \
     X(1, 1, 2, 1, 1) X(1, 1, 2, 2, 1) X(1, 1, 2, 1, 0) X(1, 2, 2, 1, 0) X(1, 4, 2, 1, 0)                \
-    X(2, 1, 1, 1, 0) X(2, 1, 1, 2, 0) X(2, 1, 1, 3, 0)
+    X(2, 1, 1, 1, 0) X(2, 1, 1, 2, 0) X(2, 1, 1, 3, 0)                                                   \
+    X(3, 1, 1, 2, 1) X(3, 1, 1, 1, 1) X(3, 1, 1, 1, 0) X(3, 2, 1, 1, 0) X(3, 4, 1, 1, 0)
 
 // per-format entry points (onpu_fmt.hip compiled with ONPU_FMT_ID = id)
 #define ONPU_FMT_DECL(id)                                                                                   \

@@ -366,6 +366,35 @@ def test_argmax_ties_and_replays(gpu, fmt, N, K, M):
     check_f32_out(lg, orc.qmm(fmt, st, N, K, xb), what="LM-head logits")
 
 
+@pytest.mark.parametrize("fmt,N,K,M", [(orc.FMT_Q4_0, 151936, 4096, 5), (orc.FMT_G128S, 4100, 2048, 17),
+                                       (orc.FMT_Q4S, 3000, 1024, 40), (orc.FMT_Q4NX, 2000, 512, 64)])
+def test_argmax_fused_equals_separate(gpu, fmt, N, K, M, monkeypatch):
+    """the argmax from the GEMV epilogue's per-workgroup keys (default up to 64 rows) gives the same
+    logits bits and indices as the GEMV followed by the argmax launch over the logits
+    (ONPU_ARGMAX_FUSED=0), also on a second call and for a row of NaNs (index 0)"""
+    import torch
+    from opennpu_amd.device import QMatrix
+    st = syn.weights(fmt, N, K, 41)
+    xb = syn.activations(M, K, 42)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        x = to_torch_bf16(xb).reshape(M, K)
+        x[M - 1] = float("nan")
+        monkeypatch.setenv("ONPU_ARGMAX_FUSED", "0")
+        lg0, i0 = q.argmax(x)
+        monkeypatch.setenv("ONPU_ARGMAX_FUSED", "1")
+        lg1, i1 = q.argmax(x)
+        lg2, i2 = q.argmax(x)
+        torch.cuda.synchronize()
+        assert torch.equal(lg0.view(torch.int32), lg1.view(torch.int32)), "logits differ"
+        assert torch.equal(i0, i1) and torch.equal(i1, i2), "argmax differs"
+        assert int(i1[M - 1]) == 0, "a row of NaNs gives index 0"
+        lg, idx = from_torch(lg1), i1.cpu().numpy()
+    finally:
+        q.free()
+    assert np.array_equal(idx[:M - 1], orc.argmax(lg[:M - 1])), "argmax of the returned logits"
+
+
 def test_rows_zero_and_reuse(gpu):
     """M = 0 is a no-op; one handle serves several calls with different M."""
     import torch
