@@ -167,17 +167,33 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float * __restr
 
 // the first maximum of each row from the LM-head GEMV's keys (one per workgroup, [row][P]); the key
 // order is the value order with ties to the lower index, as in k_argmax
-__global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax_keys(const uint64_t * __restrict__ keys, int64_t P,
-                                                                int32_t * __restrict__ out) {
+// A thread issues its (up to) 4 loads of a pass before comparing, so a row of up to 4096 keys costs
+// one memory round trip.
+constexpr int AKEY_THREADS = 1024, AKEY_U = 4;
+__global__ __launch_bounds__(AKEY_THREADS) void k_argmax_keys(const uint64_t * __restrict__ keys, int64_t P,
+                                                              int32_t * __restrict__ out) {
     const int64_t row = blockIdx.x;
+    const uint64_t * kr = keys + row * P;
     uint64_t k = 0;
-    for (int64_t p = threadIdx.x; p < P; p += ARGMAX_THREADS) {
-        const uint64_t kp = keys[row * P + p];
-        k = kp > k ? kp : k;
+    for (int64_t p0 = 0; p0 < P; p0 += AKEY_THREADS * AKEY_U) {
+        uint64_t v[AKEY_U];
+#pragma unroll
+        for (int u = 0; u < AKEY_U; u++) {
+            const int64_t p = p0 + u * AKEY_THREADS + threadIdx.x;
+            v[u] = p < P ? kr[p] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < AKEY_U; u++) k = v[u] > k ? v[u] : k;
     }
-    __shared__ uint64_t wk[ARGMAX_THREADS / 64];
-    k = block_umax64(k, wk);
-    if (threadIdx.x == 0) out[row] = (int32_t) (0xffffffffu - (uint32_t) k);
+    __shared__ uint64_t wk[AKEY_THREADS / 64];
+    k = wave_umax64(k);
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        k = threadIdx.x < AKEY_THREADS / 64 ? wk[threadIdx.x] : 0;
+        k = wave_umax64(k);
+        if (threadIdx.x == 0) out[row] = (int32_t) (0xffffffffu - (uint32_t) k);
+    }
 }
 
 // ------------------------------------------------------------------ int8 GEMV
@@ -561,7 +577,7 @@ hipError_t launch_argmax(const float * v, int64_t rows, int64_t N, int32_t * out
 hipError_t launch_argmax_keys(const uint64_t * keys, int64_t P, int64_t rows, int32_t * out, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (rows > 65535 || P <= 0) return hipErrorInvalidValue;
-    k_argmax_keys<<<dim3((unsigned) rows), ARGMAX_THREADS, 0, s>>>(keys, P, out);
+    k_argmax_keys<<<dim3((unsigned) rows), AKEY_THREADS, 0, s>>>(keys, P, out);
     CHECK_LAUNCH();
     return hipSuccess;
 }
