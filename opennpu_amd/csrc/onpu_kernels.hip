@@ -22,6 +22,9 @@ __global__ __launch_bounds__(64) void k_route(const float * __restrict__ logits,
 // One workgroup. entries i = t * k + j (T * k of them) sorted by expert:
 //   cnt[e], off[e] (exclusive scan, off[E] = total), perm[off[e] + rank] = i and inv[i] = its position,
 //   work list of (expert, first position, rows <= rows_per_item) items -> items[], nitems
+// Items are listed by A blocks (ceil(rows / 16), rows_per_item <= 64), most first: the grouped GEMMs
+// take one item per grid row, so the longest items are dispatched first and the short ones fill
+// the end of the launch. (The order changes no result: every item's rows are computed alone.)
 __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict__ ids, int64_t n, int E,
                                                       int rows_per_item, int32_t * __restrict__ off,
                                                       int32_t * __restrict__ perm, int32_t * __restrict__ inv,
@@ -34,33 +37,46 @@ __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict
     for (int64_t i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&cnt[ids[i]], 1);
     __syncthreads();
     if (threadIdx.x < 64) {
-        // wave 0: lane l owns experts [l * EP, (l + 1) * EP); exclusive scans of rows and items
+        // wave 0: lane l owns experts [l * EP, (l + 1) * EP); exclusive scans of rows and of items
+        // per class c = A blocks - 1 (classes listed from 3 down to 0)
         const int lane = threadIdx.x, EP = (E + 63) / 64, e0 = lane * EP, e1 = e0 + EP < E ? e0 + EP : E;
-        int32_t rs = 0, is = 0;
+        auto cls = [](int32_t rows) { return (rows + 15) / 16 - 1; };
+        int32_t rs = 0, is[4] = {0, 0, 0, 0};
         for (int e = e0; e < e1; e++) {
             rs += cnt[e];
-            is += (cnt[e] + rows_per_item - 1) / rows_per_item;
+            for (int32_t r0 = 0; r0 < cnt[e]; r0 += rows_per_item)
+                is[cls(cnt[e] - r0 < rows_per_item ? cnt[e] - r0 : rows_per_item)]++;
         }
-        int32_t ri = rs, ii = is;                     // inclusive scans across lanes
+        int32_t ri = rs, ii[4] = {is[0], is[1], is[2], is[3]};     // inclusive scans across lanes
         for (int o = 1; o < 64; o <<= 1) {
-            const int32_t a = __shfl_up(ri, o), b = __shfl_up(ii, o);
-            if (lane >= o) { ri += a; ii += b; }
+            const int32_t a = __shfl_up(ri, o);
+            int32_t b[4];
+            for (int c = 0; c < 4; c++) b[c] = __shfl_up(ii[c], o);
+            if (lane >= o) {
+                ri += a;
+                for (int c = 0; c < 4; c++) ii[c] += b[c];
+            }
         }
-        int32_t s = ri - rs, it = ii - is;            // exclusive: this lane's first row / item
+        int32_t tot[4], it[4];
+        for (int c = 0; c < 4; c++) tot[c] = __shfl(ii[c], 63);
+        for (int c = 3, base = 0; c >= 0; base += tot[c], c--) it[c] = base + ii[c] - is[c];
+        int32_t s = ri - rs;                          // exclusive: this lane's first row
         for (int e = e0; e < e1; e++) {
             pos[e] = s;
             off[e] = s;
             for (int32_t r0 = 0; r0 < cnt[e]; r0 += rows_per_item) {
-                items[3 * it] = e;
-                items[3 * it + 1] = s + r0;
-                items[3 * it + 2] = cnt[e] - r0 < rows_per_item ? cnt[e] - r0 : rows_per_item;
-                it++;
+                const int32_t rows = cnt[e] - r0 < rows_per_item ? cnt[e] - r0 : rows_per_item;
+                const int c = cls(rows);
+                items[3 * it[c]] = e;
+                items[3 * it[c] + 1] = s + r0;
+                items[3 * it[c] + 2] = rows;
+                it[c]++;
             }
             s += cnt[e];
         }
         if (lane == 63) {
             off[E] = ri;
-            *nitems = ii;
+            *nitems = tot[0] + tot[1] + tot[2] + tot[3];
         }
     }
     __syncthreads();
