@@ -789,8 +789,8 @@ def main():
                     help="only the measured ceilings (HBM read, copy, LDS, MFMA, clock, vendor bf16 GEMM)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build runs the int4 path on a single MI355X; --gpus {args.gpus} "
-              "is not supported (see DESIGN.md for how the path would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: the int4 path runs on a single MI355X; --gpus {args.gpus} is not "
+              "supported (across GPUs the decode GEMVs would split N, the MoE layer its experts)", file=sys.stderr)
         sys.exit(2)
     import torch
     from opennpu_amd import require_gpu, synthetic as syn
