@@ -161,7 +161,8 @@ def test_moe_qwen3_30b_a3b(gpu, T, check_tokens):
 
 
 @pytest.mark.parametrize("fmt,E,H,I,k,T", [(orc.FMT_G128S, 128, 2048, 768, 8, 1), (orc.FMT_Q4S, 64, 512, 256, 4, 3),
-                                             (orc.FMT_Q4NX, 24, 384, 160, 6, 4), (orc.FMT_G128S, 16, 256, 128, 16, 2)])
+                                             (orc.FMT_Q4NX, 24, 384, 160, 6, 4), (orc.FMT_G128S, 16, 256, 128, 16, 2),
+                                             (orc.FMT_Q4S, 256, 256, 128, 8, 2)])
 def test_moe_decode_routed_gate_up(gpu, fmt, E, H, I, k, T, monkeypatch):
     """decode from logits at T <= 4 (the default path): the gate+up launch routes each workgroup's
     token and writes ids / w, equal to the oracle router; y within the bf16 bound of the oracle layer
