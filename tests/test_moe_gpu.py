@@ -211,6 +211,35 @@ def test_moe_decode_routed_gate_up(gpu, fmt, E, H, I, k, T, monkeypatch):
     check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=False, what=f"routed decode fmt {fmt} E {E} T {T}")
 
 
+@pytest.mark.parametrize("fmt,T", [(orc.FMT_G128S, 8), (orc.FMT_Q4S, 40)])
+def test_moe_decode_prompt_path(gpu, fmt, T, monkeypatch):
+    """decode from logits past the decode path's 4 tokens: the router kernel, then the grouped
+    products; ids / w equal the oracle router, y the oracle layer (grouped bounds) and, bit for bit,
+    an explicit route + FFN"""
+    import torch
+    monkeypatch.delenv("ONPU_MOE_FUSED", raising=False)
+    E, H, I, k = 32, 256, 128, 4
+    gu, dn = _experts(fmt, E, H, I, 800 + T)
+    xb = syn.activations(T, H, 801 + T)
+    lg = syn.logits(T, E, 802 + T)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        x = to_torch_bf16(xb).reshape(T, H)
+        lgd = torch.from_numpy(lg).cuda()
+        y, ids, w = f.decode(lgd, x, k)
+        i2, w2 = f.route(lgd, k)
+        y2 = f.ffn(x, i2, w2)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, i2) and torch.equal(w, w2) and torch.equal(y, y2)
+        ids, w, y = ids.cpu().numpy(), w.cpu().numpy(), from_torch(y)
+    finally:
+        f.free()
+    rid, rw = orc.route(lg, k)
+    assert np.array_equal(ids, rid)
+    np.testing.assert_allclose(w, rw, rtol=2e-6, atol=1e-7)
+    check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=True, what=f"decode prompt path fmt {fmt} T {T}")
+
+
 # g128s needs whole 128-wide groups along the down projection's K = I: no I = 160 case for it
 _ONE_LAUNCH = [(fmt, *shape) for fmt in (orc.FMT_G128S, orc.FMT_Q4S, orc.FMT_Q4NX)
                for shape in ((128, 2048, 768, 8, 1), (128, 2048, 768, 8, 4), (16, 512, 256, 4, 3), (24, 384, 160, 6, 2))
