@@ -13,10 +13,10 @@
  *   - geometry: the values the reference formula gives at the benchmark shapes.
  *   - act / weighted sum / attention step / int8 GEMV: also against the reference's own
  *     onpu_cpu.cpp compiled under oracle/_ref (tests/test_oracle_ref.py).
- * The search quantizers (orc_quant_sym / orc_quant_asym32) are off the measured path and are
- * checked by invariants only: exact grids come back exactly, sign symmetry (-x gives the same
- * codes and the negated scale), power-of-two equivariance. Their candidate tables and refit order
- * are not fixed by those: parity unpinned. The GGUF codecs (orc_quant_q4_0, orc_transcode_q4k)
+ *   - f2bf, geometry and the search quantizers (orc_quant_sym32 / orc_quant_asym32): byte for
+ *     byte against the reference's own opennpu_core.hpp:37-169 compiled as written under oracle/_ref
+ *     (tests/test_quant_ref.py, 2^20 groups per format of eight kinds), besides the invariants of
+ *     tests/test_oracle.py (exact grids, sign symmetry, power-of-two equivariance). The GGUF codecs (orc_quant_q4_0, orc_transcode_q4k)
  * are checked on hand-built blocks whose results are exact, by the closed forms of the formats
  * (Q4_0's truncation at exact half-way inputs included), and the transcode's choice by a
  * brute-force neighbourhood.
@@ -281,7 +281,15 @@ void orc_geometry(int64_t N, int64_t K, int ncols, int sym, int64_t * out) {
 }
 
 /* ---------------------------------------------------------------- search quantizers (load time)
- * q4s over n weights (n = 32: q4s, 128: g128s): 16 candidate scales around absmax, least-squares
+ * clamp as std::min(hi, std::max(lo, v)) evaluates it (opennpu_core.hpp:118,128,136,152,160,167):
+ * std::max(a, b) is (a < b) ? b : a and std::min(a, b) is (b < a) ? b : a, so a NaN code (0 * inf
+ * when a tiny range's reciprocal overflows) becomes lo. */
+static float clamp_std(float v, float lo, float hi) {
+    const float u = lo < v ? v : lo;
+    return u < hi ? u : hi;
+}
+
+/* q4s over n weights (n = 32: q4s, 128: g128s): 16 candidate scales around absmax, least-squares
  * refit, bf16, least SSE wins (opennpu_core.hpp:142-169, written there for n = 32). */
 void orc_quant_sym(const float * x, int n, uint8_t * q, uint16_t * d_bf) {
     float mx = 0;
@@ -293,8 +301,7 @@ void orc_quant_sym(const float * x, int n, uint8_t * q, uint16_t * d_bf) {
         const float d0 = mx / dv;
         float sqq = 0, sqx = 0;
         for (int i = 0; i < n; i++) {
-            float v = nearbyintf(x[i] / d0);
-            v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
+            const float v = clamp_std(nearbyintf(x[i] / d0), -8.f, 7.f);
             sqq += v * v;
             sqx += v * x[i];
         }
@@ -303,16 +310,14 @@ void orc_quant_sym(const float * x, int n, uint8_t * q, uint16_t * d_bf) {
         if (d == 0) continue;
         float e = 0;
         for (int i = 0; i < n; i++) {
-            float v = nearbyintf(x[i] / d);
-            v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
+            const float v = clamp_std(nearbyintf(x[i] / d), -8.f, 7.f);
             const float r = v * d - x[i];
             e += r * r;
         }
         if (e < best_e) { best_e = e; best_d = d; }
     }
     for (int i = 0; i < n; i++) {
-        float v = nearbyintf(x[i] / best_d);
-        v = v < -8.f ? -8.f : (v > 7.f ? 7.f : v);
+        const float v = clamp_std(nearbyintf(x[i] / best_d), -8.f, 7.f);
         q[i] = (uint8_t) (v + 8);
     }
     *d_bf = orc_f2bf(best_d);
@@ -321,7 +326,7 @@ void orc_quant_sym(const float * x, int n, uint8_t * q, uint16_t * d_bf) {
 void orc_quant_sym32(const float * x, uint8_t * q, uint16_t * d_bf) { orc_quant_sym(x, 32, q, d_bf); }
 
 /* q4nx per 32: 21 stretched grids over [min, max], (s, m) refit by least squares, bf16
- * (opennpu_core.hpp:103-138). Parity unpinned: invariants only. */
+ * (opennpu_core.hpp:103-138). */
 void orc_quant_asym32(const float * x, uint8_t * q, uint16_t * s_bf, uint16_t * m_bf) {
     float lo = x[0], hi = x[0];
     for (int i = 1; i < 32; i++) { if (x[i] < lo) lo = x[i]; if (x[i] > hi) hi = x[i]; }
@@ -332,8 +337,7 @@ void orc_quant_asym32(const float * x, uint8_t * q, uint16_t * s_bf, uint16_t * 
         const float isc = (-1.0f + 0.1f * st + 15.0f) / range;
         float sl = 0, sll = 0, sx = 0, slx = 0;
         for (int i = 0; i < 32; i++) {
-            float l = nearbyintf(isc * (x[i] - lo));
-            l = l < 0.f ? 0.f : (l > 15.f ? 15.f : l);
+            const float l = clamp_std(nearbyintf(isc * (x[i] - lo)), 0.f, 15.f);
             sl += l; sll += l * l; sx += x[i]; slx += l * x[i];
         }
         const float D = 32 * sll - sl * sl;
@@ -344,8 +348,7 @@ void orc_quant_asym32(const float * x, uint8_t * q, uint16_t * s_bf, uint16_t * 
         if (!(sc > 0)) continue;
         float e = 0;
         for (int i = 0; i < 32; i++) {
-            float l = nearbyintf((x[i] - mn) / sc);
-            l = l < 0.f ? 0.f : (l > 15.f ? 15.f : l);
+            const float l = clamp_std(nearbyintf((x[i] - mn) / sc), 0.f, 15.f);
             const float d = l * sc + mn - x[i];
             e += d * d;
         }
@@ -354,8 +357,7 @@ void orc_quant_asym32(const float * x, uint8_t * q, uint16_t * s_bf, uint16_t * 
     best_s = orc_bf2f(orc_f2bf(best_s));
     best_m = orc_bf2f(orc_f2bf(best_m));
     for (int i = 0; i < 32; i++) {
-        float l = nearbyintf((x[i] - best_m) / best_s);
-        l = l < 0.f ? 0.f : (l > 15.f ? 15.f : l);
+        const float l = clamp_std(nearbyintf((x[i] - best_m) / best_s), 0.f, 15.f);
         q[i] = (uint8_t) l;
     }
     *s_bf = orc_f2bf(best_s);

@@ -151,3 +151,30 @@ def test_codec_argument_errors(gpu):
     finally:
         q1.free()
         q2.free()
+
+
+@pytest.mark.parametrize("fmt", [orc.FMT_Q4S, orc.FMT_Q4NX])
+def test_quantize_dev_equals_reference_build(gpu, fmt):
+    """onpu_quantize_dev writes the reference's own q4s / q4nx choices (opennpu_core.hpp:103-169
+    compiled as written, oracle/_ref) on 2^20 groups per format: normal, heavy-tailed, all-positive,
+    tiny and huge magnitudes, exact grids and planted ties. Compared through the handle's
+    dequantized weights, bit for bit (codes, scales and the sign of -0 all show there)."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    from quantref import KINDS, groups, staging_source
+    stage, label = staging_source()
+    for kind in KINDS:
+        X = groups(kind, 1 << 17, 500 + KINDS.index(kind))
+        W, want_st = stage(fmt, X)
+        N, K = W.shape
+        q = QMatrix(N, K, fmt)
+        try:
+            print(f"quantize_dev vs {label}: fmt {fmt} kind {kind} N={N} K={K}", flush=True)
+            q.quantize(torch.from_numpy(W).cuda())
+            torch.cuda.synchronize()
+            got = q.dequant()
+        finally:
+            q.free()
+        want = orc.dequant(fmt, want_st, N, K)
+        bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+        assert bad.size == 0, f"{kind}: {bad.size} weights differ from the {label}, first at {bad[:4]}"

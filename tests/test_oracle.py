@@ -253,8 +253,9 @@ def test_geometry_known_values(N, K, ncols, want):
 
 # ------------------------------------------------------------------ search quantizers
 def test_quant_sym32_exact_grid_round_trip():
-    """groups that are exactly v * d (d a power of two, v spanning -8..7) come back exactly;
-    the exact scale choice on general inputs stays parity unpinned"""
+    """groups that are exactly v * d (d a power of two, v spanning -8..7) come back exactly (the
+    exact scale choice on general inputs is pinned against the reference's own build in
+    tests/test_quant_ref.py)"""
     rng = np.random.default_rng(7)
     for t in range(50):
         d = np.float32(2.0 ** rng.integers(-12, 2))
