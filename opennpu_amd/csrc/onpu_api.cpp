@@ -76,20 +76,37 @@ Device & device() {
     return d;
 }
 
-struct DBuf {                              // grow-only device buffer (freed with its owner)
+// Grow-only device buffer, freed with its owner. Buffers of the device-pointer calls (which a caller
+// may capture into a HIP graph) keep every allocation they outgrow until release(): a graph captured
+// at a smaller size holds the old pointer, and later calls at a larger size must not free it under
+// the graph's replays. Allocation runs in relaxed capture mode (hipMalloc is not stream-ordered), so
+// a first call may come under capture.
+struct DBuf {
     void * p = nullptr;
     size_t n = 0;
+    bool keep = false;                     // keep outgrown allocations until release()
+    std::vector<void *> old;
     hipError_t ensure(size_t bytes) {
         if (bytes <= n) return hipSuccess;
-        if (p) (void) hipFree(p);
+        if (p) {
+            if (keep) old.push_back(p);
+            else (void) hipFree(p);
+        }
         p = nullptr;
         n = 0;
-        const hipError_t e = hipMalloc(&p, std::max<size_t>(bytes, 256));
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        hipError_t e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return e;
+        e = hipMalloc(&p, std::max<size_t>(bytes, 256));
+        (void) hipThreadExchangeStreamCaptureMode(&mode);
         if (e == hipSuccess) n = std::max<size_t>(bytes, 256);
+        else p = nullptr;
         return e;
     }
     void release() {
         if (p) (void) hipFree(p);
+        for (void * q : old) (void) hipFree(q);
+        old.clear();
         p = nullptr;
         n = 0;
     }
@@ -109,15 +126,20 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     uint8_t * dev = nullptr;
     uint8_t * stage = nullptr;             // host staging, E * sstride bytes (lazy)
     int64_t sstride = 0;
-    DBuf am_keys;                          // argmax: per-workgroup keys of the _dev calls on this handle
-    DBuf am_cnt;                           // argmax row counters (zeroed once; each call leaves them zero)
+    // argmax workspace of the _dev calls on this handle (kept across growth: see DBuf)
+    DBuf am_keys{nullptr, 0, true};        // per-workgroup keys of the GEMV epilogue (<= 64 rows)
+    DBuf am_big{nullptr, 0, true};         // keys of the argmax launch over the logits
+    DBuf am_cnt{nullptr, 0, true};         // its row counters (zeroed once; each call leaves them zero)
 };
 
 struct Ffn {
     Mat4 * gu = nullptr, * dn = nullptr;
     bool fused = false;
-    DBuf ws[7];                            // ffn_core: decode act; prompt permutation, items, act, o
-    DBuf md_act, md_sync;                  // k_moe_decode: act rows, counters (zeroed once)
+    // ffn_core: decode act; prompt permutation, items, act, o. k_moe_decode: act rows, counters
+    // (zeroed once). All on the device-pointer calls' paths: kept across growth (see DBuf).
+    DBuf ws[7] = {{nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true},
+                  {nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true}};
+    DBuf md_act{nullptr, 0, true}, md_sync{nullptr, 0, true};
 };
 
 int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
@@ -150,6 +172,7 @@ void free_mat(Mat4 * m) {
     if (m->dev) (void) hipFree(m->dev);
     std::free(m->stage);
     m->am_keys.release();
+    m->am_big.release();
     m->am_cnt.release();
     delete m;
 }
@@ -180,6 +203,14 @@ hipError_t upload(Mat4 * m, int64_t e0, int64_t n, const uint8_t * src, int64_t 
 int env_int(const char * name, int dflt) {
     const char * v = std::getenv(name);
     return v && *v ? std::atoi(v) : dflt;
+}
+
+// poll limit of the kernels' bounded waits (split-K exchange, one-launch MoE decode). ONPU_SPIN_LIMIT
+// overrides it; 0 makes every such wait give up without polling, so that a test can force the
+// timed-out path from the host while every kernel still ends normally.
+uint32_t spin_limit(uint32_t dflt) {
+    const char * v = std::getenv("ONPU_SPIN_LIMIT");
+    return v && *v ? (uint32_t) std::strtoul(v, nullptr, 10) : dflt;
 }
 
 struct Plan {
@@ -323,26 +354,38 @@ bool plan_gsk(int64_t M, int64_t NT, int64_t KB, int cus, int & cfg, int64_t & g
     return true;
 }
 
-// k_qgemm_sk workspace, one per stream (not per matrix): partial tiles, the slot words and the
-// control words. Launches on one stream run in order, so they share it safely; launches on
-// different streams get different workspaces.
+// k_qgemm_sk workspace: partial tiles, the slot words and the control words. Eager launches use
+// their stream's (launches on one stream run in order, so they share it safely; launches on
+// different streams get different workspaces); a launch captured into a graph uses a workspace of
+// its own capture, so graphs captured on one stream (torch.cuda.graph without stream= captures
+// every graph on one side stream) never share one, whatever streams they are replayed on.
 struct GskWs { DBuf part, sync; };
+struct GskKey {
+    hipStream_t s;
+    unsigned long long capture;            // capture id, 0 for eager launches
+    bool operator==(const GskKey & o) const { return s == o.s && capture == o.capture; }
+};
 std::mutex g_gsk_mu;
-std::vector<std::pair<hipStream_t, GskWs *>> g_gsk;      // a few streams: a linear search
+std::vector<std::pair<GskKey, GskWs *>> g_gsk;           // a few streams and graphs: a linear search
 
-// The split-K workspace of stream s, created on the stream's first split-K call at its full size
-// (a partial tile for every CU: a launch cuts at most one tile per workgroup and runs at most one
-// workgroup per CU), so it never moves: a graph that captured a GEMM keeps valid pointers. Its sync
-// words are cleared by a kernel on s (under capture, a node of the graph ahead of the GEMM), so the
-// first call may be captured.
+// The split-K workspace of stream s (or of its capture in progress), created on the first split-K
+// call at its full size (a partial tile for every CU: a launch cuts at most one tile per workgroup
+// and runs at most one workgroup per CU), so it never moves: a graph that captured a GEMM keeps
+// valid pointers. Its sync words are cleared by a kernel on s (under capture, a node of the graph
+// ahead of the GEMM), so the first call may be captured. Each one is 64 MiB, held until the process
+// ends.
 hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** sync, int32_t ** ctl) {
     size_t slot = 0;
     for (const GskCfg & c : GSK_CFGS) slot = std::max(slot, (size_t) c.wv * c.mbg * c.ntw * 1024);
     if (cut > device().cus) return hipErrorInvalidValue;
+    hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    if (const hipError_t e = hipStreamGetCaptureInfo(s, &cst, &cid); e != hipSuccess) return e;
+    const GskKey key{s, cst == hipStreamCaptureStatusActive ? cid : 0ull};
     std::lock_guard<std::mutex> lk(g_gsk_mu);
     GskWs * w = nullptr;
     for (auto & p : g_gsk)
-        if (p.first == s) w = p.second;
+        if (p.first == key) w = p.second;
     if (!w) {
         w = new GskWs;
         const int64_t ints = (int64_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_INTS;
@@ -362,12 +405,30 @@ hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** s
             delete w;
             return e;
         }
-        g_gsk.emplace_back(s, w);
+        g_gsk.emplace_back(key, w);
     }
     *part = w->part.as<float>();
     *sync = w->sync.as<int32_t>();
     *ctl = w->sync.as<int32_t>((size_t) device().cus * GSK_SYNC_STRIDE * 4);
     return hipSuccess;
+}
+
+int32_t * gsk_err_word(GskWs * w) {
+    return w->sync.as<int32_t>(((size_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_ERR) * 4);
+}
+
+// the timed-out-wait flag of stream s's eager workspace, read after the stream has finished: 1 if
+// set (then cleared), 0 if not or if s has none, -1 on a HIP failure
+int gsk_take_flag(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(g_gsk_mu);
+    for (auto & p : g_gsk) {
+        if (!(p.first == GskKey{s, 0ull})) continue;
+        int32_t flag = 0;
+        if (hipMemcpy(&flag, gsk_err_word(p.second), 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+        if (flag && hipMemset(gsk_err_word(p.second), 0, 4) != hipSuccess) return -1;
+        return flag != 0;
+    }
+    return 0;
 }
 
 // the timed-out-wait flags of every split-K workspace: 1 if any was set (then cleared)
@@ -376,7 +437,7 @@ int gsk_status() {
     if (hipDeviceSynchronize() != hipSuccess) return -1;
     int any = 0;
     for (auto & p : g_gsk) {
-        int32_t * f = p.second->sync.as<int32_t>(((size_t) device().cus * GSK_SYNC_STRIDE + GSK_CTL_ERR) * 4);
+        int32_t * f = gsk_err_word(p.second);
         int32_t flag = 0;
         if (hipMemcpy(&flag, f, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
         if (flag && hipMemset(f, 0, 4) != hipSuccess) return -1;
@@ -402,6 +463,12 @@ hipError_t gemv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * 
 // again. Keys: the handle's argmax workspace.
 hipError_t argmax_gemv(Mat4 * m, const uint16_t * x, int64_t M, float * logits, int32_t * argmax, hipStream_t s) {
     const Plan p = plan_gemv(m->fmt, m->g.NT, m->g.KB, (int) M, 1, EPI_ARGMAX_);
+    if (m->am_keys.n == 0) {               // sized once for the largest row count (64) it serves
+        size_t most = 0;
+        for (int r = 1; r <= 64; r++)
+            most = std::max(most, (size_t) r * (size_t) plan_gemv(m->fmt, m->g.NT, m->g.KB, r, 1, EPI_ARGMAX_).gx * 8);
+        if (const hipError_t e = m->am_keys.ensure(most); e != hipSuccess) return e;
+    }
     hipError_t e = m->am_keys.ensure((size_t) (M * p.gx * 8));
     if (e != hipSuccess) return e;
     QArgs a{};
@@ -431,7 +498,7 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         if (e != hipSuccess) return e;
         ga.W = W; ga.NT = m->g.NT; ga.KB = m->g.KB; ga.N = m->N; ga.K = m->K; ga.M = M;
         ga.x = x; ga.ldx = m->K; ga.y = y; ga.ldy = m->N; ga.yf32 = yf32;
-        ga.spin = 1u << 22;
+        ga.spin = spin_limit(1u << 22);
         return launch_qgemm_sk(m->fmt, ga, cfg, (int) grid, s);
     }
     // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
@@ -489,9 +556,9 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
         return hipErrorNotSupported;
     hipError_t e = f->md_act.ensure((size_t) (MD_MAX_T * MD_MAX_K) * (size_t) I * 2);
     if (e != hipSuccess) return e;
-    if (f->md_sync.n == 0) {
+    if (f->md_sync.n == 0) {              // zeroed once by a kernel on s (capturable); calls leave it zero
         if ((e = f->md_sync.ensure(MD_SYNC_INTS * 4)) != hipSuccess) return e;
-        if ((e = hipMemset(f->md_sync.p, 0, MD_SYNC_INTS * 4)) != hipSuccess) return e;
+        if ((e = launch_zero_i32(f->md_sync.as<int32_t>(), MD_SYNC_INTS, s)) != hipSuccess) return e;
     }
     MDArgs a{};
     a.Wg = gu->dev; a.gstride = gu->dstride; a.gNT = gu->g.NT; a.gKB = gu->g.KB;
@@ -501,7 +568,7 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
     a.ids = ids; a.w = w; a.act = f->md_act.as<uint16_t>(); a.y = y; a.yf32 = yf32;
     a.sync = f->md_sync.as<int32_t>();
     a.npairs = T * k * (I / 16); a.nunits = T * dn->g.NT;
-    a.spin = 1u << 20;
+    a.spin = spin_limit(1u << 20);
     return launch_moe_decode(gu->fmt, a, device().cus, s);
 }
 
@@ -514,7 +581,8 @@ hipError_t moe_decode_two(Ffn * f, const uint16_t * x, int64_t T, int k, const i
                           int renorm = 1) {
     Mat4 * gu = f->gu, * dn = f->dn;
     const int64_t I = gu->N / 2, Nd = dn->N, n = T * k;
-    hipError_t e = f->ws[0].ensure((size_t) (n * I * 2));
+    // act rows, sized once for 4 tokens of 16 slots (more only if ONPU_MOE_DECODE_MAX raises T)
+    hipError_t e = f->ws[0].ensure((size_t) (std::max<int64_t>(n, 4 * 16) * I * 2));
     if (e != hipSuccess) return e;
     uint16_t * act = f->ws[0].as<uint16_t>();
     const Plan pg = plan_gemv(gu->fmt, gu->g.NT, gu->g.KB, 1, n, EPI_ACT_);
@@ -604,6 +672,33 @@ hipError_t x_to_dev(DBuf & fbuf, DBuf & bbuf, const float * x, int64_t n, hipStr
     if (e == hipSuccess) e = hipMemcpyAsync(fbuf.p, x, (size_t) n * 4, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = launch_f32_to_bf16(fbuf.as<float>(), n, bbuf.as<uint16_t>(), s);
     return e;
+}
+
+// A bounded wait inside one of the call's kernels gave up (its poll limit ran out), so the call's
+// results are invalid. The reference aborts on a device failure (ONPU_ASSERT throws across
+// extern "C", opennpu_core.hpp:30-32, and run.wait's timeout is one, :429), and so does this library,
+// unless ONPU_WAIT_TIMEOUT=error: then the n floats of y are set to NaN, onpu_last_error says why, and
+// the call returns (onpu_ffn_run / _many then return 0, "not done", whose caller falls back to its
+// unfused path).
+void wait_failed(const char * who, const char * what, float * y, int64_t n) {
+    const std::string msg = std::string(who) + ": " + what + " gave up at its poll limit; the results are invalid";
+    const char * mode = std::getenv("ONPU_WAIT_TIMEOUT");
+    if (!(mode && std::strcmp(mode, "error") == 0)) {
+        std::fprintf(stderr, "libonpu_hip: %s\n", msg.c_str());
+        std::abort();
+    }
+    for (int64_t i = 0; i < n; i++) y[i] = __builtin_nanf("");
+    g_err = msg;
+}
+
+// the one-launch MoE decode kernel's timed-out-wait flag, read after its stream has finished: 1 if
+// set (then cleared), 0 if not or if the FFN never ran that kernel, -1 on a HIP failure
+int md_take_flag(Ffn * f) {
+    if (f->md_sync.n == 0) return 0;
+    int32_t flag = 0;
+    if (hipMemcpy(&flag, f->md_sync.as<int32_t>(MD_SYNC_ERR * 4), 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (flag && hipMemset(f->md_sync.as<int32_t>(MD_SYNC_ERR * 4), 0, 4) != hipSuccess) return -1;
+    return flag != 0;
 }
 
 struct Timer {
@@ -724,6 +819,10 @@ void onpu_dense_mv(void * h, const float * x, int64_t rows, float * y) {
     HIPX(mv_core(m, 0, g_hws[1].as<uint16_t>(), rows, g_hws[2].p, 1, s));
     HIPX(hipMemcpyAsync(y, g_hws[2].p, (size_t) (rows * m->N * 4), hipMemcpyDeviceToHost, s));
     HIPX(hipStreamSynchronize(s));
+    // more than 64 rows run the split-K GEMM, whose partial-tile exchange waits are bounded
+    const int timed_out = rows > 64 ? gsk_take_flag(s) : 0;
+    if (timed_out < 0) die("onpu_dense_mv: reading the split-K wait flag", hipErrorUnknown);
+    if (timed_out) wait_failed("onpu_dense_mv", "a split-K partial-tile wait", y, rows * m->N);
 }
 
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream) {
@@ -735,21 +834,22 @@ int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, 
 int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream) {
     auto * m = (Mat4 *) h;
     if (M <= 0) return 0;
-    // per-workgroup keys and per-row counters of the argmax: workspace of the handle (allocated on
-    // the first call with this many rows; calls that overlap on one handle must not share it)
-    if (m->am_cnt.n < (size_t) M * ARGMAX_PAD) {
-        HIPR(m->am_cnt.ensure((size_t) M * ARGMAX_PAD));
-        HIPR(hipMemset(m->am_cnt.p, 0, m->am_cnt.n));
-    }
-    // up to 64 rows: per-workgroup keys from the GEMV's epilogue (ONPU_ARGMAX_FUSED=0: the argmax
-    // launch over the logits)
+    // The argmax workspace belongs to the handle (calls that overlap on one handle must not share
+    // it). Up to 64 rows: per-workgroup keys from the GEMV's epilogue, sized once for 64 rows.
+    // Otherwise (or with ONPU_ARGMAX_FUSED=0) the argmax launch over the logits, with its keys and
+    // per-row counters (grown to the rows of the call; new counters zeroed by a kernel on the stream,
+    // and each call leaves them zero). Outgrown buffers are kept, so graphs keep valid pointers.
     if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0 && env_int("ONPU_ARGMAX_FUSED", 1)) {
         HIPR(argmax_gemv(m, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;
     }
-    HIPR(m->am_keys.ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
+    if (m->am_cnt.n < (size_t) M * ARGMAX_PAD) {
+        HIPR(m->am_cnt.ensure((size_t) M * ARGMAX_PAD));
+        HIPR(launch_zero_i32(m->am_cnt.as<int32_t>(), (int64_t) (m->am_cnt.n / 4), (hipStream_t) stream));
+    }
+    HIPR(m->am_big.ensure((size_t) (M * argmax_parts(m->N) * ARGMAX_PAD)));
     HIPR(mv_core(m, 0, (const uint16_t *) x, M, logits, 1, (hipStream_t) stream));
-    HIPR(launch_argmax(logits, M, m->N, argmax, m->am_keys.as<uint64_t>(), m->am_cnt.as<uint32_t>(),
+    HIPR(launch_argmax(logits, M, m->N, argmax, m->am_big.as<uint64_t>(), m->am_cnt.as<uint32_t>(),
                        (hipStream_t) stream));
     return 0;
 }
@@ -945,6 +1045,8 @@ void onpu_ffn_free(void * h) {
     free_mat(f->gu);
     free_mat(f->dn);
     for (auto & b : f->ws) b.release();
+    f->md_act.release();
+    f->md_sync.release();
     delete f;
 }
 
@@ -964,6 +1066,13 @@ static int ffn_host(Ffn * f, const float * x, int64_t T, const int32_t * ids, in
     HIPX(ffn_core(f, b[1].as<uint16_t>(), T, b[2].as<int32_t>(), k, b[2].as<float>((size_t) n * 4), b[3].p, 1, s));
     HIPX(hipMemcpyAsync(y, b[3].p, (size_t) (T * Nd * 4), hipMemcpyDeviceToHost, s));
     HIPX(hipStreamSynchronize(s));
+    // the one-launch decode kernel (ONPU_MOE_FUSED=1) waits, bounded, for the act rows
+    const int timed_out = md_take_flag(f);
+    if (timed_out < 0) die("onpu_ffn_run: reading the MoE decode wait flag", hipErrorUnknown);
+    if (timed_out) {
+        wait_failed("onpu_ffn_run", "the one-launch MoE decode's wait for its act rows", y, T * Nd);
+        return 0;
+    }
     return 1;
 }
 

@@ -192,14 +192,15 @@ DEV void decode_scale(const Par<FMT> & p, float (&s)[4]) {
     }
 }
 
-// q4nx (w = s u + m): scale and additive offset per MFMA step with w = s (128 + u) + boff,
-// boff = m - 128 s
+// q4nx (w = s u + m): scale s, min m and nb = -128 s (exact) per MFMA step, for
+// w = s (128 + u) + nb + m
 template <int FMT>
-DEV void decode_par(const Par<FMT> & p, float (&s)[4], float (&bo)[4]) {
+DEV void decode_par(const Par<FMT> & p, float (&s)[4], float (&m)[4], float (&nb)[4]) {
     for (int j = 0; j < 4; j++) {
         const uint32_t pj = p.v[j % (sizeof(p.v) / 4)];
         s[j] = bf16_to_f32((uint16_t) (pj & 0xffff));
-        bo[j] = bf16_to_f32((uint16_t) (pj >> 16)) - 128.0f * s[j];
+        m[j] = bf16_to_f32((uint16_t) (pj >> 16));
+        nb[j] = -128.0f * s[j];
     }
 }
 
@@ -336,16 +337,18 @@ DEV void route_token(const float * __restrict__ l, int E, int k, int renorm, int
 // group sums of x times xsum_mul (shared by all row tiles):
 //   symmetric formats:  cg = x . (128 + u)^T + cs = x . (u - 8)^T,   acc += s_j * cg
 //                       (G128S: the four steps chain into one cg, one scale per block)
-//   q4nx:               cg = x . (128 + u)^T,   acc += s_j * cg + boff_j * cs
+//   q4nx:               cg = x . (128 + u)^T,   acc += (s_j * cg - 128 s_j * cs) + m_j * cs
+//                       (in that order: for one x row of 1 the bracket is u s exactly and the sum
+//                       one rounding of u s + m, the reference's dequantized weight)
 // cs[mb][j] comes from the caller (G128S: cs[mb][0] is over the whole block), in the MFMA C layout:
 // lane (q, r) holds the sums of rows 16 mb + 4 q + v.
 // With one A block (MB = 1) x row m sits in MFMA row perm16(m), so C element v of lane quarter q
 // holds x row 4 v + q: RV (compile time) = the elements that hold rows below M (1 for M <= 4, 2 for
 // M <= 8, else 4), and the accumulate touches those alone. MB > 1 keeps rows in order and all four.
 // rows: the C elements that hold x rows below M (compile time), the only ones accumulated
-DEV void acc4(f32x4 & acc, float s, float bo, const f32x4 & cg, const f32x4 & cs, int rows) {
+DEV void acc4(f32x4 & acc, float s, float m, float nb, const f32x4 & cg, const f32x4 & cs, int rows) {
 #pragma unroll
-    for (int v = 0; v < rows; v++) acc[v] = fmaf(s, cg[v], fmaf(bo, cs[v], acc[v]));
+    for (int v = 0; v < rows; v++) acc[v] = fmaf(m, cs[v], fmaf(s, cg[v], fmaf(nb, cs[v], acc[v])));
 }
 
 DEV void acc1(f32x4 & acc, float s, const f32x4 & cg, int rows) {
@@ -378,13 +381,13 @@ DEV void qacc_block(const bool (&valid)[RT], const u32x4 (&wv)[RT], const Par<FM
     } else if (FMT == ONPU_Q4NX) {
         for (int rt = 0; rt < RT; rt++) {
             if (!valid[rt]) continue;
-            float s[4], bo[4];
-            decode_par<FMT>(par[rt], s, bo);
+            float s[4], m[4], nb[4];
+            decode_par<FMT>(par[rt], s, m, nb);
             for (int j = 0; j < 4; j++) {
                 const u32x4 bw = unpack_biased(wv[rt][j], mag);
                 for (int mb = 0; mb < MB; mb++) {
                     const f32x4 cg = mfma(xa[mb][j], bw, z);
-                    acc4(acc[rt][mb], s[j], bo[j], cg, cs[mb][j], rows);
+                    acc4(acc[rt][mb], s[j], m[j], nb[j], cg, cs[mb][j], rows);
                 }
             }
         }
@@ -665,10 +668,11 @@ struct XStage {
 enum { EPI_STORE = 0, EPI_ACT = 1, EPI_SLOTSUM = 2, EPI_ARGMAX = 3 };
 
 // argmax key of value v at index n: the value's order-preserving bits above the complement of the
-// index, so the larger key is the larger value and, among equal values, the lower index. A NaN key
-// has zero value bits, so NaN never wins and a row of NaNs gives index 0.
+// index, so the larger key is the larger value and, among equal values, the lower index. A NaN gets
+// the top value bits, above +inf: a row holding a NaN gives its first NaN's index, as the reference's
+// numpy / torch argmax over the logits does (npu4/engine.py:358, runtime.py:348).
 DEV uint64_t argmax_key(float v, int64_t n) {
-    return ((uint64_t) (v != v ? 0u : ord_key(v)) << 32) | (uint32_t) (0xffffffffu - (uint32_t) n);
+    return ((uint64_t) (v != v ? 0xffffffffu : ord_key(v)) << 32) | (uint32_t) (0xffffffffu - (uint32_t) n);
 }
 
 DEV uint64_t wave_umax64(uint64_t v) {
@@ -1385,7 +1389,8 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
             if (tid == 0) {
                 __hip_atomic_store(sc + 2 + h, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 uint32_t polls = 0;
-                while (__hip_atomic_load(sc + 3 - h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != s_tag) {
+                // a poll limit of 0 gives up without polling (the host forces a time-out with it)
+                while (a.spin == 0 || __hip_atomic_load(sc + 3 - h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != s_tag) {
                     if (++polls > a.spin) {
                         __hip_atomic_store(a.ctl + GSK_CTL_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;
@@ -1421,7 +1426,7 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
         } else {                                          // second: wait for the partial, add, store
             if (tid == 0) {
                 uint32_t polls = 0;
-                while (__hip_atomic_load(sc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != s_tag) {
+                while (a.spin == 0 || __hip_atomic_load(sc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != s_tag) {
                     if (++polls > a.spin) {
                         __hip_atomic_store(a.ctl + GSK_CTL_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;
@@ -1601,8 +1606,9 @@ __global__ __launch_bounds__(512, 1) void k_moe_gemm(MArgs a) {
 // across the XCDs' L2 caches once complete), waits for its stores to complete and adds its pair
 // count to sync[0]; a workgroup with units waits until sync[0] counts every pair (a wait on workgroups that never wait themselves,
 // bounded by a.spin polls; a timeout raises sync[MD_SYNC_ERR]), reads the act rows with agent-scope
-// loads and finishes its units. The last workgroup with units clears sync[0] and sync[MD_SYNC_DONE]
-// again, so the counters are zero between launches (and a captured graph replays without resets).
+// loads and finishes its units. The last workgroup with units takes the launch's npairs off sync[0]
+// and clears sync[MD_SYNC_DONE], so the counters are zero between launches (and a captured graph
+// replays without resets).
 
 // x rows [T][H] -> LDS xs[T][xl] (bf16, zero past H) and their group sums times xsum_mul,
 // xg[T][KB * GPB], by the whole workgroup: thread u takes 8 elements, a group's threads are
@@ -1783,7 +1789,8 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
     // phase B: wait until every pair is published
     if (threadIdx.x == 0) {
         uint32_t polls = 0;
-        while (__hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (int32_t) a.npairs) {
+        // a poll limit of 0 gives up without polling (the host forces a time-out with it)
+        while (a.spin == 0 || __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (int32_t) a.npairs) {
             if (++polls > a.spin) {
                 __hip_atomic_store(a.sync + MD_SYNC_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
@@ -1830,11 +1837,13 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
         }
         __syncthreads();
     }
-    // the last workgroup with units clears the counters for the next launch
+    // the last workgroup with units returns the counters to zero for the next launch: it takes this
+    // launch's npairs arrivals off sync[0] instead of storing zero, so that an arrival still to come
+    // (after a wait that gave up) cannot leave a count behind: every launch adds npairs in all
     if (threadIdx.x == 0) {
         const int32_t consumers = (int32_t) (a.nunits < G ? a.nunits : G);
         if (__hip_atomic_fetch_add(a.sync + MD_SYNC_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == consumers - 1) {
-            __hip_atomic_store(a.sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.sync, -(int32_t) a.npairs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(a.sync + MD_SYNC_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }

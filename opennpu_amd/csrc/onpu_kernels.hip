@@ -120,8 +120,8 @@ __global__ __launch_bounds__(256) void k_moe_combine(const uint16_t * __restrict
 // first maximum of v[row][0..N) in one launch. Each of a row's gridDim.x workgroups reduces
 // ARGMAX_CHUNK values (a thread issues all of its loads before its first compare) to one key: the
 // value's order-preserving bits above the complement of the index, so the larger key is the larger
-// value and, among equal values, the lower index. A NaN key has zero value bits, so NaN never wins
-// and a row of NaNs gives index 0. The workgroup publishes its key and counts in on the row's
+// value and, among equal values, the lower index. A NaN key has the top value bits, so a row with a
+// NaN gives its first NaN's index (numpy's and torch's argmax rule). The workgroup publishes its key and counts in on the row's
 // counter; the one that arrives last reduces the row's keys, writes the index and puts the counter
 // back to zero, so the counters are zero between calls with no clearing step (graph replays too).
 // Keys and counters sit ARGMAX_PAD bytes apart: atomics of different workgroups on one cache line

@@ -241,13 +241,16 @@ void orc_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * i
     }
 }
 
-/* argmax per row, first maximum wins (numpy / torch argmax on the logits,
- * opennpu/native/npu4/engine.py:358, opennpu/native/runtime.py:348) */
+/* argmax per row as numpy / torch argmax over the logits does it (opennpu/native/npu4/engine.py:358,
+ * opennpu/native/runtime.py:348): the first NaN if the row has one, else the first maximum */
 void orc_argmax(const float * v, int64_t rows, int64_t N, int32_t * out) {
     for (int64_t r = 0; r < rows; r++) {
         const float * x = v + r * N;
         int64_t b = 0;
-        for (int64_t n = 1; n < N; n++) if (x[n] > x[b]) b = n;
+        for (int64_t n = 0; n < N; n++) {
+            if (x[n] != x[n]) { b = n; break; }
+            if (x[n] > x[b]) b = n;
+        }
         out[r] = (int32_t) b;
     }
 }

@@ -202,7 +202,7 @@ def moe_sum(o, ids, w, bias=None):
 
 
 def argmax(v):
-    """first maximum per row (engine.py:358)."""
+    """numpy argmax per row (engine.py:358): the first NaN if the row has one, else the first maximum."""
     v = np.ascontiguousarray(v, np.float32)
     rows, N = v.shape
     out = np.empty(rows, np.int32)

@@ -161,7 +161,7 @@ def test_quantize_dev_equals_reference_build(gpu, fmt):
     dequantized weights, bit for bit (codes, scales and the sign of -0 all show there)."""
     import torch
     from opennpu_amd.device import QMatrix
-    from quantref import KINDS, groups, staging_source
+    from tests.quantref import KINDS, groups, staging_source
     stage, label = staging_source()
     for kind in KINDS:
         X = groups(kind, 1 << 17, 500 + KINDS.index(kind))

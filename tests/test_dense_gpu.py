@@ -395,6 +395,81 @@ def test_argmax_fused_equals_separate(gpu, fmt, N, K, M, monkeypatch):
     assert np.array_equal(idx[:M - 1], orc.argmax(lg[:M - 1])), "argmax of the returned logits"
 
 
+def _plant_nan_scale(fmt, st, N, K, row):
+    """the first scale (Q4_0: the fp16 d of the first block) of weight row `row` set to NaN, so
+    that every row's logit `row` is NaN"""
+    st = st.copy()
+    if fmt == orc.FMT_Q4_0:
+        st[row * (K // 32 * 18):][:2] = np.frombuffer(np.uint16(0x7e00).tobytes(), np.uint8)
+    else:
+        off = N * K // 2 + row * (K // orc.group(fmt)) * 2
+        st[off:off + 2] = np.frombuffer(np.uint16(0x7fc0).tobytes(), np.uint8)
+    return st
+
+
+@pytest.mark.parametrize("fmt,N,K,M", [(orc.FMT_Q4_0, 151936, 4096, 5), (orc.FMT_G128S, 4100, 2048, 17),
+                                       (orc.FMT_Q4NX, 2000, 512, 70)])
+def test_argmax_first_nan_wins(gpu, fmt, N, K, M, monkeypatch):
+    """numpy's and torch's argmax, which the reference takes over the logits (npu4/engine.py:358,
+    runtime.py:348), return the first NaN of a row that holds one. Rows with NaN logits at two
+    columns (NaN scales planted in weight rows N/3 and N/5) give N/5, by the fused keys (<= 64
+    rows) and by the argmax launch over the logits (ONPU_ARGMAX_FUSED=0, and 70 rows) alike; the
+    oracle agrees with numpy."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    st = syn.weights(fmt, N, K, 43)
+    for row in (N // 5, N // 3):
+        st = _plant_nan_scale(fmt, st, N, K, row)
+    xb = syn.activations(M, K, 44)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        x = to_torch_bf16(xb).reshape(M, K)
+        outs = []
+        for fused in ("1", "0"):
+            monkeypatch.setenv("ONPU_ARGMAX_FUSED", fused)
+            lg, idx = q.argmax(x)
+            torch.cuda.synchronize()
+            outs.append((from_torch(lg), idx.cpu().numpy()))
+    finally:
+        q.free()
+    for lg, idx in outs:
+        assert np.isnan(lg[:, N // 5]).all() and np.isnan(lg[:, N // 3]).all()
+        assert (idx == N // 5).all(), idx
+        assert np.array_equal(idx, np.argmax(lg, axis=1)) and np.array_equal(idx, orc.argmax(lg))
+
+
+def test_argmax_workspace_survives_growth_under_a_graph(gpu):
+    """A graph captured at M = 1 keeps the argmax workspace pointers of that capture. Eager calls at
+    larger M (the fused keys up to 64 rows, and 70 rows through the argmax launch over the logits)
+    must not free or move what the graph holds: replays after them give the eager results, bit for
+    bit."""
+    import torch
+    from opennpu_amd.device import QMatrix
+    fmt, N, K = orc.FMT_Q4_0, 30000, 1024
+    st = syn.weights(fmt, N, K, 45)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        x1 = to_torch_bf16(syn.activations(1, K, 46)).reshape(1, K)
+        lg_e, i_e = q.argmax(x1)
+        lgg = torch.empty_like(lg_e)
+        ig = torch.empty_like(i_e)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            q.argmax(x1, lgg, ig)
+        for M in (5, 64, 70, 3):
+            xm = to_torch_bf16(syn.activations(M, K, 47 + M)).reshape(M, K)
+            lg, idx = q.argmax(xm)
+            ig.fill_(-1)
+            lgg.fill_(0)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(ig, i_e) and torch.equal(lgg.view(torch.int32), lg_e.view(torch.int32)), M
+            assert np.array_equal(idx.cpu().numpy(), orc.argmax(from_torch(lg))), M
+    finally:
+        q.free()
+
+
 def test_rows_zero_and_reuse(gpu):
     """M = 0 is a no-op; one handle serves several calls with different M."""
     import torch

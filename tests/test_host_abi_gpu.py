@@ -264,3 +264,65 @@ def test_moe_act_and_sum(L):
         y = np.full((T, N), np.nan, np.float32)
         L.onpu_moe_sum(ha.fp(o), T, k, N, ha.ip(sids), ha.fp(w), ha.fp(b), ha.fp(y))
         assert np.allclose(y, orc.moe_sum(o, sids, w, b), rtol=1e-5, atol=1e-5)
+
+
+def test_dense_mv_reports_a_timed_out_wait(L, monkeypatch):
+    """More than 64 rows run the split-K GEMM, whose partial-tile exchange waits are bounded. A wait
+    that gives up leaves Y invalid, and onpu_dense_mv must say so rather than return stale rows (the
+    reference aborts on a device failure: ONPU_ASSERT, opennpu_core.hpp:30-32). The time-out is
+    forced from the host: ONPU_SPIN_LIMIT=0 makes every bounded wait give up without polling, and
+    every kernel still ends normally. With ONPU_WAIT_TIMEOUT=error the call returns y all NaN and
+    onpu_last_error names the wait (the default is the reference's abort). The next call, at the
+    default limit, is right again: the workspace's flags and tags survive the forced time-out."""
+    rng = np.random.default_rng(77)
+    N, K, M = 16384, 1024, 512        # 2 x 64 tiles of 256 x 256 on 256 CUs: every tile cut in half
+    W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    h = ha.dense(L, W, 1)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    try:
+        monkeypatch.setenv("ONPU_SPIN_LIMIT", "0")
+        monkeypatch.setenv("ONPU_WAIT_TIMEOUT", "error")
+        y = ha.dense_mv(L, h, x, N)
+        assert np.isnan(y).all(), "a timed-out split-K wait returned numbers"
+        assert b"split-K partial-tile wait gave up" in L.onpu_last_error()
+        monkeypatch.delenv("ONPU_SPIN_LIMIT")
+        y = ha.dense_mv(L, h, x, N)
+        r = ref_mm(x[::16], qdq(W, 1))
+        assert rel(y[::16], r) <= 1e-2, "the call after the forced time-out"
+    finally:
+        L.onpu_dense_free(h)
+
+
+def test_ffn_run_reports_a_timed_out_wait(L, monkeypatch):
+    """The one-launch MoE decode (ONPU_MOE_FUSED=1) waits, bounded, for the act rows the other
+    workgroups publish. Forced to give up (ONPU_SPIN_LIMIT=0), onpu_ffn_run returns 0, "not done",
+    which sends the reference's caller to its bank path, with y NaN and the reason in
+    onpu_last_error (ONPU_WAIT_TIMEOUT=error). The next call is right: the kernel's counters come
+    back to zero even when its consumers gave up before every producer arrived."""
+    rng = np.random.default_rng(78)
+    E, H, I, k = 8, 256, 128, 8
+    gu, dn = _experts(rng, E, H, I)
+    f = L.onpu_ffn_new(2 * I, H, H, I, E, 1)
+    assert f and L.onpu_ffn_fused(f) == 1
+    try:
+        ha.bank(L, gu, 1, 1, h=L.onpu_ffn_gu(f))
+        ha.bank(L, dn, 1, 1, h=L.onpu_ffn_dn(f))
+        x = rng.standard_normal((1, H)).astype(np.float32)
+        ids, w = _routes(rng, 1, E, k)
+        r = _layer_ref(x, gu, dn, ids, w, 0)
+        monkeypatch.setenv("ONPU_MOE_FUSED", "1")
+        monkeypatch.setenv("ONPU_WAIT_TIMEOUT", "error")
+        for limit in ("0", None, "0", None):
+            if limit is None:
+                monkeypatch.delenv("ONPU_SPIN_LIMIT", raising=False)
+            else:
+                monkeypatch.setenv("ONPU_SPIN_LIMIT", limit)
+            y = np.full((1, H), 7.0, np.float32)
+            done = L.onpu_ffn_run(f, ha.fp(x), ha.ip(ids), k, ha.fp(w), ha.fp(y))
+            if limit is None:
+                assert done == 1 and rel(y, r) <= 1e-2, "the call after a forced time-out"
+            else:
+                assert done == 0 and np.isnan(y).all(), "a timed-out MoE decode wait"
+                assert b"MoE decode's wait for its act rows gave up" in L.onpu_last_error()
+    finally:
+        L.onpu_ffn_free(f)

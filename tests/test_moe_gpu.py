@@ -298,3 +298,37 @@ def test_moe_decode_one_launch(gpu, fmt, E, H, I, k, T, monkeypatch):
     assert np.array_equal(ids, rid)
     np.testing.assert_allclose(w, rw, rtol=2e-6, atol=1e-7)
     check_moe(y, fmt, gu, dn, E, H, I, xb, rid, rw, grouped=False, what=f"one-launch moe fmt {fmt} E {E} T {T}")
+
+
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_moe_decode_workspace_survives_growth_under_a_graph(gpu, fused, monkeypatch):
+    """A graph captured around a T = 1 decode keeps the FFN workspace pointers of that capture;
+    eager calls at T = 4 and at a prompt's T = 40 (grouped path: permutation, items, act rows) must
+    not free or move what the graph holds. Replays after them give the eager T = 1 bits, for the
+    two-launch decode and the one-launch kernel (ONPU_MOE_FUSED=1)."""
+    import torch
+    monkeypatch.setenv("ONPU_MOE_FUSED", fused)
+    E, H, I, k = 16, 512, 256, 8
+    fmt = orc.FMT_G128S
+    gu, dn = _experts(fmt, E, H, I, 900)
+    f = _ffn(fmt, E, H, I, gu, dn)
+    try:
+        x1 = to_torch_bf16(syn.activations(1, H, 901)).reshape(1, H)
+        lg1 = torch.from_numpy(syn.logits(1, E, 902)).cuda()
+        y1, i1, w1 = f.decode(lg1, x1, k)
+        yg, ig, wg = torch.empty_like(y1), torch.empty_like(i1), torch.empty_like(w1)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            f.decode(lg1, x1, k, out=yg, ids=ig, w=wg)
+        for T in (4, 40, 2):
+            xT = to_torch_bf16(syn.activations(T, H, 903 + T)).reshape(T, H)
+            lgT = torch.from_numpy(syn.logits(T, E, 904 + T)).cuda()
+            f.decode(lgT, xT, k)
+            yg.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(yg, y1) and torch.equal(ig, i1) and torch.equal(wg, w1), T
+        assert f.status() == 0
+    finally:
+        f.free()

@@ -693,3 +693,23 @@ def test_cpu_baseline_kernel_against_the_oracle(fmt, isa):
         y, used = orc.cpu_mv(fmt, st, N, K, orc.bf2f(xb).reshape(M, K), threads=2, isa_max=isa)
         assert used <= isa
         assert orc.max_rel_err(y, orc.qmm(fmt, st, N, K, xb)) <= 1e-5, (fmt, isa, M)
+
+
+def test_argmax_nan_rows_like_numpy():
+    """orc_argmax follows numpy's argmax, which the reference calls on the logits
+    (npu4/engine.py:358): the first NaN of a row that has one, else the first maximum; ties and
+    infinities included"""
+    rng = np.random.default_rng(12)
+    v = rng.standard_normal((64, 300)).astype(np.float32)
+    v[1, 17] = v[1, 200] = np.nan
+    v[2, :] = np.nan
+    v[3, 299] = np.nan
+    v[4, 5] = v[4, 9] = np.inf
+    v[5, 0] = np.nan
+    v[6, 40] = v[6, 41] = 10.0
+    v[7, 3] = -np.inf
+    v[7, 250] = np.nan
+    v[8:20, rng.integers(0, 300, 12)] = np.nan
+    got = orc.argmax(v)
+    assert np.array_equal(got, np.argmax(v, axis=1))
+    assert list(got[1:8]) == [17, 0, 299, 5, 0, 40, 250]

@@ -27,7 +27,7 @@ import pytest
 
 import oracle.oracle as orc
 from opennpu_amd import _lib
-from quantref import GPR, KINDS, G_PER_KIND, SEEDS, REFCORE, REF, groups, load, p, ref_asym, ref_staging, ref_sym
+from tests.quantref import GPR, KINDS, G_PER_KIND, SEEDS, REFCORE, REF, groups, load, p, ref_asym, ref_staging, ref_sym
 
 
 @pytest.fixture(scope="module")
