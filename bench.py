@@ -49,6 +49,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def unit_gain_sigma(K):
+    """scale sigma for which a g128s GEMV over K has a gain of ~1: sqrt(K * 21.5) * sigma = 1, with
+    21.5 the mean of (u - 8)^2 over uniform codes"""
+    return 1.0 / np.sqrt(21.5 * K)
+
+
 def wbytes(fmt, N, K):
     """algorithmic weight bytes: int4 codes + scales"""
     if fmt == Q4_0:
@@ -120,13 +126,17 @@ def decode_layers(torch, QMatrix, QChain, syn, Ms, steps, warmup):
     first 4096 values of qkv (standing in for the attention output), gate+up reads o, down reads the
     first 12288 values of gate+up (standing in for SiLU(gate) * up). It runs as per-launch kernels in
     one HIP graph and as one chained launch (entries wait for the outputs they read) in a graph; the
-    faster is the headline. The synthetic weights have a gain of ~6 per GEMV and the step has no
-    normalisation, so values overflow to inf / NaN after ~10 layers; bit patterns do not change the
-    kernels' timing, and the two paths are compared on layer 0. At M = 4, 8 the GEMVs read fixed
-    inputs (per-launch graph only)."""
+    faster is the headline. The step has no normalisation, so the synthetic scales are drawn as
+    config 0's |N(0, sigma)| + 1e-4 with sigma = 1 / sqrt(21.5 K) instead of 0.02 and a random sign:
+    uniform codes give u - 8 a mean of -1/2, which positive scales turn into a common component that
+    grows ~7x per GEMV; with signed scales the weights have mean zero, 21.5 is the mean of (u - 8)^2,
+    and each output keeps its input's RMS, so all 144 outputs stay finite (signs and magnitudes do
+    not change the bytes or the kernels). Every output of the chained launch is compared with the
+    per-launch graph's, starting from cleared outputs. At M = 4, 8 the GEMVs read fixed inputs
+    (per-launch graph only)."""
     mats = {}
     for name, N, K in QWEN3_8B:
-        st = syn.weights(G128S, N, K, 100 + N + K)
+        st = syn.weights(G128S, N, K, 100 + N + K, scale_sigma=unit_gain_sigma(K), signed=True)
         mats[name] = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
         del st
     res = {}
@@ -162,22 +172,24 @@ def decode_layers(torch, QMatrix, QChain, syn, Ms, steps, warmup):
                         mats[name][layer].mv(xs[K], out=ys[name])
 
         g = GraphStep(step, torch)
-        # the graph's outputs equal eager launches' (bit patterns: values may be inf / NaN)
+        # the graph's outputs, from cleared outputs, equal eager launches' bit for bit, and are finite
+        outs = [ys[name][layer] for name, layer in order] if M == 1 else list(ys.values())
+        for y in outs:
+            y.zero_()
         g()
         torch.cuda.synchronize()
-        last = ys["gate_up"][LAYERS - 1] if M == 1 else ys["gate_up"]
-        y_graph = last.clone()
+        y_graph = [y.clone() for y in outs]
+        assert all(bool(torch.isfinite(y.float()).all()) for y in y_graph), "a decode output is not finite"
         step()
         torch.cuda.synchronize()
-        assert torch.equal(y_graph.view(torch.int16), last.view(torch.int16)), "graph replay differs from eager launches"
+        assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(y_graph, outs)), \
+            "graph replay differs from eager launches"
         t = time_it(torch, g, steps, warmup)
         res[M] = {"ms_per_step": t * 1e3, "GBps": byts / t / 1e9, "hbm_frac": byts / t / HBM_PEAK,
                   "bytes_per_step": byts, "tokens_per_s_equiv": M / t, "launch": g.mode}
         if M == 1:
-            layer0 = [ys[name][0].clone() for name, _, _ in QWEN3_8B]
-            ch = QChain([mats[nm][ly] for nm, ly in order], [x_of(nm, ly) for nm, ly in order],
-                        [ys[nm][ly] for nm, ly in order])
-            res[M]["chained"] = chained(torch, ch, ys, layer0, byts, steps, warmup)
+            ch = QChain([mats[nm][ly] for nm, ly in order], [x_of(nm, ly) for nm, ly in order], outs)
+            res[M]["chained"] = chained(torch, ch, outs, y_graph, byts, steps, warmup)
         else:
             res[M]["chained"] = {"skipped": "chained entries link to earlier outputs at M = 1 (this step reads "
                                             "ranges of them)"}
@@ -199,22 +211,29 @@ def decode_layers(torch, QMatrix, QChain, syn, Ms, steps, warmup):
     return res
 
 
-def chained(torch, ch, ys, layer0, byts, steps, warmup):
-    """the decode step's GEMVs as one chained launch (each entry waits for the output it reads)"""
+def chained(torch, ch, outs, ref, byts, steps, warmup):
+    """the decode step's GEMVs as one chained launch (each entry waits for the output it reads).
+    From cleared outputs, every entry's output is compared with the per-launch graph's: the chain
+    splits K differently, so the two differ by fp32 and bf16 rounding, compounding over the 144
+    dependent entries (relative L2 ~1e-2 at the end); an entry that read its input before it was
+    written would read zeros and differ by ~1."""
     gc = GraphStep(ch.run, torch)
+    for y in outs:
+        y.zero_()
     gc()
     torch.cuda.synchronize()
-    # the chain's split of K may differ from the single launches': layer 0 equal to fp32 rounding
-    for (name, _, _), ref in zip(QWEN3_8B, layer0):
-        got = ys[name][0].float()
-        d = (got - ref.float()).abs().max() / ref.float().abs().max()
-        assert d <= 1e-2, f"chained {name} of layer 0 differs from the per-launch result by {d:.3e}"
+    worst = 0.0
+    for i, (got, want) in enumerate(zip(outs, ref)):
+        d = float((got.float() - want.float()).norm() / want.float().norm())
+        assert d <= 0.1, f"chained entry {i} differs from the per-launch result: relative L2 {d:.3e}"
+        worst = max(worst, d)
     tc = time_it(torch, gc, steps, warmup)
     if ch.status() != 0:
         raise RuntimeError("chained decode: a wait for an earlier entry's output timed out")
     ch.free()
     return {"ms_per_step": tc * 1e3, "GBps": byts / tc / 1e9, "hbm_frac": byts / tc / HBM_PEAK,
-            "launch": "one chained launch per step (" + gc.mode + ")"}
+            "launch": "one chained launch per step (" + gc.mode + ")",
+            "max_rel_l2_vs_per_launch": worst}
 
 
 def config0(torch, QMatrix, syn, iters):
@@ -253,37 +272,65 @@ def prefill(torch, QMatrix, syn, iters):
     return out
 
 
-def moe(torch, QFfn, syn, iters):
-    E, H, I, k = 128, 2048, 768, 8
+MOE_COPIES, MOE_ROUNDS = 8, 4
+
+
+def moe_layers(QFfn, syn):
+    """Qwen3-30B-A3B MoE layer (E 128, H 2048, I 768, g128s): MOE_COPIES copies of the 311 MB expert
+    pool in HBM (2.5 GB)"""
+    E, H, I = 128, 2048, 768
     gu = np.concatenate([syn.weights(G128S, 2 * I, H, 300 + e) for e in range(E)])
     dn = np.concatenate([syn.weights(G128S, H, I, 600 + e) for e in range(E)])
-    nl = 4                                                   # 4 layers x 311 MB rotation
     ffns = []
-    for _ in range(nl):
+    for _ in range(MOE_COPIES):
         f = QFfn(E, H, I, G128S)
         f.load(gu, dn)
         ffns.append(f)
+    return ffns
+
+
+def moe_logits(torch, syn, T, E):
+    """router logits N(0, 1), a different draw for every (copy, round): [copy][round] cuda tensors"""
+    return [[torch.from_numpy(syn.logits(T, E, 9 + 1000 * c + r)).cuda() for r in range(MOE_ROUNDS)]
+            for c in range(MOE_COPIES)]
+
+
+def moe(torch, QFfn, syn, iters):
+    """The MoE layer at T = 1 and 512, router included (at T <= 4 the gate+up launch routes). One
+    timed graph runs MOE_ROUNDS rounds over the MOE_COPIES pool copies, each call with its own
+    logits: at T = 1 the 32 calls read 32 x 8 experts = 623 MB of distinct weights (an expert
+    recurs in one copy 8 calls later at most with probability 8/128 per expert), so the 256 MB
+    Infinity Cache does not hold them. Bytes per call: the experts its routing hits."""
+    E, H, I, k = 128, 2048, 768, 8
+    ffns = moe_layers(QFfn, syn)
     per_expert = wbytes(G128S, 2 * I, H) + wbytes(G128S, H, I)
     out = {}
     for T in (1, 512):
-        lg = torch.from_numpy(syn.logits(T, E, 9)).cuda()
+        lgs = moe_logits(torch, syn, T, E)
         x = bf16_tensor(torch, syn.activations(T, H, 10)).reshape(T, H)
         y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
-        ids, w = ffns[0].route(lg, k)
-        hit = len(np.unique(ids.cpu().numpy()))
+        hits = []
+        for c in range(MOE_COPIES):
+            for r in range(MOE_ROUNDS):
+                ids, w = ffns[c].route(lgs[c][r], k)
+                hits.append(len(np.unique(ids.cpu().numpy())))
+        ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
+        w = torch.empty((T, k), dtype=torch.float32, device="cuda")
 
-        # router + experts + weighted sum per layer (at T <= 4 the gate+up launch routes)
-        def step(lg=lg, x=x, y=y, ids=ids, w=w):
-            for _ in range(GRAPH_REPS):
-                for f in ffns:
-                    f.decode(lg, x, k, out=y, ids=ids, w=w)
+        def step(lgs=lgs, x=x, y=y, ids=ids, w=w):
+            for r in range(MOE_ROUNDS):
+                for c, f in enumerate(ffns):
+                    f.decode(lgs[c][r], x, k, out=y, ids=ids, w=w)
         g = GraphStep(step, torch)
-        t = time_med(torch, g, iters, 3) / (nl * GRAPH_REPS)
-        byts = hit * per_expert + T * H * 2 * 2 + T * E * 4
+        calls = MOE_COPIES * MOE_ROUNDS
+        t = time_med(torch, g, iters, 3) / calls
+        byts = float(np.mean(hits)) * per_expert + T * H * 2 * 2 + T * E * 4
         fl = 2.0 * T * k * (2 * I * H + H * I)
         out[f"M{T}"] = {"us_per_layer": t * 1e6, "GBps": byts / t / 1e9, "hbm_frac": byts / t / HBM_PEAK,
-                        "TFLOPS": fl / t / 1e12, "mfma_frac": fl / t / BF16_PEAK, "experts_hit": hit,
-                        "tokens_per_s": T / t}
+                        "TFLOPS": fl / t / 1e12, "mfma_frac": fl / t / BF16_PEAK, "experts_hit": float(np.mean(hits)),
+                        "tokens_per_s": T / t,
+                        "rotation": f"{MOE_COPIES} pool copies x {MOE_ROUNDS} routings per graph, "
+                                    f"{sum(hits) * per_expert / 1e6:.0f} MB of expert weights read per graph"}
     for f in ffns:
         f.free()
     return out
@@ -593,7 +640,7 @@ def cpu_baseline(syn):
     # config 1: one Qwen3-8B layer (the four matrices) at M = 1, 4, 8
     lay = []
     for name, N, K in QWEN3_8B:
-        st = syn.weights(G128S, N, K, 100 + N + K)
+        st = syn.weights(G128S, N, K, 100 + N + K, scale_sigma=unit_gain_sigma(K), signed=True)
         lay.append((name, N, K, st, torch.from_numpy(cpu_dequant(orc, G128S, st, N, K))))
     dec = {}
     for M in (1, 4, 8):
@@ -714,7 +761,7 @@ def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3):
                 q.free()
             continue
         N, K = shapes[name]
-        st = syn.weights(G128S, N, K, 100 + N + K)
+        st = syn.weights(G128S, N, K, 100 + N + K, scale_sigma=unit_gain_sigma(K), signed=True)
         mats = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
         x = bf16_tensor(torch, syn.activations(1, K, K + 1)).reshape(1, K)
         y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
@@ -748,25 +795,28 @@ def profile_gemm(torch, QMatrix, syn, reps=3):
 
 def profile_moe(torch, QFfn, syn, reps=3):
     """The Qwen3-30B-A3B MoE layer alone (E 128, H 2048, I 768, top-8, g128s) at T = 512 and T = 1,
-    `reps` calls each (router, permutation, grouped GEMMs, combine / the routing gate+up and down
-    GEMVs), then one plain
-    512 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE, for hardware-counter and trace runs."""
+    each over the MOE_COPIES pool copies with MOE_ROUNDS different routings (as the bench's MoE
+    leg: the T = 1 calls read 623 MB of distinct expert weights, past the Infinity Cache), `reps`
+    times (router, permutation, grouped GEMMs, combine / the routing gate+up and down GEMVs), then
+    one plain 512 MiB device copy that calibrates FETCH_SIZE / WRITE_SIZE, for hardware-counter and
+    trace runs."""
     E, H, I, k = 128, 2048, 768, 8
-    gu = np.concatenate([syn.weights(G128S, 2 * I, H, 300 + e) for e in range(E)])
-    dn = np.concatenate([syn.weights(G128S, H, I, 600 + e) for e in range(E)])
-    f = QFfn(E, H, I, G128S)
-    f.load(gu, dn)
+    ffns = moe_layers(QFfn, syn)
     for T in (512, 1):
-        lg = torch.from_numpy(syn.logits(T, E, 9)).cuda()
+        lgs = moe_logits(torch, syn, T, E)
         x = bf16_tensor(torch, syn.activations(T, H, 10)).reshape(T, H)
         y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
         for _ in range(reps):
-            f.decode(lg, x, k, out=y)
+            for r in range(MOE_ROUNDS):
+                for c, f in enumerate(ffns):
+                    f.decode(lgs[c][r], x, k, out=y)
         torch.cuda.synchronize()
-    f.free()
+    for f in ffns:
+        f.free()
     calibration_copy(torch)
     per_expert = wbytes(G128S, 2 * I, H) + wbytes(G128S, H, I)
-    print(json.dumps({"profile_target": "Qwen3-30B-A3B MoE layer, T = 512 then T = 1", "calls_each": reps,
+    print(json.dumps({"profile_target": "Qwen3-30B-A3B MoE layer, T = 512 then T = 1",
+                      "calls_each": reps * MOE_COPIES * MOE_ROUNDS,
                       "gate_up_bytes_per_expert": wbytes(G128S, 2 * I, H), "down_bytes_per_expert": wbytes(G128S, H, I),
                       "algorithmic_bytes_T512_all_experts": E * per_expert}), flush=True)
 

@@ -29,8 +29,10 @@ def stage_bytes(fmt, N, K):
     return N * K // 2 + N * (K // g) * 2 * (2 if fmt == FMT_Q4NX else 1)
 
 
-def weights(fmt, N, K, seed, scale_sigma=None):
-    """One [N][K] matrix in the staging layout (uint8 array of stage_bytes(fmt, N, K))."""
+def weights(fmt, N, K, seed, scale_sigma=None, signed=False):
+    """One [N][K] matrix in the staging layout (uint8 array of stage_bytes(fmt, N, K)). signed: each
+    bf16 scale (and q4nx min) gets a random sign, so that the weights have mean zero (uniform codes
+    alone give u - 8 a mean of -1/2)."""
     rng = np.random.default_rng(seed)
     codes = rng.integers(0, 256, size=N * K // 2, dtype=np.uint8)
     if fmt == FMT_Q4_0:
@@ -44,6 +46,8 @@ def weights(fmt, N, K, seed, scale_sigma=None):
     g = 128 if fmt == FMT_G128S else 32
     sig = 0.02 if scale_sigma is None else scale_sigma
     s = bf16_bits(np.abs(rng.normal(0.0, sig, size=N * (K // g))) + 1e-4)
+    if signed:
+        s |= (rng.integers(0, 2, size=s.size, dtype=np.uint16) << 15).astype(np.uint16)
     parts = [codes, s.view(np.uint8)]
     if fmt == FMT_Q4NX:
         m = bf16_bits(rng.normal(0.0, sig * 4, size=N * (K // g)))
