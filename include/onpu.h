@@ -59,6 +59,9 @@ uint8_t * onpu_dense_buf(void * h);
 int64_t onpu_dense_bytes(void * h);
 void onpu_dense_sync(void * h);
 void onpu_dense_free(void * h);
+/* rows > 64 run the split-K GEMM, whose bounded waits are checked after the call's synchronisation:
+ * one that gave up aborts with the reason (the reference's ONPU_ASSERT, opennpu_core.hpp:30-32), or
+ * with ONPU_WAIT_TIMEOUT=error sets y to NaN and onpu_last_error */
 void onpu_dense_mv(void * h, const float * x, int64_t rows, float * y);
 
 /* ---- expert banks: E experts of [N][K], expert e's staging at e * onpu_bank_expert_bytes
@@ -89,6 +92,9 @@ void * onpu_ffn_gu(void * h);
 void * onpu_ffn_dn(void * h);
 int onpu_ffn_fused(void * h);
 void onpu_ffn_perm(void * h, int32_t * out /* [Ng] */);
+/* 1 done, 0 not done (the FFN shape cannot be fused, or, with ONPU_WAIT_TIMEOUT=error, the opt-in
+ * one-launch decode's bounded wait gave up: y is then NaN and onpu_last_error says why; without that
+ * setting such a wait aborts, as the reference does on a device failure) */
 int onpu_ffn_run(void * h, const float * x, const int32_t * ids, int k, const float * w, float * y);
 int onpu_ffn_run_many(void * h, const float * x, int64_t T, const int32_t * ids, int k, const float * w, float * y);
 void onpu_ffn_free(void * h);
@@ -123,15 +129,14 @@ int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
  * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels, larger M the MFMA GEMM. */
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
 /* Workspace of the calls above. M > 64 runs the split-K prefill GEMM, whose partial tiles and slot
- * words belong to the stream (one workspace per stream, whatever the handle, about 64 MiB, kept
- * until the process ends): calls ordered on one stream share it; calls on different streams use
- * different ones. Its first use on a stream allocates it with hipMalloc and clears its slot words
- * with a kernel on that stream, both legal under HIP graph capture, so a first GEMM may be captured
- * (the clearing kernel becomes a node of the graph). A graph's GEMMs use the capturing stream's
- * workspace: replay a graph while no other GEMM on that stream runs. The argmax allocates its keys
- * and clears its counters on a handle's first call with that many rows: make that call outside
- * capture (or use onpu_dense_argmax_dev_noalloc). Argmax calls on one handle share its keys: order
- * them on one stream. */
+ * words live in a workspace of about 64 MiB (kept until the process ends): one per stream for eager
+ * calls, one per capture for calls captured into a HIP graph. Its first use allocates it (relaxed
+ * capture mode) and clears its slot words with a kernel, both legal under capture, so a first GEMM
+ * may be captured (the clearing kernel becomes a node of the graph). The argmax keeps its keys per
+ * handle (sized once for 64 rows); beyond 64 rows its counters grow with the rows and are cleared by
+ * a kernel. Outgrown workspace buffers are kept until the handle is freed, so a graph captured at a
+ * small M keeps valid pointers. Argmax calls on one handle share its keys: order them on one
+ * stream. */
 /* 1 if a split-K GEMM gave up waiting for its partner workgroup since the last call (the flag is then
  * cleared and that launch's Y is invalid), 0 if not, -1 on error; synchronises the device */
 int onpu_gemm_status(void);

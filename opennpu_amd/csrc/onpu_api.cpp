@@ -130,6 +130,10 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     DBuf am_keys{nullptr, 0, true};        // per-workgroup keys of the GEMV epilogue (<= 64 rows)
     DBuf am_big{nullptr, 0, true};         // keys of the argmax launch over the logits
     DBuf am_cnt{nullptr, 0, true};         // its row counters (zeroed once; each call leaves them zero)
+    // the step-major copy of every expert (the down bank of a fused FFN; k_moe_dsplit reads it),
+    // dec_stride bytes per expert, kept equal to the tiled weights by every write of them
+    uint8_t * dec = nullptr;
+    int64_t dec_stride = 0;
 };
 
 struct Ffn {
@@ -140,6 +144,7 @@ struct Ffn {
     DBuf ws[7] = {{nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true},
                   {nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true}};
     DBuf md_act{nullptr, 0, true}, md_sync{nullptr, 0, true};
+    DBuf ds_part{nullptr, 0, true};        // k_moe_dsplit partial sums, sized once for its largest call
 };
 
 int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
@@ -170,6 +175,7 @@ Mat4 * make_mat(int64_t N, int64_t K, int64_t E, int fmt, int64_t sstride) {
 void free_mat(Mat4 * m) {
     if (!m) return;
     if (m->dev) (void) hipFree(m->dev);
+    if (m->dec) (void) hipFree(m->dec);
     std::free(m->stage);
     m->am_keys.release();
     m->am_big.release();
@@ -185,6 +191,13 @@ uint8_t * stage_of(Mat4 * m) {
     return m->stage;
 }
 
+// experts [e0, e0 + n) of the step-major copy from the tiled weights (nothing without a copy)
+hipError_t refresh_dec(Mat4 * m, int64_t e0, int64_t n, hipStream_t s) {
+    if (!m->dec || n <= 0) return hipSuccess;
+    return launch_relayout_dec(m->fmt, m->dev + e0 * m->dstride, m->dstride, m->N, m->K, m->dec + e0 * m->dec_stride,
+                               m->dec_stride, n, s);
+}
+
 // experts [e0, e0 + n) from staging bytes (stride src_stride per expert) -> HBM tiled layout
 hipError_t upload(Mat4 * m, int64_t e0, int64_t n, const uint8_t * src, int64_t src_stride, hipStream_t s) {
     void * tmp = nullptr;
@@ -194,6 +207,7 @@ hipError_t upload(Mat4 * m, int64_t e0, int64_t n, const uint8_t * src, int64_t 
     if (e == hipSuccess)
         e = launch_repack(m->fmt, (const uint8_t *) tmp, src_stride, m->N, m->K, m->dev + e0 * m->dstride, m->dstride,
                           n, s);
+    if (e == hipSuccess) e = refresh_dec(m, e0, n, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     (void) hipFree(tmp);
     return e;
@@ -572,6 +586,29 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
     return launch_moe_decode(gu->fmt, a, device().cus, s);
 }
 
+// MoE decode split along I (k_moe_dsplit + k_moe_dsum): route from logits (non-null; ids / w are then
+// written) or take ids / w. hipErrorNotSupported when the FFN has no step-major down copy, the shapes
+// are outside the kernel's, or T is above ONPU_MOE_DSPLIT_MAX_T (default 1: at Qwen3-30B-A3B shapes on
+// MI355X the split path takes 16.2 us per layer at T = 1 against 18.5 us for the two launches, but
+// 27.7 / 42.1 us at T = 2 / 4 against 22.2 / 36.1); the caller then takes the two-launch path.
+hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, int64_t T, int k, int renorm, int E,
+                           int32_t * ids, float * w, void * y, int yf32, hipStream_t s) {
+    Mat4 * gu = f->gu, * dn = f->dn;
+    const int64_t I = gu->N / 2, S = I / 32, NTq = (dn->g.NT + 3) / 4;
+    if (T > env_int("ONPU_MOE_DSPLIT_MAX_T", 1) || !dn->dec || gu->fmt != dn->fmt || dn->K != I || !moe_dsplit_fits(gu->K, I, dn->N, gu->g.KB, (int) T, k, E))
+        return hipErrorNotSupported;
+    hipError_t e = f->ds_part.ensure((size_t) (DS_MAX_T * DS_MAX_K) * (size_t) (S * NTq * 64) * 4);
+    if (e != hipSuccess) return e;
+    MSArgs a{};
+    a.Wg = gu->dev; a.gstride = gu->dstride; a.gNT = gu->g.NT; a.gKB = gu->g.KB;
+    a.Wd = dn->dec; a.dstride = dn->dec_stride; a.dNTq = NTq;
+    a.H = gu->K; a.I = I; a.S = S;
+    a.x = x; a.logits = logits; a.E = E; a.k = k; a.renorm = renorm; a.T = (int) T;
+    a.ids = ids; a.w = w; a.part = f->ds_part.as<float>();
+    if ((e = launch_moe_dsplit(gu->fmt, a, dn->N, s)) != hipSuccess) return e;
+    return launch_moe_dsum(a.part, S, NTq * 64, w, T, k, dn->N, y, yf32, s);
+}
+
 // MoE decode (T <= 4 tokens) in two launches: gate_up with SiLU(gate) * up per slot, then down with
 // the routing-weighted slot sum per token. act: bf16 [T k][I] in the FFN's workspace. With logits
 // (E <= 256 experts, k <= 16), the gate_up launch also routes: each of its workgroups picks its slot's
@@ -623,6 +660,9 @@ hipError_t ffn_core(Ffn * f, const uint16_t * x, int64_t T, const int32_t * ids,
     if (T <= decode_max && k <= 16) {
         e = moe_decode_core(f, nullptr, x, T, k, 1, (int) gu->E, const_cast<int32_t *>(ids),
                             const_cast<float *>(w), y, yf32, s);
+        if (e != hipErrorNotSupported) return e;
+        e = moe_dsplit_core(f, nullptr, x, T, k, 1, (int) gu->E, const_cast<int32_t *>(ids), const_cast<float *>(w),
+                            y, yf32, s);
         if (e != hipErrorNotSupported) return e;
         return moe_decode_two(f, x, T, k, ids, w, y, yf32, s);
     }
@@ -1021,6 +1061,15 @@ static void * ffn_make(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E
     f->dn = dn;
     // the fused kernels pair gate row tile t with up row tile t + I/16
     f->fused = Ng % 32 == 0 && Kd == Ng / 2;
+    // decode split along I (k_moe_dsplit) reads the down bank in a step-major copy: one more
+    // down-bank-sized allocation, filled with the weights (ONPU_MOE_DSPLIT=0: no copy, two launches)
+    if (f->fused && Kd % 32 == 0 && env_int("ONPU_MOE_DSPLIT", 1)) {
+        dn->dec_stride = dec_bytes(fmt, Nd, Kd);
+        if (hipMalloc((void **) &dn->dec, (size_t) (dn->dec_stride * E)) != hipSuccess) {
+            dn->dec = nullptr;
+            dn->dec_stride = 0;
+        }
+    }
     return f;
 }
 
@@ -1102,8 +1151,10 @@ int onpu_moe_decode_dev(void * h, const float * logits, const void * x, int64_t 
     auto * f = (Ffn *) h;
     if (!f->fused) { set_err("onpu_moe_decode_dev: this FFN shape has no fused path"); return -1; }
     if (E != f->gu->E) { set_err("onpu_moe_decode_dev: E differs from the bank's expert count"); return -1; }
-    const hipError_t e = moe_decode_core(f, logits, (const uint16_t *) x, T, k, renorm, E, ids, w, y, y_f32,
-                                         (hipStream_t) stream);
+    hipError_t e = moe_decode_core(f, logits, (const uint16_t *) x, T, k, renorm, E, ids, w, y, y_f32,
+                                   (hipStream_t) stream);
+    if (e == hipErrorNotSupported && T <= env_int("ONPU_MOE_DECODE_MAX", 4))
+        e = moe_dsplit_core(f, logits, (const uint16_t *) x, T, k, renorm, E, ids, w, y, y_f32, (hipStream_t) stream);
     if (e != hipErrorNotSupported) {
         HIPR(e);
         return 0;
@@ -1335,6 +1386,7 @@ static int codec_load(Mat4 * m, int64_t e0, int64_t n, hipStream_t s, Fill fill)
         if (e == hipSuccess)
             e = launch_repack(m->fmt, (const uint8_t *) tmp, sb, m->N, m->K, m->dev + (e0 + c) * m->dstride, m->dstride,
                               k, s);
+        if (e == hipSuccess) e = refresh_dec(m, e0 + c, k, s);
     }
     const hipError_t es = hipStreamSynchronize(s);
     (void) hipFree(tmp);

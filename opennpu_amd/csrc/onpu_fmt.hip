@@ -59,6 +59,24 @@ hipError_t FN(moe_decode)(const MDArgs & a, int gb, int grid, size_t lds, hipStr
     return hipGetLastError();
 }
 
+hipError_t FN(moe_dsplit)(const MSArgs & a, int nw, size_t lds, hipStream_t s) {
+    const dim3 grid((unsigned) a.S, (unsigned) (a.T * a.k));
+    const int64_t gb8 = (a.gKB + 1) / 2, dq8 = (a.dNTq + 7) / 8, gb16 = (a.gKB + 3) / 4, dq16 = (a.dNTq + 15) / 16;
+    if (nw == 16 && gb16 <= 4 && dq16 <= 2) k_moe_dsplit<F, 4, 2, 16><<<grid, 1024, lds, s>>>(a);
+    else if (nw == 16 && gb16 <= 8 && dq16 <= 4) k_moe_dsplit<F, 8, 4, 16><<<grid, 1024, lds, s>>>(a);
+    else if (gb8 <= 8 && dq8 <= 4) k_moe_dsplit<F, 8, 4, 8><<<grid, 512, lds, s>>>(a);
+    else if (gb8 <= 16 && dq8 <= 8) k_moe_dsplit<F, 16, 8, 8><<<grid, 512, lds, s>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t FN(relayout_dec)(const uint8_t * src, int64_t sstride, int64_t NT, int64_t KB, uint8_t * dst,
+                            int64_t dstride, int64_t E, hipStream_t s) {
+    const int64_t nsb = 4 * KB * ((NT + 3) / 4);
+    k_relayout_dec<F><<<dim3((unsigned) nsb, (unsigned) E), 64, 0, s>>>(src, sstride, NT, KB, dst, dstride);
+    return hipGetLastError();
+}
+
 hipError_t FN(moe_gemm)(int which, const MArgs & a, dim3 grid, hipStream_t s) {
     const bool kt = a.K % 128 != 0;
     if (which == 0) {

@@ -1849,6 +1849,220 @@ __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ MoE decode split along I
+// The step-major copy (onpu_launch.h dec_sblk): one wave per superblock (s, tq) and expert. Lane l
+// gathers dword j = s % 4 of its 16 bytes in block (4 tq + d, s / 4) for the four tiles d; lanes
+// 0..15 gather row r's parameters of that step for the four tiles.
+template <int FMT>
+__global__ __launch_bounds__(64) void k_relayout_dec(const uint8_t * __restrict__ src, int64_t sstride, int64_t NT,
+                                                     int64_t KB, uint8_t * __restrict__ dst, int64_t dstride) {
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    constexpr int SB = 1024 + (FMT == ONPU_Q4NX ? 256 : 128);
+    const int64_t NTq = (NT + 3) / 4, sb = blockIdx.x, st = sb / NTq, tq = sb - st * NTq, b = st / 4;
+    const int j = (int) (st % 4), l = threadIdx.x, r = l & 15;
+    const uint8_t * e = src + (int64_t) blockIdx.y * sstride;
+    uint8_t * o = dst + (int64_t) blockIdx.y * dstride + sb * SB;
+    u32x4 v;
+    for (int d = 0; d < 4; d++) {
+        const int64_t t = 4 * tq + d;
+        v[d] = t < NT ? *(const uint32_t *) (e + (t * KB + b) * BLK + 16 * l + 4 * j) : 0u;
+    }
+    *(u32x4 *) (o + 16 * l) = v;
+    if (l < 16) {
+        if (FMT == ONPU_Q4NX) {
+            u32x4 p;
+            for (int d = 0; d < 4; d++) {
+                const int64_t t = 4 * tq + d;
+                p[d] = t < NT ? *(const uint32_t *) (e + (t * KB + b) * BLK + 1024 + 16 * r + 4 * j) : 0u;
+            }
+            *(u32x4 *) (o + 1024 + 16 * r) = p;
+        } else {
+            uint16_t p[4];
+            for (int d = 0; d < 4; d++) {
+                const int64_t t = 4 * tq + d;
+                const int64_t off = FMT == ONPU_G128S ? 1024 + 2 * r : 1024 + 8 * r + 2 * j;
+                p[d] = t < NT ? *(const uint16_t *) (e + (t * KB + b) * BLK + off) : (uint16_t) 0;
+            }
+            *(u32x2 *) (o + 1024 + 8 * r) = (u32x2){p[0] | ((uint32_t) p[1] << 16), p[2] | ((uint32_t) p[3] << 16)};
+        }
+    }
+}
+
+// x row [H] -> LDS xs (zero past H up to KB * 128) and its group sums times xsum_mul -> xg, by the
+// threads from `first` on (wave 0 may be routing meanwhile). Units of 8 values; a group's units sit
+// on consecutive lanes of one wave (blockDim - first is a multiple of 64).
+template <int FMT>
+DEV void ds_stage_x(const uint16_t * __restrict__ x, int64_t H, int64_t KB, uint16_t * xs, float * xg, int first) {
+    constexpr int GS = FMT == ONPU_G128S ? 128 : 32, UPG = GS / 8;
+    if ((int) threadIdx.x < first) return;
+    const uint32_t nunits = (uint32_t) KB * 16, nt = blockDim.x - (uint32_t) first, tid = threadIdx.x - first;
+    for (uint32_t u0 = 0; u0 < nunits; u0 += nt) {
+        const uint32_t u = u0 + tid;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (u < nunits && (int64_t) u * 8 < H) v = *(const u32x4 *) (x + (int64_t) u * 8);
+        if (u < nunits) *LDS_U32X4(xs + (int64_t) u * 8) = v;
+        float sum = 0.f;
+        for (int d = 0; d < 4; d++) sum += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
+        for (int o = UPG / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (u < nunits && u % UPG == 0) xg[u / UPG] = sum * xsum_mul<FMT>();
+    }
+}
+
+// One wave's gate / up products over GB blocks from b0 (loaded by md_load), x from LDS. Every block
+// is computed: blocks past nb (re-reads of block b0) get zero parameters, so they add exact zeros
+// (x finite). No use of a loaded value sits behind a branch, so the compiler keeps the loads where
+// md_load issues them, all before the first MFMA, instead of sinking each to its use (one memory
+// round trip per block).
+template <int FMT, int GB>
+DEV void ds_accum(const u32x4 (&wv)[GB][1], const Par<FMT> (&par)[GB][1], int nb, const uint16_t * xr,
+                  const float * xg, int64_t b0, f32x4 (&acc)[1][1]) {
+    const int q = (threadIdx.x & 63) >> 4;
+    constexpr int GPB = FMT == ONPU_G128S ? 1 : 4;
+    const bool valid[1] = {true};
+#pragma unroll
+    for (int i = 0; i < GB; i++) {
+        const bool on = i < nb;
+        const int64_t b = b0 + (on ? i : 0);
+        Par<FMT> p[1];
+        p[0] = par[i][0];
+        if (!on) p[0].v[0] = 0u;
+        if (FMT != ONPU_G128S && !on)
+#pragma unroll
+            for (int d = 1; d < (int) (sizeof(p[0].v) / 4); d++) p[0].v[d] = 0u;
+        u32x4 xa[1][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) xa[0][j] = *LDS_U32X4(xr + b * 128 + 32 * j + 8 * q);
+        f32x4 cs[1][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float v = *(const __attribute__((address_space(3))) float *) (xg + b * GPB + (j < GPB ? j : 0));
+            cs[0][j] = (f32x4){v, v, v, v};
+        }
+        u32x4 w1[1] = {wv[i][0]};
+        qacc_block<FMT, 1, 1, 1>(valid, w1, p, xa, cs, 0x43004300u, acc);
+    }
+}
+
+// grid (S slices, T k slots), NW waves (8 or 16). Wave 0 routes the slot's token (from logits) while
+// the others stage x; then wave w loads its gate/up tile (w / P, P = NW / 4: gate tiles 2 s, 2 s + 1,
+// up tiles NT / 2 + 2 s, + 1) over K part w % P (GB blocks at most) and its down superblocks (quads
+// w, w + NW, ..., DQ at most) of step s, all at once. The gate/up partials meet in LDS, act = bf16(silu(g) u) for the 32
+// values, and each wave multiplies act into its down superblocks: A = act on every MFMA row, C starts
+// at the act sum times xsum_mul, so lanes 0..15 end with row r of each of the four tiles.
+template <int FMT, int GB, int DQ, int NW>
+__global__ __launch_bounds__(NW * 64) void k_moe_dsplit(MSArgs a) {
+    extern __shared__ float dsl[];
+    constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
+    constexpr int SB = 1024 + (FMT == ONPU_Q4NX ? 256 : 128);
+    constexpr int GS = FMT == ONPU_G128S ? 128 : 32, GPB = 128 / GS;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 15,
+              q = lane >> 4;
+    const int64_t s = blockIdx.x, slot = blockIdx.y, t = slot / a.k;
+    const int j = (int) (slot - t * a.k);
+    constexpr int P = NW / 4;                  // K parts of each gate / up tile
+    // LDS: x row and its group sums, the gate/up partials [NW][16], act [32] bf16 and its sum
+    const int64_t xl = a.gKB * 128;
+    uint16_t * xs = (uint16_t *) dsl;
+    float * xg = (float *) (xs + xl);
+    float * red = xg + (a.gKB * GPB + 3) / 4 * 4;
+    uint16_t * act = (uint16_t *) (red + NW * 16);
+    float * acs = (float *) (act + 32);
+    __shared__ int s_e;
+    if (a.logits) {
+        if (wave == 0) {
+            int my_id;
+            float my_w;
+            route_token(a.logits + t * a.E, a.E, a.k, a.renorm, my_id, my_w);
+            if (lane == 0) s_e = __builtin_amdgcn_readlane(my_id, j);
+            if (s == 0 && j == 0 && lane < a.k) {
+                a.ids[t * a.k + lane] = my_id;
+                a.w[t * a.k + lane] = my_w;
+            }
+        }
+        ds_stage_x<FMT>(a.x + t * a.H, a.H, a.gKB, xs, xg, 64);
+    } else {
+        if (threadIdx.x == 0) s_e = a.ids[slot];
+        ds_stage_x<FMT>(a.x + t * a.H, a.H, a.gKB, xs, xg, 0);
+    }
+    __syncthreads();
+    const int64_t e = s_e;
+    // gate / up tile of this wave and its K part
+    const int ti = wave / P, h = wave % P;
+    const int64_t tile = (ti < 2 ? 0 : a.gNT / 2) + 2 * s + (ti & 1);
+    const uint8_t * tb[1] = {a.Wg + e * a.gstride + tile * a.gKB * BLK};
+    const int64_t part = (a.gKB + P - 1) / P, b0 = h * part;
+    const int nb = (int) (a.gKB - b0 < part ? (a.gKB - b0 > 0 ? a.gKB - b0 : 0) : part);
+    u32x4 wv[GB][1];
+    Par<FMT> par[GB][1];
+    md_load<FMT, 1, GB>(tb, nb > 0 ? b0 : 0, nb, wv, par);
+    // down superblocks of step s: quads wave + NW i (a quad past the last re-reads quad 0)
+    const uint8_t * wd = a.Wd + e * a.dstride + s * a.dNTq * SB;
+    u32x4 dv[DQ];
+    uint32_t dp[DQ][FMT == ONPU_Q4NX ? 4 : 2];
+#pragma unroll
+    for (int i = 0; i < DQ; i++) {
+        const int64_t tq = wave + NW * i < a.dNTq ? wave + NW * i : 0;
+        dv[i] = __builtin_nontemporal_load(GLB(const u32x4, wd + tq * SB + 16 * lane));
+        if (FMT == ONPU_Q4NX) {
+            const u32x4 p = __builtin_nontemporal_load(GLB(const u32x4, wd + tq * SB + 1024 + 16 * r));
+#pragma unroll
+            for (int d = 0; d < 4; d++) dp[i][d % (sizeof(dp[i]) / 4)] = p[d];
+        } else {
+            const u32x2 p = __builtin_nontemporal_load(GLB(const u32x2, wd + tq * SB + 1024 + 8 * r));
+            dp[i][0] = p.x;
+            dp[i][1 % (sizeof(dp[i]) / 4)] = p.y;
+        }
+    }
+    // keep the down loads here, in flight during the gate / up products (the scheduler would
+    // otherwise issue them after those, adding a memory round trip)
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[1][1] = {{{0.f, 0.f, 0.f, 0.f}}};
+    ds_accum<FMT, GB>(wv, par, nb, xs, xg, nb > 0 ? b0 : 0, acc);
+    if (q == 0) red[wave * 16 + r] = acc[0][0][0];
+    __syncthreads();
+    if (threadIdx.x < 32) {                     // act of I value 32 s + i: gate / up tile i >> 4, row i & 15
+        const int i = threadIdx.x, tt = i >> 4, rr = i & 15;
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int pp = 0; pp < P; pp++) {       // the K parts in order
+            g += red[(tt * P + pp) * 16 + rr];
+            u += red[((2 + tt) * P + pp) * 16 + rr];
+        }
+        const uint16_t ab = f32_to_bf16(silu_f(g) * u);
+        act[i] = ab;
+        float sum = bf16_to_f32(ab);
+        for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (i == 0) *acs = sum * xsum_mul<FMT>();
+    }
+    __syncthreads();
+    const u32x4 xa = *LDS_U32X4(act + 8 * q);
+    const float cs1 = *acs;
+    const f32x4 csv = {cs1, cs1, cs1, cs1}, z = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t mag = 0x43004300u;
+    float * out = a.part + (slot * a.S + s) * a.dNTq * 64;
+#pragma unroll
+    for (int i = 0; i < DQ; i++) {             // every quad computed (no load's use behind a branch)
+        const int64_t tq = wave + NW * i;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const u32x4 bw = unpack_biased(dv[i][d], mag);
+            float y;
+            if (FMT == ONPU_Q4NX) {
+                // w = u s + m: (s (128 + u) . act - 128 s sum) + m sum, as the decode GEMV adds it
+                const float sc = bf16_to_f32((uint16_t) (dp[i][d % (sizeof(dp[i]) / 4)] & 0xffff));
+                const float mn = bf16_to_f32((uint16_t) (dp[i][d % (sizeof(dp[i]) / 4)] >> 16));
+                const f32x4 cg = mfma(xa, bw, z);
+                y = fmaf(mn, cs1, fmaf(sc, cg[0], fmaf(-128.0f * sc, cs1, 0.f)));
+            } else {
+                const float sc = scale_f32(FMT, (dp[i][d >> 1] >> (16 * (d & 1))) & 0xffff);
+                const f32x4 cg = mfma(xa, bw, csv);
+                y = sc * cg[0];
+            }
+            if (q == 0 && tq < a.dNTq) out[tq * 64 + 16 * d + r] = y;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ chained decode GEMVs
 // One launch runs a.n GEMVs in order (M <= 16 rows, x staged in LDS), one workgroup per CU of
 // CHAIN_WAVES compute waves and CHAIN_CTRL control waves. Entry i's tile groups (tw tiles x kw K

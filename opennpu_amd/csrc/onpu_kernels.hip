@@ -457,6 +457,88 @@ hipError_t launch_moe_decode(int fmt, const MDArgs & a, int grid, hipStream_t s)
     return hipErrorInvalidValue;
 }
 
+// ------------------------------------------------------------------ MoE decode split along I
+bool moe_dsplit_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int T, int k, int E) {
+    const int64_t NTq = ((Nd + 15) / 16 + 3) / 4;
+    return T >= 1 && T <= DS_MAX_T && k >= 1 && k <= DS_MAX_K && k <= E && E <= 256 && I >= 32 && I % 32 == 0 &&
+           H >= 8 && H % 8 == 0 && gKB >= 1 && (gKB + 1) / 2 <= 16 && Nd >= 1 && NTq <= 8 * 8;
+}
+
+hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, hipStream_t s) {
+    if (!moe_dsplit_fits(a.H, a.I, Nd, a.gKB, a.T, a.k, a.E) || a.S != a.I / 32 || a.gNT * 16 != 2 * a.I ||
+        a.dNTq != ((Nd + 15) / 16 + 3) / 4 || !a.part || (a.logits && (!a.ids || !a.w)) || (!a.logits && !a.ids))
+        return hipErrorInvalidValue;
+    // 16 waves where each then holds at most 8 blocks and 4 quads (measured against 8 on MI355X), else 8
+    const char * ev = getenv("ONPU_DS_WAVES");
+    int nw = ev && *ev ? atoi(ev) : 16;
+    if (nw != 8 && ((a.gKB + 3) / 4 > 8 || (a.dNTq + 15) / 16 > 4)) nw = 8;
+    const int GPB = fmt == ONPU_G128S ? 1 : 4;
+    const size_t lds = (size_t) a.gKB * 128 * 2 + (size_t) ((a.gKB * GPB + 3) / 4 * 4) * 4 + (size_t) nw * 16 * 4 +
+                       32 * 2 + 16;
+    switch (fmt) {
+        case 0: return moe_dsplit_f0(a, nw, lds, s);
+        case 1: return moe_dsplit_f1(a, nw, lds, s);
+        case 2: return moe_dsplit_f2(a, nw, lds, s);
+        case 3: return moe_dsplit_f3(a, nw, lds, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+constexpr int DS_SUM_MAX = 32;       // partials per lane in flight at once (I <= 1024 in one round)
+constexpr int DS_SUM_N = 16;         // outputs per workgroup of k_moe_dsum (64 B of each partial row)
+
+// y[t][n] = sum_j w[t][j] (sum_s part[t k + j][s][n]), the sums in that order. grid (ceil(Nd / 16), T),
+// 16 k threads: thread 16 j + c sums slot j's S partials of output 16 blockIdx.x + c (all its loads in
+// flight at once, rounds of DS_SUM_MAX with the index clamped to the last partial), then threads
+// c < 16 weight and add the k slots. Small workgroups spread the partials' reads over the GPU (one CU
+// keeps only so many loads in flight); 16 outputs read 64 B pieces of each partial row (8 outputs
+// fetched twice the bytes they used).
+__global__ __launch_bounds__(DS_SUM_N * DS_MAX_K) void k_moe_dsum(const float * __restrict__ part, int64_t S,
+                                                                        int64_t ld, const float * __restrict__ w, int k,
+                                                                        int64_t Nd, void * y, int yf32) {
+    __shared__ float sp[DS_MAX_K * DS_SUM_N];
+    const int j = threadIdx.x / DS_SUM_N, c = threadIdx.x % DS_SUM_N;
+    const int64_t t = blockIdx.y, n = (int64_t) blockIdx.x * DS_SUM_N + c;
+    const float * p = part + (t * k + j) * S * ld + n;
+    float acc = 0.f;
+    for (int64_t s0 = 0; s0 < S; s0 += DS_SUM_MAX) {
+        float v[DS_SUM_MAX];
+#pragma unroll
+        for (int i = 0; i < DS_SUM_MAX; i++) v[i] = p[(s0 + i < S ? s0 + i : S - 1) * ld];
+#pragma unroll
+        for (int i = 0; i < DS_SUM_MAX; i++)
+            if (s0 + i < S) acc += v[i];
+    }
+    sp[j * DS_SUM_N + c] = acc;
+    __syncthreads();
+    if ((int) threadIdx.x < DS_SUM_N && n < Nd) {
+        float v = 0.f;
+        for (int i = 0; i < k; i++) v += w[t * k + i] * sp[i * DS_SUM_N + c];
+        store_out(y, yf32, t * Nd + n, v);
+    }
+}
+
+hipError_t launch_moe_dsum(const float * part, int64_t S, int64_t ld, const float * w, int64_t T, int k, int64_t Nd,
+                           void * y, int yf32, hipStream_t s) {
+    if (T < 1 || T > DS_MAX_T || k < 1 || k > DS_MAX_K || ld % 64 || Nd > ld) return hipErrorInvalidValue;
+    k_moe_dsum<<<dim3((unsigned) ((Nd + DS_SUM_N - 1) / DS_SUM_N), (unsigned) T), (unsigned) (DS_SUM_N * k), 0, s>>>(
+        part, S, ld, w, k, Nd, y, yf32);
+    return hipGetLastError();
+}
+
+hipError_t launch_relayout_dec(int fmt, const uint8_t * src, int64_t sstride, int64_t N, int64_t K, uint8_t * dst,
+                               int64_t dstride, int64_t E, hipStream_t s) {
+    const Tiled g = tiled_geom(fmt, N, K);
+    if (E <= 0 || E > 65535 || dstride < dec_bytes(fmt, N, K)) return hipErrorInvalidValue;
+    switch (fmt) {
+        case 0: return relayout_dec_f0(src, sstride, g.NT, g.KB, dst, dstride, E, s);
+        case 1: return relayout_dec_f1(src, sstride, g.NT, g.KB, dst, dstride, E, s);
+        case 2: return relayout_dec_f2(src, sstride, g.NT, g.KB, dst, dstride, E, s);
+        case 3: return relayout_dec_f3(src, sstride, g.NT, g.KB, dst, dstride, E, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s) {
     if (a.xbytes <= 0 || a.xbytes >= ((int64_t) 1 << 31) || maxitems <= 0 || maxitems > 65535) return hipErrorInvalidValue;
     if (which == 0 && (a.NT % 2 || a.N != 16 * a.NT)) return hipErrorInvalidValue;   // gate | up halves of whole tiles

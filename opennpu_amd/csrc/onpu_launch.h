@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "onpu_common.h"
+
 // k_qgemv: y = x . deq(W)^T for M <= 64 rows of x, per slot (expert) and epilogue
 struct QArgs {
     const uint8_t * W;        // tiled weights; expert e at W + e * estride
@@ -101,6 +103,39 @@ constexpr int MD_MAX_T = 4, MD_MAX_K = 8, MD_WAVES = 8, MD_SYNC_DONE = 16, MD_SY
 constexpr int MD_MAX_GB = 4;      // gate_up K blocks per wave (H <= 8 * 4 * 128)
 constexpr int MD_MAX_DB = 8;      // down K blocks (I <= 1024)
 
+// MoE decode split along I (k_moe_dsplit, then k_moe_dsum). Workgroup (slice s, slot t k + j) takes
+// the I values [32 s, 32 s + 32) of its slot's expert: their gate and up rows (two row tiles each) give
+// act for those 32 values, which it multiplies into the expert's down weights for the same 32 K values
+// (one MFMA K step, read from the down bank's step-major copy), leaving fp32 partial sums
+// part[slot][s][n]. No workgroup waits for another. k_moe_dsum then forms y[t][n] = sum_j w[t][j]
+// sum_s part[t k + j][s][n] in that order.
+struct MSArgs {
+    const uint8_t * Wg;       // gate_up bank: expert e at Wg + e * gstride, [2 I][H] tiled
+    int64_t gstride, gNT, gKB;
+    const uint8_t * Wd;       // down bank, step-major copy: expert e at Wd + e * dstride
+    int64_t dstride, dNTq;    // dNTq = ceil(down row tiles / 4) superblocks per K step
+    int64_t H, I, S;          // S = I / 32 slices
+    const uint16_t * x;       // [T][H] bf16
+    const float * logits;     // [T][E] fp32 -> route in the kernel; nullptr: ids are inputs
+    int E, k, renorm, T;
+    int32_t * ids;            // [T][k]
+    float * w;                // [T][k]
+    float * part;             // [T k][S][dNTq * 64] fp32
+};
+constexpr int DS_MAX_T = 4, DS_MAX_K = 16;
+
+// The step-major copy of a tiled matrix that k_moe_dsplit reads (per expert, dec_bytes apart):
+// superblock (s, tq), s = 4 b + j one 32-wide K step, tq a quad of row tiles, at (s * NTq + tq) *
+// dec_sblk. Its [0, 1024) holds for lane l (= 16 q + r) the dwords D_j of tiles 4 tq + d, d = 0..3, of
+// block b (the tiled layout's dword j of lane l, zero past the last tile): the B operands of those
+// four row tiles for step s. [1024, dec_sblk) holds per row r the four tiles' parameters of step s:
+// u16 scales [16][4] (q4nx: {u16 scale, u16 min} [16][4]).
+inline int dec_sblk(int fmt) { return 1024 + (fmt == ONPU_Q4NX ? 256 : 128); }
+inline int64_t dec_bytes(int fmt, int64_t N, int64_t K) {
+    const int64_t NTq = ((N + 15) / 16 + 3) / 4, S = 4 * ((K + 127) / 128);
+    return (S * NTq * dec_sblk(fmt) + 255) / 256 * 256;
+}
+
 // chained decode GEMVs (k_qgemv_chain): entry i = y_i [M][N] = x_i [M][K] . W_i^T, in order. An
 // entry reads an external x (bf16 rows, written before the launch) or a link: words
 // (bf16 << 16 | run tag) that an earlier entry publishes for its output, rows ldl words apart
@@ -155,6 +190,15 @@ hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems
 // outside what k_moe_decode handles (moe_decode_fits; the caller then uses the multi-launch path)
 hipError_t launch_moe_decode(int fmt, const MDArgs & a, int grid, hipStream_t s);
 bool moe_decode_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int64_t dKB, int T, int k, int E);
+// MoE decode split along I (grid S x T k, then the partial sums); hipErrorInvalidValue outside what
+// moe_dsplit_fits allows
+bool moe_dsplit_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int T, int k, int E);
+hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, hipStream_t s);
+hipError_t launch_moe_dsum(const float * part, int64_t S, int64_t ld, const float * w, int64_t T, int k, int64_t Nd,
+                           void * y, int yf32, hipStream_t s);
+// experts [0, E) of a tiled matrix (src, sstride apart) -> their step-major copies (dst, dstride apart)
+hipError_t launch_relayout_dec(int fmt, const uint8_t * src, int64_t sstride, int64_t N, int64_t K, uint8_t * dst,
+                               int64_t dstride, int64_t E, hipStream_t s);
 // the chained kernel on `grid` workgroups (all resident at once)
 // (ring: CHAIN_RING_SLOTS[ring] weight blocks per compute wave)
 hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,
@@ -234,6 +278,9 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2, EPI_ARGMAX_ = 3 };
     hipError_t qgemm_sk_f##id(const GArgs & a, int cfg, int grid, hipStream_t s);                          \
     hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
     hipError_t moe_decode_f##id(const MDArgs & a, int gb, int grid, size_t lds, hipStream_t s);       \
+    hipError_t moe_dsplit_f##id(const MSArgs & a, int nw, size_t lds, hipStream_t s);                 \
+    hipError_t relayout_dec_f##id(const uint8_t * src, int64_t sstride, int64_t NT, int64_t KB, uint8_t * dst, \
+                                  int64_t dstride, int64_t E, hipStream_t s);                          \
     hipError_t chain_f##id(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,  \
                            hipStream_t s);                                                                \
     int chain_occ_f##id(int ring, size_t lds);

@@ -210,7 +210,7 @@ def argmax(v):
     return out
 
 
-def moe_layer(fmt, gu_st, dn_st, E, H, I, x_bf, ids, w, bf16w=False, bf16o=False, mag=False):
+def moe_layer(fmt, gu_st, dn_st, E, H, I, x_bf, ids, w, bf16w=False, bf16o=False, mag=False, Nd=None):
     """A routed-expert FFN layer as reference.py:71-84 computes it (dequantized experts, fp32 act),
     with the two rounding points of the device path: gate_up in fp64 -> fp32, act -> bf16 RNE as the
     down input (the device input conversion, opennpu_core.hpp:418-424), down in fp64, weighted sum.
@@ -218,16 +218,18 @@ def moe_layer(fmt, gu_st, dn_st, E, H, I, x_bf, ids, w, bf16w=False, bf16o=False
     bf16 (RNE) as the reference device's MAC sees them (gemv_any.cc:65,106-107). bf16o: each expert's
     down output rounded to bf16 before the weighted sum, as the reference device returns it
     (gemv_any.cc:120-130) to the host's fp32 sum (onpu_cpu.cpp:259-274). mag: also return
-    sum_j |w_j d_j| per output (the scale of a one-ulp difference in any rounded expert row)."""
+    sum_j |w_j d_j| per output (the scale of a one-ulp difference in any rounded expert row). Nd: the
+    down projection's rows (default H)."""
     T, k = ids.shape
-    y = np.zeros((T, H), np.float64)
-    m = np.zeros((T, H), np.float64)
+    Nd = H if Nd is None else Nd
+    y = np.zeros((T, Nd), np.float64)
+    m = np.zeros((T, Nd), np.float64)
     xb = np.asarray(x_bf, np.uint16).reshape(T, H)
     for e in np.unique(ids):
         rows, slots = np.nonzero(ids == e)
         g = qmm(fmt, gu_st[e], 2 * I, H, xb[rows], bf16w=bf16w).astype(np.float32)
         a = f2bf_np(silu_mul(g))
-        d = qmm(fmt, dn_st[e], H, I, a, bf16w=bf16w)
+        d = qmm(fmt, dn_st[e], Nd, I, a, bf16w=bf16w)
         if bf16o:
             d = bf2f(f2bf_np(d.astype(np.float32))).astype(np.float64)
         y[rows] += w[rows, slots][:, None].astype(np.float64) * d

@@ -332,3 +332,89 @@ def test_moe_decode_workspace_survives_growth_under_a_graph(gpu, fused, monkeypa
         assert f.status() == 0
     finally:
         f.free()
+
+
+_SPLIT = [(orc.FMT_G128S, 128, 2048, 768, 2048, 8, 1), (orc.FMT_G128S, 128, 2048, 768, 2048, 8, 4),
+          (orc.FMT_Q4S, 24, 544, 160, 200, 16, 4), (orc.FMT_Q4NX, 16, 512, 96, 130, 6, 3),
+          (orc.FMT_Q4_0, 8, 256, 64, 256, 8, 2), (orc.FMT_G128S, 12, 4096, 256, 4000, 4, 2)]
+
+
+@pytest.mark.parametrize("fmt,E,H,I,Nd,k,T", _SPLIT)
+def test_moe_decode_split_along_I(gpu, fmt, E, H, I, Nd, k, T, monkeypatch):
+    """The default decode path at T <= 4 (k_moe_dsplit, then k_moe_dsum): each workgroup takes 32
+    values of I of one slot's expert through gate / up, SiLU * up and down from the down bank's
+    step-major copy, no workgroup waiting for another. From logits and from given ids / w, y agrees
+    with the oracle layer (bf16 bound) and with the two-launch path (an FFN built with
+    ONPU_MOE_DSPLIT=0, so without the copy) to fp32 summation order; ids / w equal the router's.
+    Ragged down rows (Nd not a multiple of 64), K tails, k up to 16, H = 4096 (the generic variant);
+    T up to 4 (the library takes the split path for T = 1 by default; the test raises the limit)."""
+    import torch
+    from opennpu_amd.device import QFfn
+    monkeypatch.delenv("ONPU_MOE_FUSED", raising=False)
+    monkeypatch.setenv("ONPU_MOE_DSPLIT_MAX_T", "4")
+    gu = [syn.weights(fmt, 2 * I, H, 1100 + 2 * e) for e in range(E)]
+    dn = [syn.weights(fmt, Nd, I, 1101 + 2 * e) for e in range(E)]
+    xb = syn.activations(T, H, 1102 + T)
+    lg = syn.logits(T, E, 1103 + k)
+    outs = {}
+    for split in ("1", "0"):
+        monkeypatch.setenv("ONPU_MOE_DSPLIT", split)
+        f = QFfn(E, H, I, fmt, Nd=Nd)
+        try:
+            f.load(np.concatenate(gu), np.concatenate(dn))
+            x = to_torch_bf16(xb).reshape(T, H)
+            lgd = torch.from_numpy(lg).cuda()
+            print(f"moe decode split={split} fmt {fmt} E {E} H {H} I {I} Nd {Nd} k {k} T {T}", flush=True)
+            y, ids, w = f.decode(lgd, x, k, f32=True)
+            y2 = f.ffn(x, ids, w, f32=True)
+            torch.cuda.synchronize()
+            assert torch.equal(y, y2), "decode from logits and from ids / w differ"
+            outs[split] = (from_torch(y), ids.cpu().numpy(), w.cpu().numpy())
+        finally:
+            f.free()
+    (y1, i1, w1), (y0, i0, w0) = outs["1"], outs["0"]
+    rid, rw = orc.route(lg, k)
+    assert np.array_equal(i1, rid) and np.array_equal(i0, rid)
+    assert np.array_equal(w1, w0)
+    ref = orc.moe_layer(fmt, gu, dn, E, H, I, xb, rid, rw, Nd=Nd)
+    err = orc.max_rel_err(y1, ref)
+    assert err <= 4e-3, f"split decode vs oracle: {err:.3e}"
+    d = np.abs(y1 - y0).max() / np.abs(y0).max()
+    assert d <= 4e-3, f"split decode vs two launches: {d:.3e}"
+
+
+def test_moe_decode_split_follows_weight_reloads(gpu, monkeypatch):
+    """Loading new weights into some experts (from staging bytes, and by GPU quantization) updates
+    the down bank's step-major copy with them: the split decode then equals a fresh FFN holding the
+    new weights, bit for bit."""
+    import torch
+    from opennpu_amd.device import QFfn
+    monkeypatch.delenv("ONPU_MOE_FUSED", raising=False)
+    monkeypatch.delenv("ONPU_MOE_DSPLIT", raising=False)
+    monkeypatch.setenv("ONPU_MOE_DSPLIT_MAX_T", "4")
+    fmt, E, H, I, k = orc.FMT_Q4S, 8, 256, 128, 8
+    gu = [syn.weights(fmt, 2 * I, H, 1200 + e) for e in range(E)]
+    dn = [syn.weights(fmt, H, I, 1300 + e) for e in range(E)]
+    dn_new = [syn.weights(fmt, H, I, 1400 + e) for e in range(E)]
+    x = to_torch_bf16(syn.activations(2, H, 1201)).reshape(2, H)
+    lgd = torch.from_numpy(syn.logits(2, E, 1202)).cuda()
+    rng = np.random.default_rng(5)
+    Wq = torch.from_numpy((rng.standard_normal((2, H, I)) * 0.02).astype(np.float32)).cuda()
+    gq = torch.from_numpy((rng.standard_normal((2, 2 * I, H)) * 0.02).astype(np.float32)).cuda()
+    f = QFfn(E, H, I, fmt)
+    g = QFfn(E, H, I, fmt)
+    try:
+        f.load(np.concatenate(gu), np.concatenate(dn))
+        f.decode(lgd, x, k)
+        f.load(np.concatenate(gu[2:5]), np.concatenate(dn_new[2:5]), e0=2)     # experts 2..4 reloaded
+        f.quantize(gq, Wq, e0=6)                                                # experts 6, 7 quantized
+        y, _, _ = f.decode(lgd, x, k, f32=True)
+        ref_dn = dn[:2] + dn_new[2:5] + dn[5:6]
+        g.load(np.concatenate(gu[:6]), np.concatenate(ref_dn), e0=0)
+        g.quantize(gq, Wq, e0=6)
+        y2, _, _ = g.decode(lgd, x, k, f32=True)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2)
+    finally:
+        f.free()
+        g.free()
