@@ -255,6 +255,7 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     p.xl = (p.mb == 1 && (xbytes <= 52 * 1024 || (xbytes <= 112 * 1024 && groups0 * slots >= 1024))) ? 1 : 0;
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
+    if (ex == 1 && p.mb == 1 && xbytes <= 144 * 1024) p.xl = 1;
     const int64_t groups = act ? NT / 2 : NT;
     // vocabulary-sized matrices (>= 4096 tile groups) stream whole rows per wave (up to 32 blocks)
     // in workgroups of up to 8 tile groups sharing one x copy: measured on the 151936 x 4096 LM head,
@@ -296,6 +297,35 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     const int etw = env_int("ONPU_GEMV_TW", 0);
     if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= red_kib && !(act && groups % etw))
         tw = etw;
+    // Several x rows (M > 1, one A block, plain store): plans measured per shape class on MI355X (the
+    // Qwen3-8B matrices at M = 4 / 8, graphs of 36 copies, us per launch against the rule above). The
+    // x copy per workgroup grows with M, so fewer and wider workgroups share it, and long K streams in
+    // single-block chunks:
+    //   <= 256 tile groups, K <= 4096 (4096 x 4096): 16 K parts of 2 blocks, x from global memory,
+    //     5.61 / 6.07 against 6.80 / 6.49
+    //   <= 512 tile groups (6144 x 4096): two tile groups per workgroup sharing x in LDS (up to
+    //     112 KiB), 6.92 / 8.29 against 8.07 / 8.76
+    //   >= 1024 tile groups at M > 4 (24576 x 4096): six tile groups of 2 K parts, 15.06 against 15.50
+    //   K >= 8192 (4096 x 12288): single-block chunks, 10.07 / 10.71 against 10.48 / 11.33
+    if (M > 1 && p.mb == 1 && epi == EPI_STORE_ && !vocab && slots == 1 && ekw == 0 && etw == 0 && en == 0 &&
+        ex < 0) {
+        int ckw = 0, ctw = 0, cnb = 0, cxl = -1;
+        if (groups <= 256 && KB <= 32) { ckw = 16; ctw = 1; cnb = 1; cxl = 0; }
+        else if (KB >= 64) cnb = 1;
+        else if (groups <= 512) { ctw = 2; cxl = xbytes <= 112 * 1024 ? 1 : -1; }
+        else if (groups >= 1024 && M > 4) { ckw = 2; ctw = 6; }
+        if (ckw) {
+            p.bpw = (KB + ckw - 1) / ckw;
+            p.kw = (int) ((KB + p.bpw - 1) / p.bpw);
+        }
+        if (cnb && qgemv_has_variant(epi, p.mb, p.rt, cnb, cxl >= 0 ? cxl : p.xl)) p.nb = cnb;
+        if (cxl >= 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, cxl)) p.xl = cxl;
+        if (ctw) tw = ctw;
+        if (tw * p.kw > qgemv_max_waves(p.mb, p.rt, p.nb, p.xl) || tw * p.kw * p.rt * p.mb > red_kib) {
+            tw = std::max(1, std::min(tw, qgemv_max_waves(p.mb, p.rt, p.nb, p.xl) / p.kw));
+            while (tw > 1 && tw * p.kw * p.rt * p.mb > red_kib) tw--;
+        }
+    }
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
     return p;
