@@ -7,8 +7,12 @@
  * Conventions (as in the reference):
  *   - x and y of the host-pointer calls are row-major fp32; x is rounded to bf16 (nearest even)
  *     before the product, y is overwritten and the call is synchronous.
- *   - weights: a handle owns a host staging buffer (*_buf) that the caller fills with the staging
- *     layout below, then *_sync uploads it to HBM and repacks it into the GPU layout.
+ *   - weights: a handle owns a host buffer (*_buf) that the caller fills (onpu_pack writes it), then
+ *     *_sync uploads it to HBM and repacks it into the GPU layout. For q4nx and q4s the buffers of
+ *     the reference calls (onpu_dense_new2 on 8 columns, onpu_bank_new2 on ncols, onpu_ffn_new on 1)
+ *     hold the reference's NPU packing below, byte for byte, so that bytes packed by the reference
+ *     or cached by it (npu4's PackCache, model.py:712-759) load unchanged; the other formats and
+ *     the *_new3 handles take the staging layout.
  *   - construction returns NULL for an unsupported shape or format; a HIP failure inside a void
  *     call prints the error and aborts the process (the reference throws across extern "C").
  *     onpu_last_error() reports the last failure of an int-returning call on this thread.
@@ -26,8 +30,16 @@
  *   G128S: codes u8 [N][K/2], scales bf16 [N][K/128]
  *   Q4_0 : GGUF block_q4_0 rows [N][K/32] x {fp16 d, u8 qs[16]} (element j <- qs[j] & 15,
  *          element j+16 <- qs[j] >> 4)
- * Handles made by the reference calls keep the reference's buffer sizes (onpu_geometry2's
- * nbytes, which the staging layout always fits in); *_new3 handles use onpu_stage_bytes().
+ * NPU packing of one matrix (pack_mat, opennpu_core.hpp:174-254), in the geometry onpu_geometry2
+ * reports (R row blocks of rows_col rows x S K slices of ks columns, cb bytes per column block):
+ * column block c = r*S + s at c*cb, all zero if it holds no weight; inside it, packets of 64 rows x
+ * 256 columns in the order [tile t][K step kk][core row cr] (rows cr*tiles*64 + t*64 + [0, 64)),
+ * each: codes [8 row octets][32 column octets][8 columns][4 bytes of a row pair, even row low],
+ * then bf16 scales [8 groups][64 rows], then (q4nx) mins likewise; past the matrix, code 8 (q4s)
+ * or 0 (q4nx) and zero parameters.
+ * Handles made by the reference calls keep the reference's buffer sizes (onpu_geometry2's nbytes,
+ * which the staging layout of formats 2 and 3 always fits in); *_new3 handles use
+ * onpu_stage_bytes().
  */
 #ifndef ONPU_H
 #define ONPU_H
@@ -86,7 +98,10 @@ void onpu_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * 
                   const float * bias, float * y);
 
 /* ---- fused expert FFN (onpu_api.cpp:292-496): gate_up, SiLU * up and down of a token's experts
- * without host round trips. perm is the identity here (rows keep the [gate | up] order). */
+ * without host round trips. onpu_ffn_perm: the gate_up row the caller packs at each row of gu's
+ * buffer; where the reference fuses the shape (onpu_api.cpp:307-322), its order, so that packed
+ * banks and cached files carry the reference's bytes (the upload restores the [gate | up] order),
+ * else the identity. */
 void * onpu_ffn_new(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int sym);
 void * onpu_ffn_gu(void * h);
 void * onpu_ffn_dn(void * h);
@@ -100,8 +115,9 @@ int onpu_ffn_run_many(void * h, const float * x, int64_t T, const int32_t * ids,
 void onpu_ffn_free(void * h);
 
 /* ---- packing (onpu_api.cpp:499-529): quantize fp32 W [N][K] with the reference's search
- * quantizers (q4nx / q4s per 32; g128s per 128; Q4_0 as ggml) into the staging layout; returns
- * onpu_geometry2's nbytes (0: unsupported) */
+ * quantizers (q4nx / q4s per 32; g128s per 128; Q4_0 as ggml): q4nx and q4s into the reference's
+ * NPU packing for ncols columns (its pack_mat's bytes), g128s and Q4_0 into the staging layout,
+ * zero-padded; returns onpu_geometry2's nbytes (0: unsupported) */
 int64_t onpu_pack(const float * W, int64_t N, int64_t K, int ncols, int sym, uint8_t * out, int threads);
 void onpu_quant_dequant(const float * W, int64_t N, int64_t K, int sym, float * out, int threads);
 
@@ -184,7 +200,8 @@ int onpu_moe_status(void * h);
  * completed; calls on one handle are serialised by the library mutex. 0 ok, -1 error
  * (onpu_last_error). */
 /* experts [e0, e0 + n) of a dense (E = 1) or bank handle from W [n][N][ldw] (row stride ldw >= K
- * elements), fp32 (w_bf16 = 0) or bf16 (1), with the handle's format: the bytes onpu_pack writes */
+ * elements), fp32 (w_bf16 = 0) or bf16 (1), with the handle's format: the codes and parameters
+ * onpu_pack writes */
 int onpu_quantize_dev(void * h, int64_t e0, int64_t n, const void * W, int64_t ldw, int w_bf16, void * stream);
 /* q4nx handle, K a multiple of 256: experts [e0, e0 + n) from GGUF Q4_K rows of K / 256 super-blocks
  * (144 bytes each), rows ld bytes apart, experts N * ld bytes apart */

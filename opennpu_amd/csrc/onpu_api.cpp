@@ -126,6 +126,12 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     uint8_t * dev = nullptr;
     uint8_t * stage = nullptr;             // host staging, E * sstride bytes (lazy)
     int64_t sstride = 0;
+    // handles of the reference's constructors for q4nx / q4s: *_buf holds the reference's NPU
+    // packing in geometry rg (sstride = rg.nbytes per expert), turned into the staging layout on the
+    // device at *_sync; rowmap (device, N entries, or null): the staging row of each packed row
+    bool npu = false;
+    RefGeom rg{};
+    int32_t * rowmap = nullptr;
     // argmax workspace of the _dev calls on this handle (kept across growth: see DBuf)
     DBuf am_keys{nullptr, 0, true};        // per-workgroup keys of the GEMV epilogue (<= 64 rows)
     DBuf am_big{nullptr, 0, true};         // keys of the argmax launch over the logits
@@ -145,6 +151,7 @@ struct Ffn {
                   {nullptr, 0, true}, {nullptr, 0, true}, {nullptr, 0, true}};
     DBuf md_act{nullptr, 0, true}, md_sync{nullptr, 0, true};
     DBuf ds_part{nullptr, 0, true};        // k_moe_dsplit partial sums, sized once for its largest call
+    std::vector<int32_t> perm;             // gate_up row packed at each row of gu's buffer (onpu_ffn_perm)
 };
 
 int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
@@ -176,6 +183,7 @@ void free_mat(Mat4 * m) {
     if (!m) return;
     if (m->dev) (void) hipFree(m->dev);
     if (m->dec) (void) hipFree(m->dec);
+    if (m->rowmap) (void) hipFree(m->rowmap);
     std::free(m->stage);
     m->am_keys.release();
     m->am_big.release();
@@ -198,19 +206,35 @@ hipError_t refresh_dec(Mat4 * m, int64_t e0, int64_t n, hipStream_t s) {
                                m->dec_stride, n, s);
 }
 
-// experts [e0, e0 + n) from staging bytes (stride src_stride per expert) -> HBM tiled layout
-hipError_t upload(Mat4 * m, int64_t e0, int64_t n, const uint8_t * src, int64_t src_stride, hipStream_t s) {
+// experts [e0, e0 + n) from host bytes (stride src_stride per expert) -> HBM tiled layout. The bytes
+// are the staging layout, or (npu_src) the reference's NPU packing of m->rg, which a kernel first
+// turns into the staging layout. Through a device temporary of at most 256 MiB (or one expert),
+// freed before returning.
+hipError_t upload(Mat4 * m, int64_t e0, int64_t n, const uint8_t * src, int64_t src_stride, bool npu_src,
+                  hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t sb = round_up(stage_bytes(m->fmt, m->N, m->K), 256);
+    const int64_t chunk = std::max<int64_t>(
+        1, std::min<int64_t>(n, ((int64_t) 256 << 20) / (src_stride + (npu_src ? sb : 0))));
+    const int64_t raw_bytes = round_up(chunk * src_stride, 256);
     void * tmp = nullptr;
-    hipError_t e = hipMalloc(&tmp, (size_t) (n * src_stride));
+    hipError_t e = hipMalloc(&tmp, (size_t) (raw_bytes + (npu_src ? chunk * sb : 0)));
     if (e != hipSuccess) return e;
-    e = hipMemcpyAsync(tmp, src, (size_t) (n * src_stride), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess)
-        e = launch_repack(m->fmt, (const uint8_t *) tmp, src_stride, m->N, m->K, m->dev + e0 * m->dstride, m->dstride,
-                          n, s);
-    if (e == hipSuccess) e = refresh_dec(m, e0, n, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    uint8_t * raw = (uint8_t *) tmp, * st = raw + raw_bytes;
+    const NpuGeom g = npu_geom(m->rg.S, m->rg.tiles, m->rg.kc, m->rg.ks, m->rg.rows_col, m->rg.cb, m->fmt == ONPU_Q4S);
+    for (int64_t c = 0; c < n && e == hipSuccess; c += chunk) {
+        const int64_t k = std::min(chunk, n - c);
+        e = hipMemcpyAsync(raw, src + c * src_stride, (size_t) (k * src_stride), hipMemcpyHostToDevice, s);
+        if (e == hipSuccess && npu_src)
+            e = launch_npu_stage(m->fmt, raw, src_stride, g, m->rowmap, m->N, m->K, st, sb, k, s);
+        if (e == hipSuccess)
+            e = launch_repack(m->fmt, npu_src ? st : raw, npu_src ? sb : src_stride, m->N, m->K,
+                              m->dev + (e0 + c) * m->dstride, m->dstride, k, s);
+        if (e == hipSuccess) e = refresh_dec(m, e0 + c, k, s);
+    }
+    const hipError_t es = hipStreamSynchronize(s);
     (void) hipFree(tmp);
-    return e;
+    return e == hipSuccess ? es : e;
 }
 
 // ------------------------------------------------------------------ launch plans
@@ -307,8 +331,10 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     //     112 KiB), 6.92 / 8.29 against 8.07 / 8.76
     //   >= 1024 tile groups at M > 4 (24576 x 4096): six tile groups of 2 K parts, 15.06 against 15.50
     //   K >= 8192 (4096 x 12288): single-block chunks, 10.07 / 10.71 against 10.48 / 11.33
-    if (M > 1 && p.mb == 1 && epi == EPI_STORE_ && !vocab && slots == 1 && ekw == 0 && etw == 0 && en == 0 &&
-        ex < 0) {
+    // The argmax epilogue takes the same plans, so that its logits equal those of a plain store
+    // followed by the separate argmax launch, bit for bit.
+    if (M > 1 && p.mb == 1 && (epi == EPI_STORE_ || epi == EPI_ARGMAX_) && !vocab && slots == 1 && ekw == 0 &&
+        etw == 0 && en == 0 && ex < 0) {
         int ckw = 0, ctw = 0, cnb = 0, cxl = -1;
         if (groups <= 256 && KB <= 32) { ckw = 16; ctw = 1; cnb = 1; cxl = 0; }
         else if (KB >= 64) cnb = 1;
@@ -828,10 +854,21 @@ int64_t onpu_stage_bytes(int fmt, int64_t N, int64_t K) {
 }
 
 // ---------------------------------------------------------------- dense
+// a handle whose *_buf memory takes the reference's NPU packing in geometry g (q4nx, q4s) or, for
+// this library's own formats, the staging layout in g.nbytes bytes per expert
+static Mat4 * make_ref_mat(int64_t N, int64_t K, int64_t E, int fmt, const RefGeom & g) {
+    Mat4 * m = make_mat(N, K, E, fmt, g.nbytes);
+    if (m) {
+        m->npu = fmt == ONPU_Q4NX || fmt == ONPU_Q4S;
+        m->rg = g;
+    }
+    return m;
+}
+
 void * onpu_dense_new2(int64_t N, int64_t K, int sym) {
     const RefGeom g = ref_geometry(N, K, 8, sym != 0);
     if (!g.ok) { set_err("onpu_dense_new2: the shape has no reference geometry"); return nullptr; }
-    return make_mat(N, K, 1, sym, g.nbytes);
+    return make_ref_mat(N, K, 1, sym, g);
 }
 void * onpu_dense_new(int64_t N, int64_t K) { return onpu_dense_new2(N, K, 0); }
 void * onpu_dense_new3(int64_t N, int64_t K, int fmt) {
@@ -844,7 +881,7 @@ int64_t onpu_dense_bytes(void * h) { return ((Mat4 *) h)->sstride; }
 void onpu_dense_sync(void * h) {
     auto * m = (Mat4 *) h;
     std::lock_guard<std::mutex> lk(g_mu);
-    HIPX(upload(m, 0, m->E, stage_of(m), m->sstride, device().stream));
+    HIPX(upload(m, 0, m->E, stage_of(m), m->sstride, m->npu, device().stream));
 }
 
 void onpu_dense_free(void * h) {
@@ -855,7 +892,7 @@ void onpu_dense_free(void * h) {
 int onpu_dense_load(void * h, const void * stage) {
     auto * m = (Mat4 *) h;
     std::lock_guard<std::mutex> lk(g_mu);
-    HIPR(upload(m, 0, 1, (const uint8_t *) stage, stage_bytes(m->fmt, m->N, m->K), device().stream));
+    HIPR(upload(m, 0, 1, (const uint8_t *) stage, stage_bytes(m->fmt, m->N, m->K), false, device().stream));
     return 0;
 }
 
@@ -952,7 +989,7 @@ int onpu_dense_argmax_dev_noalloc(void * h, const void * x, int64_t M, float * l
 void * onpu_bank_new2(int64_t N, int64_t K, int64_t E, int ncols, int sym) {
     const RefGeom g = ref_geometry(N, K, ncols, sym != 0);
     if (!g.ok) { set_err("onpu_bank_new2: the shape has no reference geometry"); return nullptr; }
-    return make_mat(N, K, E, sym, g.nbytes);
+    return make_ref_mat(N, K, E, sym, g);
 }
 void * onpu_bank_new(int64_t N, int64_t K, int64_t E, int ncols) { return onpu_bank_new2(N, K, E, ncols, 0); }
 void * onpu_bank_new3(int64_t N, int64_t K, int64_t E, int fmt) {
@@ -968,7 +1005,7 @@ int onpu_bank_load(void * h, int64_t e0, int64_t n, const void * stage) {
     auto * m = (Mat4 *) h;
     if (e0 < 0 || n < 0 || e0 + n > m->E) { set_err("onpu_bank_load: experts out of range"); return -1; }
     std::lock_guard<std::mutex> lk(g_mu);
-    HIPR(upload(m, e0, n, (const uint8_t *) stage, stage_bytes(m->fmt, m->N, m->K), device().stream));
+    HIPR(upload(m, e0, n, (const uint8_t *) stage, stage_bytes(m->fmt, m->N, m->K), false, device().stream));
     return 0;
 }
 
@@ -1082,15 +1119,16 @@ void onpu_moe_sum(const float * o, int64_t T, int k, int64_t N, const int32_t * 
 }
 
 // ---------------------------------------------------------------- fused expert FFN
-static void * ffn_make(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int fmt, int64_t sg, int64_t sd) {
-    Mat4 * gu = make_mat(Ng, Kg, E, fmt, sg);
-    Mat4 * dn = gu ? make_mat(Nd, Kd, E, fmt, sd) : nullptr;
-    if (!gu || !dn) { free_mat(gu); return nullptr; }
+static void * ffn_make(Mat4 * gu, Mat4 * dn, int64_t Nd, int64_t Kd, int64_t E, int fmt) {
+    if (!gu || !dn) { free_mat(gu); free_mat(dn); return nullptr; }
+    const int64_t Ng = gu->N;
     auto * f = new Ffn;
     f->gu = gu;
     f->dn = dn;
     // the fused kernels pair gate row tile t with up row tile t + I/16
     f->fused = Ng % 32 == 0 && Kd == Ng / 2;
+    f->perm.resize((size_t) Ng);
+    for (int64_t r = 0; r < Ng; r++) f->perm[r] = (int32_t) r;
     // decode split along I (k_moe_dsplit) reads the down bank in a step-major copy: one more
     // down-bank-sized allocation, filled with the weights (ONPU_MOE_DSPLIT=0: no copy, two launches)
     if (f->fused && Kd % 32 == 0 && env_int("ONPU_MOE_DSPLIT", 1)) {
@@ -1103,20 +1141,54 @@ static void * ffn_make(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E
     return f;
 }
 
+// The gate_up row order of the reference's fused FFN (onpu_api.cpp:307-322 of the reference): when
+// its rule holds (one row block and one K slice per matrix, I = Ng / 2 = Kd a multiple of 256, all
+// Ng rows in one column, Kg <= 2048, an even tile count), its NPU writes the outputs of a column in
+// [tile pair][core row][128 rows] order, so the caller packs gate_up row perm[r] at row r. The same
+// order is given here, so that packed banks, the reference's cache files included, carry the same
+// bytes; the upload puts packed row r back at row perm[r].
+static bool ref_ffn_order(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, const RefGeom & gg, const RefGeom & gd,
+                          std::vector<int32_t> & perm) {
+    const int64_t I = Ng / 2;
+    if (!(gg.R == 1 && gg.S == 1 && gd.R == 1 && gd.S == 1 && Ng % 2 == 0 && Kd == I && I % 256 == 0 &&
+          gg.rows_col == Ng && Kg <= 2048 && gg.tiles % 2 == 0))
+        return false;
+    (void) Nd;
+    const int64_t pairs = gg.tiles / 2;
+    for (int64_t t2 = 0; t2 < pairs; t2++)
+        for (int64_t cr = 0; cr < 4; cr++)
+            for (int64_t i = 0; i < 128; i++)
+                perm[(size_t) (cr * gg.tiles * 64 + t2 * 128 + i)] = (int32_t) ((t2 * 4 + cr) * 128 + i);
+    return true;
+}
+
 void * onpu_ffn_new(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int sym) {
     const RefGeom gg = ref_geometry(Ng, Kg, 1, sym != 0), gd = ref_geometry(Nd, Kd, 1, sym != 0);
     if (!gg.ok || !gd.ok) { set_err("onpu_ffn_new: a shape has no reference geometry"); return nullptr; }
-    return ffn_make(Ng, Kg, Nd, Kd, E, sym, gg.nbytes, gd.nbytes);
+    auto * f = (Ffn *) ffn_make(make_ref_mat(Ng, Kg, E, sym, gg), make_ref_mat(Nd, Kd, E, sym, gd), Nd, Kd, E, sym);
+    if (f && f->fused && f->gu->npu && ref_ffn_order(Ng, Kg, Nd, Kd, gg, gd, f->perm)) {
+        const size_t bytes = f->perm.size() * sizeof(int32_t);
+        hipError_t e = hipMalloc((void **) &f->gu->rowmap, bytes);
+        if (e == hipSuccess) e = hipMemcpy(f->gu->rowmap, f->perm.data(), bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            set_err("onpu_ffn_new: the gate_up row order", e);
+            onpu_ffn_free(f);
+            return nullptr;
+        }
+    }
+    return f;
 }
 void * onpu_ffn_new3(int64_t Ng, int64_t Kg, int64_t Nd, int64_t Kd, int64_t E, int fmt) {
     if (!fmt_valid(fmt) || Kg % fmt_group(fmt) != 0 || Kd % fmt_group(fmt) != 0) return nullptr;
-    return ffn_make(Ng, Kg, Nd, Kd, E, fmt, stage_bytes(fmt, Ng, Kg), stage_bytes(fmt, Nd, Kd));
+    return ffn_make(make_mat(Ng, Kg, E, fmt, stage_bytes(fmt, Ng, Kg)), make_mat(Nd, Kd, E, fmt, stage_bytes(fmt, Nd, Kd)),
+                    Nd, Kd, E, fmt);
 }
 void * onpu_ffn_gu(void * h) { return ((Ffn *) h)->gu; }
 void * onpu_ffn_dn(void * h) { return ((Ffn *) h)->dn; }
 int onpu_ffn_fused(void * h) { return ((Ffn *) h)->fused ? 1 : 0; }
 void onpu_ffn_perm(void * h, int32_t * out) {
-    for (int64_t i = 0; i < ((Ffn *) h)->gu->N; i++) out[i] = (int32_t) i;
+    const auto & p = ((Ffn *) h)->perm;
+    std::copy(p.begin(), p.end(), out);
 }
 void onpu_ffn_free(void * h) {
     std::lock_guard<std::mutex> lk(g_mu);
@@ -1374,9 +1446,13 @@ void onpu_chain_free(void * h) {
 }
 
 // ---------------------------------------------------------------- packing
+// q4nx and q4s (sym 0 / 1): the reference's NPU packing, byte for byte (pack_mat,
+// opennpu_core.hpp:174-254), which the handles of the reference calls take in their *_buf memory;
+// this library's formats 2 and 3: their staging layout, zero-padded to nbytes
 int64_t onpu_pack(const float * W, int64_t N, int64_t K, int ncols, int sym, uint8_t * out, int threads) {
     const RefGeom g = ref_geometry(N, K, ncols, sym != 0);
     if (!g.ok || !fmt_valid(sym) || K % fmt_group(sym) != 0) return 0;
+    if (sym == ONPU_Q4NX || sym == ONPU_Q4S) return pack_npu(sym, W, N, K, g, out, threads) ? g.nbytes : 0;
     const int64_t sb = stage_bytes(sym, N, K);
     if (sb > g.nbytes) return 0;
     if (!pack_staging(sym, W, N, K, out, threads)) return 0;

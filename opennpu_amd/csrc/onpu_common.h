@@ -92,3 +92,50 @@ ONPU_HD float f16_to_f32(uint16_t h) {
 
 // nibble position of element e (0..7) inside a dword D_j
 ONPU_HD int nib_pos(int e) { return (e >> 1) + 4 * (e & 1); }
+
+// The reference's NPU packing (opennpu_core.hpp:174-254, Mat.pack model.py:189-217), the byte layout
+// of the *_buf memory of handles the reference calls create (q4nx and q4s), so that packed bytes,
+// also those the reference's own library or its numpy packer wrote (npu4's PackCache files,
+// model.py:712-759), mean the same thing here. With the Mat geometry (R row blocks of rows_col rows x
+// S K-slices of ks = 256 kc columns): column block c = r S + s at c * cb bytes; inside it, packets of
+// 64 rows x 256 columns in the order [tile t][K step kk][core row cr], a packet holding the rows
+// cr * tiles * 64 + t * 64 + [0, 64) and columns kk * 256 + [0, 256): nibbles
+// [8 row octets][32 column octets][8 columns][4 bytes of two rows, the even row in the low nibble],
+// then bf16 scales [8 groups of 32][64 rows] and (q4nx) mins likewise. Rows and columns past the
+// matrix hold code 8 (q4s) or 0 (q4nx) with zero scales; a column block with no rows or columns of
+// the matrix is all zero bytes.
+struct NpuGeom {
+    int64_t S, tiles, kc, ks, rows_col, cb, pkt;
+};
+
+ONPU_HD NpuGeom npu_geom(int64_t S, int64_t tiles, int64_t kc, int64_t ks, int64_t rows_col, int64_t cb, int sym) {
+    NpuGeom g;
+    g.S = S; g.tiles = tiles; g.kc = kc; g.ks = ks; g.rows_col = rows_col; g.cb = cb;
+    g.pkt = 64 * 256 / 2 + (sym ? 1 : 2) * 2 * 8 * 64;
+    return g;
+}
+
+// byte offset of the packet holding weight (n, k); its row within the packet (0..63) and column
+// within the packet's 256 (0..255)
+ONPU_HD int64_t npu_packet(const NpuGeom & g, int64_t n, int64_t k, int & prow, int & pcol) {
+    const int64_t r = n / g.rows_col, lr = n - r * g.rows_col, s = k / g.ks, lc = k - s * g.ks;
+    const int64_t cr = lr / (g.tiles * 64), t = (lr - cr * g.tiles * 64) / 64, kk = lc / 256;
+    prow = (int) (lr % 64);
+    pcol = (int) (lc % 256);
+    return (r * g.S + s) * g.cb + ((t * g.kc + kk) * 4 + cr) * g.pkt;
+}
+
+// byte holding the code of weight (n, k) and the nibble's shift in it
+ONPU_HD int64_t npu_code_byte(const NpuGeom & g, int64_t n, int64_t k, int & shift) {
+    int pr, pc;
+    const int64_t p = npu_packet(g, n, k, pr, pc);
+    shift = 4 * (pr & 1);
+    return p + (pr >> 3) * 1024 + (pc >> 3) * 32 + (pc & 7) * 4 + ((pr & 7) >> 1);
+}
+
+// byte offset of the bf16 scale of the 32-group of weight (n, k); the min (q4nx) is 1024 bytes on
+ONPU_HD int64_t npu_scale_off(const NpuGeom & g, int64_t n, int64_t k) {
+    int pr, pc;
+    const int64_t p = npu_packet(g, n, k, pr, pc);
+    return p + 64 * 256 / 2 + ((pc >> 5) * 64 + pr) * 2;
+}

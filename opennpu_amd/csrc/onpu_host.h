@@ -15,5 +15,7 @@ bool pack_staging(int fmt, const float * W, int64_t N, int64_t K, uint8_t * out,
 // GGUF Q4_K rows (K / 256 super-blocks of 144 bytes each, rows ld bytes apart) -> q4nx staging
 bool pack_q4k_staging(const uint8_t * blocks, int64_t ld, int64_t N, int64_t K, uint8_t * out, int threads);
 void dequant_staging(int fmt, const uint8_t * st, int64_t N, int64_t K, float * out, int threads);
+// W [N][K] -> the reference's NPU packing (q4s when sym, else q4nx) in geometry rg (rg.nbytes bytes)
+bool pack_npu(int sym, const float * W, int64_t N, int64_t K, const RefGeom & rg, uint8_t * out, int threads);
 
 }  // namespace onpu

@@ -615,6 +615,45 @@ hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s) {
 
 int64_t argmax_parts(int64_t N) { return (N + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK; }
 
+// The reference's NPU packing (onpu_common.h) -> the staging layout (q4nx, q4s). One workgroup per
+// (packed row r, 512 columns) of expert blockIdx.y: thread j gathers the codes of columns 2j, 2j + 1
+// into one staging byte, threads 0..15 the scale (and min) of the chunk's groups. Packed row r is
+// staging row rowmap[r] (r without a map).
+__global__ __launch_bounds__(256) void k_npu_stage(const uint8_t * __restrict__ src, int64_t sstride, NpuGeom g,
+                                                   int sym, const int32_t * __restrict__ rowmap, int64_t N, int64_t K,
+                                                   int64_t kch, uint8_t * __restrict__ dst, int64_t dstride) {
+    const int64_t r = blockIdx.x / kch, c0 = (int64_t) (blockIdx.x % kch) * 512;
+    const uint8_t * S = src + (int64_t) blockIdx.y * sstride;
+    uint8_t * D = dst + (int64_t) blockIdx.y * dstride;
+    const int64_t n = rowmap ? rowmap[r] : r;
+    const int64_t k = c0 + 2 * (int64_t) threadIdx.x;
+    if (k < K) {
+        int s0, s1;
+        const int64_t o0 = npu_code_byte(g, r, k, s0), o1 = npu_code_byte(g, r, k + 1, s1);
+        D[n * (K / 2) + k / 2] = (uint8_t) (((S[o0] >> s0) & 15) | (((S[o1] >> s1) & 15) << 4));
+    }
+    const int64_t kg = c0 + 32 * (int64_t) threadIdx.x;
+    if (threadIdx.x < 16 && kg < K) {
+        const int64_t so = npu_scale_off(g, r, kg), G = K / 32;
+        uint16_t * sc = (uint16_t *) (D + N * K / 2);
+        sc[n * G + kg / 32] = (uint16_t) (S[so] | (S[so + 1] << 8));
+        if (!sym) sc[N * G + n * G + kg / 32] = (uint16_t) (S[so + 1024] | (S[so + 1025] << 8));
+    }
+}
+
+hipError_t launch_npu_stage(int fmt, const uint8_t * src, int64_t sstride, const NpuGeom & g, const int32_t * rowmap,
+                            int64_t N, int64_t K, uint8_t * dst, int64_t dstride, int64_t E, hipStream_t s) {
+    if ((fmt != ONPU_Q4NX && fmt != ONPU_Q4S) || N <= 0 || K <= 0 || K % 32 || E <= 0 || E > 65535 ||
+        dstride < stage_bytes(fmt, N, K) || g.S * g.ks < K)
+        return hipErrorInvalidValue;
+    const int64_t kch = (K + 511) / 512;
+    if (N * kch > INT32_MAX) return hipErrorInvalidValue;
+    k_npu_stage<<<dim3((unsigned) (N * kch), (unsigned) E), 256, 0, s>>>(src, sstride, g, fmt == ONPU_Q4S, rowmap, N,
+                                                                        K, kch, dst, dstride);
+    CHECK_LAUNCH();
+    return hipSuccess;
+}
+
 // ------------------------------------------------------------------ argmax scratch without allocation
 // For callers that cannot allocate (graph capture, serving loops): the argmax's row counters and
 // per-workgroup keys live in this file-scope array, ARGMAX_SCRATCH_BYTES per GPU, held until the

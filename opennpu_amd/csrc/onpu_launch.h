@@ -205,6 +205,10 @@ hipError_t launch_chain(int fmt, int ring, const ChainArgs & a, const ChainEntry
                         hipStream_t s);
 // workgroups of the chained kernel that fit one CU at this LDS size
 int chain_occupancy(int fmt, int ring, size_t lds);
+// experts [0, E) of the reference's NPU packing in geometry g (src, sstride apart) -> the staging
+// layout (dst, dstride apart); packed row r becomes staging row rowmap[r] (r when rowmap is null)
+hipError_t launch_npu_stage(int fmt, const uint8_t * src, int64_t sstride, const NpuGeom & g, const int32_t * rowmap,
+                            int64_t N, int64_t K, uint8_t * dst, int64_t dstride, int64_t E, hipStream_t s);
 // p[0, n) = 0 by a kernel on stream s (a graph node under capture, unlike a memset)
 hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s);
 // y[t] = sum_j w[t][j] o[inv[t k + j]] (o bf16 rows, fp32 sum)

@@ -1,6 +1,6 @@
-// Load-time host code of libonpu_hip: the reference geometry (reported for compatibility) and the
-// weight quantizers behind onpu_pack / onpu_quant_dequant, writing the staging layout
-// (include/onpu.h). Nothing here runs per token.
+// Load-time host code of libonpu_hip: the reference geometry, the weight quantizers behind onpu_pack /
+// onpu_quant_dequant, writing the staging layout (include/onpu.h) or the reference's NPU packing
+// (onpu_common.h). Nothing here runs per token.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -114,6 +114,54 @@ bool pack_staging(int fmt, const float * W, int64_t N, int64_t K, uint8_t * out,
 bool pack_q4k_staging(const uint8_t * blocks, int64_t ld, int64_t N, int64_t K, uint8_t * out, int threads) {
     if (N <= 0 || K <= 0 || K % 256 != 0 || ld < K / 256 * Q4K_BLOCK) return false;
     parallel_rows(N, threads, [&](int64_t a, int64_t b) { q4k_rows(blocks, ld, N, K, a, b, out); });
+    return true;
+}
+
+// W [N][K] -> the reference's NPU packing (onpu_common.h) in Mat geometry rg, rg.nbytes at out, with
+// the q4s (sym) or q4nx quantizers of onpu_codec.h. Column blocks are first filled with their padding
+// (all zero when the block holds no weight; else code 8 (q4s) or 0 (q4nx) and zero parameters), then
+// every group of 32 is quantized and its codes and parameters written at their places. Threads take
+// pairs of rows, which share their bytes.
+bool pack_npu(int sym, const float * W, int64_t N, int64_t K, const RefGeom & rg, uint8_t * out, int threads) {
+    if (!rg.ok || N <= 0 || K <= 0 || K % 32 != 0) return false;
+    const NpuGeom g = npu_geom(rg.S, rg.tiles, rg.kc, rg.ks, rg.rows_col, rg.cb, sym);
+    const int64_t npk = rg.tiles * rg.kc * 4;                 // packets per column block
+    for (int64_t c = 0; c < rg.R * rg.S; c++) {
+        uint8_t * blk = out + c * rg.cb;
+        const int64_t r = c / rg.S, sl = c % rg.S;
+        if (r * rg.rows_col >= N || sl * rg.ks >= K) {
+            std::memset(blk, 0, (size_t) rg.cb);
+            continue;
+        }
+        for (int64_t p = 0; p < npk; p++) {
+            std::memset(blk + p * g.pkt, sym ? 0x88 : 0x00, 64 * 256 / 2);
+            std::memset(blk + p * g.pkt + 64 * 256 / 2, 0, (size_t) (g.pkt - 64 * 256 / 2));
+        }
+    }
+    const int64_t pairs = (N + 1) / 2;
+    parallel_rows(pairs, threads, [&](int64_t p0, int64_t p1) {
+        float x[32];
+        uint8_t q[32];
+        for (int64_t n = 2 * p0; n < std::min(N, 2 * p1); n++)
+            for (int64_t k0 = 0; k0 < K; k0 += 32) {
+                std::memcpy(x, W + n * K + k0, sizeof(x));
+                uint16_t sc = 0, mn = 0;
+                if (sym) quant_sym<32>(x, q, sc);
+                else quant_asym32(x, q, sc, mn);
+                for (int i = 0; i < 32; i++) {
+                    int sh;
+                    const int64_t o = npu_code_byte(g, n, k0 + i, sh);
+                    out[o] = (uint8_t) ((out[o] & ~(0xF << sh)) | (q[i] << sh));
+                }
+                const int64_t so = npu_scale_off(g, n, k0);
+                out[so] = (uint8_t) (sc & 0xff);
+                out[so + 1] = (uint8_t) (sc >> 8);
+                if (!sym) {
+                    out[so + 1024] = (uint8_t) (mn & 0xff);
+                    out[so + 1025] = (uint8_t) (mn >> 8);
+                }
+            }
+    });
     return true;
 }
 

@@ -45,7 +45,7 @@ class QMatrix:
 
     def quantize(self, W):
         """Quantize W (fp32 or bf16 cuda tensor [N][>=K], rows contiguous) on the GPU into this
-        matrix, with the format's quantizer (the bytes onpu_pack writes)."""
+        matrix, with the format's quantizer (the codes and parameters onpu_pack writes)."""
         import torch
         assert W.is_cuda and W.dtype in (torch.float32, torch.bfloat16) and W.dim() == 2 and W.stride(1) == 1
         assert W.shape[0] == self.N and W.shape[1] >= self.K

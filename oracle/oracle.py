@@ -314,6 +314,106 @@ def quantize(fmt, W):
     return out
 
 
+def _params(fmt, st, N, K):
+    """bf16 scales [N][K/32] and (q4nx) mins of q4nx / q4s staging bytes"""
+    v = np.asarray(st, np.uint8)[N * K // 2:].view(np.uint16)
+    G = K // 32
+    return v[:N * G].reshape(N, G), (v[N * G:2 * N * G].reshape(N, G) if fmt == FMT_Q4NX else None)
+
+
+def npu_pack(fmt, W, ncols):
+    """W [N][K] fp32 -> the reference's packed bytes for Mat(N, K, ncols, q4s?) (pack_mat,
+    opennpu_core.hpp:230-254, with pack_block_fn :176-215), quantized by quantize(). Column block
+    c = r S + s at c * cb; empty blocks zero. Inside a block, rows_col x ks codes (code 8 for q4s, 0
+    for q4nx, past the matrix) and zero-padded parameters, streamed as packets [tile][K step][core
+    row], each: nibbles [8 row octets][32 column octets][8 columns][4 row pairs] (even row in the low
+    nibble), then bf16 scales [8 groups][64 rows], then (q4nx) mins likewise."""
+    if fmt not in (FMT_Q4NX, FMT_Q4S):
+        raise ValueError("the NPU packing holds q4nx or q4s")
+    W = np.ascontiguousarray(W, np.float32)
+    N, K = W.shape
+    sym = fmt == FMT_Q4S
+    R, S, tiles, kc, ks, rows_col, cb, nbytes = geometry(N, K, ncols, sym)
+    if nbytes == 0:
+        raise ValueError(f"[{N}, {K}] has no geometry on {ncols} columns")
+    st = quantize(fmt, W)
+    q = unpack(fmt, st, N, K)
+    sc, mn = _params(fmt, st, N, K)
+    out = np.zeros(nbytes, np.uint8)
+    for r in range(R):
+        for s in range(S):
+            r0, r1, k0, k1 = r * rows_col, min(N, (r + 1) * rows_col), s * ks, min(K, (s + 1) * ks)
+            if r1 <= r0 or k1 <= k0:
+                continue
+            qb = np.full((rows_col, ks), 8 if sym else 0, np.uint8)
+            qb[:r1 - r0, :k1 - k0] = q[r0:r1, k0:k1]
+            # [core row, tile, packet row (8 octets x 8), K step, packet column (32 octets x 8)]
+            qv = qb.reshape(4, tiles, 8, 8, kc, 32, 8).transpose(1, 4, 0, 2, 5, 6, 3)
+            nib = (qv[..., 0::2] | (qv[..., 1::2] << 4)).reshape(tiles, kc, 4, 8192)
+            parts = [nib]
+            for a in ([sc] if sym else [sc, mn]):
+                pb = np.zeros((rows_col, ks // 32), np.uint16)
+                pb[:r1 - r0, :(k1 - k0) // 32] = a[r0:r1, k0 // 32:k1 // 32]
+                pv = pb.reshape(4, tiles, 64, kc, 8).transpose(1, 3, 0, 4, 2)
+                parts.append(np.ascontiguousarray(pv).view(np.uint8).reshape(tiles, kc, 4, 1024))
+            c = r * S + s
+            out[c * cb:(c + 1) * cb] = np.concatenate(parts, axis=3).ravel()
+    return out
+
+
+def npu_to_stage(fmt, buf, N, K, ncols, rowmap=None):
+    """The inverse of npu_pack's layout: packed bytes of Mat(N, K, ncols) -> staging bytes of fmt;
+    packed row r becomes staging row rowmap[r] (r without a map)."""
+    sym = fmt == FMT_Q4S
+    R, S, tiles, kc, ks, rows_col, cb, nbytes = geometry(N, K, ncols, sym)
+    buf = np.asarray(buf, np.uint8)[:nbytes]
+    q = np.zeros((N, K), np.uint8)
+    pars = [np.zeros((N, K // 32), np.uint16) for _ in range(1 if sym else 2)]
+    npar = len(pars)
+    for r in range(R):
+        for s in range(S):
+            r0, r1, k0, k1 = r * rows_col, min(N, (r + 1) * rows_col), s * ks, min(K, (s + 1) * ks)
+            if r1 <= r0 or k1 <= k0:
+                continue
+            c = r * S + s
+            blk = buf[c * cb:(c + 1) * cb].reshape(tiles, kc, 4, 8192 + npar * 1024)
+            nib = blk[..., :8192].reshape(tiles, kc, 4, 8, 32, 8, 4)
+            qv = np.empty(nib.shape[:-1] + (8,), np.uint8)
+            qv[..., 0::2], qv[..., 1::2] = nib & 15, nib >> 4
+            qb = qv.transpose(2, 0, 3, 6, 1, 4, 5).reshape(rows_col, ks)
+            q[r0:r1, k0:k1] = qb[:r1 - r0, :k1 - k0]
+            for i, a in enumerate(pars):
+                pv = np.ascontiguousarray(blk[..., 8192 + 1024 * i:8192 + 1024 * (i + 1)]).view(np.uint16)
+                pb = pv.reshape(tiles, kc, 4, 8, 64).transpose(2, 0, 4, 1, 3).reshape(rows_col, ks // 32)
+                a[r0:r1, k0 // 32:k1 // 32] = pb[:r1 - r0, :(k1 - k0) // 32]
+    if rowmap is not None:
+        order = np.empty(N, np.int64)
+        order[np.asarray(rowmap)] = np.arange(N)
+        q, pars = q[order], [a[order] for a in pars]
+    codes = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return np.concatenate([codes.ravel()] + [a.ravel().view(np.uint8) for a in pars])
+
+
+def ffn_order(Ng, Kg, Nd, Kd, sym):
+    """The gate_up row packed at each row of a fused FFN's bank (onpu_ffn_perm, onpu_api.cpp:307-322):
+    when the reference fuses the shape (one row block and one K slice per matrix, I = Ng / 2 = Kd a
+    multiple of 256, all Ng rows in one column, Kg <= 2048, an even tile count), its NPU writes a
+    column's outputs as [tile pair][core row][128 rows], and row r of the bank holds the gate_up row
+    that lands at r's output position; else the identity."""
+    perm = np.arange(Ng, dtype=np.int32)
+    gg, gd = geometry(Ng, Kg, 1, sym), geometry(Nd, Kd, 1, sym)
+    I = Ng // 2
+    if not (gg[7] and gd[7] and gg[0] == gg[1] == gd[0] == gd[1] == 1 and Ng % 2 == 0 and Kd == I
+            and I % 256 == 0 and gg[5] == Ng and Kg <= 2048 and gg[2] % 2 == 0):
+        return perm
+    tiles = gg[2]
+    for t2 in range(tiles // 2):
+        for cr in range(4):
+            r = cr * tiles * 64 + t2 * 128
+            perm[r:r + 128] = (t2 * 4 + cr) * 128 + np.arange(128)
+    return perm
+
+
 def stage_q4nx(q, s, m):
     """codes [N][K] + bf16 s, m [N][K/32] -> q4nx staging bytes (low nibble = even k)."""
     q = np.asarray(q, np.uint8)

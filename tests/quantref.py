@@ -1,7 +1,7 @@
-"""Shared by tests/test_quant_ref.py (CPU) and tests/test_codec_gpu.py (GPU): the reference's
-bf16 rounding, Mat geometry and search quantizers built from llama/ggml-opennpu/opennpu_core.hpp
-lines 37-169 (oracle/Makefile `ref`, oracle/ref_core.cpp; outputs in oracle/_ref/), and the weight
-groups the comparisons run on."""
+"""Shared by tests/test_quant_ref.py, tests/test_npu_layout.py (CPU) and tests/test_codec_gpu.py
+(GPU): the reference's bf16 rounding, Mat geometry, search quantizers, packing and output gather
+built from llama/ggml-opennpu/opennpu_core.hpp lines 37-254 and 540-561 (oracle/Makefile `ref`,
+oracle/ref_core.cpp; outputs in oracle/_ref/), and the weight groups the comparisons run on."""
 import ctypes as C
 import subprocess
 from pathlib import Path
@@ -28,7 +28,19 @@ def load(name):
     L.ref_quant_sym32_n.argtypes = [P, I64, P, P]
     L.ref_quant_asym32_n.argtypes = [P, I64, P, P, P]
     L.ref_f2bf_n.argtypes = [P, I64, P]
+    L.ref_pack_mat.restype, L.ref_pack_mat.argtypes = I64, [P, I64, I64, I, I, P]
+    L.ref_gather.argtypes = [I64, I64, I, I, P, P]
     return L
+
+
+def ref_pack(L, fmt, W, ncols):
+    """pack_mat(Mat(N, K, ncols, q4s?), W) by the reference's own code: its nbytes packed bytes"""
+    W = np.ascontiguousarray(W, np.float32)
+    N, K = W.shape
+    nbytes = orc.geometry(N, K, ncols, fmt == orc.FMT_Q4S)[7]
+    out = np.zeros(nbytes, np.uint8)
+    assert L.ref_pack_mat(p(W), N, K, ncols, fmt, p(out)) == nbytes
+    return out
 
 
 def p(a):

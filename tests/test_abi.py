@@ -111,9 +111,28 @@ def test_launch_plans_are_built_variants(fmt):
             assert (kw // k) * bpw >= KB
 
 
+@pytest.mark.parametrize("fmt", [0, 1, 2, 3])
+def test_argmax_epilogue_plans_sum_like_the_store(fmt):
+    """the argmax epilogue's GEMV plan (onpu_dense_argmax_dev) and the plain store's (the no-alloc
+    entry point, which stores logits and then runs the separate argmax) agree in everything that
+    sets the order of the fp32 sums (K parts, blocks per wave, x from LDS or global, row blocks,
+    tile groups per workgroup), for every row count up to 64; only the chunk size may differ"""
+    L = _lib.lib()
+    a, b = (C.c_int64 * 10)(), (C.c_int64 * 10)()
+    for N in (64, 300, 3000, 4096, 6144, 20000, 24576, 151936):
+        for K in (256, 512, 1024, 4096, 12288):
+            if K % orc.group(fmt):
+                continue
+            for M in range(1, 65):
+                L.onpu_plan_gemv(fmt, N, K, M, 1, 0, a)
+                L.onpu_plan_gemv(fmt, N, K, M, 1, 3, b)
+                keep = (0, 1, 3, 4, 5, 6, 7)                 # mb, rt, xl, tw, kw, bpw, gx
+                assert [a[i] for i in keep] == [b[i] for i in keep], (N, K, M, tuple(a), tuple(b))
+
+
 def test_pack_round_trip_q4s():
-    """onpu_pack writes the staging layout with the reference's q4s search quantizer; its
-    dequantization equals onpu_quant_dequant, and its codes and scales equal the oracle's."""
+    """onpu_pack writes the reference's packing with its q4s search quantizer; its dequantization
+    equals onpu_quant_dequant, and its codes and scales equal the oracle's."""
     L = _lib.lib()
     rng = np.random.default_rng(0)
     N, K = 24, 256
@@ -123,7 +142,7 @@ def test_pack_round_trip_q4s():
     out = np.zeros(g[7], np.uint8)
     n = L.onpu_pack(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 8, 1, out.ctypes.data_as(C.POINTER(C.c_uint8)), 2)
     assert n == g[7]
-    st = out[:orc.stage_bytes(1, N, K)]
+    st = orc.npu_to_stage(1, out, N, K, 8)
     deq = orc.dequant(1, st, N, K)
     qd = np.empty_like(W)
     L.onpu_quant_dequant(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 1, qd.ctypes.data_as(C.POINTER(C.c_float)), 2)
@@ -140,8 +159,9 @@ def test_pack_round_trip_q4s():
 
 @pytest.mark.parametrize("fmt", [0, 1, 2, 3])
 def test_pack_equals_oracle_quantize(fmt):
-    """onpu_pack (host quantizers of onpu_codec.h) writes exactly the oracle's staging bytes, for
-    every format, Gaussian weights with a few outliers and an all-zero row"""
+    """onpu_pack (host quantizers of onpu_codec.h) writes exactly the oracle's bytes, for every
+    format (the reference's packing for q4nx / q4s, the staging layout zero-padded for the others),
+    Gaussian weights with a few outliers and an all-zero row"""
     L = _lib.lib()
     rng = np.random.default_rng(20 + fmt)
     N, K = 19, 512
@@ -154,6 +174,9 @@ def test_pack_equals_oracle_quantize(fmt):
     out = np.zeros(g[7], np.uint8)
     n = L.onpu_pack(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 8, fmt, out.ctypes.data_as(C.POINTER(C.c_uint8)), 3)
     assert n == g[7]
+    if fmt in (orc.FMT_Q4NX, orc.FMT_Q4S):
+        assert np.array_equal(out, orc.npu_pack(fmt, W, 8))
+        return
     sb = orc.stage_bytes(fmt, N, K)
     assert np.array_equal(out[:sb], orc.quantize(fmt, W))
     assert not out[sb:].any()

@@ -43,20 +43,20 @@ def test_no_geometry_is_all_zero(L):
 
 @pytest.mark.parametrize("sym,fmt", [(1, orc.FMT_Q4S), (0, orc.FMT_Q4NX)])
 def test_pack_fills_nbytes_and_quant_dequant_reads_it(L, sym, fmt):
-    """onpu_pack writes exactly nbytes (the staging layout, zero padded) and onpu_quant_dequant
-    returns what those bytes dequantize to (the HIPREC residual pass of model.py:816 uses it)"""
+    """onpu_pack writes exactly nbytes (the reference's packing) and onpu_quant_dequant returns what
+    those bytes dequantize to (the HIPREC residual pass of model.py:816 uses it)"""
     rng = np.random.default_rng(0)
     N, K = 40, 256
     W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
     nbytes = ha.geometry(L, N, K, 8, sym)[7]
     buf = np.full(nbytes, 0xAB, np.uint8)
     assert ha.pack_into(L, W, 8, sym, buf.ctypes.data_as(ha.U8P)) == nbytes
-    sb = orc.stage_bytes(fmt, N, K)
-    assert np.array_equal(buf[:sb], orc.quantize(fmt, W))
-    assert not buf[sb:].any()
+    assert np.array_equal(buf, orc.npu_pack(fmt, W, 8))
+    st = orc.npu_to_stage(fmt, buf, N, K, 8)
+    assert np.array_equal(st, orc.quantize(fmt, W))
     qd = np.empty_like(W)
     L.onpu_quant_dequant(ha.fp(W), N, K, sym, ha.fp(qd), 3)
-    assert np.array_equal(qd.view(np.uint32), orc.dequant(fmt, buf[:sb], N, K).view(np.uint32))
+    assert np.array_equal(qd.view(np.uint32), orc.dequant(fmt, st, N, K).view(np.uint32))
 
 
 def test_pack_rejects_k_off_the_group(L):

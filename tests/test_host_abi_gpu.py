@@ -9,9 +9,9 @@ made as plain ctypes calls (tests/hostabi.py) against libonpu_hip on the GPU:
           _dn, then onpu_ffn_run (one token) and onpu_ffn_run_many (model.py:926-1020)
   helpers onpu_moe_act, onpu_moe_sum (onpu_cpu.cpp:233-274)
 
-Expected values come from the oracle alone: the staging bytes are the oracle's quantization of the
-fp32 weights (the library's pack equals it byte for byte, tests/test_host_abi.py), dequantized by the
-reference formula and multiplied in fp64 with the bf16-rounded input (the device's input
+Expected values come from the oracle alone: the packed bytes hold the oracle's quantization of the
+fp32 weights (the library's pack equals the oracle's byte for byte, tests/test_host_abi.py),
+dequantized by the reference formula and multiplied in fp64 with the bf16-rounded input (the device's input
 conversion). Tolerances: fp32 outputs of the GEMV path max|y-r|/max|r| <= 1e-4 (fp32
 accumulation); rows > 64 take the MFMA GEMM, whose weights enter as bf16 RNE of the dequant
 (<= 1e-4 against that, <= 1e-2 against the exact weights); expert FFNs (bf16 activation between the

@@ -2,11 +2,11 @@
 the oracle's restatements (orc_f2bf, orc_geometry, orc_quant_sym32, orc_quant_asym32) and the
 library's host codecs (onpu_geometry2, onpu_pack for q4s and q4nx).
 
-The reference code is lines 37-169 of llama/ggml-opennpu/opennpu_core.hpp (namespace onpu:
-f2bf / bf2f :50-62, Mat :65-97, quant_asym32 :103-138, quant_sym32 :142-169), copied unedited from
-the reference checkout at build time and compiled through oracle/ref_core.cpp (oracle/Makefile
-`ref`; outputs in oracle/_ref/, never committed). Those lines need only standard headers; the XRT
-includes of the header serve the device code after them.
+The reference code is lines 37-254 of llama/ggml-opennpu/opennpu_core.hpp (namespace onpu:
+f2bf / bf2f :50-62, Mat :65-97, quant_asym32 :103-138, quant_sym32 :142-169, pack_mat :174-254),
+copied unedited from the reference checkout at build time and compiled through
+oracle/ref_core.cpp (oracle/Makefile `ref`; outputs in oracle/_ref/, never committed). Those lines
+need only standard headers; the XRT includes of the header serve the device code after them.
 
 Two builds:
 - as written (-ffp-contract=off): the oracle and the library must equal it byte for byte, on more
@@ -27,7 +27,8 @@ import pytest
 
 import oracle.oracle as orc
 from opennpu_amd import _lib
-from tests.quantref import GPR, KINDS, G_PER_KIND, SEEDS, REFCORE, REF, groups, load, p, ref_asym, ref_staging, ref_sym
+from tests.quantref import (GPR, KINDS, G_PER_KIND, SEEDS, REFCORE, REF, groups, load, p, ref_asym, ref_pack,
+                            ref_staging, ref_sym)
 
 
 @pytest.fixture(scope="module")
@@ -45,7 +46,7 @@ def ref_native():
 
 
 def pack(fmt, W):
-    """the library's onpu_pack (host codecs) into a Mat-sized buffer; the staging bytes it wrote"""
+    """the library's onpu_pack (host codecs) for 8 columns: the reference's packed bytes"""
     L = _lib.lib()
     N, K = W.shape
     g = (C.c_int64 * 8)()
@@ -53,35 +54,33 @@ def pack(fmt, W):
     out = np.zeros(g[7], np.uint8)
     n = L.onpu_pack(W.ctypes.data_as(C.POINTER(C.c_float)), N, K, 8, fmt, out.ctypes.data_as(C.POINTER(C.c_uint8)), 8)
     assert n == g[7]
-    sb = orc.stage_bytes(fmt, N, K)
-    assert not out[sb:].any()
-    return out[:sb]
+    return out
 
 
 @pytest.mark.parametrize("kind", KINDS)
 def test_quant_sym32_equals_reference(ref, kind):
-    """q4s: the oracle's orc_quant_sym32 and the library's onpu_pack write the reference's codes and
-    bf16 scales, byte for byte"""
+    """q4s: the oracle's orc_quant_sym32 writes the reference's codes and bf16 scales, and the
+    library's onpu_pack the bytes of the reference's pack_mat, byte for byte"""
     for seed in range(SEEDS):
         X = groups(kind, G_PER_KIND, 1000 * KINDS.index(kind) + seed)
         W, want = ref_staging(ref, orc.FMT_Q4S, X)
         got = orc.quantize(orc.FMT_Q4S, W)
         bad = np.flatnonzero(got != want)
         assert bad.size == 0, f"{kind} seed {seed}: oracle differs at {bad.size} bytes, first {bad[:4]}"
-        assert np.array_equal(pack(orc.FMT_Q4S, W), want), f"{kind} seed {seed}: onpu_pack differs"
+        assert np.array_equal(pack(orc.FMT_Q4S, W), ref_pack(ref, orc.FMT_Q4S, W, 8)), f"{kind} seed {seed}: onpu_pack"
 
 
 @pytest.mark.parametrize("kind", KINDS)
 def test_quant_asym32_equals_reference(ref, kind):
-    """q4nx: the oracle's orc_quant_asym32 and the library's onpu_pack write the reference's codes
-    and bf16 (scale, min) pairs, byte for byte"""
+    """q4nx: the oracle's orc_quant_asym32 writes the reference's codes and bf16 (scale, min) pairs,
+    and the library's onpu_pack the bytes of the reference's pack_mat, byte for byte"""
     for seed in range(SEEDS):
         X = groups(kind, G_PER_KIND, 2000 * KINDS.index(kind) + seed)
         W, want = ref_staging(ref, orc.FMT_Q4NX, X)
         got = orc.quantize(orc.FMT_Q4NX, W)
         bad = np.flatnonzero(got != want)
         assert bad.size == 0, f"{kind} seed {seed}: oracle differs at {bad.size} bytes, first {bad[:4]}"
-        assert np.array_equal(pack(orc.FMT_Q4NX, W), want), f"{kind} seed {seed}: onpu_pack differs"
+        assert np.array_equal(pack(orc.FMT_Q4NX, W), ref_pack(ref, orc.FMT_Q4NX, W, 8)), f"{kind} seed {seed}: onpu_pack"
 
 
 def test_single_group_wrappers_equal_reference(ref):
