@@ -736,11 +736,12 @@ def calibration_copy(torch):
     torch.cuda.synchronize()
 
 
-def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3):
-    """Decode GEMVs alone, for hardware-counter runs: each named Qwen3-8B matrix (g128s, M=1) over
-    its 36 HBM copies (or, for "lm_head", the Q4_0 LM head with its argmax at M = 1 and 5 over 2
-    copies), `reps` eager launches each, in the order given, then one plain 512 MiB device copy
-    (torch copy_) whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters' unit."""
+def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3, rows=(1,)):
+    """Decode GEMVs alone, for hardware-counter runs: each named Qwen3-8B matrix (g128s) at each row
+    count in `rows` over its 36 HBM copies (or, for "lm_head", the Q4_0 LM head with its argmax at
+    M = 1 and 5 over 2 copies), `reps` eager launches each, in the order given, then one plain
+    512 MiB device copy (torch copy_) whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
+    counters' unit."""
     shapes = {name: (N, K) for name, N, K in QWEN3_8B}
     out = []
     for name in names:
@@ -763,16 +764,17 @@ def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3):
         N, K = shapes[name]
         st = syn.weights(G128S, N, K, 100 + N + K, scale_sigma=unit_gain_sigma(K), signed=True)
         mats = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
-        x = bf16_tensor(torch, syn.activations(1, K, K + 1)).reshape(1, K)
-        y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
-        for _ in range(reps):
-            for q in mats:
-                q.mv(x, out=y)
-        torch.cuda.synchronize()
+        for M in rows:
+            x = bf16_tensor(torch, syn.activations(M, K, K + M)).reshape(M, K)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            for _ in range(reps):
+                for q in mats:
+                    q.mv(x, out=y)
+            torch.cuda.synchronize()
+            out.append({"matrix": f"{name} {N}x{K} g128s M={M}", "launches": reps * LAYERS,
+                        "algorithmic_bytes_per_launch": wbytes(G128S, N, K) + M * K * 2 + M * N * 2})
         for q in mats:
             q.free()
-        out.append({"matrix": f"{name} {N}x{K} g128s M=1", "launches": reps * LAYERS,
-                    "algorithmic_bytes_per_launch": wbytes(G128S, N, K) + K * 2 + N * 2})
     calibration_copy(torch)
     print(json.dumps({"profile_target": out, "calibration_copy_bytes": 512 << 20}), flush=True)
 
@@ -831,6 +833,8 @@ def main():
     ap.add_argument("--profile", nargs="?", const="gate_up", default=None,
                     help="only the named decode GEMVs (comma-separated: qkv, o, gate_up, down, lm_head; default "
                          "gate_up) plus a calibration copy, for rocprofv3 --pmc runs")
+    ap.add_argument("--profile-rows", default="1",
+                    help="row counts of the decode GEMVs under --profile (comma-separated, default 1)")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only the prefill GEMMs, for rocprofv3 --pmc runs")
     ap.add_argument("--profile-moe", action="store_true",
@@ -848,7 +852,8 @@ def main():
     require_gpu()
     torch.cuda.set_device(0)
     if args.profile:
-        profile_target(torch, QMatrix, syn, tuple(args.profile.split(",")))
+        profile_target(torch, QMatrix, syn, tuple(args.profile.split(",")),
+                       rows=tuple(int(v) for v in args.profile_rows.split(",")))
         return
     if args.profile_gemm:
         profile_gemm(torch, QMatrix, syn)

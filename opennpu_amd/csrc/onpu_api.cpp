@@ -272,15 +272,18 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     const bool act = epi == EPI_ACT_;
     p.rt = act ? 2 : 1;
+    // two row tiles per wave for a plain store (tile t and t + stride, sharing each x fragment)
+    const int ert = env_int("ONPU_GEMV_RT", 0);
+    if (ert == 2 && epi == EPI_STORE_ && p.mb == 1 && slots == 1) p.rt = 2;
     const int64_t xbytes = (int64_t) M * (KB * 128 + 8) * 2 + KB * (fmt == ONPU_G128S ? 1 : 4) * 64;
     // gfx950 gives a workgroup up to 160 KiB of LDS. x in LDS up to 52 KiB keeps several workgroups
     // per CU; up to 112 KiB (one workgroup per CU) only pays off with many tile groups to share it
-    const int64_t groups0 = act ? NT / 2 : NT;
+    const int64_t groups0 = act ? NT / 2 : (p.rt == 2 ? (NT + 1) / 2 : NT);
     p.xl = (p.mb == 1 && (xbytes <= 52 * 1024 || (xbytes <= 112 * 1024 && groups0 * slots >= 1024))) ? 1 : 0;
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
     if (ex == 1 && p.mb == 1 && xbytes <= 144 * 1024) p.xl = 1;
-    const int64_t groups = act ? NT / 2 : NT;
+    const int64_t groups = groups0;
     // vocabulary-sized matrices (>= 4096 tile groups) stream whole rows per wave (up to 32 blocks)
     // in workgroups of up to 8 tile groups sharing one x copy: measured on the 151936 x 4096 LM head,
     // M = 5: 65.7 us against 75.0 us with two K parts per tile and 4 tiles (M = 1: equal)
@@ -334,7 +337,7 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     // The argmax epilogue takes the same plans, so that its logits equal those of a plain store
     // followed by the separate argmax launch, bit for bit.
     if (M > 1 && p.mb == 1 && (epi == EPI_STORE_ || epi == EPI_ARGMAX_) && !vocab && slots == 1 && ekw == 0 &&
-        etw == 0 && en == 0 && ex < 0) {
+        etw == 0 && en == 0 && ex < 0 && ert == 0) {
         int ckw = 0, ctw = 0, cnb = 0, cxl = -1;
         if (groups <= 256 && KB <= 32) { ckw = 16; ctw = 1; cnb = 1; cxl = 0; }
         else if (KB >= 64) cnb = 1;
@@ -352,6 +355,10 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
             while (tw > 1 && tw * p.kw * p.rt * p.mb > red_kib) tw--;
         }
     }
+    // 5-8 rows, x in LDS, few blocks per wave: the variant that sums x's groups on the MFMAs
+    // (measured: 6144 x 4096 at M = 8, 4 blocks per wave, 8.3 -> 7.5 us; at 16 blocks per wave the
+    // doubled MFMAs cost more than the staging's sums)
+    if (p.xl == 1 && M > 4 && M <= 8 && p.bpw <= 4 && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
     return p;

@@ -494,7 +494,7 @@ DEV void load_chunk(WChunk<FMT, RT, NB> & c, const uint8_t * const (&tb)[RT], co
 }
 
 // The MFMAs of one chunk (blocks c0 .. c0 + NB - 1, those below b1)
-template <int FMT, int MB, int RT, int NB, bool XL, int RV>
+template <int FMT, int MB, int RT, int NB, bool XL, int RV, bool MS = false>
 DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, const XSrc & X, int M, int64_t K,
                        int r, int q, uint32_t mag, f32x4 (&acc)[RT][MB]) {
     if (XL) {                             // x from LDS, one block at a time (short latency)
@@ -504,10 +504,14 @@ DEV void compute_chunk(const WChunk<FMT, RT, NB> & ch, int64_t c0, int64_t b1, c
             load_x_lds<MB>(X, M, c0 + i, r, q, xa);
             f32x4 cs[MB][4];
             constexpr int GPB = FMT == ONPU_G128S ? 1 : 4;
-            for (int mb = 0; mb < MB; mb++)
-                for (int j = 0; j < GPB; j++)
-                    cs[mb][j] = *(const __attribute__((address_space(3))) f32x4 *) (X.xsum + ((c0 + i) * GPB + j) * 16 +
-                                                                                   16 * mb + 4 * q);
+            if (!MS) {                        // the group sums the staging left in LDS
+                for (int mb = 0; mb < MB; mb++)
+                    for (int j = 0; j < GPB; j++)
+                        cs[mb][j] = *(const __attribute__((address_space(3))) f32x4 *) (X.xsum + ((c0 + i) * GPB + j) *
+                                                                                       16 + 16 * mb + 4 * q);
+            } else {                          // on the matrix core (the staging skipped them)
+                xsum_mfma<FMT, MB>(xa, cs);
+            }
             qacc_block<FMT, MB, RT, RV>(ch.ok[i], ch.wv[i], ch.par[i], xa, cs, mag, acc);
         }
     } else {                              // x from global memory, each block's just before its MFMAs
@@ -540,7 +544,7 @@ DEV const uint8_t * qacc_start(WChunk<FMT, RT, NB> & ca, const uint8_t * const (
 
 // the chunk loop after qacc_start (acc accumulates; the caller zeroes it); b1 and last as
 // qacc_start left them
-template <int FMT, int MB, int RT, int NB, bool XL, int RV>
+template <int FMT, int MB, int RT, int NB, bool XL, int RV, bool MS = false>
 DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], const uint8_t * last, int64_t b0,
                    int64_t b1, const XSrc & X, int M, int64_t K, f32x4 (&acc)[RT][MB]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
@@ -551,16 +555,16 @@ DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], co
     int64_t i = 0;
     for (; i + 2 < nc; i += 2) {                     // chunks i + 1 and i + 2 exist
         load_chunk<FMT, RT, NB>(cb, tb, last, b0 + (i + 1) * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL, RV>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV, MS>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
         load_chunk<FMT, RT, NB>(ca, tb, last, b0 + (i + 2) * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL, RV>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV, MS>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
     }
     if (i + 1 < nc) {                                // two chunks left: ca (loaded) and one more
         load_chunk<FMT, RT, NB>(cb, tb, last, b0 + (i + 1) * NB, b1, lane, r);
-        compute_chunk<FMT, MB, RT, NB, XL, RV>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
-        compute_chunk<FMT, MB, RT, NB, XL, RV>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV, MS>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV, MS>(cb, b0 + (i + 1) * NB, b1, X, M, K, r, q, mag, acc);
     } else {
-        compute_chunk<FMT, MB, RT, NB, XL, RV>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
+        compute_chunk<FMT, MB, RT, NB, XL, RV, MS>(ca, b0 + i * NB, b1, X, M, K, r, q, mag, acc);
     }
 }
 
@@ -572,7 +576,7 @@ DEV void qacc_rest(WChunk<FMT, RT, NB> & ca, const uint8_t * const (&tb)[RT], co
 // before the first loads are issued and post() right after (the workgroup's LDS staging of x: its
 // loads first, then the LDS writes and the barrier while the weights stream); every wave calls
 // both, also one with no blocks. (Issuing both chunks before the barrier measured slower.)
-template <int FMT, int MB, int RT, int NB, bool XL, int RV, class Pre, class Post>
+template <int FMT, int MB, int RT, int NB, bool XL, int RV, bool MS, class Pre, class Post>
 DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const uint8_t * safe, const XSrc & X, int M,
                   int64_t K, Pre pre, Post post, f32x4 (&acc)[RT][MB]) {
     for (int rt = 0; rt < RT; rt++)
@@ -581,20 +585,23 @@ DEV void qacc_run(const uint8_t * const (&tb)[RT], int64_t b0, int64_t b1, const
     pre();
     const uint8_t * last = qacc_start<FMT, RT, NB>(ca, tb, b0, b1, safe);
     post();
-    qacc_rest<FMT, MB, RT, NB, XL, RV>(ca, tb, last, b0, b1, X, M, K, acc);
+    qacc_rest<FMT, MB, RT, NB, XL, RV, MS>(ca, tb, last, b0, b1, X, M, K, acc);
 }
 
 // The workgroup's LDS copy of x [M][K] (bf16) for the XL variants, in 16 B units u = tid + i *
 // blockDim; rows are zero-padded from K to Kpad = 128 * KB and followed by the column sums of x per
 // 32-group (G128S: per 128) times xsum_mul, xsum[group][16 MFMA rows] (MB = 1: x row m at
-// perm16(m)). pre() loads the first 4 units per thread and is called before the weight loads are
+// perm16(m)). pre() loads the first PRE units per thread and is called before the weight loads are
 // issued; post() stores them, copies any further units and ends with a barrier, while the weights
-// stream. The first 4 units are buffer loads over x's M rows (the host keeps M * ldx * 2 < 2^31):
+// stream. A unit copied there is loaded after the weights, and its wait then also waits for them,
+// which holds the next weight chunk back by a memory round trip: PRE = 8 covers up to 8 x rows of
+// K = 4096 in a workgroup of 8 waves. The first PRE units are buffer loads over x's M rows (the
+// host keeps M * ldx * 2 < 2^31):
 // units past the rows or past K get an offset out of the buffer's range, which returns zeros
 // without a memory access, so the loads need no branch (a load under a branch gets a wait for
 // every outstanding load at the branch's end, which would hold the weight loads back by a full
 // memory round trip) and no clamped address (which would send every wave to one L2 line).
-template <int FMT, int MB>
+template <int FMT, int MB, int PRE, bool MS>
 struct XStage {
     const uint16_t * x;
     int64_t ldx, K;
@@ -602,13 +609,14 @@ struct XStage {
     int64_t xls;
     float * xsum;
     uint32_t kp8, nunits, bd, xbytes;
-    u32x4 xv[4];
+    bool sums;                                // MS: group sums staged (not at 5-8 rows)
+    u32x4 xv[PRE];
     static constexpr int UPG = (FMT == ONPU_G128S ? 128 : 32) / 8;     // 16 B units per group
 
     __device__ __forceinline__ XStage(const uint16_t * x_, int64_t ldx_, int64_t K_, int64_t KB, int M, uint16_t * xs_,
                                       int64_t xls_, float * xsum_)
         : x(x_), ldx(ldx_), K(K_), xs(xs_), xls(xls_), xsum(xsum_), kp8((uint32_t) KB * 16),
-          nunits((uint32_t) M * (uint32_t) KB * 16), bd(blockDim.x), xbytes((uint32_t) (M * ldx_ * 2)) {}
+          nunits((uint32_t) M * (uint32_t) KB * 16), bd(blockDim.x), xbytes((uint32_t) (M * ldx_ * 2)), sums(!MS || M <= 4 || M > 8) {}
 
     __device__ __forceinline__ u32x4 unit(uint32_t u) const {
         const uint32_t m = u / kp8, k = (u - m * kp8) * 8;
@@ -622,7 +630,7 @@ struct XStage {
     __device__ __forceinline__ void pre() {
         const float inv = 1.0f / (float) kp8;
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void *) x, (short) 0, (int) xbytes, 0x00020000);
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < PRE; i++) {
             if ((uint32_t) i * bd >= nunits) break;
             const uint32_t u = threadIdx.x + i * bd;
             uint32_t m = (uint32_t) ((float) u * inv);
@@ -639,6 +647,7 @@ struct XStage {
             const uint32_t m = u / kp8;
             *LDS_U32X4(xs + (int64_t) m * xls + (u - m * kp8) * 8) = v;
         }
+        if (MS && !sums) return;
         float t = 0.f;
         for (int d = 0; d < 4; d++) t += __uint_as_float(v[d] << 16) + __uint_as_float(v[d] & 0xffff0000u);
         for (int o = UPG / 2; o > 0; o >>= 1) t += __shfl_xor(t, o);
@@ -647,16 +656,16 @@ struct XStage {
             xsum[g * 16 + (MB == 1 ? perm16(m) : m)] = t * xsum_mul<FMT>();
         }
     }
-    // REST: copy units past the first 4 per thread (a kernel that never has them leaves the loop
+    // REST: copy units past the first PRE per thread (a kernel that never has them leaves the loop
     // out: its loads would make the compiler's wait counts after it assume a pending load)
     template <bool REST = true>
     __device__ __forceinline__ void post() {
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < PRE; i++) {
             if ((uint32_t) i * bd >= nunits) break;
             stage(threadIdx.x + i * bd, xv[i]);
         }
         if (REST)
-            for (uint32_t u0 = 4 * bd; u0 < nunits; u0 += bd) {      // same trip count for every lane
+            for (uint32_t u0 = PRE * bd; u0 < nunits; u0 += bd) {    // same trip count for every lane
                 const uint32_t u = u0 + threadIdx.x;
                 stage(u, u < nunits ? unit(u) : (u32x4){0u, 0u, 0u, 0u});
             }
@@ -695,7 +704,9 @@ constexpr int qgemv_lb(int MB, int RT, int NB, int XL) { return (MB == 1 && RT *
 // grid: (tile groups, slots), block: waves * 64 threads. A workgroup holds a.tw tile groups x KW
 // K parts (KW = waves / a.tw): wave w works on tile group w / KW (RT row tiles: t and t + stride,
 // stride = gridDim.x * a.tw) and K part w % KW. Dynamic LDS: the cross-wave reduction buffer
-// (waves * RT * MB KiB), then with XL the x rows [M][xls] bf16 shared by all waves.
+// (waves * RT * MB KiB), then with XL the x rows [M][xls] bf16 shared by all waves. XL = 2 is XL = 1
+// except at 5-8 rows, where x's group sums come from one MFMA per group against a constant B
+// instead of the staging's VALU sums (for waves with few blocks, whose staging dominates).
 //   STORE  : slot = blockIdx.y; y[m][n] = sum of the K parts
 //   ACT    : RT = 2, tiles (gate t, up t + stride); out[m][16 t + r] = silu(g) * u
 //   SLOTSUM: a.tw = 1; wave w -> slot w / ksplit (its expert and x row), K part w % ksplit;
@@ -728,7 +739,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
     // XL: column sums of x per 32-group (G128S: per 128) times xsum_mul after the x rows:
     // xsum[group][16 MFMA rows] (x row m at perm16(m))
     float * xsum = (float *) (xs + (int64_t) a.M * a.xls);
-    XStage<FMT, MB> xst(x, a.ldx, a.K, a.KB, a.M, xs, a.xls, xsum);
+    XStage<FMT, MB, MB == 1 && EPI != EPI_ACT ? 8 : 4, XL == 2> xst(x, a.ldx, a.K, a.KB, a.M, xs, a.xls, xsum);
     int64_t e = 0;
     const bool route = EPI == EPI_ACT && a.logits != nullptr;
     if (route) {
@@ -770,9 +781,9 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         if (XL) xst.post();
     };
     f32x4 acc[RT][MB];
-    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
-    else if (MB == 1 && a.M <= 8) qacc_run<FMT, MB, RT, NB, XL != 0, 2>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
-    else qacc_run<FMT, MB, RT, NB, XL != 0, 4>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
+    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1, false>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
+    else if (MB == 1 && a.M <= 8) qacc_run<FMT, MB, RT, NB, XL != 0, 2, XL == 2>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
+    else qacc_run<FMT, MB, RT, NB, XL != 0, 4, false>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
 
     // cross-wave reduction through LDS: red[wave][((rt * MB + mb) * 4 + v) * 64 + lane]
     for (int rt = 0; rt < RT; rt++)

@@ -268,7 +268,8 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2, EPI_ARGMAX_ = 3 };
     X(0, 1, 1, 1, 0) X(0, 1, 1, 2, 0) X(0, 1, 2, 1, 0) X(0, 2, 1, 1, 0) X(0, 2, 1, 2, 0) X(0, 4, 1, 1, 0) \
     X(1, 1, 2, 1, 1) X(1, 1, 2, 2, 1) X(1, 1, 2, 1, 0) X(1, 2, 2, 1, 0) X(1, 4, 2, 1, 0)                \
     X(2, 1, 1, 1, 0) X(2, 1, 1, 2, 0) X(2, 1, 1, 3, 0)                                                   \
-    X(3, 1, 1, 2, 1) X(3, 1, 1, 1, 1) X(3, 1, 1, 1, 0) X(3, 2, 1, 1, 0) X(3, 4, 1, 1, 0)
+    X(3, 1, 1, 2, 1) X(3, 1, 1, 1, 1) X(3, 1, 1, 1, 0) X(3, 2, 1, 1, 0) X(3, 4, 1, 1, 0)                 \
+    X(0, 1, 1, 1, 2) X(0, 1, 1, 2, 2) X(3, 1, 1, 1, 2) X(3, 1, 1, 2, 2)
 
 // per-format entry points (onpu_fmt.hip compiled with ONPU_FMT_ID = id)
 #define ONPU_FMT_DECL(id)                                                                                   \
