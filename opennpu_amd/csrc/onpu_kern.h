@@ -1460,8 +1460,9 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 }
 
 // ------------------------------------------------------------------ MoE prefill: grouped GEMM
-// Work item = (expert e, first permuted position, rows <= 64) from k_moe_permute; blockIdx.y =
-// item, blockIdx.x = a group of output columns. Workgroup: WV waves x 2 weight tiles, the item's
+// Work item = (expert e, first permuted position, rows <= 64) from k_moe_permute, taken with a group
+// cg of output columns by each workgroup (k_moe_gemm below maps workgroups to (item, cg) so that an
+// item's column groups share one XCD). Workgroup: WV waves x 2 weight tiles, the item's
 // rows of X (gathered) as MBG = ceil(rows / 16) A blocks of 16 rows, MBG chosen per item (the
 // matrix cores do not overlap the dequant's VALU work, so MFMAs on rows past the item cost their
 // full time: with 4096 routed rows over 128 experts an item averages ~32 rows). Per 128-wide K block
@@ -1469,14 +1470,14 @@ __global__ __launch_bounds__(64 * WV, 1) void k_qgemm_sk(GArgs a) {
 // to LDS, each lane from its own row (rows past the item land as zeros), and each wave dequantizes
 // its two weight tiles in registers (the k_qgemm scheme over one expert's weights). Every column
 // group re-reads the item's X, so wider groups (WV = 8) halve that traffic.
-//   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = WV blockIdx.x + w and up tile
+//   WHICH 0 (gate_up + SiLU * up): wave w holds gate tile g = WV cg + w and up tile
 //           g + NT / 2; act[position][16 g + r] = bf16(silu(gate) * up)
-//   WHICH 1 (down): wave w holds tiles 2 WV blockIdx.x + 2 w + {0, 1}; o[position][n] = bf16 (the
+//   WHICH 1 (down): wave w holds tiles 2 WV cg + 2 w + {0, 1}; o[position][n] = bf16 (the
 //           reference device's output precision per expert: its GEMV flushes each row to bf16,
 //           gemv_any.cc:120-130, and the host sums the weighted rows in fp32, onpu_cpu.cpp:259-274)
 // X rows: WHICH 0 token perm[position] / k of x [T][K]; WHICH 1 position of act [T k][K].
 template <int FMT, int WHICH, int WV, int MBG, bool KT>
-DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, u32x4 * xs0, u32x4 * xs1) {
+DEV void moe_gemm_item(const MArgs & a, int64_t cg, int32_t e, int32_t first, int32_t rows, u32x4 * xs0, u32x4 * xs1) {
     // X fragments f = FPW wave + i (i < FPW, f < 4 MBG): (mb, j) = (f / 4, f % 4); FPW divides 4,
     // so that a wave's fragments share one A block and each lane one row
     constexpr int NF = 4 * MBG, FPW0 = (NF + WV - 1) / WV, FPW = FPW0 <= 1 ? 1 : FPW0 <= 2 ? 2 : 4;
@@ -1485,8 +1486,8 @@ DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, 
     const int q = lane >> 4;
     const uint8_t * W = a.W + (int64_t) e * a.estride;
     int64_t t[2];
-    if (WHICH == 0) { t[0] = (int64_t) blockIdx.x * WV + wave; t[1] = t[0] + a.NT / 2; }
-    else { t[0] = (int64_t) blockIdx.x * 2 * WV + 2 * wave; t[1] = t[0] + 1; }
+    if (WHICH == 0) { t[0] = cg * WV + wave; t[1] = t[0] + a.NT / 2; }
+    else { t[0] = cg * 2 * WV + 2 * wave; t[1] = t[0] + 1; }
     const bool ok0 = WHICH == 0 ? t[0] < a.NT / 2 : t[0] < a.NT;
     const bool ok1 = WHICH == 0 ? ok0 : t[1] < a.NT;
     __amdgpu_buffer_rsrc_t wrs[2];
@@ -1582,16 +1583,22 @@ DEV void moe_gemm_item(const MArgs & a, int32_t e, int32_t first, int32_t rows, 
 
 // KT: K % 128 != 0 (launched with KT = false otherwise, so that no block pays for the tail check)
 template <int FMT, int WHICH, bool KT>
+// grid: (column groups G, item slots, a multiple of 8). Workgroup L = x + G y runs on XCD L % 8; its
+// position j = L / 8 there takes item 8 (j / G) + L % 8 and column group j % G, so the G column
+// groups of an item run together on one XCD and fetch the item's X rows into that XCD's L2 once
+// (items in the list's order, the longest first, one per XCD at a time)
 __global__ __launch_bounds__(512, 1) void k_moe_gemm(MArgs a) {
     constexpr int WV = 8;
     __shared__ u32x4 xs0[4 * 4 * 64], xs1[4 * 4 * 64];         // 2 x 16 KiB: up to 4 A blocks
-    const int item = blockIdx.y;
+    const int64_t G = gridDim.x, L = blockIdx.x + G * blockIdx.y, j = L / 8;
+    const int item = (int) (8 * (j / G) + L % 8);
+    const int64_t cg = j % G;
     if (item >= *a.nitems) return;
     const int32_t e = a.items[3 * item], first = a.items[3 * item + 1], rows = a.items[3 * item + 2];
-    if (rows <= 16) moe_gemm_item<FMT, WHICH, WV, 1, KT>(a, e, first, rows, xs0, xs1);
-    else if (rows <= 32) moe_gemm_item<FMT, WHICH, WV, 2, KT>(a, e, first, rows, xs0, xs1);
-    else if (rows <= 48) moe_gemm_item<FMT, WHICH, WV, 3, KT>(a, e, first, rows, xs0, xs1);
-    else moe_gemm_item<FMT, WHICH, WV, 4, KT>(a, e, first, rows, xs0, xs1);
+    if (rows <= 16) moe_gemm_item<FMT, WHICH, WV, 1, KT>(a, cg, e, first, rows, xs0, xs1);
+    else if (rows <= 32) moe_gemm_item<FMT, WHICH, WV, 2, KT>(a, cg, e, first, rows, xs0, xs1);
+    else if (rows <= 48) moe_gemm_item<FMT, WHICH, WV, 3, KT>(a, cg, e, first, rows, xs0, xs1);
+    else moe_gemm_item<FMT, WHICH, WV, 4, KT>(a, cg, e, first, rows, xs0, xs1);
 }
 
 

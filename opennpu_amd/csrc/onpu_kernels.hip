@@ -540,11 +540,11 @@ hipError_t launch_relayout_dec(int fmt, const uint8_t * src, int64_t sstride, in
 }
 
 hipError_t launch_moe_gemm(int fmt, int which, const MArgs & a, int64_t maxitems, hipStream_t s) {
-    if (a.xbytes <= 0 || a.xbytes >= ((int64_t) 1 << 31) || maxitems <= 0 || maxitems > 65535) return hipErrorInvalidValue;
+    if (a.xbytes <= 0 || a.xbytes >= ((int64_t) 1 << 31) || maxitems <= 0 || maxitems > 65528) return hipErrorInvalidValue;
     if (which == 0 && (a.NT % 2 || a.N != 16 * a.NT)) return hipErrorInvalidValue;   // gate | up halves of whole tiles
     constexpr int wv = 8;                                   // k_moe_gemm: 8 waves x 2 weight tiles
     const int64_t gx = which == 0 ? (a.NT / 2 + wv - 1) / wv : (a.NT + 2 * wv - 1) / (2 * wv);
-    const dim3 grid((unsigned) gx, (unsigned) maxitems);
+    const dim3 grid((unsigned) gx, (unsigned) ((maxitems + 7) / 8 * 8));   // item slots: whole XCD rounds
     switch (fmt) {
         case 0: return moe_gemm_f0(which, a, grid, s);
         case 1: return moe_gemm_f1(which, a, grid, s);
