@@ -282,7 +282,7 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     p.xl = (p.mb == 1 && (xbytes <= 52 * 1024 || (xbytes <= 112 * 1024 && groups0 * slots >= 1024))) ? 1 : 0;
     const int ex = env_int("ONPU_GEMV_XL", -1);
     if (ex == 0) p.xl = 0;
-    if (ex == 1 && p.mb == 1 && xbytes <= 144 * 1024) p.xl = 1;
+    if ((ex == 1 || ex == 2) && p.mb == 1 && xbytes <= 144 * 1024) p.xl = ex;
     const int64_t groups = groups0;
     // vocabulary-sized matrices (>= 4096 tile groups) stream whole rows per wave (up to 32 blocks)
     // in workgroups of up to 8 tile groups sharing one x copy: measured on the 151936 x 4096 LM head,
@@ -355,10 +355,12 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
             while (tw > 1 && tw * p.kw * p.rt * p.mb > red_kib) tw--;
         }
     }
-    // 5-8 rows, x in LDS, few blocks per wave: the variant that sums x's groups on the MFMAs
-    // (measured: 6144 x 4096 at M = 8, 4 blocks per wave, 8.3 -> 7.5 us; at 16 blocks per wave the
-    // doubled MFMAs cost more than the staging's sums)
-    if (p.xl == 1 && M > 4 && M <= 8 && p.bpw <= 4 && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
+    // 5-8 rows, x in LDS: the variant that sums x's groups on the MFMAs and leaves them out of LDS.
+    // Measured with the plan pinned, every format, Qwen3-8B QKV and gate+up at M = 5 and 8: 0.4-1.3
+    // us faster per launch (the staging's VALU sums go, and for gate+up at M = 8 the smaller LDS
+    // footprint fits two workgroups per CU); the 151936 x 4096 LM head at M = 5-7 1.2-1.5 us, at
+    // M = 8 87.4 -> 68.7 us (two workgroups per CU instead of one)
+    if (p.xl == 1 && M > 4 && M <= 8 && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
     return p;

@@ -706,7 +706,7 @@ constexpr int qgemv_lb(int MB, int RT, int NB, int XL) { return (MB == 1 && RT *
 // stride = gridDim.x * a.tw) and K part w % KW. Dynamic LDS: the cross-wave reduction buffer
 // (waves * RT * MB KiB), then with XL the x rows [M][xls] bf16 shared by all waves. XL = 2 is XL = 1
 // except at 5-8 rows, where x's group sums come from one MFMA per group against a constant B
-// instead of the staging's VALU sums (for waves with few blocks, whose staging dominates).
+// instead of the staging's VALU sums, and are not kept in LDS.
 //   STORE  : slot = blockIdx.y; y[m][n] = sum of the K parts
 //   ACT    : RT = 2, tiles (gate t, up t + stride); out[m][16 t + r] = silu(g) * u
 //   SLOTSUM: a.tw = 1; wave w -> slot w / ksplit (its expert and x row), K part w % ksplit;
