@@ -355,12 +355,18 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
             while (tw > 1 && tw * p.kw * p.rt * p.mb > red_kib) tw--;
         }
     }
-    // 5-8 rows, x in LDS: the variant that sums x's groups on the MFMAs and leaves them out of LDS.
-    // Measured with the plan pinned, every format, Qwen3-8B QKV and gate+up at M = 5 and 8: 0.4-1.3
-    // us faster per launch (the staging's VALU sums go, and for gate+up at M = 8 the smaller LDS
-    // footprint fits two workgroups per CU); the 151936 x 4096 LM head at M = 5-7 1.2-1.5 us, at
-    // M = 8 87.4 -> 68.7 us (two workgroups per CU instead of one)
-    if (p.xl == 1 && M > 4 && M <= 8 && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
+    // x in LDS, up to 8 rows: the variant that sums x's groups on the MFMAs and leaves them out of
+    // LDS, where it measured faster with the plan pinned (Qwen3-8B shapes, per launch, staged xl = 1
+    // against xl = 2 alternating in one process, repeated on several boxes):
+    //   per-32 formats (q4nx, q4s, Q4_0; four staged sums per block): 0.1-1.0 us faster at every
+    //     shape and row count;
+    //   g128s: 0.4-0.9 us faster at 2-8 rows for waves of at most 4 blocks (QKV); 0.2 us slower at
+    //     one row; for gate+up (8-16 blocks per wave) -1.4 to +1.4 us from box to box, so it
+    //     keeps the staged sums;
+    //   the 151936 x 4096 LM head (Q4_0): 0.6-1.3 us faster at 4-7 rows, 87.4 -> 68.7 us at 8 (its
+    //     workgroup then fits twice per CU), 0.6-1.0 us slower at 1-2 rows.
+    const bool msums = M <= 8 && (vocab ? M >= 4 : fmt != ONPU_G128S || (M > 1 && p.bpw <= 4));
+    if (p.xl == 1 && msums && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
     return p;

@@ -609,14 +609,14 @@ struct XStage {
     int64_t xls;
     float * xsum;
     uint32_t kp8, nunits, bd, xbytes;
-    bool sums;                                // MS: group sums staged (not at 5-8 rows)
+    bool sums;                                // MS: group sums staged (only past 8 rows)
     u32x4 xv[PRE];
     static constexpr int UPG = (FMT == ONPU_G128S ? 128 : 32) / 8;     // 16 B units per group
 
     __device__ __forceinline__ XStage(const uint16_t * x_, int64_t ldx_, int64_t K_, int64_t KB, int M, uint16_t * xs_,
                                       int64_t xls_, float * xsum_)
         : x(x_), ldx(ldx_), K(K_), xs(xs_), xls(xls_), xsum(xsum_), kp8((uint32_t) KB * 16),
-          nunits((uint32_t) M * (uint32_t) KB * 16), bd(blockDim.x), xbytes((uint32_t) (M * ldx_ * 2)), sums(!MS || M <= 4 || M > 8) {}
+          nunits((uint32_t) M * (uint32_t) KB * 16), bd(blockDim.x), xbytes((uint32_t) (M * ldx_ * 2)), sums(!MS || M > 8) {}
 
     __device__ __forceinline__ u32x4 unit(uint32_t u) const {
         const uint32_t m = u / kp8, k = (u - m * kp8) * 8;
@@ -705,7 +705,7 @@ constexpr int qgemv_lb(int MB, int RT, int NB, int XL) { return (MB == 1 && RT *
 // K parts (KW = waves / a.tw): wave w works on tile group w / KW (RT row tiles: t and t + stride,
 // stride = gridDim.x * a.tw) and K part w % KW. Dynamic LDS: the cross-wave reduction buffer
 // (waves * RT * MB KiB), then with XL the x rows [M][xls] bf16 shared by all waves. XL = 2 is XL = 1
-// except at 5-8 rows, where x's group sums come from one MFMA per group against a constant B
+// except up to 8 rows, where x's group sums come from one MFMA per group against a constant B
 // instead of the staging's VALU sums, and are not kept in LDS.
 //   STORE  : slot = blockIdx.y; y[m][n] = sum of the K parts
 //   ACT    : RT = 2, tiles (gate t, up t + stride); out[m][16 t + r] = silu(g) * u
@@ -781,7 +781,7 @@ __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
         if (XL) xst.post();
     };
     f32x4 acc[RT][MB];
-    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1, false>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
+    if (MB == 1 && a.M <= 4) qacc_run<FMT, MB, RT, NB, XL != 0, 1, XL == 2>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
     else if (MB == 1 && a.M <= 8) qacc_run<FMT, MB, RT, NB, XL != 0, 2, XL == 2>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
     else qacc_run<FMT, MB, RT, NB, XL != 0, 4, false>(tb, b0, b1, W, X, a.M, a.K, pre, post, acc);
 

@@ -390,9 +390,9 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
     if (waves < 1 || waves > qgemv_max_waves(mb, rt, nb, xl) || !qgemv_has_variant(epi, mb, rt, nb, xl))
         return hipErrorInvalidValue;
     const size_t red = (size_t) waves * rt * mb * 1024;
-    // x rows, then the column sums [KB * groups per block][16] floats (not with xl = 2 at 5-8 rows,
+    // x rows, then the column sums [KB * groups per block][16] floats (not with xl = 2 up to 8 rows,
     // which sums on the MFMAs)
-    const bool sums = xl == 1 || (xl == 2 && (a.M <= 4 || a.M > 8));
+    const bool sums = xl == 1 || (xl == 2 && a.M > 8);
     const size_t xb = xl ? (size_t) a.M * a.xls * 2 + (sums ? (size_t) a.KB * (fmt == 2 ? 1 : 4) * 64 : 0) : 0;
     if (xl && (a.M > 16 || (int64_t) a.M * a.ldx * 2 >= ((int64_t) 1 << 31))) return hipErrorInvalidValue;
     // gfx950: 160 KiB per workgroup (the argmax epilogue's row keys take 1 KiB of static LDS)
