@@ -93,6 +93,21 @@ def test_gemv_qwen3_8b(gpu, name, N, K, M):
     check_bf16_out(y, orc.qmm(orc.FMT_G128S, st, N, K, xb), what=f"{name} M {M}")
 
 
+@pytest.mark.parametrize("fmt,N,K,M", [(orc.FMT_Q4NX, 24576, 4096, 8), (orc.FMT_Q4S, 6144, 4096, 1),
+                                       (orc.FMT_Q4S, 6144, 4096, 5), (orc.FMT_Q4_0, 4096, 12288, 1),
+                                       (orc.FMT_Q4NX, 4096, 4096, 1), (orc.FMT_G128S, 6144, 4096, 2)])
+def test_gemv_group_sum_variants(gpu, fmt, N, K, M):
+    """Qwen3-8B shapes whose plans take x's group sums from the MFMAs (per-32 formats up to 8 rows,
+    g128s waves of at most 4 blocks at 2-8 rows), every output row against the oracle."""
+    import ctypes as C
+    from opennpu_amd import _lib
+    o = (C.c_int64 * 10)()
+    _lib.lib().onpu_plan_gemv(fmt, N, K, M, 1, 0, o)
+    assert o[3] == 2, tuple(o)                       # the case exercises the MFMA-sum variant
+    st, xb, y = _mv(fmt, N, K, M, 7 + K + N + M)
+    check_bf16_out(y, orc.qmm(fmt, st, N, K, xb), what=f"fmt {fmt} {N}x{K} M {M}")
+
+
 def test_gemv_config0(gpu):
     """M=1, K=N=4096 g128s, seed 0."""
     st, xb, y = _mv(orc.FMT_G128S, 4096, 4096, 1, 0)
@@ -294,9 +309,10 @@ def test_scratch_over_a_model_of_handles(gpu):
         mats[0].L.onpu_release_scratch()
 
 
-@pytest.mark.parametrize("M", [1, 5])
+@pytest.mark.parametrize("M", [1, 5, 8])
 def test_lm_head_q4_0(gpu, M):
-    """151936 x 4096 GGUF Q4_0 LM head: fp32 logits and argmax (first maximum)."""
+    """151936 x 4096 GGUF Q4_0 LM head: fp32 logits and argmax (first maximum). M = 5 and 8 run the
+    MFMA group-sum variant (at 8 its workgroups fit twice per CU only without the staged sums)."""
     from opennpu_amd.device import QMatrix
     N, K = 151936, 4096
     st = syn.weights(orc.FMT_Q4_0, N, K, 4)
