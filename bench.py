@@ -42,7 +42,7 @@ QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("
 # HBM bytes moved per gate+up launch (M=1), from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of
 # `bench.py --profile`, each scaled by what the counter reads for a plain 512 MiB copy
 # (profiles/qgemv_g128s_gate_up_24576x4096_pmc.md); a hardware-counter figure, not re-measured here
-GATE_UP_TRAFFIC = 52_196_527
+GATE_UP_TRAFFIC = 52_218_291
 
 
 def log(*a):
