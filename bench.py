@@ -739,18 +739,19 @@ def calibration_copy(torch):
 def profile_target(torch, QMatrix, syn, names=("gate_up",), reps=3, rows=(1,)):
     """Decode GEMVs alone, for hardware-counter runs: each named Qwen3-8B matrix (g128s) at each row
     count in `rows` over its 36 HBM copies (or, for "lm_head", the Q4_0 LM head with its argmax at
-    M = 1 and 5 over 2 copies), `reps` eager launches each, in the order given, then one plain
+    M = 1 and 5, or at the row counts given when they are not just 1, over 2 copies), `reps` eager
+    launches each, in the order given, then one plain
     512 MiB device copy (torch copy_) whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
     counters' unit."""
     shapes = {name: (N, K) for name, N, K in QWEN3_8B}
     out = []
     for name in names:
         if name == "lm_head":
-            # the Q4_0 151936 x 4096 LM head with its argmax at M = 1 then 5, on 2 copies
+            # the Q4_0 151936 x 4096 LM head with its argmax at M = 1 then 5 (or `rows`), on 2 copies
             N, K = 151936, 4096
             st = syn.weights(Q4_0, N, K, 11)
             mats = [QMatrix(N, K, Q4_0, st) for _ in range(2)]
-            for M in (1, 5):
+            for M in ((1, 5) if tuple(rows) == (1,) else rows):
                 x = bf16_tensor(torch, syn.activations(M, K, 12)).reshape(M, K)
                 for _ in range(reps):
                     for q in mats:
