@@ -108,6 +108,29 @@ def test_gemv_group_sum_variants(gpu, fmt, N, K, M):
     check_bf16_out(y, orc.qmm(fmt, st, N, K, xb), what=f"fmt {fmt} {N}x{K} M {M}")
 
 
+# one shape per launch-plan class of plan_gemv (onpu_api.cpp): <= 256 tile groups with K <= 4096,
+# K >= 8192, <= 512 tile groups, >= 1024 tile groups (the rule taken at M > 4), vocabulary-sized;
+# ragged N where the class allows it
+PLAN_CLASS_SHAPES = [(2048, 2048), (1000, 8192), (6000, 2048), (17000, 1024), (70000, 512)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_gemv_plan_classes(gpu, fmt):
+    """every plan class of the decode GEMV at 1-13 rows, all formats, every output row against the
+    oracle; the cases take x from global memory, staged with VALU sums and staged with MFMA sums"""
+    import ctypes as C
+    from opennpu_amd import _lib
+    o = (C.c_int64 * 10)()
+    seen = set()
+    for i, (N, K) in enumerate(PLAN_CLASS_SHAPES):
+        for M in (1, 3, 6, 8, 13):
+            _lib.lib().onpu_plan_gemv(fmt, N, K, M, 1, 0, o)
+            seen.add(o[3])
+            st, xb, y = _mv(fmt, N, K, M, 31 * i + M + fmt)
+            check_bf16_out(y, orc.qmm(fmt, st, N, K, xb), what=f"fmt {fmt} {N}x{K} M {M} plan {tuple(o)}")
+    assert seen == {0, 1, 2}, seen
+
+
 def test_gemv_config0(gpu):
     """M=1, K=N=4096 g128s, seed 0."""
     st, xb, y = _mv(orc.FMT_G128S, 4096, 4096, 1, 0)
