@@ -665,7 +665,14 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
 hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, int64_t T, int k, int renorm, int E,
                            int32_t * ids, float * w, void * y, int yf32, hipStream_t s) {
     Mat4 * gu = f->gu, * dn = f->dn;
-    const int64_t I = gu->N / 2, S = I / 32, NTq = (dn->g.NT + 3) / 4;
+    // values of I per workgroup: 16 while every workgroup still gets a CU of its own (a workgroup's
+    // ~100 KB of loads in flight arrive at a fixed rate per CU, so halving them halves that phase),
+    // else 32. Measured at Qwen3-30B-A3B, T = 1 (I 768; k slots: 48 k workgroups of 16 values against
+    // 24 k of 32): 12.4-13.8 against 14.2-15.9 us for k = 1..5, 18.0 against 16.1 us at k = 6
+    const int64_t I = gu->N / 2;
+    const int esv = env_int("ONPU_DS_SV", 0);
+    const int sv = esv == 16 || esv == 32 ? esv : (T * k * (I / 16) <= device().cus ? 16 : 32);
+    const int64_t S = I / sv, NTq = (dn->g.NT + 3) / 4;
     if (T > env_int("ONPU_MOE_DSPLIT_MAX_T", 1) || !dn->dec || gu->fmt != dn->fmt || dn->K != I || !moe_dsplit_fits(gu->K, I, dn->N, gu->g.KB, (int) T, k, E))
         return hipErrorNotSupported;
     hipError_t e = f->ds_part.ensure((size_t) (DS_MAX_T * DS_MAX_K) * (size_t) (S * NTq * 64) * 4);
@@ -676,7 +683,7 @@ hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, in
     a.H = gu->K; a.I = I; a.S = S;
     a.x = x; a.logits = logits; a.E = E; a.k = k; a.renorm = renorm; a.T = (int) T;
     a.ids = ids; a.w = w; a.part = f->ds_part.as<float>();
-    if ((e = launch_moe_dsplit(gu->fmt, a, dn->N, s)) != hipSuccess) return e;
+    if ((e = launch_moe_dsplit(gu->fmt, a, dn->N, sv, s)) != hipSuccess) return e;
     return launch_moe_dsum(a.part, S, NTq * 64, w, T, k, dn->N, y, yf32, s);
 }
 

@@ -59,14 +59,26 @@ hipError_t FN(moe_decode)(const MDArgs & a, int gb, int grid, size_t lds, hipStr
     return hipGetLastError();
 }
 
-hipError_t FN(moe_dsplit)(const MSArgs & a, int nw, size_t lds, hipStream_t s) {
+hipError_t FN(moe_dsplit)(const MSArgs & a, int nw, int sv, size_t lds, hipStream_t s) {
     const dim3 grid((unsigned) a.S, (unsigned) (a.T * a.k));
-    const int64_t gb8 = (a.gKB + 1) / 2, dq8 = (a.dNTq + 7) / 8, gb16 = (a.gKB + 3) / 4, dq16 = (a.dNTq + 15) / 16;
-    if (nw == 16 && gb16 <= 4 && dq16 <= 2) k_moe_dsplit<F, 4, 2, 16><<<grid, 1024, lds, s>>>(a);
-    else if (nw == 16 && gb16 <= 8 && dq16 <= 4) k_moe_dsplit<F, 8, 4, 16><<<grid, 1024, lds, s>>>(a);
-    else if (gb8 <= 8 && dq8 <= 4) k_moe_dsplit<F, 8, 4, 8><<<grid, 512, lds, s>>>(a);
-    else if (gb8 <= 16 && dq8 <= 8) k_moe_dsplit<F, 16, 8, 8><<<grid, 512, lds, s>>>(a);
-    else return hipErrorInvalidValue;
+    const int64_t dq8 = (a.dNTq + 7) / 8, dq16 = (a.dNTq + 15) / 16;
+    if (sv == 32) {
+        const int64_t gb8 = (a.gKB + 1) / 2, gb16 = (a.gKB + 3) / 4;
+        if (nw == 16 && gb16 <= 4 && dq16 <= 2) k_moe_dsplit<F, 4, 2, 16, 32><<<grid, 1024, lds, s>>>(a);
+        else if (nw == 16 && gb16 <= 8 && dq16 <= 4) k_moe_dsplit<F, 8, 4, 16, 32><<<grid, 1024, lds, s>>>(a);
+        else if (gb8 <= 8 && dq8 <= 4) k_moe_dsplit<F, 8, 4, 8, 32><<<grid, 512, lds, s>>>(a);
+        else if (gb8 <= 16 && dq8 <= 8) k_moe_dsplit<F, 16, 8, 8, 32><<<grid, 512, lds, s>>>(a);
+        else return hipErrorInvalidValue;
+    } else if (sv == 16) {
+        const int64_t gb8 = (a.gKB + 3) / 4, gb16 = (a.gKB + 7) / 8;
+        if (nw == 16 && gb16 <= 2 && dq16 <= 2) k_moe_dsplit<F, 2, 2, 16, 16><<<grid, 1024, lds, s>>>(a);
+        else if (nw == 16 && gb16 <= 4 && dq16 <= 4) k_moe_dsplit<F, 4, 4, 16, 16><<<grid, 1024, lds, s>>>(a);
+        else if (gb8 <= 4 && dq8 <= 4) k_moe_dsplit<F, 4, 4, 8, 16><<<grid, 512, lds, s>>>(a);
+        else if (gb8 <= 8 && dq8 <= 8) k_moe_dsplit<F, 8, 8, 8, 16><<<grid, 512, lds, s>>>(a);
+        else return hipErrorInvalidValue;
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

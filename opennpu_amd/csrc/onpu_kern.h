@@ -1961,13 +1961,17 @@ DEV void ds_accum(const u32x4 (&wv)[GB][1], const Par<FMT> (&par)[GB][1], int nb
     }
 }
 
-// grid (S slices, T k slots), NW waves (8 or 16). Wave 0 routes the slot's token (from logits) while
-// the others stage x; then wave w loads its gate/up tile (w / P, P = NW / 4: gate tiles 2 s, 2 s + 1,
-// up tiles NT / 2 + 2 s, + 1) over K part w % P (GB blocks at most) and its down superblocks (quads
-// w, w + NW, ..., DQ at most) of step s, all at once. The gate/up partials meet in LDS, act = bf16(silu(g) u) for the 32
-// values, and each wave multiplies act into its down superblocks: A = act on every MFMA row, C starts
-// at the act sum times xsum_mul, so lanes 0..15 end with row r of each of the four tiles.
-template <int FMT, int GB, int DQ, int NW>
+// grid (S slices, T k slots), NW waves (8 or 16); SV = 32 or 16 values of I per slice. Wave 0 routes
+// the slot's token (from logits) while the others stage x; then wave w loads its gate/up tile
+// (w / P, P = NW / (SV / 8) K parts per tile; SV 32: gate tiles 2 s, 2 s + 1, up tiles NT / 2 + 2 s,
+// + 1; SV 16: gate tile s, up tile NT / 2 + s) over K part w % P (GB blocks at most) and its down
+// superblocks (quads w, w + NW, ..., DQ at most) of the slice's 32-wide K step (s, or s / 2 for SV
+// 16, whose slice is half of the step: the lanes of the other two K groups load nothing), all at
+// once. The gate/up partials meet in LDS, act = bf16(silu(g) u) for the slice's values (zero in the
+// rest of the step), and each wave multiplies act into its down superblocks: A = act on every MFMA
+// row, C starts at the act sum times xsum_mul, so lanes 0..15 end with row r of each of the four
+// tiles.
+template <int FMT, int GB, int DQ, int NW, int SV>
 __global__ __launch_bounds__(NW * 64) void k_moe_dsplit(MSArgs a) {
     extern __shared__ float dsl[];
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
@@ -1977,7 +1981,9 @@ __global__ __launch_bounds__(NW * 64) void k_moe_dsplit(MSArgs a) {
               q = lane >> 4;
     const int64_t s = blockIdx.x, slot = blockIdx.y, t = slot / a.k;
     const int j = (int) (slot - t * a.k);
-    constexpr int P = NW / 4;                  // K parts of each gate / up tile
+    static_assert(SV == 32 || SV == 16, "slices of 32 or 16 values of I");
+    constexpr int NTL = SV / 8;                // gate / up tiles per workgroup
+    constexpr int P = NW / NTL;                // K parts of each gate / up tile
     // LDS: x row and its group sums, the gate/up partials [NW][16], act [32] bf16 and its sum
     const int64_t xl = a.gKB * 128;
     uint16_t * xs = (uint16_t *) dsl;
@@ -2006,21 +2012,28 @@ __global__ __launch_bounds__(NW * 64) void k_moe_dsplit(MSArgs a) {
     const int64_t e = s_e;
     // gate / up tile of this wave and its K part
     const int ti = wave / P, h = wave % P;
-    const int64_t tile = (ti < 2 ? 0 : a.gNT / 2) + 2 * s + (ti & 1);
+    const int64_t tile = SV == 32 ? (ti < 2 ? 0 : a.gNT / 2) + 2 * s + (ti & 1) : (ti == 0 ? 0 : a.gNT / 2) + s;
     const uint8_t * tb[1] = {a.Wg + e * a.gstride + tile * a.gKB * BLK};
     const int64_t part = (a.gKB + P - 1) / P, b0 = h * part;
     const int nb = (int) (a.gKB - b0 < part ? (a.gKB - b0 > 0 ? a.gKB - b0 : 0) : part);
     u32x4 wv[GB][1];
     Par<FMT> par[GB][1];
     md_load<FMT, 1, GB>(tb, nb > 0 ? b0 : 0, nb, wv, par);
-    // down superblocks of step s: quads wave + NW i (a quad past the last re-reads quad 0)
-    const uint8_t * wd = a.Wd + e * a.dstride + s * a.dNTq * SB;
+    // down superblocks of the slice's step: quads wave + NW i (a quad past the last re-reads quad 0).
+    // SV 16: the lanes of the other half of the step (K groups q / 2 != s % 2) get an offset past the
+    // range, so their loads return zeros without a memory access (and act is zero there)
+    const int64_t step = SV == 32 ? s : s >> 1;
+    const uint8_t * wd = a.Wd + e * a.dstride + step * a.dNTq * SB;
+    const __amdgpu_buffer_rsrc_t wdr =
+        __builtin_amdgcn_make_buffer_rsrc((void *) wd, (short) 0, (int) (uint32_t) (a.dNTq * SB), 0x00020000);
+    const uint32_t dvo = SV == 32 || (q >> 1) == (int) (s & 1) ? 16u * lane : 0x80000000u;
     u32x4 dv[DQ];
     uint32_t dp[DQ][FMT == ONPU_Q4NX ? 4 : 2];
 #pragma unroll
     for (int i = 0; i < DQ; i++) {
         const int64_t tq = wave + NW * i < a.dNTq ? wave + NW * i : 0;
-        dv[i] = __builtin_nontemporal_load(GLB(const u32x4, wd + tq * SB + 16 * lane));
+        if (SV == 32) dv[i] = __builtin_nontemporal_load(GLB(const u32x4, wd + tq * SB + 16 * lane));
+        else dv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wdr, dvo, (uint32_t) (tq * SB), 2));
         if (FMT == ONPU_Q4NX) {
             const u32x4 p = __builtin_nontemporal_load(GLB(const u32x4, wd + tq * SB + 1024 + 16 * r));
 #pragma unroll
@@ -2038,15 +2051,17 @@ __global__ __launch_bounds__(NW * 64) void k_moe_dsplit(MSArgs a) {
     ds_accum<FMT, GB>(wv, par, nb, xs, xg, nb > 0 ? b0 : 0, acc);
     if (q == 0) red[wave * 16 + r] = acc[0][0][0];
     __syncthreads();
-    if (threadIdx.x < 32) {                     // act of I value 32 s + i: gate / up tile i >> 4, row i & 15
-        const int i = threadIdx.x, tt = i >> 4, rr = i & 15;
+    if (threadIdx.x < 32) {                     // act of the step's K position i
+        // SV 32: I value 32 s + i, gate / up tile i >> 4, row i & 15; SV 16: position i holds I value
+        // 16 s + (i & 15) when i >> 4 == s % 2 (row i & 15 of the slice's gate / up tile), else zero
+        const int i = threadIdx.x, tt = SV == 32 ? i >> 4 : 0, rr = i & 15;
         float g = 0.f, u = 0.f;
 #pragma unroll
         for (int pp = 0; pp < P; pp++) {       // the K parts in order
             g += red[(tt * P + pp) * 16 + rr];
-            u += red[((2 + tt) * P + pp) * 16 + rr];
+            u += red[((NTL / 2 + tt) * P + pp) * 16 + rr];
         }
-        const uint16_t ab = f32_to_bf16(silu_f(g) * u);
+        const uint16_t ab = SV == 32 || (i >> 4) == (int) (s & 1) ? f32_to_bf16(silu_f(g) * u) : (uint16_t) 0;
         act[i] = ab;
         float sum = bf16_to_f32(ab);
         for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o);

@@ -466,8 +466,9 @@ bool moe_dsplit_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int T, int k
            H >= 8 && H % 8 == 0 && gKB >= 1 && (gKB + 1) / 2 <= 16 && Nd >= 1 && NTq <= 8 * 8;
 }
 
-hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, hipStream_t s) {
-    if (!moe_dsplit_fits(a.H, a.I, Nd, a.gKB, a.T, a.k, a.E) || a.S != a.I / 32 || a.gNT * 16 != 2 * a.I ||
+hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, int sv, hipStream_t s) {
+    if (!moe_dsplit_fits(a.H, a.I, Nd, a.gKB, a.T, a.k, a.E) || (sv != 32 && sv != 16) || a.S != a.I / sv ||
+        a.gNT * 16 != 2 * a.I ||
         a.dNTq != ((Nd + 15) / 16 + 3) / 4 || !a.part || (a.logits && (!a.ids || !a.w)) || (!a.logits && !a.ids))
         return hipErrorInvalidValue;
     // 16 waves where each then holds at most 8 blocks and 4 quads (measured against 8 on MI355X), else 8
@@ -478,10 +479,10 @@ hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, hipStream_t 
     const size_t lds = (size_t) a.gKB * 128 * 2 + (size_t) ((a.gKB * GPB + 3) / 4 * 4) * 4 + (size_t) nw * 16 * 4 +
                        32 * 2 + 16;
     switch (fmt) {
-        case 0: return moe_dsplit_f0(a, nw, lds, s);
-        case 1: return moe_dsplit_f1(a, nw, lds, s);
-        case 2: return moe_dsplit_f2(a, nw, lds, s);
-        case 3: return moe_dsplit_f3(a, nw, lds, s);
+        case 0: return moe_dsplit_f0(a, nw, sv, lds, s);
+        case 1: return moe_dsplit_f1(a, nw, sv, lds, s);
+        case 2: return moe_dsplit_f2(a, nw, sv, lds, s);
+        case 3: return moe_dsplit_f3(a, nw, sv, lds, s);
     }
     return hipErrorInvalidValue;
 }

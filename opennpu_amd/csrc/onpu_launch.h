@@ -104,17 +104,17 @@ constexpr int MD_MAX_GB = 4;      // gate_up K blocks per wave (H <= 8 * 4 * 128
 constexpr int MD_MAX_DB = 8;      // down K blocks (I <= 1024)
 
 // MoE decode split along I (k_moe_dsplit, then k_moe_dsum). Workgroup (slice s, slot t k + j) takes
-// the I values [32 s, 32 s + 32) of its slot's expert: their gate and up rows (two row tiles each) give
-// act for those 32 values, which it multiplies into the expert's down weights for the same 32 K values
-// (one MFMA K step, read from the down bank's step-major copy), leaving fp32 partial sums
-// part[slot][s][n]. No workgroup waits for another. k_moe_dsum then forms y[t][n] = sum_j w[t][j]
-// sum_s part[t k + j][s][n] in that order.
+// the I values [SV s, SV s + SV) of its slot's expert (SV = 32, or 16: half of a 32-wide K step):
+// their gate and up rows (SV / 16 row tiles each) give act for those values, which it multiplies
+// into the expert's down weights for the same K values (one MFMA K step, read from the down bank's
+// step-major copy), leaving fp32 partial sums part[slot][s][n]. No workgroup waits for another.
+// k_moe_dsum then forms y[t][n] = sum_j w[t][j] sum_s part[t k + j][s][n] in that order.
 struct MSArgs {
     const uint8_t * Wg;       // gate_up bank: expert e at Wg + e * gstride, [2 I][H] tiled
     int64_t gstride, gNT, gKB;
     const uint8_t * Wd;       // down bank, step-major copy: expert e at Wd + e * dstride
     int64_t dstride, dNTq;    // dNTq = ceil(down row tiles / 4) superblocks per K step
-    int64_t H, I, S;          // S = I / 32 slices
+    int64_t H, I, S;          // S = I / 32 slices of 32 values of I (I / 16 of 16)
     const uint16_t * x;       // [T][H] bf16
     const float * logits;     // [T][E] fp32 -> route in the kernel; nullptr: ids are inputs
     int E, k, renorm, T;
@@ -193,7 +193,8 @@ bool moe_decode_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int64_t dKB,
 // MoE decode split along I (grid S x T k, then the partial sums); hipErrorInvalidValue outside what
 // moe_dsplit_fits allows
 bool moe_dsplit_fits(int64_t H, int64_t I, int64_t Nd, int64_t gKB, int T, int k, int E);
-hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, hipStream_t s);
+// sv: values of I per slice (32 or 16; a.S = a.I / sv)
+hipError_t launch_moe_dsplit(int fmt, const MSArgs & a, int64_t Nd, int sv, hipStream_t s);
 hipError_t launch_moe_dsum(const float * part, int64_t S, int64_t ld, const float * w, int64_t T, int k, int64_t Nd,
                            void * y, int yf32, hipStream_t s);
 // experts [0, E) of a tiled matrix (src, sstride apart) -> their step-major copies (dst, dstride apart)
@@ -283,7 +284,7 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2, EPI_ARGMAX_ = 3 };
     hipError_t qgemm_sk_f##id(const GArgs & a, int cfg, int grid, hipStream_t s);                          \
     hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
     hipError_t moe_decode_f##id(const MDArgs & a, int gb, int grid, size_t lds, hipStream_t s);       \
-    hipError_t moe_dsplit_f##id(const MSArgs & a, int nw, size_t lds, hipStream_t s);                 \
+    hipError_t moe_dsplit_f##id(const MSArgs & a, int nw, int sv, size_t lds, hipStream_t s);         \
     hipError_t relayout_dec_f##id(const uint8_t * src, int64_t sstride, int64_t NT, int64_t KB, uint8_t * dst, \
                                   int64_t dstride, int64_t E, hipStream_t s);                          \
     hipError_t chain_f##id(int ring, const ChainArgs & a, const ChainEntry * ents, int grid, size_t lds,  \

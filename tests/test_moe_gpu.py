@@ -339,11 +339,13 @@ _SPLIT = [(orc.FMT_G128S, 128, 2048, 768, 2048, 8, 1), (orc.FMT_G128S, 128, 2048
           (orc.FMT_Q4_0, 8, 256, 64, 256, 8, 2), (orc.FMT_G128S, 12, 4096, 256, 4000, 4, 2)]
 
 
+@pytest.mark.parametrize("sv", ["16", "32"])
 @pytest.mark.parametrize("fmt,E,H,I,Nd,k,T", _SPLIT)
-def test_moe_decode_split_along_I(gpu, fmt, E, H, I, Nd, k, T, monkeypatch):
-    """The default decode path at T <= 4 (k_moe_dsplit, then k_moe_dsum): each workgroup takes 32
-    values of I of one slot's expert through gate / up, SiLU * up and down from the down bank's
-    step-major copy, no workgroup waiting for another. From logits and from given ids / w, y agrees
+def test_moe_decode_split_along_I(gpu, fmt, E, H, I, Nd, k, T, sv, monkeypatch):
+    """The default decode path at T <= 4 (k_moe_dsplit, then k_moe_dsum): each workgroup takes 16
+    or 32 values of I (ONPU_DS_SV; the library picks 16 while every workgroup gets a CU of its own) of
+    one slot's expert through gate / up, SiLU * up and down from the down bank's step-major copy (a
+    16-value slice is half a 32-wide K step), no workgroup waiting for another. From logits and from given ids / w, y agrees
     with the oracle layer (bf16 bound) and with the two-launch path (an FFN built with
     ONPU_MOE_DSPLIT=0, so without the copy) to fp32 summation order; ids / w equal the router's.
     Ragged down rows (Nd not a multiple of 64), K tails, k up to 16, H = 4096 (the generic variant);
@@ -352,6 +354,7 @@ def test_moe_decode_split_along_I(gpu, fmt, E, H, I, Nd, k, T, monkeypatch):
     from opennpu_amd.device import QFfn
     monkeypatch.delenv("ONPU_MOE_FUSED", raising=False)
     monkeypatch.setenv("ONPU_MOE_DSPLIT_MAX_T", "4")
+    monkeypatch.setenv("ONPU_DS_SV", sv)
     gu = [syn.weights(fmt, 2 * I, H, 1100 + 2 * e) for e in range(E)]
     dn = [syn.weights(fmt, Nd, I, 1101 + 2 * e) for e in range(E)]
     xb = syn.activations(T, H, 1102 + T)
@@ -364,7 +367,7 @@ def test_moe_decode_split_along_I(gpu, fmt, E, H, I, Nd, k, T, monkeypatch):
             f.load(np.concatenate(gu), np.concatenate(dn))
             x = to_torch_bf16(xb).reshape(T, H)
             lgd = torch.from_numpy(lg).cuda()
-            print(f"moe decode split={split} fmt {fmt} E {E} H {H} I {I} Nd {Nd} k {k} T {T}", flush=True)
+            print(f"moe decode split={split} sv={sv} fmt {fmt} E {E} H {H} I {I} Nd {Nd} k {k} T {T}", flush=True)
             y, ids, w = f.decode(lgd, x, k, f32=True)
             y2 = f.ffn(x, ids, w, f32=True)
             torch.cuda.synchronize()
