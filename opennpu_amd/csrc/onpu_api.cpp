@@ -331,6 +331,36 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     const int etw = env_int("ONPU_GEMV_TW", 0);
     if (etw > 0 && etw * p.kw <= maxw && etw * p.kw * p.rt * p.mb <= red_kib && !(act && groups % etw))
         tw = etw;
+    // One x row, plans measured on MI355X for the shapes of larger models (graphs of 36 copies, us per
+    // launch against the rule above; the Qwen3-8B matrices and the LM head keep theirs):
+    //   >= 2048 tile groups: 4 K parts of more blocks (57344 x 8192: 40.9 against 50.6; 34816 x 5120:
+    //     19.4 against 21.8; 51200 x 5120: 26.2 against 29.6)
+    //   x too long for LDS: single-block chunks over 8 K parts, two tile groups per workgroup
+    //     (8192 x 28672: 32.9 against 38.2; 5120 x 25600: 28.2 against 31.6)
+    //   one to two workgroups per CU of at least 5 blocks per wave: twice the tile groups per
+    //     workgroup, so that each CU holds one (5120 x 17408: 13.7 against 17.4; 7168 x 5120: 7.1
+    //     against 7.6; 5120 x 5120: 6.9 against 7.0; 8192 x 8192: 9.1 against 9.2)
+    if (M == 1 && p.mb == 1 && (epi == EPI_STORE_ || epi == EPI_ARGMAX_) && !vocab && slots == 1 && ekw == 0 &&
+        etw == 0 && en == 0 && ex < 0 && ert == 0) {
+        const int64_t cus = device().cus > 0 ? device().cus : 256;
+        int ckw = 0, ctw = 0;
+        if (groups >= 2048) {
+            ckw = 4;
+        } else if (p.xl == 0) {
+            ckw = 8;
+            ctw = 2;
+            if (qgemv_has_variant(epi, p.mb, p.rt, 1, 0)) p.nb = 1;
+        } else if ((groups + tw - 1) / tw > cus && (groups + tw - 1) / tw <= 2 * cus && p.bpw >= 5) {
+            if (2 * tw * p.kw <= maxw) ctw = 2 * tw;
+            else if (p.kw >= 2) { ckw = p.kw / 2; ctw = 2 * tw; }
+        }
+        if (ckw) {
+            p.bpw = (KB + ckw - 1) / ckw;
+            p.kw = (int) ((KB + p.bpw - 1) / p.bpw);
+            tw = std::max(1, std::min(tw, maxw / p.kw));
+        }
+        if (ctw && ctw * p.kw <= maxw && ctw * p.kw * p.rt * p.mb <= red_kib) tw = ctw;
+    }
     // Several x rows (M > 1, one A block, plain store): plans measured per shape class on MI355X (the
     // Qwen3-8B matrices at M = 4 / 8, graphs of 36 copies, us per launch against the rule above). The
     // x copy per workgroup grows with M, so fewer and wider workgroups share it, and long K streams in
