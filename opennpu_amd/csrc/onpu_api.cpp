@@ -370,14 +370,29 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     //   <= 512 tile groups (6144 x 4096): two tile groups per workgroup sharing x in LDS (up to
     //     112 KiB), 6.92 / 8.29 against 8.07 / 8.76
     //   >= 1024 tile groups at M > 4 (24576 x 4096): six tile groups of 2 K parts, 15.06 against 15.50
-    //   K >= 8192 (4096 x 12288): single-block chunks, 10.07 / 10.71 against 10.48 / 11.33
+    //   K >= 8192 (4096 x 12288): single-block chunks, 10.07 / 10.71 against 10.48 / 11.33; with
+    //     x too long for LDS and K >= 16384, 8 K parts of more blocks (8192 x 28672: 33.0 / 36.9
+    //     against 34.4 / 38.4; 5120 x 17408: 20.5 / 23.3 against 22.3 / 24.7)
+    //   >= 2048 tile groups, up to 8 rows (57344 x 8192, 34816 x 5120): six tile groups of 2 K
+    //     parts, x staged with the MFMA group sums where it fits, 48.6 / 61.3 against 67.5 / 79.1 and
+    //     21.9 / 26.9 against 25.5 / 29.0
     // The argmax epilogue takes the same plans, so that its logits equal those of a plain store
     // followed by the separate argmax launch, bit for bit.
     if (M > 1 && p.mb == 1 && (epi == EPI_STORE_ || epi == EPI_ARGMAX_) && !vocab && slots == 1 && ekw == 0 &&
         etw == 0 && en == 0 && ex < 0 && ert == 0) {
         int ckw = 0, ctw = 0, cnb = 0, cxl = -1;
-        if (groups <= 256 && KB <= 32) { ckw = 16; ctw = 1; cnb = 1; cxl = 0; }
-        else if (KB >= 64) cnb = 1;
+        // x rows without their sums, as the MFMA-sum variant (up to 8 rows) stages them
+        const int64_t xrows = (int64_t) M * (KB * 128 + 8) * 2;
+        if (groups >= 2048 && M <= 8) {
+            ckw = 2;
+            ctw = 6;
+            if (xrows + 12 * 1024 + (epi == EPI_ARGMAX_ ? 1024 : 0) <= 163840) cxl = 2;
+        }
+        else if (groups <= 256 && KB <= 32) { ckw = 16; ctw = 1; cnb = 1; cxl = 0; }
+        else if (KB >= 64) {
+            cnb = 1;
+            if (p.xl == 0 && KB >= 128) ckw = 8;
+        }
         else if (groups <= 512) { ctw = 2; cxl = xbytes <= 112 * 1024 ? 1 : -1; }
         else if (groups >= 1024 && M > 4) { ckw = 2; ctw = 6; }
         if (ckw) {
@@ -397,12 +412,12 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     // against xl = 2 alternating in one process, repeated on several boxes):
     //   per-32 formats (q4nx, q4s, Q4_0; four staged sums per block): 0.1-1.0 us faster at every
     //     shape and row count;
-    //   g128s: 0.4-0.9 us faster at 2-8 rows for waves of at most 4 blocks (QKV); 0.2 us slower at
-    //     one row; for gate+up (8-16 blocks per wave) -1.4 to +1.4 us from box to box, so it
-    //     keeps the staged sums;
+    //   g128s: 0.4-0.9 us faster at 2-8 rows for waves of at most 4 blocks (QKV), 0.8 / 1.6 us at
+    //     4 / 8 rows for waves of 5 (7168 x 5120); 0.2 us slower at one row; for gate+up (8-16 blocks
+    //     per wave) -1.4 to +1.4 us from box to box, so that keeps the staged sums;
     //   the 151936 x 4096 LM head (Q4_0): 0.6-1.3 us faster at 4-7 rows, 87.4 -> 68.7 us at 8 (its
     //     workgroup then fits twice per CU), 0.6-1.0 us slower at 1-2 rows.
-    const bool msums = M <= 8 && (vocab ? M >= 4 : fmt != ONPU_G128S || (M > 1 && p.bpw <= 4));
+    const bool msums = M <= 8 && (vocab ? M >= 4 : fmt != ONPU_G128S || (M > 1 && p.bpw < 8));
     if (p.xl == 1 && msums && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
