@@ -419,6 +419,10 @@ Plan plan_gemv(int fmt, int64_t NT, int64_t KB, int M, int64_t slots, int epi) {
     //     workgroup then fits twice per CU), 0.6-1.0 us slower at 1-2 rows.
     const bool msums = M <= 8 && (vocab ? M >= 4 : fmt != ONPU_G128S || (M > 1 && p.bpw < 8));
     if (p.xl == 1 && msums && ex < 0 && qgemv_has_variant(epi, p.mb, p.rt, p.nb, 2)) p.xl = 2;
+    // vocabulary-sized matrices with K parts (K > 4096): single-block chunks (128256 x 8192 and
+    // 151936 x 5120: 83.8 / 63.7 us against 92.8 / 74.9 at M = 1, 100.1 / 73.6 against 101.8 / 81.8
+    // at M = 5; at K = 4096, one K part, the two-block chunks stay faster)
+    if (vocab && p.kw >= 2 && en == 0 && qgemv_has_variant(epi, p.mb, p.rt, 1, p.xl)) p.nb = 1;
     p.tw = tw;
     p.gx = (groups + tw - 1) / tw;
     return p;

@@ -111,9 +111,9 @@ def test_gemv_group_sum_variants(gpu, fmt, N, K, M):
 # one shape per launch-plan class of plan_gemv (onpu_api.cpp): <= 256 tile groups with K <= 4096,
 # K >= 8192, <= 512 tile groups, >= 1024 tile groups (the rule taken at M > 4), vocabulary-sized,
 # and the one-row rules for larger models (>= 2048 tile groups; x too long for LDS; one to two
-# workgroups per CU); ragged N where the class allows it
+# workgroups per CU), vocabulary-sized with two K parts; ragged N where the class allows it
 PLAN_CLASS_SHAPES = [(2048, 2048), (1000, 8192), (6000, 2048), (17000, 1024), (70000, 512), (33600, 1024),
-                     (600, 28672), (5120, 5120)]
+                     (600, 28672), (5120, 5120), (66000, 4224)]
 
 
 @pytest.mark.parametrize("fmt", FMTS)
