@@ -731,6 +731,11 @@ hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, in
     const int64_t S = I / sv, NTq = (dn->g.NT + 3) / 4;
     if (T > env_int("ONPU_MOE_DSPLIT_MAX_T", 1) || !dn->dec || gu->fmt != dn->fmt || dn->K != I || !moe_dsplit_fits(gu->K, I, dn->N, gu->g.KB, (int) T, k, E))
         return hipErrorNotSupported;
+    // only while its workgroups (of 32 values) fit one per CU: past that each CU runs several
+    // ~100-200 KB workgroups in turn and the partial sums grow with I, so the two launches win
+    // (measured at T = 1: Qwen3-235B-A22B experts 47.4 against 33.3 us, Mixtral-8x7B 101.6
+    // against 65.2 us; Qwen3-30B-A3B 16.6 against 18.6 us)
+    if (esv == 0 && T * k * (I / 32) > device().cus) return hipErrorNotSupported;
     hipError_t e = f->ds_part.ensure((size_t) (DS_MAX_T * DS_MAX_K) * (size_t) (S * NTq * 64) * 4);
     if (e != hipSuccess) return e;
     MSArgs a{};
