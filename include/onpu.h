@@ -142,14 +142,15 @@ void onpu_dense_info(void * h, int64_t * out /* [8] */);
 /* dequantized weights of expert e as the GPU stores them: fp32 (bf16 = 0) or bf16 RNE bits */
 int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
 /* y [M][N] = x [M][K] . W^T on `stream` (hipStream_t; NULL: the default stream); x bf16 in HBM,
- * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels, larger M the MFMA GEMM. */
+ * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels (from 24-48 rows up, depending on
+ * N K, the MFMA GEMM, which is faster there), larger M the MFMA GEMM. */
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
-/* Workspace of the calls above. M > 64 runs the split-K prefill GEMM, whose partial tiles and slot
- * words live in a workspace of about 64 MiB (kept until the process ends): one per stream for eager
+/* Workspace of the calls above. The MFMA GEMM splits K (fp32 partials of K ranges, or the partial
+ * tiles and slot words of its 256-row stream-K form above 128 rows) in a workspace of about 64 MiB (kept until the process ends): one per stream for eager
  * calls, one per capture for calls captured into a HIP graph. Its first use allocates it (relaxed
  * capture mode) and clears its slot words with a kernel, both legal under capture, so a first GEMM
  * may be captured (the clearing kernel becomes a node of the graph). The argmax keeps its keys per
- * handle (sized once for 64 rows); beyond 64 rows its counters grow with the rows and are cleared by
+ * handle (sized once for 64 rows); when the rows run the GEMM its counters grow with the rows and are cleared by
  * a kernel. Outgrown workspace buffers are kept until the handle is freed, so a graph captured at a
  * small M keeps valid pointers. Argmax calls on one handle share its keys: order them on one
  * stream. */

@@ -515,9 +515,13 @@ std::vector<std::pair<GskKey, GskWs *>> g_gsk;           // a few streams and gr
 // valid pointers. Its sync words are cleared by a kernel on s (under capture, a node of the graph
 // ahead of the GEMM), so the first call may be captured. Each one is 64 MiB, held until the process
 // ends.
-hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** sync, int32_t ** ctl) {
+size_t gsk_part_bytes() {
     size_t slot = 0;
     for (const GskCfg & c : GSK_CFGS) slot = std::max(slot, (size_t) c.wv * c.mbg * c.ntw * 1024);
+    return slot * (size_t) std::max(device().cus, 0);
+}
+
+hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** sync, int32_t ** ctl) {
     if (cut > device().cus) return hipErrorInvalidValue;
     hipStreamCaptureStatus cst = hipStreamCaptureStatusNone;
     unsigned long long cid = 0;
@@ -537,7 +541,7 @@ hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** s
             delete w;
             return e;
         }
-        e = w->part.ensure(slot * (size_t) device().cus);
+        e = w->part.ensure(gsk_part_bytes());
         if (e == hipSuccess) e = w->sync.ensure((size_t) ints * 4);
         (void) hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess || (e = launch_zero_i32(w->sync.as<int32_t>(), ints, s)) != hipSuccess) {
@@ -624,14 +628,30 @@ hipError_t argmax_gemv(Mat4 * m, const uint16_t * x, int64_t M, float * logits, 
     return launch_argmax_keys(a.akeys, p.gx, M, argmax, s);
 }
 
+// Up to 64 rows: the decode GEMV, whose time grows with the rows, unless the split-K GEMM (about
+// the same time from 8 to 128 rows) is faster. Crossovers measured on MI355X (g128s, us GEMV ->
+// GEMM): 6144 x 4096 at 48 rows 27.9 -> 24.2, 4096 x 4096 none up to 64 (19.5 / 21.6 at 64);
+// 14336 x 4096 at 32 rows 34.2 -> 28.7, 8192 x 8192 34.6 -> 29.5, 4096 x 12288 26.6 / 28.9 (stays);
+// 10240 x 8192 at 24 rows 41.2 -> 34.1, 57344 x 8192 175 -> 131, 151936 x 4096 247 -> 179; at 16 rows
+// the GEMV wins everywhere (57344 x 8192 127 / 129). ONPU_FORCE_GEMM = 1 takes the GEMM, -1 the GEMV.
+bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
+    const int f = env_int("ONPU_FORCE_GEMM", 0);
+    if (M > 64 || f == 1) return false;
+    if (f == -1) return true;
+    const int64_t nk = N * K;
+    return !((M >= 48 && nk >= 20000000) || (M >= 32 && nk >= 56000000) || (M >= 24 && nk >= 80000000));
+}
+
 hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
     if (M <= 0) return hipSuccess;
     const uint8_t * W = m->dev + e * m->dstride;
-    if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0) return gemv_core(m, e, x, M, y, yf32, s);
+    if (rows_take_gemv(M, m->N, m->K)) return gemv_core(m, e, x, M, y, yf32, s);
     int cfg = 0;
     int64_t grid = 0;
     GArgs ga{};
-    if (env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ga) &&
+    // the 256-row tiles of k_qgemm_sk compute at least half padding at M <= 128, where k_qgemm's
+    // 128-row tiles (split along K below) are faster: 57344 x 8192 at M = 96 140 us against 194 us
+    if (M > 128 && env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ga) &&
         M * m->K * 2 < ((int64_t) 1 << 31)) {
         // cut tiles: the R tail tiles (two-phase split) or the workgroup boundaries (stream-K)
         const int64_t cut = ga.sched == 1 ? ga.R : grid;
@@ -650,6 +670,31 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
     if (entw >= 2 && entw <= 4) ntw = entw;
     // the kernel addresses X with 32-bit buffer offsets: launches of at most 2^31 bytes of X rows
     const int64_t rows_max = std::max<int64_t>(128, (((int64_t) 1 << 31) - 1) / (m->K * 2) / 128 * 128);
+    // split-K when the tiles leave CUs without work: S K ranges, S x the workgroups (two per CU at
+    // most, at least 4 K blocks each), fp32 partials in the split-K workspace, then their sum
+    const int64_t wgs = ((M + 127) / 128) * ((m->g.NT + 4 * ntw - 1) / (4 * ntw));
+    int64_t S = 1, kbs = m->g.KB;
+    if (M <= rows_max) {
+        const int es = env_int("ONPU_GEMM_SPLIT", 0);
+        S = es >= 1 ? es : std::min<int64_t>(m->g.KB / 4, 2 * device().cus / wgs);
+        S = std::max<int64_t>(1, std::min<int64_t>(S, m->g.KB));
+        while (S > 1 && (size_t) (S * M * m->N * 4) > gsk_part_bytes()) S--;
+        if (S > 1) {
+            kbs = (m->g.KB + S - 1) / S;
+            S = (m->g.KB + kbs - 1) / kbs;
+        }
+    }
+    if (S > 1) {
+        GArgs a{};
+        int32_t * sync = nullptr, * ctl = nullptr;
+        hipError_t e = gsk_workspace(s, 0, &a.ws, &sync, &ctl);
+        if (e != hipSuccess) return e;
+        a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
+        a.x = x; a.ldx = m->K; a.ldy = m->N; a.yf32 = 1; a.y = a.ws;
+        a.splits = (int) S; a.kbs = kbs;
+        if ((e = launch_qgemm(m->fmt, a, ntw, s)) != hipSuccess) return e;
+        return launch_gemm_split_sum(a.ws, (int) S, M, m->N, y, m->N, yf32, s);
+    }
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         GArgs a{};
         a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = std::min(rows_max, M - r0);
@@ -1009,8 +1054,8 @@ void onpu_dense_mv(void * h, const float * x, int64_t rows, float * y) {
     HIPX(mv_core(m, 0, g_hws[1].as<uint16_t>(), rows, g_hws[2].p, 1, s));
     HIPX(hipMemcpyAsync(y, g_hws[2].p, (size_t) (rows * m->N * 4), hipMemcpyDeviceToHost, s));
     HIPX(hipStreamSynchronize(s));
-    // more than 64 rows run the split-K GEMM, whose partial-tile exchange waits are bounded
-    const int timed_out = rows > 64 ? gsk_take_flag(s) : 0;
+    // more than 128 rows may run the stream-K GEMM, whose partial-tile exchange waits are bounded
+    const int timed_out = rows > 128 ? gsk_take_flag(s) : 0;
     if (timed_out < 0) die("onpu_dense_mv: reading the split-K wait flag", hipErrorUnknown);
     if (timed_out) wait_failed("onpu_dense_mv", "a split-K partial-tile wait", y, rows * m->N);
 }
@@ -1025,11 +1070,11 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
     auto * m = (Mat4 *) h;
     if (M <= 0) return 0;
     // The argmax workspace belongs to the handle (calls that overlap on one handle must not share
-    // it). Up to 64 rows: per-workgroup keys from the GEMV's epilogue, sized once for 64 rows.
+    // it). Rows that run the GEMV: per-workgroup keys from its epilogue, sized once for 64 rows.
     // Otherwise (or with ONPU_ARGMAX_FUSED=0) the argmax launch over the logits, with its keys and
     // per-row counters (grown to the rows of the call; new counters zeroed by a kernel on the stream,
     // and each call leaves them zero). Outgrown buffers are kept, so graphs keep valid pointers.
-    if (M <= 64 && env_int("ONPU_FORCE_GEMM", 0) == 0 && env_int("ONPU_ARGMAX_FUSED", 1)) {
+    if (rows_take_gemv(M, m->N, m->K) && env_int("ONPU_ARGMAX_FUSED", 1)) {
         HIPR(argmax_gemv(m, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;
     }

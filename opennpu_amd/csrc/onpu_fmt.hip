@@ -37,7 +37,7 @@ hipError_t FN(qgemv)(int epi, const QArgs & a, int mb, int rt, int nb, int xl, d
 
 hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
     const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * ntw - 1) / (4 * ntw);
-    const dim3 grid((unsigned) (gm * gn));
+    const dim3 grid((unsigned) (gm * gn * (a.splits > 1 ? a.splits : 1)));
     if (ntw == 4) k_qgemm<F, 4><<<grid, 256, 0, s>>>(a);
     else if (ntw == 3) k_qgemm<F, 3><<<grid, 256, 0, s>>>(a);
     else k_qgemm<F, 2><<<grid, 256, 0, s>>>(a);

@@ -3,11 +3,12 @@
 //
 //   k_repack     staging layout -> tiled HBM layout (onpu_common.h), once per weight upload
 //   k_dequant    tiled -> fp32 or bf16 (RNE) dequantized weights (parity checks)
-//   k_qgemv      M <= 64 rows: the decode GEMV family. Integer MFMA on biased codes (128 + u) in
+//   k_qgemv      up to 64 rows: the decode GEMV family. Integer MFMA on biased codes (128 + u) in
 //                bf16, group scales applied in fp32 between MFMA steps, x column sums from an
 //                extra MFMA against ones; epilogues: store, SiLU(gate) * up, MoE slot sum
-//   k_qgemm      M > 64 (prefill): x tile in LDS, int4 tile dequantized to bf16 RNE((u-8)s) in
-//                registers and fed to v_mfma_f32_16x16x32_bf16, fp32 accumulate
+//   k_qgemm      prefill (and 24-64 rows of larger matrices): x tile in LDS, int4 tile dequantized
+//                to bf16 RNE((u-8)s) in registers and fed to v_mfma_f32_16x16x32_bf16, fp32
+//                accumulate; split along K into fp32 partials when the tiles leave CUs idle
 //   k_moe_gemm   grouped expert products (MoE prompts) over a device work list
 #pragma once
 #include <hip/hip_runtime.h>
@@ -904,7 +905,7 @@ DEV void par_sc(const GPar<FMT> & p, int j, float & s, float & c) {
     }
 }
 
-// Y[M][N] = X[M][K] . deq(W)^T for M > 64. Workgroup: 4 waves, tile 128 rows of X x 64 NTW rows of
+// Y[M][N] = X[M][K] . deq(W)^T (128-row tiles). Workgroup: 4 waves, tile 128 rows of X x 64 NTW rows of
 // W; wave w owns NTW 16-row weight tiles and all 128 X rows (8 x NTW accumulators of 16 x 16).
 // Per 128-wide K block the X tile (32 KiB of MFMA A fragments [mb][j][lane]) sits in one of two
 // LDS buffers. The buffers are filled straight from global memory by buffer_load_dwordx4 ... lds
@@ -1026,6 +1027,21 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
     // GMS M tiles x 64 / GMS N columns, so each X tile and each weight tile is read by many of them
     constexpr int64_t GMS = 4;
     const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * NTW - 1) / (4 * NTW);
+    // split-K: logical workgroups split-major (an XCD's contiguous range holds whole splits, whose
+    // tiles share X columns), K blocks [kb0, kb1), fp32 partials in the split's plane
+    int64_t kb0 = 0, kb1 = a.KB;
+    void * yo = a.y;
+    int64_t ldy = a.ldy;
+    int yf32 = a.yf32;
+    if (a.splits > 1) {
+        const int64_t sp = lid / (gm * gn);
+        lid -= sp * (gm * gn);
+        kb0 = sp * a.kbs;
+        kb1 = kb0 + a.kbs < a.KB ? kb0 + a.kbs : a.KB;
+        yo = a.ws + sp * a.M * a.N;
+        ldy = a.N;
+        yf32 = 1;
+    }
     const int64_t grp = lid / (GMS * gn), in = lid % (GMS * gn);
     const int64_t gms = gm - grp * GMS < GMS ? gm - grp * GMS : GMS;       // M tiles in this group
     const int64_t mblk = grp * GMS + in % gms, nblk = in / gms;
@@ -1060,13 +1076,13 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
     // two register sets for the weights, alternating with the two LDS buffers (no copies)
     u32x4 wa[NTW], wb[NTW];
     GPar<FMT> pa[NTW], pb[NTW];
-    gemm_load_x(xr, xo, 0, ktail && a.KB == 1, a.K, wave, q, xs0);
-    gemm_load_w<FMT, NTW>(wrs, 0, lane, r, wa, pa);
+    gemm_load_x(xr, xo, kb0, ktail && kb0 + 1 == a.KB, a.K, wave, q, xs0);
+    gemm_load_w<FMT, NTW>(wrs, kb0, lane, r, wa, pa);
     __builtin_amdgcn_s_waitcnt(0x0f70);                  // vmcnt(0): the DMA into xs0 is done
     __syncthreads();
     // pairs of blocks, one loop exit (acc merges once); an odd last block after the loop
-    int64_t b = 0;
-    for (; b + 2 <= a.KB; b += 2) {
+    int64_t b = kb0;
+    for (; b + 2 <= kb1; b += 2) {
         // even block from (xs0, wa) while block b + 1 streams into (xs1, wb)
         gemm_load_x(xr, xo, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, xs1);
         gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wb, pb);
@@ -1074,7 +1090,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
         // odd block from (xs1, wb) while block b + 2 streams into (xs0, wa)
-        if (b + 2 < a.KB) {
+        if (b + 2 < kb1) {
             gemm_load_x(xr, xo, b + 2, ktail && b + 3 == a.KB, a.K, wave, q, xs0);
             gemm_load_w<FMT, NTW>(wrs, b + 2, lane, r, wa, pa);
         }
@@ -1082,7 +1098,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
-    if (b < a.KB) gemm_block<FMT, NTW, 8>(xs0, wa, pa, lane, acc);
+    if (b < kb1) gemm_block<FMT, NTW, 8>(xs0, wa, pa, lane, acc);
     // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
 #pragma unroll
     for (int mb = 0; mb < 8; mb++)
@@ -1093,7 +1109,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
             if (n >= a.N) continue;
             for (int v = 0; v < 4; v++) {
                 const int64_t m = m0 + 16 * mb + 4 * q + v;
-                if (m < a.M) store_out(a.y, a.yf32, m * a.ldy + n, acc[mb][i][v]);
+                if (m < a.M) store_out(yo, yf32, m * ldy + n, acc[mb][i][v]);
             }
         }
 }

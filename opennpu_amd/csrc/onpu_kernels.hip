@@ -408,6 +408,10 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
 }
 
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s) {
+    // split-K: every split holds at least one K block, the splits cover all KB, the grid fits 32 bits
+    if (a.splits > 1 && (!a.ws || a.kbs < 1 || (a.splits - 1) * a.kbs >= a.KB || a.splits * a.kbs < a.KB ||
+                         ((a.M + 127) / 128) * ((a.NT + 4 * ntw - 1) / (4 * ntw)) * a.splits >= ((int64_t) 1 << 31)))
+        return hipErrorInvalidValue;
     switch (fmt) {
         case 0: return qgemm_f0(a, ntw, s);
         case 1: return qgemm_f1(a, ntw, s);
@@ -612,6 +616,38 @@ __global__ void k_zero_i32(int32_t * p, int64_t n) {
 hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     k_zero_i32<<<(unsigned) std::min<int64_t>((n + 255) / 256, 1024), 256, 0, s>>>(p, n);
+    CHECK_LAUNCH();
+    return hipSuccess;
+}
+
+// split-K GEMM epilogue: four consecutive columns of a row per thread, the planes added in order
+// (the same fp32 sum whatever the launch shape)
+__global__ __launch_bounds__(256) void k_gemm_split_sum(const float * __restrict__ part, int S, int64_t M, int64_t N,
+                                                        void * __restrict__ y, int64_t ldy, int yf32) {
+    const int64_t plane = M * N, nq = (N + 3) / 4;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < M * nq; i += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t m = i / nq, n0 = 4 * (i % nq);
+        const float * p = part + m * N + n0;
+        if (N % 4 == 0) {                                  // planes and rows 16-byte aligned
+            f32x4 acc = *(const f32x4 *) p;
+            for (int s = 1; s < S; s++) acc += *(const f32x4 *) (p + s * plane);
+            for (int v = 0; v < 4; v++) store_out(y, yf32, m * ldy + n0 + v, acc[v]);
+        } else {
+            for (int v = 0; v < 4 && n0 + v < N; v++) {
+                float acc = p[v];
+                for (int s = 1; s < S; s++) acc += p[s * plane + v];
+                store_out(y, yf32, m * ldy + n0 + v, acc);
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm_split_sum(const float * part, int S, int64_t M, int64_t N, void * y, int64_t ldy, int yf32,
+                                 hipStream_t s) {
+    if (S < 1 || M < 0 || N < 0 || ldy < N) return hipErrorInvalidValue;
+    const int64_t n4 = M * ((N + 3) / 4);
+    if (n4 == 0) return hipSuccess;
+    k_gemm_split_sum<<<(unsigned) std::min<int64_t>((n4 + 255) / 256, 8192), 256, 0, s>>>(part, S, M, N, y, ldy, yf32);
     CHECK_LAUNCH();
     return hipSuccess;
 }

@@ -59,6 +59,11 @@ struct GArgs {
     // blocks [s, KB) of c tiles. sched 0: the ipw ranges above.
     int sched;
     int64_t F, R, s, c;
+    // k_qgemm split-K (splits > 1): the workgroups of split sp take K blocks [sp kbs, (sp + 1) kbs)
+    // of every tile and store fp32 partials to ws + sp M N ([M][N], row stride N); k_gemm_split_sum
+    // adds the splits in order into Y
+    int splits;
+    int64_t kbs;
 };
 constexpr int GSK_SYNC_STRIDE = 16;
 constexpr int GSK_CTL_TAG = 0, GSK_CTL_DONE = 16, GSK_CTL_ERR = 32, GSK_CTL_INTS = 48;
@@ -171,6 +176,10 @@ int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl);
 
 int qgemv_max_waves(int mb, int rt, int nb, int xl);
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
+// Y [M][N] (row stride ldy; bf16 RNE or fp32) = the sum over s = 0 .. S-1, in that order, of
+// part + s M N ([M][N] fp32)
+hipError_t launch_gemm_split_sum(const float * part, int S, int64_t M, int64_t N, void * y, int64_t ldy, int yf32,
+                                 hipStream_t s);
 // k_qgemm_sk configuration: {weight tiles per wave, 16-row A blocks, waves}; rows and columns of the
 // workgroup tile are 16 * MBG and 16 * NTW * WV. (Measured on MI355X against 256 x 64 per wave with
 // one wave per SIMD and 256 x 32 with four waves: both slower, the first by ~30 %; and against

@@ -162,6 +162,117 @@ def test_gemm_ragged(gpu, fmt, M):
     check_gemm(y, fmt, st, N, K, xb, what=f"gemm fmt {fmt} M {M}")
 
 
+# (M, N, K) cases of the 128-row GEMM split along K (mv_core: S = min(KB / 4, 2 x CUs / workgroups)
+# ranges of K blocks): 96 x 1000 x 8192 in 16 ranges of 4 blocks; 130 x 998 x 4096, two row tiles and
+# N % 4 != 0 (the sum's per-element path), in 8; 40 x 14000 x 4096, a GEMM below 65 rows (the
+# crossover rule), in 4
+SPLIT_CASES = [(96, 1000, 8192), (130, 998, 4096), (40, 14000, 4096)]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,N,K", SPLIT_CASES)
+def test_gemm_split_k(gpu, fmt, M, N, K, monkeypatch):
+    """k_qgemm split along K (fp32 partials per range, summed in range order by k_gemm_split_sum):
+    a 384-column slice over all rows and three full rows against the oracle; a second call gives
+    the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges (a shorter last one) and no
+    split agree to fp32 summation order"""
+    import torch
+    from opennpu_amd.device import QMatrix
+    if fmt != orc.FMT_G128S:
+        K -= 32                                       # a K tail inside the last 128-wide block
+    st = syn.weights(fmt, N, K, 51 + M)
+    xb = syn.activations(M, K, 52 + M)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        x = to_torch_bf16(xb).reshape(M, K)
+        y1 = q.mv(x, f32=True)
+        y2 = q.mv(x, f32=True)
+        yb = q.mv(x)
+        monkeypatch.setenv("ONPU_GEMM_SPLIT", "3")
+        y3 = q.mv(x, f32=True)
+        monkeypatch.setenv("ONPU_GEMM_SPLIT", "1")
+        y0 = q.mv(x, f32=True)
+        monkeypatch.delenv("ONPU_GEMM_SPLIT")
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), "split-K GEMM is not deterministic"
+        assert torch.equal(yb, y1.to(torch.bfloat16)), "bf16 output is not the RNE of the fp32 sums"
+        for other, what in ((y0, "no split"), (y3, "3 ranges")):
+            d = ((y1 - other).abs().max() / other.abs().max()).item()
+            assert d <= 1e-5, f"split-K vs {what} differ by {d:.3e} of max|y|"
+        rows = [0, M // 2, M - 1]
+        yc = from_torch(yb[:, N - 384:])
+        yr = from_torch(yb[rows])
+        yf = from_torch(y1[rows])
+    finally:
+        q.free()
+    check_gemm(yc, fmt, st, N, K, xb, N - 384, N, what=f"split-K fmt {fmt} {M}x{N}x{K} column slice")
+    check_gemm(yr, fmt, st, N, K, xb[rows], what=f"split-K fmt {fmt} {M}x{N}x{K} rows")
+    check_f32_out(yf, orc.qmm(fmt, st, N, K, xb[rows], bf16w=True), what=f"split-K fmt {fmt} fp32 rows")
+
+
+def test_gemm_split_k_under_capture(gpu):
+    """split-K GEMMs recorded in a graph (their partials in the capture's own workspace) at 96 and
+    40 rows: replays interleaved with eager split-K GEMMs on the default stream each equal the eager
+    results bit for bit"""
+    import torch
+    from opennpu_amd.device import QMatrix
+    shapes = [(96, 4096, 14336), (40, 14336, 4096)]
+    mats = [QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 70 + M)) for M, N, K in shapes]
+    try:
+        xs = [to_torch_bf16(syn.activations(M, K, 71 + M)).reshape(M, K) for M, _, K in shapes]
+        ref = [q.mv(x) for q, x in zip(mats, xs)]
+        torch.cuda.synchronize()
+        outs = [torch.empty_like(r) for r in ref]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for q, x, o in zip(mats, xs, outs):
+                q.mv(x, out=o)
+        for rep in range(3):
+            for o in outs:
+                o.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            for o, r in zip(outs, ref):
+                assert torch.equal(o, r), f"replay {rep} differs from the eager GEMM"
+            ye = mats[0].mv(xs[0])
+            torch.cuda.synchronize()
+            assert torch.equal(ye, ref[0]), "eager GEMM after a replay differs"
+    finally:
+        for q in mats:
+            q.free()
+
+
+def test_argmax_at_gemm_rows(gpu, monkeypatch):
+    """a vocabulary-sized LM head at 24 and 48 rows takes the split-K GEMM and the argmax launch
+    over its fp32 logits (the crossover rule): logits against the bf16-weight oracle on a column
+    slice and two rows, argmax equal to the oracle argmax of the returned logits, and to the
+    fused GEMV path's argmax (ONPU_FORCE_GEMM=-1) wherever that row's top two logits are apart"""
+    import torch
+    from opennpu_amd.device import QMatrix
+    fmt, N, K = orc.FMT_G128S, 20000, 4096
+    st = syn.weights(fmt, N, K, 81)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        for M in (24, 48):
+            xb = syn.activations(M, K, 82 + M)
+            x = to_torch_bf16(xb).reshape(M, K)
+            lg, idx = q.argmax(x)
+            monkeypatch.setenv("ONPU_FORCE_GEMM", "-1")
+            lgv, idv = q.argmax(x)
+            monkeypatch.delenv("ONPU_FORCE_GEMM")
+            torch.cuda.synchronize()
+            lg, idx, lgv, idv = from_torch(lg), idx.cpu().numpy(), from_torch(lgv), idv.cpu().numpy()
+            assert np.array_equal(idx, orc.argmax(lg)) and np.array_equal(idv, orc.argmax(lgv))
+            rows = [0, M - 1]
+            check_f32_out(lg[:, :512], orc.qmm(fmt, st, N, K, xb, 0, 512, bf16w=True), what=f"M {M} columns")
+            check_f32_out(lg[rows], orc.qmm(fmt, st, N, K, xb[rows], bf16w=True), what=f"M {M} rows")
+            top2 = np.sort(lg, axis=1)[:, -2:]
+            apart = top2[:, 1] - top2[:, 0] > 1e-2 * np.abs(lg).max()
+            assert apart.sum() >= M // 4 and np.array_equal(idx[apart], idv[apart])
+    finally:
+        q.free()
+
+
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("M,N,K", [(2100, 7400, 640), (1000, 14300, 512)])
 def test_gemm_stream_k(gpu, fmt, M, N, K, monkeypatch):
