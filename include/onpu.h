@@ -137,13 +137,18 @@ int onpu_bank_load(void * h, int64_t e0, int64_t n, const void * stage);
 /* the decode-GEMV launch plan (host only): mb, rt, nb, xl, tw, kw, bpw, grid x, built, max waves
  * for an [N][K] matrix of fmt at M rows over `slots` slots; epi 0 store, 1 SiLU-gate, 2 slot sum */
 void onpu_plan_gemv(int fmt, int64_t N, int64_t K, int M, int64_t slots, int epi, int64_t * out /* [10] */);
+/* what onpu_dense_mv_dev runs for M rows of an [N][K] matrix (host only; no counterpart in the
+ * reference, whose NPU dispatch has no such choice): path (0 the decode GEMV, 1 the GEMM with tiles
+ * of 16 mb rows, 2 the 256-row stream-K GEMM), mb, weight tiles per wave, K ranges S, K blocks per
+ * range, workgroups per range */
+void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out /* [6] */);
 /* N, K, fmt, E, row tiles, K blocks, HBM bytes per expert, HBM base address */
 void onpu_dense_info(void * h, int64_t * out /* [8] */);
 /* dequantized weights of expert e as the GPU stores them: fp32 (bf16 = 0) or bf16 RNE bits */
 int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
 /* y [M][N] = x [M][K] . W^T on `stream` (hipStream_t; NULL: the default stream); x bf16 in HBM,
- * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels (from 24-48 rows up, depending on
- * N K, the MFMA GEMM, which is faster there), larger M the MFMA GEMM. */
+ * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels (from 4-64 rows up, depending on
+ * N K, the MFMA GEMM, which is faster there: onpu_plan_mv), larger M the MFMA GEMM. */
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
 /* Workspace of the calls above. The MFMA GEMM splits K (fp32 partials of K ranges, or the partial
  * tiles and slot words of its 256-row stream-K form above 128 rows) in a workspace of about 64 MiB (kept until the process ends): one per stream for eager

@@ -70,6 +70,7 @@ def _declare(lib):
         "onpu_bank_load": (I32, [P, I64, I64, P]),
         "onpu_dense_info": (None, [P, I64P]),
         "onpu_plan_gemv": (None, [I32, I64, I64, I32, I64, I32, I64P]),
+        "onpu_plan_mv": (None, [I32, I64, I64, I64, I64P]),
         "onpu_dense_dequant": (I32, [P, I64, P, I32]),
         "onpu_dense_mv_dev": (I32, [P, P, I64, P, I32, P]),
         "onpu_dense_argmax_dev": (I32, [P, P, I64, P, P, P]),

@@ -515,10 +515,11 @@ std::vector<std::pair<GskKey, GskWs *>> g_gsk;           // a few streams and gr
 // valid pointers. Its sync words are cleared by a kernel on s (under capture, a node of the graph
 // ahead of the GEMM), so the first call may be captured. Each one is 64 MiB, held until the process
 // ends.
-size_t gsk_part_bytes() {
+// bytes of a split-K workspace's partials: a 256 x 256 fp32 partial tile per CU
+size_t gsk_part_bytes(int cus) {
     size_t slot = 0;
     for (const GskCfg & c : GSK_CFGS) slot = std::max(slot, (size_t) c.wv * c.mbg * c.ntw * 1024);
-    return slot * (size_t) std::max(device().cus, 0);
+    return slot * (size_t) std::max(cus, 0);
 }
 
 hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** sync, int32_t ** ctl) {
@@ -541,7 +542,7 @@ hipError_t gsk_workspace(hipStream_t s, int64_t cut, float ** part, int32_t ** s
             delete w;
             return e;
         }
-        e = w->part.ensure(gsk_part_bytes());
+        e = w->part.ensure(gsk_part_bytes(device().cus));
         if (e == hipSuccess) e = w->sync.ensure((size_t) ints * 4);
         (void) hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess || (e = launch_zero_i32(w->sync.as<int32_t>(), ints, s)) != hipSuccess) {
@@ -628,31 +629,85 @@ hipError_t argmax_gemv(Mat4 * m, const uint16_t * x, int64_t M, float * logits, 
     return launch_argmax_keys(a.akeys, p.gx, M, argmax, s);
 }
 
-// Up to 64 rows: the decode GEMV, whose time grows with the rows, unless the split-K GEMM (about
-// the same time from 8 to 128 rows) is faster. Crossovers measured on MI355X (g128s, us GEMV ->
-// GEMM): 6144 x 4096 at 48 rows 27.9 -> 24.2, 4096 x 4096 none up to 64 (19.5 / 21.6 at 64);
-// 14336 x 4096 at 32 rows 34.2 -> 28.7, 8192 x 8192 34.6 -> 29.5, 4096 x 12288 26.6 / 28.9 (stays);
-// 10240 x 8192 at 24 rows 41.2 -> 34.1, 57344 x 8192 175 -> 131, 151936 x 4096 247 -> 179; at 16 rows
-// the GEMV wins everywhere (57344 x 8192 127 / 129). ONPU_FORCE_GEMM = 1 takes the GEMM, -1 the GEMV.
+// Up to 64 rows: the decode GEMV, whose time grows with the rows, unless the GEMM with a tile of
+// 16-64 rows split along K (about the same time from 1 to 16 rows) is faster. Crossovers measured
+// on MI355X over >= 600 MB of distinct weight copies (g128s unless named, us GEMV -> GEMM):
+// 4096 x 4096 at 64 rows 19.6 -> 17.5 (48: 15.2 / 16.2 stays); 6144 x 4096 at 24 rows 16.4 -> 14.3
+// (16: 12.0 / 13.0 stays); 4096 x 12288 at 16 rows 16.8 -> 16.6, 24576 x 4096 27.5 -> 19.7 (12: 16.6
+// / 19.5 stays), q4nx 24576 x 4096 29.3 -> 22.5; 151936 x 4096 at 12 rows 97.3 -> 74.9 (Q4_0 98.4 ->
+// 81.1; 8: 67.7 / 72.1 stays); 8192 x 28672 at 8 rows 38.6 -> 35.7 (4: 34.1 / 35.3 stays); 57344 x
+// 8192 at 4 rows 62.2 -> 58.0 (2: 48.9 / 57.7 stays). ONPU_FORCE_GEMM = 1 takes the GEMM, -1 the GEMV.
 bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
     const int f = env_int("ONPU_FORCE_GEMM", 0);
     if (M > 64 || f == 1) return false;
     if (f == -1) return true;
     const int64_t nk = N * K;
-    return !((M >= 48 && nk >= 20000000) || (M >= 32 && nk >= 56000000) || (M >= 24 && nk >= 80000000));
+    return !((M >= 64 && nk >= 16000000) || (M >= 24 && nk >= 24000000) || (M >= 16 && nk >= 40000000) ||
+             (M >= 12 && nk >= 200000000) || (M >= 8 && nk >= 200000000 && K >= 8192) ||
+             (M >= 4 && nk >= 400000000 && K >= 8192));
 }
 
-hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
-    if (M <= 0) return hipSuccess;
-    const uint8_t * W = m->dev + e * m->dstride;
-    if (rows_take_gemv(M, m->N, m->K)) return gemv_core(m, e, x, M, y, yf32, s);
+// mv_core's choice for M rows: the decode GEMV (path 0), k_qgemm with mb A blocks of 16 rows and ntw
+// weight tiles per wave, in S ranges of kbs K blocks (path 1), or k_qgemm_sk (path 2); wgs: k_qgemm's
+// workgroups per K range
+struct MvPlan { int path, mb, ntw; int64_t S, kbs, wgs; };
+
+MvPlan plan_mv(int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus) {
+    MvPlan p{0, 8, 2, 1, KB, 0};
+    if (rows_take_gemv(M, N, K)) return p;
     int cfg = 0;
     int64_t grid = 0;
     GArgs ga{};
     // the 256-row tiles of k_qgemm_sk compute at least half padding at M <= 128, where k_qgemm's
     // 128-row tiles (split along K below) are faster: 57344 x 8192 at M = 96 140 us against 194 us
-    if (M > 128 && env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ga) &&
-        M * m->K * 2 < ((int64_t) 1 << 31)) {
+    if (M > 128 && env_int("ONPU_GEMM_SK", 1) && plan_gsk(M, NT, KB, cus, cfg, grid, ga) && M * K * 2 < ((int64_t) 1 << 31)) {
+        p.path = 2;
+        return p;
+    }
+    p.path = 1;
+    // A blocks of 16 rows per workgroup tile: 1 / 2 / 4 up to 16 / 32 / 64 rows, else 8 (128 rows).
+    // MFMAs and LDS reads on rows past M cost their full time: the 151936 x 4096 LM head at 16 / 32
+    // / 64 rows 171 / 176 / 184 us with 128-row tiles, 73 / 94 / 134 us with 16- / 32- / 64-row tiles
+    p.mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8;
+    const int emb = env_int("ONPU_GEMM_MB", 0);
+    if (emb == 1 || emb == 2 || emb == 4 || emb == 8) p.mb = emb;
+    // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
+    // workgroups, else 2 (128 x 128); 4 (128 x 256) runs out of registers and is slower
+    const int64_t wg3 = ((M + 127) / 128) * ((NT + 11) / 12);
+    p.ntw = p.mb == 8 && wg3 >= 512 ? 3 : 2;
+    const int entw = env_int("ONPU_GEMM_NTW", 0);
+    if (entw >= 2 && entw <= 4) p.ntw = entw;
+    if (p.ntw != 2) p.mb = 8;
+    // the kernel addresses X with 32-bit buffer offsets: launches of at most 2^31 bytes of X rows
+    const int64_t rows_max = std::max<int64_t>(128, (((int64_t) 1 << 31) - 1) / (K * 2) / 128 * 128);
+    // split-K when the tiles leave CUs without work: S K ranges, S x the workgroups (two per CU,
+    // at least 4 K blocks each), fp32 partials in the split-K workspace, then their sum. A sweep of
+    // S over 1-16 (65-512 rows, seven shapes; 1-64 rows, thirteen shapes and formats) put this rule
+    // 1.5-2 % from the best S on average
+    p.wgs = ((M + 16 * p.mb - 1) / (16 * p.mb)) * ((NT + 4 * p.ntw - 1) / (4 * p.ntw));
+    if (M <= rows_max) {
+        const int es = env_int("ONPU_GEMM_SPLIT", 0);
+        int64_t S = es >= 1 ? es : std::min<int64_t>(KB / 4, 2 * (int64_t) cus / p.wgs);
+        S = std::max<int64_t>(1, std::min<int64_t>(S, KB));
+        while (S > 1 && (size_t) (S * M * N * 4) > gsk_part_bytes(cus)) S--;
+        if (S > 1) {
+            p.kbs = (KB + S - 1) / S;
+            p.S = (KB + p.kbs - 1) / p.kbs;
+        }
+    }
+    return p;
+}
+
+hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const uint8_t * W = m->dev + e * m->dstride;
+    const MvPlan p = plan_mv(m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
+    if (p.path == 0) return gemv_core(m, e, x, M, y, yf32, s);
+    if (p.path == 2) {
+        int cfg = 0;
+        int64_t grid = 0;
+        GArgs ga{};
+        if (!plan_gsk(M, m->g.NT, m->g.KB, device().cus, cfg, grid, ga)) return hipErrorInvalidValue;
         // cut tiles: the R tail tiles (two-phase split) or the workgroup boundaries (stream-K)
         const int64_t cut = ga.sched == 1 ? ga.R : grid;
         hipError_t e = gsk_workspace(s, cut, &ga.ws, &ga.sync, &ga.ctl);
@@ -662,45 +717,24 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         ga.spin = spin_limit(1u << 22);
         return launch_qgemm_sk(m->fmt, ga, cfg, (int) grid, s);
     }
-    // 3 weight tiles per wave (workgroup tile 128 x 192) when that still fills every CU with two
-    // workgroups, else 2 (128 x 128); 4 (128 x 256) runs out of registers and is slower
-    const int64_t wg3 = ((M + 127) / 128) * ((m->g.NT + 11) / 12);
-    int ntw = wg3 >= 512 ? 3 : 2;
-    const int entw = env_int("ONPU_GEMM_NTW", 0);
-    if (entw >= 2 && entw <= 4) ntw = entw;
-    // the kernel addresses X with 32-bit buffer offsets: launches of at most 2^31 bytes of X rows
-    const int64_t rows_max = std::max<int64_t>(128, (((int64_t) 1 << 31) - 1) / (m->K * 2) / 128 * 128);
-    // split-K when the tiles leave CUs without work: S K ranges, S x the workgroups (two per CU at
-    // most, at least 4 K blocks each), fp32 partials in the split-K workspace, then their sum
-    const int64_t wgs = ((M + 127) / 128) * ((m->g.NT + 4 * ntw - 1) / (4 * ntw));
-    int64_t S = 1, kbs = m->g.KB;
-    if (M <= rows_max) {
-        const int es = env_int("ONPU_GEMM_SPLIT", 0);
-        S = es >= 1 ? es : std::min<int64_t>(m->g.KB / 4, 2 * device().cus / wgs);
-        S = std::max<int64_t>(1, std::min<int64_t>(S, m->g.KB));
-        while (S > 1 && (size_t) (S * M * m->N * 4) > gsk_part_bytes()) S--;
-        if (S > 1) {
-            kbs = (m->g.KB + S - 1) / S;
-            S = (m->g.KB + kbs - 1) / kbs;
-        }
-    }
-    if (S > 1) {
+    if (p.S > 1) {
         GArgs a{};
         int32_t * sync = nullptr, * ctl = nullptr;
         hipError_t e = gsk_workspace(s, 0, &a.ws, &sync, &ctl);
         if (e != hipSuccess) return e;
         a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
         a.x = x; a.ldx = m->K; a.ldy = m->N; a.yf32 = 1; a.y = a.ws;
-        a.splits = (int) S; a.kbs = kbs;
-        if ((e = launch_qgemm(m->fmt, a, ntw, s)) != hipSuccess) return e;
-        return launch_gemm_split_sum(a.ws, (int) S, M, m->N, y, m->N, yf32, s);
+        a.splits = (int) p.S; a.kbs = p.kbs;
+        if ((e = launch_qgemm(m->fmt, a, p.ntw, p.mb, s)) != hipSuccess) return e;
+        return launch_gemm_split_sum(a.ws, (int) p.S, M, m->N, y, m->N, yf32, s);
     }
+    const int64_t rows_max = std::max<int64_t>(128, (((int64_t) 1 << 31) - 1) / (m->K * 2) / 128 * 128);
     for (int64_t r0 = 0; r0 < M; r0 += rows_max) {
         GArgs a{};
         a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = std::min(rows_max, M - r0);
         a.x = x + r0 * m->K; a.ldx = m->K; a.ldy = m->N; a.yf32 = yf32;
         a.y = (char *) y + r0 * m->N * (yf32 ? 4 : 2);
-        const hipError_t e = launch_qgemm(m->fmt, a, ntw, s);
+        const hipError_t e = launch_qgemm(m->fmt, a, p.ntw, p.mb, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -969,6 +1003,13 @@ int onpu_has_shape(int, int, int) { return device().ok; }
 
 // the GEMV launch plan for an [N][K] matrix of fmt at M rows over `slots` (host only, no GPU):
 // out = mb, rt, nb, xl, tw, kw, bpw, gx, built (1 if that kernel variant exists), max waves
+void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out) {
+    const Tiled g = tiled_geom(fmt, N, K);
+    const MvPlan p = plan_mv(N, K, g.NT, g.KB, M, device().cus > 0 ? device().cus : 256);
+    const int64_t v[6] = {p.path, p.mb, p.ntw, p.S, p.kbs, p.wgs};
+    for (int i = 0; i < 6; i++) out[i] = v[i];
+}
+
 void onpu_plan_gemv(int fmt, int64_t N, int64_t K, int M, int64_t slots, int epi, int64_t * out) {
     const Tiled g = tiled_geom(fmt, N, K);
     const Plan p = epi == EPI_SLOTSUM_ ? plan_slotsum(g.KB, (int) slots) : plan_gemv(fmt, g.NT, g.KB, M, slots, epi);

@@ -35,12 +35,16 @@ hipError_t FN(qgemv)(int epi, const QArgs & a, int mb, int rt, int nb, int xl, d
     return hipErrorInvalidValue;
 }
 
-hipError_t FN(qgemm)(const GArgs & a, int ntw, hipStream_t s) {
-    const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * ntw - 1) / (4 * ntw);
+hipError_t FN(qgemm)(const GArgs & a, int ntw, int mb, hipStream_t s) {
+    const int64_t gm = (a.M + 16 * mb - 1) / (16 * mb), gn = (a.NT + 4 * ntw - 1) / (4 * ntw);
     const dim3 grid((unsigned) (gm * gn * (a.splits > 1 ? a.splits : 1)));
-    if (ntw == 4) k_qgemm<F, 4><<<grid, 256, 0, s>>>(a);
-    else if (ntw == 3) k_qgemm<F, 3><<<grid, 256, 0, s>>>(a);
-    else k_qgemm<F, 2><<<grid, 256, 0, s>>>(a);
+    if (mb == 1 && ntw == 2) k_qgemm<F, 2, 1><<<grid, 256, 0, s>>>(a);
+    else if (mb == 2 && ntw == 2) k_qgemm<F, 2, 2><<<grid, 256, 0, s>>>(a);
+    else if (mb == 4 && ntw == 2) k_qgemm<F, 2, 4><<<grid, 256, 0, s>>>(a);
+    else if (mb != 8) return hipErrorInvalidValue;
+    else if (ntw == 4) k_qgemm<F, 4, 8><<<grid, 256, 0, s>>>(a);
+    else if (ntw == 3) k_qgemm<F, 3, 8><<<grid, 256, 0, s>>>(a);
+    else k_qgemm<F, 2, 8><<<grid, 256, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -6,7 +6,7 @@
 //   k_qgemv      up to 64 rows: the decode GEMV family. Integer MFMA on biased codes (128 + u) in
 //                bf16, group scales applied in fp32 between MFMA steps, x column sums from an
 //                extra MFMA against ones; epilogues: store, SiLU(gate) * up, MoE slot sum
-//   k_qgemm      prefill (and 24-64 rows of larger matrices): x tile in LDS, int4 tile dequantized
+//   k_qgemm      prefill (and 4-64 rows of larger matrices): x tile in LDS, int4 tile dequantized
 //                to bf16 RNE((u-8)s) in registers and fed to v_mfma_f32_16x16x32_bf16, fp32
 //                accumulate; split along K into fp32 partials when the tiles leave CUs idle
 //   k_moe_gemm   grouped expert products (MoE prompts) over a device work list
@@ -905,10 +905,11 @@ DEV void par_sc(const GPar<FMT> & p, int j, float & s, float & c) {
     }
 }
 
-// Y[M][N] = X[M][K] . deq(W)^T (128-row tiles). Workgroup: 4 waves, tile 128 rows of X x 64 NTW rows of
-// W; wave w owns NTW 16-row weight tiles and all 128 X rows (8 x NTW accumulators of 16 x 16).
-// Per 128-wide K block the X tile (32 KiB of MFMA A fragments [mb][j][lane]) sits in one of two
-// LDS buffers. The buffers are filled straight from global memory by buffer_load_dwordx4 ... lds
+// Y[M][N] = X[M][K] . deq(W)^T. Workgroup: 4 waves, tile MT = 16 MB rows of X (MB = 8, or 2 / 4
+// A blocks for up to 32 / 64 rows: MFMAs and LDS reads on rows past M would cost their full time)
+// x 64 NTW rows of W; wave w owns NTW 16-row weight tiles and all MT X rows (MB x NTW accumulators
+// of 16 x 16). Per 128-wide K block the X tile (MB x 4 KiB of MFMA A fragments [mb][j][lane]) sits
+// in one of two LDS buffers. The buffers are filled straight from global memory by buffer_load_dwordx4 ... lds
 // (lane l of a wave writes 16 B at base + 16 l, so one load fills one A fragment; rows past M and
 // k past K read out of the buffer's range and land as zeros), so X never occupies registers.
 // Each wave dequantizes its own weight blocks in registers one 32-wide K step at a time and runs
@@ -972,16 +973,17 @@ DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (
     }
 }
 
-// The X tile of block b into LDS buffer buf: wave w fills fragments f = 8 w + i, (mb, j) =
-// (f / 4, f % 4); lane (q, r) brings row m0 + 16 mb + r, k = 128 b + 32 j + 8 q. xo[i] is the
-// lane's byte offset of its element at b = 0 (0x80000000, past the buffer, for rows >= M: those
-// land as zeros); block b adds 256 b in the scalar offset. kfix: the last block when K % 128 != 0
-// (its k >= K lanes read past the buffer too).
-DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xo)[8], int64_t b, bool kfix, int64_t K,
+// The X tile of block b (MB A blocks of 16 rows) into LDS buffer buf: wave w of 4 fills fragments
+// f = MB w + i, (mb, j) = (f / 4, f % 4); lane (q, r) brings row m0 + 16 mb + r, k = 128 b + 32 j +
+// 8 q. xo[i] is the lane's byte offset of its element at b = 0 (0x80000000, past the buffer, for
+// rows >= M: those land as zeros); block b adds 256 b in the scalar offset. kfix: the last block
+// when K % 128 != 0 (its k >= K lanes read past the buffer too).
+template <int MB>
+DEV void gemm_load_x(const __amdgpu_buffer_rsrc_t & xr, const uint32_t (&xo)[MB], int64_t b, bool kfix, int64_t K,
                      int wave, int q, u32x4 * buf) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int f = 8 * wave + i, j = f & 3;
+    for (int i = 0; i < MB; i++) {
+        const int f = MB * wave + i, j = f & 3;
         uint32_t off = xo[i];
         if (kfix && 128 * b + 32 * j + 8 * q >= K) off = 0x80000000u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *) (buf + f * 64), 16, off, (uint32_t) (256 * b), 0, 0);
@@ -1014,9 +1016,10 @@ DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int la
     for (int i = 0; i < NTW; i++) gemm_load_w1<FMT>(wrs[i], b, lane, r, w[i], p[i]);
 }
 
-template <int FMT, int NTW>
-__global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
-    __shared__ u32x4 xs0[8 * 4 * 64], xs1[8 * 4 * 64];     // 2 x 32 KiB
+template <int FMT, int NTW, int MB>
+__global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
+    __shared__ u32x4 xs0[MB * 4 * 64], xs1[MB * 4 * 64];   // 2 x MB x 4 KiB
+    constexpr int MT = 16 * MB;                           // rows of the workgroup tile
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15;
     const int q = lane >> 4;
@@ -1026,7 +1029,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
     // groups of GMS M tiles x all N columns, M fastest: the 64 workgroups an XCD runs at once cover
     // GMS M tiles x 64 / GMS N columns, so each X tile and each weight tile is read by many of them
     constexpr int64_t GMS = 4;
-    const int64_t gm = (a.M + 127) / 128, gn = (a.NT + 4 * NTW - 1) / (4 * NTW);
+    const int64_t gm = (a.M + MT - 1) / MT, gn = (a.NT + 4 * NTW - 1) / (4 * NTW);
     // split-K: logical workgroups split-major (an XCD's contiguous range holds whole splits, whose
     // tiles share X columns), K blocks [kb0, kb1), fp32 partials in the split's plane
     int64_t kb0 = 0, kb1 = a.KB;
@@ -1045,7 +1048,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
     const int64_t grp = lid / (GMS * gn), in = lid % (GMS * gn);
     const int64_t gms = gm - grp * GMS < GMS ? gm - grp * GMS : GMS;       // M tiles in this group
     const int64_t mblk = grp * GMS + in % gms, nblk = in / gms;
-    const int64_t m0 = mblk * 128;
+    const int64_t m0 = mblk * MT;
     const int64_t t0 = nblk * (4 * NTW) + wave * NTW;     // first weight tile of this wave
     // tiles past NT (the last column of workgroups) recompute tile t0 (or 0) and are not stored
     int nt_ok = (int) (a.NT - t0 < NTW ? a.NT - t0 : NTW);
@@ -1059,18 +1062,18 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
     }
     const __amdgpu_buffer_rsrc_t xr =
         __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) (uint32_t) (a.M * a.ldx * 2), 0x00020000);
-    uint32_t xo[8];
+    uint32_t xo[MB];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int f = 8 * wave + i, mb = f >> 2, j = f & 3;
+    for (int i = 0; i < MB; i++) {
+        const int f = MB * wave + i, mb = f >> 2, j = f & 3;
         const int64_t m = m0 + 16 * mb + r;
         xo[i] = m < a.M ? (uint32_t) ((m * a.ldx + 32 * j + 8 * q) * 2) : 0x80000000u;
     }
     const bool ktail = a.K % 128 != 0;
 
-    f32x4 acc[8][NTW];
+    f32x4 acc[MB][NTW];
 #pragma unroll
-    for (int mb = 0; mb < 8; mb++)
+    for (int mb = 0; mb < MB; mb++)
 #pragma unroll
         for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
     // two register sets for the weights, alternating with the two LDS buffers (no copies)
@@ -1086,7 +1089,7 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
         // even block from (xs0, wa) while block b + 1 streams into (xs1, wb)
         gemm_load_x(xr, xo, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, xs1);
         gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wb, pb);
-        gemm_block<FMT, NTW, 8>(xs0, wa, pa, lane, acc);
+        gemm_block<FMT, NTW, MB>(xs0, wa, pa, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
         // odd block from (xs1, wb) while block b + 2 streams into (xs0, wa)
@@ -1094,14 +1097,14 @@ __global__ __launch_bounds__(256, 2) void k_qgemm(GArgs a) {
             gemm_load_x(xr, xo, b + 2, ktail && b + 3 == a.KB, a.K, wave, q, xs0);
             gemm_load_w<FMT, NTW>(wrs, b + 2, lane, r, wa, pa);
         }
-        gemm_block<FMT, NTW, 8>(xs1, wb, pb, lane, acc);
+        gemm_block<FMT, NTW, MB>(xs1, wb, pb, lane, acc);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
-    if (b < kb1) gemm_block<FMT, NTW, 8>(xs0, wa, pa, lane, acc);
+    if (b < kb1) gemm_block<FMT, NTW, MB>(xs0, wa, pa, lane, acc);
     // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
 #pragma unroll
-    for (int mb = 0; mb < 8; mb++)
+    for (int mb = 0; mb < MB; mb++)
 #pragma unroll
         for (int i = 0; i < NTW; i++) {
             if (i >= nt_ok) continue;

@@ -407,16 +407,18 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s) {
+hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, int mb, hipStream_t s) {
+    if (!(mb == 8 && ntw >= 2 && ntw <= 4) && !((mb == 1 || mb == 2 || mb == 4) && ntw == 2)) return hipErrorInvalidValue;
     // split-K: every split holds at least one K block, the splits cover all KB, the grid fits 32 bits
     if (a.splits > 1 && (!a.ws || a.kbs < 1 || (a.splits - 1) * a.kbs >= a.KB || a.splits * a.kbs < a.KB ||
-                         ((a.M + 127) / 128) * ((a.NT + 4 * ntw - 1) / (4 * ntw)) * a.splits >= ((int64_t) 1 << 31)))
+                         ((a.M + 16 * mb - 1) / (16 * mb)) * ((a.NT + 4 * ntw - 1) / (4 * ntw)) * a.splits >=
+                             ((int64_t) 1 << 31)))
         return hipErrorInvalidValue;
     switch (fmt) {
-        case 0: return qgemm_f0(a, ntw, s);
-        case 1: return qgemm_f1(a, ntw, s);
-        case 2: return qgemm_f2(a, ntw, s);
-        case 3: return qgemm_f3(a, ntw, s);
+        case 0: return qgemm_f0(a, ntw, mb, s);
+        case 1: return qgemm_f1(a, ntw, mb, s);
+        case 2: return qgemm_f2(a, ntw, mb, s);
+        case 3: return qgemm_f3(a, ntw, mb, s);
     }
     return hipErrorInvalidValue;
 }

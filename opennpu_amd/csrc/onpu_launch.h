@@ -175,7 +175,8 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
 int qgemv_has_variant(int epi, int mb, int rt, int nb, int xl);
 
 int qgemv_max_waves(int mb, int rt, int nb, int xl);
-hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, hipStream_t s);
+// mb: 16-row A blocks per workgroup tile, 8 (ntw 2-4) or, with ntw 2, 1, 2 or 4 (up to 16 / 32 / 64 rows)
+hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, int mb, hipStream_t s);
 // Y [M][N] (row stride ldy; bf16 RNE or fp32) = the sum over s = 0 .. S-1, in that order, of
 // part + s M N ([M][N] fp32)
 hipError_t launch_gemm_split_sum(const float * part, int S, int64_t M, int64_t N, void * y, int64_t ldy, int yf32,
@@ -289,7 +290,7 @@ enum { EPI_STORE_ = 0, EPI_ACT_ = 1, EPI_SLOTSUM_ = 2, EPI_ARGMAX_ = 3 };
                              hipStream_t s);                                                              \
     hipError_t qgemv_f##id(int epi, const QArgs & a, int mb, int rt, int nb, int xl, dim3 grid, int waves,       \
                            size_t lds, hipStream_t s);                                                    \
-    hipError_t qgemm_f##id(const GArgs & a, int ntw, hipStream_t s);                                       \
+    hipError_t qgemm_f##id(const GArgs & a, int ntw, int mb, hipStream_t s);                                       \
     hipError_t qgemm_sk_f##id(const GArgs & a, int cfg, int grid, hipStream_t s);                          \
     hipError_t moe_gemm_f##id(int which, const MArgs & a, dim3 grid, hipStream_t s);                  \
     hipError_t moe_decode_f##id(const MDArgs & a, int gb, int grid, size_t lds, hipStream_t s);       \

@@ -111,6 +111,33 @@ def test_launch_plans_are_built_variants(fmt):
             assert (kw // k) * bpw >= KB
 
 
+def test_mv_plans():
+    """onpu_plan_mv (what onpu_dense_mv_dev runs) over shapes and row counts: the GEMV only up to 64
+    rows; GEMM tiles of the fewest 16-row blocks that hold the rows up to 64 (1 / 2 / 4), 128 rows
+    beyond; K ranges that cover every K block, none empty, at least 4 blocks each unless forced, and
+    fp32 partials within the 64 MiB split-K workspace; the stream-K kernel only above 128 rows"""
+    L = _lib.lib()
+    o = (C.c_int64 * 6)()
+    seen = set()
+    for N in (64, 1000, 4096, 14336, 24576, 57344, 151936):
+        for K in (512, 4096, 8192, 14336, 28672):
+            KB = -(-K // 128)
+            for M in (1, 2, 4, 8, 12, 16, 17, 24, 32, 33, 48, 64, 65, 96, 128, 129, 256, 512, 2048):
+                L.onpu_plan_mv(2, N, K, M, o)
+                path, mb, ntw, S, kbs, wgs = tuple(o)
+                seen.add((path, mb if path == 1 else 0))
+                assert path in (0, 1, 2) and (path != 0 or M <= 64) and (path != 2 or M > 128), (N, K, M, tuple(o))
+                if path != 1:
+                    continue
+                want = 1 if M <= 16 else 2 if M <= 32 else 4 if M <= 64 else 8
+                assert mb == want and (ntw == 2 or mb == 8), (N, K, M, tuple(o))
+                assert S * kbs >= KB and (S - 1) * kbs < KB, (N, K, M, tuple(o))
+                if S > 1:
+                    assert kbs >= 4 and S * M * N * 4 <= 256 * 256 * 1024, (N, K, M, tuple(o))
+                assert wgs == -(-M // (16 * mb)) * -(-(-(-N // 16)) // (4 * ntw)), (N, K, M, tuple(o))
+    assert {(0, 0), (1, 1), (1, 2), (1, 4), (1, 8), (2, 0)} <= seen, seen
+
+
 @pytest.mark.parametrize("fmt", [0, 1, 2, 3])
 def test_argmax_epilogue_plans_sum_like_the_store(fmt):
     """the argmax epilogue's GEMV plan (onpu_dense_argmax_dev) and the plain store's (the no-alloc

@@ -117,11 +117,13 @@ PLAN_CLASS_SHAPES = [(2048, 2048), (1000, 8192), (6000, 2048), (17000, 1024), (7
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_gemv_plan_classes(gpu, fmt):
+def test_gemv_plan_classes(gpu, fmt, monkeypatch):
     """every plan class of the decode GEMV at 1-13 rows, all formats, every output row against the
-    oracle; the cases take x from global memory, staged with VALU sums and staged with MFMA sums"""
+    oracle; the cases take x from global memory, staged with VALU sums and staged with MFMA sums (the
+    GEMV forced where the largest shapes would take the GEMM at 13 rows)"""
     import ctypes as C
     from opennpu_amd import _lib
+    monkeypatch.setenv("ONPU_FORCE_GEMM", "-1")
     o = (C.c_int64 * 10)()
     seen = set()
     for i, (N, K) in enumerate(PLAN_CLASS_SHAPES):
@@ -162,24 +164,31 @@ def test_gemm_ragged(gpu, fmt, M):
     check_gemm(y, fmt, st, N, K, xb, what=f"gemm fmt {fmt} M {M}")
 
 
-# (M, N, K) cases of the 128-row GEMM split along K (mv_core: S = min(KB / 4, 2 x CUs / workgroups)
-# ranges of K blocks): 96 x 1000 x 8192 in 16 ranges of 4 blocks; 130 x 998 x 4096, two row tiles and
-# N % 4 != 0 (the sum's per-element path), in 8; 40 x 14000 x 4096, a GEMM below 65 rows (the
-# crossover rule), in 4
-SPLIT_CASES = [(96, 1000, 8192), (130, 998, 4096), (40, 14000, 4096)]
+# (M, N, K) cases of the GEMM split along K (plan_mv: S = min(KB / 4, 2 x CUs / workgroups) ranges of
+# K blocks), with the tile rows they take: 96 x 1000 x 8192 (128-row tiles) in 16 ranges of 4 blocks;
+# 130 x 998 x 4096, two row tiles and N % 4 != 0 (the sum's per-element path), in 8; GEMMs below 65
+# rows (the crossover rule): 40 x 14000 x 4096 (64-row tiles) in 4, 24 x 7000 x 4096 (32-row tiles)
+# in 8, 16 x 10000 x 4096 (16-row tiles) in 6 of 6 blocks (the last of 2)
+SPLIT_CASES = [(96, 1000, 8192, 8), (130, 998, 4096, 8), (40, 14000, 4096, 4), (24, 7000, 4096, 2),
+               (16, 10000, 4096, 1)]
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("M,N,K", SPLIT_CASES)
-def test_gemm_split_k(gpu, fmt, M, N, K, monkeypatch):
-    """k_qgemm split along K (fp32 partials per range, summed in range order by k_gemm_split_sum):
-    a 384-column slice over all rows and three full rows against the oracle; a second call gives
-    the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges (a shorter last one) and no
-    split agree to fp32 summation order"""
+@pytest.mark.parametrize("M,N,K,mb", SPLIT_CASES)
+def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
+    """k_qgemm split along K (fp32 partials per range, summed in range order by k_gemm_split_sum)
+    with tiles of 16 mb rows: a 384-column slice over all rows and three full rows against the
+    oracle; a second call gives the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges
+    (a shorter last one) and no split agree to fp32 summation order"""
+    import ctypes as C
     import torch
+    from opennpu_amd import _lib
     from opennpu_amd.device import QMatrix
     if fmt != orc.FMT_G128S:
         K -= 32                                       # a K tail inside the last 128-wide block
+    o = (C.c_int64 * 6)()
+    _lib.lib().onpu_plan_mv(fmt, N, K, M, o)
+    assert o[0] == 1 and o[1] == mb and o[3] > 1, tuple(o)     # the split GEMM with these tiles
     st = syn.weights(fmt, N, K, 51 + M)
     xb = syn.activations(M, K, 52 + M)
     q = QMatrix(N, K, fmt, st)
@@ -243,7 +252,7 @@ def test_gemm_split_k_under_capture(gpu):
 
 
 def test_argmax_at_gemm_rows(gpu, monkeypatch):
-    """a vocabulary-sized LM head at 24 and 48 rows takes the split-K GEMM and the argmax launch
+    """a vocabulary-sized LM head at 16, 24 and 48 rows takes the split-K GEMM and the argmax launch
     over its fp32 logits (the crossover rule): logits against the bf16-weight oracle on a column
     slice and two rows, argmax equal to the oracle argmax of the returned logits, and to the
     fused GEMV path's argmax (ONPU_FORCE_GEMM=-1) wherever that row's top two logits are apart"""
@@ -253,7 +262,7 @@ def test_argmax_at_gemm_rows(gpu, monkeypatch):
     st = syn.weights(fmt, N, K, 81)
     q = QMatrix(N, K, fmt, st)
     try:
-        for M in (24, 48):
+        for M in (16, 24, 48):
             xb = syn.activations(M, K, 82 + M)
             x = to_torch_bf16(xb).reshape(M, K)
             lg, idx = q.argmax(x)

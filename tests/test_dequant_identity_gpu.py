@@ -6,9 +6,9 @@ of its own. Here the GEMV, the prefill GEMM and the grouped MoE GEMM dequantize 
   the reference's fp32 dequant (u - 8) s, or u s + m for q4nx, as onpu_quant_dequant defines it
   (onpu_api.cpp:508-529): every group but the one holding k adds exact zeros, and the symmetric
   formats' (u - 8) s and q4nx's u s are exact products (4 by 8 significant bits);
-- prefill GEMM (M > 64: k_qgemm_sk with its split-K exchange, k_qgemm with the K-tail variant): X
-  the identity gives Y = W^T as the bf16 RNE of each dequantized weight, the value the reference
-  device feeds its MAC (gemv_any.cc:65,106-107);
+- prefill GEMM (k_qgemm_sk with its split-K exchange, k_qgemm with the K-tail variant and split
+  into K ranges, also at 40 rows): X the identity (or rows of it) gives Y = W^T as the bf16 RNE of
+  each dequantized weight, the value the reference device feeds its MAC (gemv_any.cc:65,106-107);
 - grouped MoE GEMM (the prompt path, k_moe_gemm gate+up then down): weights designed so that one
   product passes the other's values through unchanged (a gate of 32 makes silu exact, 32 * u and
   u / 32 are exact), so that the routed layer returns the bf16 RNE of every up weight, or of every
@@ -133,6 +133,33 @@ def test_gemm_returns_the_bf16_weights(gpu, fmt, case):
         q.free()
     bad = np.argwhere(~(y == Wb.T))
     assert bad.size == 0, f"fmt {fmt} {case}: Y[{bad[0]}] = {y[tuple(bad[0])]!r}, weight {Wb.T[tuple(bad[0])]!r}"
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_split_gemm_returns_the_bf16_weights(gpu, fmt):
+    """the GEMM split along K at few rows on a 7000 x 8192 matrix (16, 24, 40 rows: GEMMs below 65
+    rows with tiles of 16, 32, 64 rows; 96: 128-row tiles in 9 K ranges), rows one-hot at columns
+    spread over K and across range boundaries: every range but the one holding the column adds exact
+    zeros to the partial sum, so Y is the bf16 RNE of those weight columns"""
+    import torch
+    from opennpu_amd.device import QMatrix
+    N, K = 7000, (8192 if fmt == orc.FMT_G128S else 8224)
+    st = random_weights(fmt, N, K, 80 + fmt)
+    Wb = orc.bf2f(orc.dequant_bf16(fmt, st, N, K)).reshape(N, K)
+    q = QMatrix(N, K, fmt, st)
+    try:
+        for M in (16, 24, 40, 96):
+            cols = np.unique(np.linspace(0, K - 1, M).astype(np.int64))
+            cols = np.concatenate([cols, np.arange(K - (M - cols.size), K)])[:M]
+            print(f"split gemm identity fmt {fmt} N={N} K={K} M={M}", flush=True)
+            x = to_torch_bf16(one_hot(M, K, cols)).reshape(M, K)
+            y = from_torch(q.mv(x, f32=True))
+            torch.cuda.synchronize()
+            want = Wb[:, cols].T
+            bad = np.argwhere(~(y == want))
+            assert bad.size == 0, f"fmt {fmt} M {M}: Y[{bad[0]}] = {y[tuple(bad[0])]!r}, weight {want[tuple(bad[0])]!r}"
+    finally:
+        q.free()
 
 
 def designed(fmt, N, K, kind):
