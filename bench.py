@@ -12,7 +12,8 @@ headline (config.launch says which). value = algorithmic bytes per step (int4 co
 
 Also measured in the same run (the "configs" object): M=4 and M=8 decode steps, a single
 4096x4096 GEMV rotated over 64 copies, the Llama-3.1-8B prefill FFN GEMMs (M=2048, TFLOPS), the
-Qwen3-30B-A3B MoE layer (decode M=1 and prefill M=512, router included), and the 151936x4096
+same GEMMs at 96 rows and the Q4_0 LM head at 16 rows (the GEMM at few rows), the Qwen3-30B-A3B
+MoE layer (decode M=1 and prefill M=512, router included), and the 151936x4096
 Q4_0 LM head with argmax (M=1, 5), the load-time weight codecs on one layer (GPU quantization
 into each format and the GGUF Q4_K transcode, beside the host quantizer), and the per-token steps
 the reference runs on the host (decode attention, the int8 shared-expert GEMV). The roofline object is the dominant kernel: the gate+up GEMV,
@@ -269,6 +270,37 @@ def prefill(torch, QMatrix, syn, iters):
         fl = 2.0 * M * N * K
         out[name] = {"us_per_call": t * 1e6, "TFLOPS": fl / t / 1e12, "mfma_frac": fl / t / BF16_PEAK}
         q.free()
+    return out
+
+
+def few_rows(torch, QMatrix, syn, iters):
+    """the GEMM at few rows (speculative verification, a prompt chunk, batched decode): the
+    Llama-3.1-8B FFN at 96 rows (128-row tiles split along K), and the Q4_0 LM head with argmax at 16
+    rows (16-row tiles); each over >= 600 MB of distinct weight copies, so HBM serves every call"""
+    out = {}
+    for name, fmt, N, K, M in [("ffn_up_M96", G128S, 14336, 4096, 96), ("ffn_down_M96", G128S, 4096, 14336, 96),
+                               ("lm_head_q4_0_M16", Q4_0, 151936, 4096, 16)]:
+        st = syn.weights(fmt, N, K, 13)
+        copies = [QMatrix(N, K, fmt, st) for _ in range(max(2, -(-600_000_000 // st.nbytes)))]
+        x = bf16_tensor(torch, syn.activations(M, K, 14)).reshape(M, K)
+        lm = name.startswith("lm_head")
+        y = torch.empty((M, N), dtype=torch.float32 if lm else torch.bfloat16, device="cuda")
+        idx = torch.empty((M,), dtype=torch.int32, device="cuda")
+
+        def step(x=x, y=y, idx=idx, copies=copies, lm=lm):
+            for q in copies:
+                if lm:
+                    q.argmax(x, y, idx)
+                else:
+                    q.mv(x, out=y)
+        g = GraphStep(step, torch)
+        t = time_med(torch, g, iters, 3) / len(copies)
+        b = wbytes(fmt, N, K) + M * K * 2 + M * N * (4 if lm else 2)
+        fl = 2.0 * M * N * K
+        out[name] = {"us_per_call": t * 1e6, "GBps": b / t / 1e9, "hbm_frac": b / t / HBM_PEAK,
+                     "TFLOPS": fl / t / 1e12}
+        for q in copies:
+            q.free()
     return out
 
 
@@ -796,6 +828,35 @@ def profile_gemm(torch, QMatrix, syn, reps=3):
                       "launches_each": reps, "flop_per_launch": 2 * M * 14336 * 4096}), flush=True)
 
 
+def profile_few_rows(torch, QMatrix, syn, reps=2):
+    """The GEMM at few rows alone, for rocprofv3 runs: the Llama-3.1-8B FFN at 96 rows (up 14336x4096,
+    down 4096x14336, g128s) and the Q4_0 151936x4096 LM head with argmax at 16 rows, `reps` passes
+    over the same >= 600 MB of distinct copies as the bench, then one plain 512 MiB device copy that
+    calibrates the byte counters."""
+    out = []
+    for name, fmt, N, K, M in [("ffn_up", G128S, 14336, 4096, 96), ("ffn_down", G128S, 4096, 14336, 96),
+                               ("lm_head_q4_0", Q4_0, 151936, 4096, 16)]:
+        st = syn.weights(fmt, N, K, 13)
+        copies = [QMatrix(N, K, fmt, st) for _ in range(max(2, -(-600_000_000 // st.nbytes)))]
+        x = bf16_tensor(torch, syn.activations(M, K, 14)).reshape(M, K)
+        lm = name.startswith("lm_head")
+        y = torch.empty((M, N), dtype=torch.float32 if lm else torch.bfloat16, device="cuda")
+        for _ in range(reps):
+            for q in copies:
+                if lm:
+                    q.argmax(x, y)
+                else:
+                    q.mv(x, out=y)
+        torch.cuda.synchronize()
+        out.append({"matrix": f"{name} {N}x{K} M={M}", "launches": reps * len(copies),
+                    "algorithmic_bytes_per_call": wbytes(fmt, N, K) + M * K * 2 + M * N * (4 if lm else 2),
+                    "flop_per_call": 2 * M * N * K})
+        for q in copies:
+            q.free()
+    calibration_copy(torch)
+    print(json.dumps({"profile_target": out, "calibration_copy_bytes": 512 << 20}), flush=True)
+
+
 def profile_moe(torch, QFfn, syn, reps=3):
     """The Qwen3-30B-A3B MoE layer alone (E 128, H 2048, I 768, top-8, g128s) at T = 512 and T = 1,
     each over the MOE_COPIES pool copies with MOE_ROUNDS different routings (as the bench's MoE
@@ -838,6 +899,8 @@ def main():
                     help="row counts of the decode GEMVs under --profile (comma-separated, default 1)")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only the prefill GEMMs, for rocprofv3 --pmc runs")
+    ap.add_argument("--profile-few-rows", action="store_true",
+                    help="only the GEMMs at few rows (FFN at 96 rows, LM head at 16), for rocprofv3 runs")
     ap.add_argument("--profile-moe", action="store_true",
                     help="only the MoE layer (T = 512 and T = 1), for rocprofv3 runs")
     ap.add_argument("--ceilings", action="store_true",
@@ -858,6 +921,9 @@ def main():
         return
     if args.profile_gemm:
         profile_gemm(torch, QMatrix, syn)
+        return
+    if args.profile_few_rows:
+        profile_few_rows(torch, QMatrix, syn)
         return
     if args.profile_moe:
         profile_moe(torch, QFfn, syn)
@@ -881,6 +947,8 @@ def main():
         configs["gemv_4096"] = config0(torch, QMatrix, syn, 50)
         log("prefill ...")
         configs["llama31_8b_prefill_ffn"] = prefill(torch, QMatrix, syn, 20)
+        log("few-row GEMMs ...")
+        configs["few_rows_gemm"] = few_rows(torch, QMatrix, syn, 20)
         log("moe ...")
         configs["qwen3_30b_a3b_moe"] = moe(torch, QFfn, syn, 30)
         log("lm head ...")
