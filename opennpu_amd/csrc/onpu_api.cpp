@@ -133,7 +133,7 @@ struct Mat4 {                              // one [N][K] matrix (E = 1) or a ban
     RefGeom rg{};
     int32_t * rowmap = nullptr;
     // argmax workspace of the _dev calls on this handle (kept across growth: see DBuf)
-    DBuf am_keys{nullptr, 0, true};        // per-workgroup keys of the GEMV epilogue (<= 64 rows)
+    DBuf am_keys{nullptr, 0, true};        // per-workgroup keys of the GEMV's or the small GEMM's epilogue
     DBuf am_big{nullptr, 0, true};         // keys of the argmax launch over the logits
     DBuf am_cnt{nullptr, 0, true};         // its row counters (zeroed once; each call leaves them zero)
     // the step-major copy of every expert (the down bank of a fused FFN; k_moe_dsplit reads it),
@@ -1107,6 +1107,22 @@ int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, 
     return 0;
 }
 
+// LM head at rows that run the GEMM with one row tile of at most 64 rows and no split along K: its
+// epilogue leaves each workgroup's key per row (keys [M][N blocks], the handle's argmax workspace)
+// and k_argmax_keys reduces them, so the logits are not read again (Q4_0 151936 x 4096 at 16 rows:
+// the argmax launch over the logits took 13.7 us of 96)
+static hipError_t argmax_gemm(Mat4 * m, const MvPlan & p, const uint16_t * x, int64_t M, float * logits,
+                              int32_t * argmax, hipStream_t s) {
+    const int64_t gn = (m->g.NT + 4 * p.ntw - 1) / (4 * p.ntw);
+    if (const hipError_t e = m->am_keys.ensure((size_t) (M * gn * 8)); e != hipSuccess) return e;
+    GArgs a{};
+    a.W = m->dev; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
+    a.x = x; a.ldx = m->K; a.y = logits; a.ldy = m->N; a.yf32 = 1;
+    a.akeys = m->am_keys.as<uint64_t>();
+    if (const hipError_t e = launch_qgemm(m->fmt, a, p.ntw, p.mb, s); e != hipSuccess) return e;
+    return launch_argmax_keys(a.akeys, gn, M, argmax, s);
+}
+
 int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, int32_t * argmax, void * stream) {
     auto * m = (Mat4 *) h;
     if (M <= 0) return 0;
@@ -1115,8 +1131,14 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
     // Otherwise (or with ONPU_ARGMAX_FUSED=0) the argmax launch over the logits, with its keys and
     // per-row counters (grown to the rows of the call; new counters zeroed by a kernel on the stream,
     // and each call leaves them zero). Outgrown buffers are kept, so graphs keep valid pointers.
-    if (rows_take_gemv(M, m->N, m->K) && env_int("ONPU_ARGMAX_FUSED", 1)) {
+    const bool fused = env_int("ONPU_ARGMAX_FUSED", 1) != 0;
+    if (rows_take_gemv(M, m->N, m->K) && fused) {
         HIPR(argmax_gemv(m, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
+        return 0;
+    }
+    const MvPlan p = plan_mv(m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
+    if (fused && p.path == 1 && p.S == 1 && p.mb <= 4 && p.ntw == 2 && M <= 16 * p.mb) {
+        HIPR(argmax_gemm(m, p, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;
     }
     if (m->am_cnt.n < (size_t) M * ARGMAX_PAD) {

@@ -1016,7 +1016,9 @@ DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int la
     for (int i = 0; i < NTW; i++) gemm_load_w1<FMT>(wrs[i], b, lane, r, w[i], p[i]);
 }
 
-template <int FMT, int NTW, int MB>
+// AK: one row tile (M <= 16 MB), no split: the epilogue also leaves the workgroup's argmax key of
+// each row over its columns in a.akeys[m][N block] (argmax_key: larger value, then lower column)
+template <int FMT, int NTW, int MB, bool AK = false>
 __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     __shared__ u32x4 xs0[MB * 4 * 64], xs1[MB * 4 * 64];   // 2 x MB x 4 KiB
     constexpr int MT = 16 * MB;                           // rows of the workgroup tile
@@ -1115,6 +1117,34 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
                 if (m < a.M) store_out(yo, yf32, m * ldy + n, acc[mb][i][v]);
             }
         }
+    if constexpr (AK) {
+        // per row: the maximum key over the lane's columns, then over the 16 lanes of its row group
+        // (lanes 16 q .. 16 q + 15), then over the 4 waves in LDS
+        __shared__ uint64_t kw[4][16 * MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                uint64_t k = 0;
+#pragma unroll
+                for (int i = 0; i < NTW; i++) {
+                    const int64_t n = 16 * (t0 + i) + r;
+                    const uint64_t c = argmax_key(acc[mb][i][v], n);
+                    if (i < nt_ok && n < a.N && c > k) k = c;
+                }
+                for (int o = 1; o < 16; o <<= 1) {
+                    const uint64_t u = __shfl_xor(k, o);
+                    k = u > k ? u : k;
+                }
+                if (r == 0) kw[wave][16 * mb + 4 * q + v] = k;
+            }
+        __syncthreads();
+        if (threadIdx.x < 16 * MB && threadIdx.x < a.M) {
+            uint64_t k = kw[0][threadIdx.x];
+            for (int w = 1; w < 4; w++) k = kw[w][threadIdx.x] > k ? kw[w][threadIdx.x] : k;
+            a.akeys[(int64_t) threadIdx.x * gn + nblk] = k;
+        }
+    }
 }
 
 // ------------------------------------------------------------------ prefill GEMM, 256-row tiles

@@ -409,6 +409,8 @@ hipError_t launch_qgemv(int fmt, int epi, const QArgs & a, int mb, int rt, int n
 
 hipError_t launch_qgemm(int fmt, const GArgs & a, int ntw, int mb, hipStream_t s) {
     if (!(mb == 8 && ntw >= 2 && ntw <= 4) && !((mb == 1 || mb == 2 || mb == 4) && ntw == 2)) return hipErrorInvalidValue;
+    // argmax keys: tiles of at most 64 rows that hold every row, no split, fp32 logits
+    if (a.akeys && (mb == 8 || a.M > 16 * mb || a.splits > 1 || !a.yf32)) return hipErrorInvalidValue;
     // split-K: every split holds at least one K block, the splits cover all KB, the grid fits 32 bits
     if (a.splits > 1 && (!a.ws || a.kbs < 1 || (a.splits - 1) * a.kbs >= a.KB || a.splits * a.kbs < a.KB ||
                          ((a.M + 16 * mb - 1) / (16 * mb)) * ((a.NT + 4 * ntw - 1) / (4 * ntw)) * a.splits >=

@@ -64,6 +64,8 @@ struct GArgs {
     // adds the splits in order into Y
     int splits;
     int64_t kbs;
+    // k_qgemm, one row tile and no split: also each workgroup's argmax key per row, akeys[m][N block]
+    uint64_t * akeys;
 };
 constexpr int GSK_SYNC_STRIDE = 16;
 constexpr int GSK_CTL_TAG = 0, GSK_CTL_DONE = 16, GSK_CTL_ERR = 32, GSK_CTL_INTS = 48;

@@ -251,14 +251,22 @@ def test_gemm_split_k_under_capture(gpu):
             q.free()
 
 
-def test_argmax_at_gemm_rows(gpu, monkeypatch):
-    """a vocabulary-sized LM head at 16, 24 and 48 rows takes the split-K GEMM and the argmax launch
-    over its fp32 logits (the crossover rule): logits against the bf16-weight oracle on a column
-    slice and two rows, argmax equal to the oracle argmax of the returned logits, and to the
-    fused GEMV path's argmax (ONPU_FORCE_GEMM=-1) wherever that row's top two logits are apart"""
+@pytest.mark.parametrize("N", [20000, 40000])
+def test_argmax_at_gemm_rows(gpu, N, monkeypatch):
+    """a vocabulary-sized LM head at 16, 24 and 48 rows takes the GEMM (the crossover rule): split
+    along K with the argmax launch over its fp32 logits (20000 columns), or unsplit with the argmax
+    keys from its epilogue (40000): logits against the bf16-weight oracle on a column slice and two
+    rows, argmax equal to the oracle argmax of the returned logits, and to the fused GEMV path's
+    argmax (ONPU_FORCE_GEMM=-1) wherever that row's top two logits are apart"""
+    import ctypes as C
     import torch
+    from opennpu_amd import _lib
     from opennpu_amd.device import QMatrix
-    fmt, N, K = orc.FMT_G128S, 20000, 4096
+    fmt, K = orc.FMT_G128S, 4096
+    o = (C.c_int64 * 6)()
+    for M in (16, 24, 48):
+        _lib.lib().onpu_plan_mv(fmt, N, K, M, o)
+        assert o[0] == 1 and (o[3] > 1) == (N == 20000), (N, M, tuple(o))
     st = syn.weights(fmt, N, K, 81)
     q = QMatrix(N, K, fmt, st)
     try:
@@ -528,11 +536,13 @@ def test_argmax_ties_and_replays(gpu, fmt, N, K, M):
 
 
 @pytest.mark.parametrize("fmt,N,K,M", [(orc.FMT_Q4_0, 151936, 4096, 5), (orc.FMT_G128S, 4100, 2048, 17),
-                                       (orc.FMT_Q4S, 3000, 1024, 40), (orc.FMT_Q4NX, 2000, 512, 64)])
+                                       (orc.FMT_Q4S, 3000, 1024, 40), (orc.FMT_Q4NX, 2000, 512, 64),
+                                       (orc.FMT_G128S, 40000, 4096, 24), (orc.FMT_Q4_0, 40000, 4096, 64)])
 def test_argmax_fused_equals_separate(gpu, fmt, N, K, M, monkeypatch):
-    """the argmax from the GEMV epilogue's per-workgroup keys (default up to 64 rows) gives the same
-    logits bits and indices as the GEMV followed by the argmax launch over the logits
-    (ONPU_ARGMAX_FUSED=0), also on a second call and for a row of NaNs (index 0)"""
+    """the argmax from the per-workgroup keys of the GEMV's epilogue (or, at 24 and 64 rows of a
+    40000 x 4096 head, of the unsplit small-tile GEMM's) gives the same logits bits and indices as
+    the same product followed by the argmax launch over the logits (ONPU_ARGMAX_FUSED=0), also on
+    a second call and for a row of NaNs (index 0)"""
     import torch
     from opennpu_amd.device import QMatrix
     st = syn.weights(fmt, N, K, 41)
@@ -569,7 +579,7 @@ def _plant_nan_scale(fmt, st, N, K, row):
 
 
 @pytest.mark.parametrize("fmt,N,K,M", [(orc.FMT_Q4_0, 151936, 4096, 5), (orc.FMT_G128S, 4100, 2048, 17),
-                                       (orc.FMT_Q4NX, 2000, 512, 70)])
+                                       (orc.FMT_Q4NX, 2000, 512, 70), (orc.FMT_G128S, 40000, 4096, 16)])
 def test_argmax_first_nan_wins(gpu, fmt, N, K, M, monkeypatch):
     """numpy's and torch's argmax, which the reference takes over the logits (npu4/engine.py:358,
     runtime.py:348), return the first NaN of a row that holds one. Rows with NaN logits at two
