@@ -828,6 +828,50 @@ def profile_gemm(torch, QMatrix, syn, reps=3):
                       "launches_each": reps, "flop_per_launch": 2 * M * 14336 * 4096}), flush=True)
 
 
+def profile_chain(torch, QMatrix, QChain, syn, reps=5):
+    """The chained decode step alone, for rocprofv3 runs: the headline's 144 Qwen3-8B GEMVs at M = 1
+    (36 HBM copies of each matrix) as one chained launch, first dependent (each entry reads the
+    output before it, as in the headline), then independent (every entry reads a fixed input), `reps`
+    launches each, then one plain 512 MiB device copy that calibrates the byte counters. The
+    difference between the two launches is what the 144 waits on earlier outputs cost."""
+    mats = {}
+    for name, N, K in QWEN3_8B:
+        st = syn.weights(G128S, N, K, 100 + N + K, scale_sigma=unit_gain_sigma(K), signed=True)
+        mats[name] = [QMatrix(N, K, G128S, st) for _ in range(LAYERS)]
+    order = [(name, layer) for layer in range(LAYERS) for name, _, _ in QWEN3_8B]
+    shape = {name: (N, K) for name, N, K in QWEN3_8B}
+    ys = {key: torch.zeros((1, shape[key[0]][0]), dtype=torch.bfloat16, device="cuda") for key in order}
+    h0 = bf16_tensor(torch, syn.activations(1, 4096, 4097)).reshape(1, 4096)
+    fixed = {K: bf16_tensor(torch, syn.activations(1, K, K + 1)).reshape(1, K) for K in (4096, 12288)}
+
+    def x_dep(name, layer):
+        if name == "qkv":
+            return h0 if layer == 0 else ys[("down", layer - 1)]
+        if name == "o":
+            return ys[("qkv", layer)][:, :4096]
+        if name == "gate_up":
+            return ys[("o", layer)]
+        return ys[("gate_up", layer)][:, :12288]
+    out = []
+    for kind in ("dependent", "independent"):
+        xs = [x_dep(nm, ly) if kind == "dependent" else fixed[shape[nm][1]] for nm, ly in order]
+        ch = QChain([mats[nm][ly] for nm, ly in order], xs, [ys[key] for key in order])
+        for _ in range(reps):
+            ch.run()
+        torch.cuda.synchronize()
+        if ch.status() != 0:
+            raise RuntimeError("chained decode: a wait for an earlier entry's output timed out")
+        ch.free()
+        out.append({"chain": kind, "entries": len(order), "launches": reps})
+    for v in mats.values():
+        for q in v:
+            q.free()
+    calibration_copy(torch)
+    byts = LAYERS * sum(wbytes(G128S, N, K) + K * 2 + N * 2 for _, N, K in QWEN3_8B)
+    print(json.dumps({"profile_target": out, "algorithmic_bytes_per_launch": byts,
+                      "calibration_copy_bytes": 512 << 20}), flush=True)
+
+
 def profile_few_rows(torch, QMatrix, syn, reps=2):
     """The GEMM at few rows alone, for rocprofv3 runs: the Llama-3.1-8B FFN at 96 rows (up 14336x4096,
     down 4096x14336, g128s) and the Q4_0 151936x4096 LM head with argmax at 16 rows, `reps` passes
@@ -899,6 +943,8 @@ def main():
                     help="row counts of the decode GEMVs under --profile (comma-separated, default 1)")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only the prefill GEMMs, for rocprofv3 --pmc runs")
+    ap.add_argument("--profile-chain", action="store_true",
+                    help="only the chained decode step, dependent then independent, for rocprofv3 runs")
     ap.add_argument("--profile-few-rows", action="store_true",
                     help="only the GEMMs at few rows (FFN at 96 rows, LM head at 16), for rocprofv3 runs")
     ap.add_argument("--profile-moe", action="store_true",
@@ -921,6 +967,9 @@ def main():
         return
     if args.profile_gemm:
         profile_gemm(torch, QMatrix, syn)
+        return
+    if args.profile_chain:
+        profile_chain(torch, QMatrix, QChain, syn)
         return
     if args.profile_few_rows:
         profile_few_rows(torch, QMatrix, syn)

@@ -179,9 +179,10 @@ class QFfn:
 
 
 class QChain:
-    """GEMVs y_i = x_i . W_i^T over QMatrix handles, executed in order in one launch with a grid
-    barrier between entries (x_i may be an earlier entry's y). xs / ys: bf16 (ys fp32 if f32) cuda
-    tensors [M][K_i] / [M][N_i], fixed for the life of the chain; keep them alive."""
+    """GEMVs y_i = x_i . W_i^T over QMatrix handles, executed in order in one launch (x_i may be an
+    earlier entry's y: that entry publishes y as tagged link words and entry i waits, bounded, until
+    every word it reads carries the run's tag). xs / ys: bf16 (ys fp32 if f32) cuda tensors [M][K_i]
+    / [M][N_i], fixed for the life of the chain; keep them alive."""
 
     def __init__(self, mats, xs, ys, f32=False):
         self.L = require_gpu()
