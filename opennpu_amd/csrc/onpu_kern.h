@@ -973,6 +973,58 @@ DEV void gemm_block(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (
     }
 }
 
+// one 128-wide K block with the decode GEMV's arithmetic, for 16-row tiles: the codes
+// enter the MFMA as the bf16 integers 128 + u (one and-or per pair), each group's MFMA starts from
+// -136 (sum of x over the group) (symmetric formats; the sums from MFMAs against a constant
+// fragment), so that it ends at x . (u - 8) exactly, and the group scale is applied to the fp32
+// result: the exact dequant (u - 8) s, or u s + m for q4nx (m sum(x) + s x . (128 + u) - 128 s
+// sum(x)), as the GEMV computes it, with ~5 VALU ops per MFMA instead of a dequant per weight
+// (19-23 ops per 8 weights for one MFMA at this tile height; 151936 x 4096 g128s at 4 / 8 / 16 rows
+// 80 / 78 / 77 -> 61 / 63 / 71 us)
+template <int FMT, int NTW, int MBG>
+DEV void gemm_block_biased(const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW], int lane,
+                           f32x4 (&acc)[MBG][NTW]) {
+    const uint32_t mag = 0x43004300u;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    u32x4 xa[MBG][4];
+#pragma unroll
+    for (int mb = 0; mb < MBG; mb++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) xa[mb][j] = *LDS_U32X4(&xsb[(mb * 4 + j) * 64 + lane]);
+    f32x4 cs[MBG][4];
+    xsum_mfma<FMT, MBG>(xa, cs);
+#pragma unroll
+    for (int i = 0; i < NTW; i++) {
+        if (FMT == ONPU_G128S) {
+            float s, c;
+            par_sc<FMT>(pr[i], 0, s, c);
+            f32x4 cg[MBG];
+#pragma unroll
+            for (int mb = 0; mb < MBG; mb++) cg[mb] = cs[mb][0];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const u32x4 bw = unpack_biased(wr[i][j], mag);
+#pragma unroll
+                for (int mb = 0; mb < MBG; mb++) cg[mb] = mfma(xa[mb][j], bw, cg[mb]);
+            }
+#pragma unroll
+            for (int mb = 0; mb < MBG; mb++) acc1(acc[mb][i], s, cg[mb], 4);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float s, m;
+                par_sc<FMT>(pr[i], j, s, m);
+                const u32x4 bw = unpack_biased(wr[i][j], mag);
+#pragma unroll
+                for (int mb = 0; mb < MBG; mb++) {
+                    if (FMT == ONPU_Q4NX) acc4(acc[mb][i], s, m, -128.0f * s, mfma(xa[mb][j], bw, z), cs[mb][j], 4);
+                    else acc1(acc[mb][i], s, mfma(xa[mb][j], bw, cs[mb][j]), 4);
+                }
+            }
+        }
+    }
+}
+
 // The X tile of block b (MB A blocks of 16 rows) into LDS buffer buf: wave w of 4 fills fragments
 // f = MB w + i, (mb, j) = (f / 4, f % 4); lane (q, r) brings row m0 + 16 mb + r, k = 128 b + 32 j +
 // 8 q. xo[i] is the lane's byte offset of its element at b = 0 (0x80000000, past the buffer, for
@@ -1078,6 +1130,14 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     for (int mb = 0; mb < MB; mb++)
 #pragma unroll
         for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // 16-row tiles compute as the decode GEMV does (biased codes, scales after the MFMA: exact
+    // dequant); taller tiles feed the MFMA the bf16 RNE dequantized weights, whose dequant a
+    // fragment's 2-8 MFMAs share (the biased block there held 2-4 times the registers, so two
+    // workgroups per CU instead of four, and measured 0-25 % slower at 17-64 rows)
+    auto blk = [&](const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW]) {
+        if constexpr (MB == 1) gemm_block_biased<FMT, NTW, MB>(xsb, wr, pr, lane, acc);
+        else gemm_block<FMT, NTW, MB>(xsb, wr, pr, lane, acc);
+    };
     // two register sets for the weights, alternating with the two LDS buffers (no copies)
     u32x4 wa[NTW], wb[NTW];
     GPar<FMT> pa[NTW], pb[NTW];
@@ -1091,7 +1151,7 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
         // even block from (xs0, wa) while block b + 1 streams into (xs1, wb)
         gemm_load_x(xr, xo, b + 1, ktail && b + 2 == a.KB, a.K, wave, q, xs1);
         gemm_load_w<FMT, NTW>(wrs, b + 1, lane, r, wb, pb);
-        gemm_block<FMT, NTW, MB>(xs0, wa, pa, lane, acc);
+        blk(xs0, wa, pa);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
         // odd block from (xs1, wb) while block b + 2 streams into (xs0, wa)
@@ -1099,11 +1159,11 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
             gemm_load_x(xr, xo, b + 2, ktail && b + 3 == a.KB, a.K, wave, q, xs0);
             gemm_load_w<FMT, NTW>(wrs, b + 2, lane, r, wa, pa);
         }
-        gemm_block<FMT, NTW, MB>(xs1, wb, pb, lane, acc);
+        blk(xs1, wb, pb);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __syncthreads();
     }
-    if (b < kb1) gemm_block<FMT, NTW, MB>(xs0, wa, pa, lane, acc);
+    if (b < kb1) blk(xs0, wa, pa);
     // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
 #pragma unroll
     for (int mb = 0; mb < MB; mb++)

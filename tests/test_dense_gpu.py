@@ -178,7 +178,8 @@ SPLIT_CASES = [(96, 1000, 8192, 8), (130, 998, 4096, 8), (40, 14000, 4096, 4), (
 def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
     """k_qgemm split along K (fp32 partials per range, summed in range order by k_gemm_split_sum)
     with tiles of 16 mb rows: a 384-column slice over all rows and three full rows against the
-    oracle; a second call gives the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges
+    oracle (the bf16-weight one, or for 16-row tiles, which compute as the GEMV does, the exact
+    one); a second call gives the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges
     (a shorter last one) and no split agree to fp32 summation order"""
     import ctypes as C
     import torch
@@ -214,6 +215,11 @@ def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
         yf = from_torch(y1[rows])
     finally:
         q.free()
+    if mb == 1:                    # 16-row tiles compute as the GEMV does: the exact dequant
+        check_bf16_out(yc, orc.qmm(fmt, st, N, K, xb, N - 384, N), what=f"split-K fmt {fmt} {M}x{N}x{K} columns")
+        check_bf16_out(yr, orc.qmm(fmt, st, N, K, xb[rows]), what=f"split-K fmt {fmt} {M}x{N}x{K} rows")
+        check_f32_out(yf, orc.qmm(fmt, st, N, K, xb[rows]), what=f"split-K fmt {fmt} fp32 rows")
+        return
     check_gemm(yc, fmt, st, N, K, xb, N - 384, N, what=f"split-K fmt {fmt} {M}x{N}x{K} column slice")
     check_gemm(yr, fmt, st, N, K, xb[rows], what=f"split-K fmt {fmt} {M}x{N}x{K} rows")
     check_f32_out(yf, orc.qmm(fmt, st, N, K, xb[rows], bf16w=True), what=f"split-K fmt {fmt} fp32 rows")
@@ -281,8 +287,9 @@ def test_argmax_at_gemm_rows(gpu, N, monkeypatch):
             lg, idx, lgv, idv = from_torch(lg), idx.cpu().numpy(), from_torch(lgv), idv.cpu().numpy()
             assert np.array_equal(idx, orc.argmax(lg)) and np.array_equal(idv, orc.argmax(lgv))
             rows = [0, M - 1]
-            check_f32_out(lg[:, :512], orc.qmm(fmt, st, N, K, xb, 0, 512, bf16w=True), what=f"M {M} columns")
-            check_f32_out(lg[rows], orc.qmm(fmt, st, N, K, xb[rows], bf16w=True), what=f"M {M} rows")
+            bw = M > 16                # 16-row tiles compute the exact dequant, taller ones bf16 weights
+            check_f32_out(lg[:, :512], orc.qmm(fmt, st, N, K, xb, 0, 512, bf16w=bw), what=f"M {M} columns")
+            check_f32_out(lg[rows], orc.qmm(fmt, st, N, K, xb[rows], bf16w=bw), what=f"M {M} rows")
             top2 = np.sort(lg, axis=1)[:, -2:]
             apart = top2[:, 1] - top2[:, 0] > 1e-2 * np.abs(lg).max()
             assert apart.sum() >= M // 4 and np.array_equal(idx[apart], idv[apart])

@@ -140,12 +140,14 @@ def test_split_gemm_returns_the_bf16_weights(gpu, fmt):
     """the GEMM split along K at few rows on a 7000 x 8192 matrix (16, 24, 40 rows: GEMMs below 65
     rows with tiles of 16, 32, 64 rows; 96: 128-row tiles in 9 K ranges), rows one-hot at columns
     spread over K and across range boundaries: every range but the one holding the column adds exact
-    zeros to the partial sum, so Y is the bf16 RNE of those weight columns"""
+    zeros to the partial sum, so Y is the bf16 RNE of those weight columns, or with 16-row tiles
+    (the GEMV's arithmetic) the fp32 dequantized weights themselves"""
     import torch
     from opennpu_amd.device import QMatrix
     N, K = 7000, (8192 if fmt == orc.FMT_G128S else 8224)
     st = random_weights(fmt, N, K, 80 + fmt)
     Wb = orc.bf2f(orc.dequant_bf16(fmt, st, N, K)).reshape(N, K)
+    W = orc.dequant(fmt, st, N, K)
     q = QMatrix(N, K, fmt, st)
     try:
         for M in (16, 24, 40, 96):
@@ -155,7 +157,7 @@ def test_split_gemm_returns_the_bf16_weights(gpu, fmt):
             x = to_torch_bf16(one_hot(M, K, cols)).reshape(M, K)
             y = from_torch(q.mv(x, f32=True))
             torch.cuda.synchronize()
-            want = Wb[:, cols].T
+            want = (W if M <= 16 else Wb)[:, cols].T
             bad = np.argwhere(~(y == want))
             assert bad.size == 0, f"fmt {fmt} M {M}: Y[{bad[0]}] = {y[tuple(bad[0])]!r}, weight {want[tuple(bad[0])]!r}"
     finally:
