@@ -1130,12 +1130,13 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     for (int mb = 0; mb < MB; mb++)
 #pragma unroll
         for (int i = 0; i < NTW; i++) acc[mb][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    // 16-row tiles compute as the decode GEMV does (biased codes, scales after the MFMA: exact
-    // dequant); taller tiles feed the MFMA the bf16 RNE dequantized weights, whose dequant a
-    // fragment's 2-8 MFMAs share (the biased block there held 2-4 times the registers, so two
-    // workgroups per CU instead of four, and measured 0-25 % slower at 17-64 rows)
+    // 16-row tiles, and g128s 32-row tiles, compute as the decode GEMV does (biased codes, scales
+    // after the MFMA: exact dequant); the others feed the MFMA the bf16 RNE dequantized weights,
+    // whose dequant a fragment's 2-8 MFMAs share (there the biased block needs more than the 128
+    // registers of four workgroups per CU; with two it measured 0-25 % slower at 17-64 rows; g128s
+    // 32-row tiles fit, 151936 x 4096 at 17 / 24 rows 101.4 / 109.6 -> 91.3 / 102.7 us)
     auto blk = [&](const u32x4 * xsb, const u32x4 (&wr)[NTW], const GPar<FMT> (&pr)[NTW]) {
-        if constexpr (MB == 1) gemm_block_biased<FMT, NTW, MB>(xsb, wr, pr, lane, acc);
+        if constexpr (MB == 1 || (MB == 2 && FMT == ONPU_G128S)) gemm_block_biased<FMT, NTW, MB>(xsb, wr, pr, lane, acc);
         else gemm_block<FMT, NTW, MB>(xsb, wr, pr, lane, acc);
     };
     // two register sets for the weights, alternating with the two LDS buffers (no copies)

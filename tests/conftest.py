@@ -31,6 +31,13 @@ def from_torch(t):
     return t.float().cpu().numpy()
 
 
+def gemm_exact(fmt, M):
+    """whether the GEMM computes the exact dequant at M <= 64 rows (its 16-row tiles, and g128s
+    32-row tiles, take the decode GEMV's arithmetic) rather than bf16 RNE weights"""
+    import oracle.oracle as orc
+    return M <= 16 or (M <= 32 and fmt == orc.FMT_G128S)
+
+
 def check_bf16_out(y, ref, tol=1e-2, what="", floor=2e-5):
     """bf16 outputs against the fp64 oracle: the stated tolerance max|y-r|/max|r| <= tol, and per
     element within half a bf16 ulp of the exact result plus an fp32-accumulation floor."""

@@ -10,7 +10,7 @@ import pytest
 
 import oracle.oracle as orc
 from opennpu_amd import synthetic as syn
-from tests.conftest import check_bf16_out, check_f32_out, from_torch, to_torch_bf16
+from tests.conftest import check_bf16_out, check_f32_out, from_torch, gemm_exact, to_torch_bf16
 
 pytestmark = pytest.mark.gpu
 FMTS = [orc.FMT_Q4NX, orc.FMT_Q4S, orc.FMT_G128S, orc.FMT_Q4_0]
@@ -178,8 +178,7 @@ SPLIT_CASES = [(96, 1000, 8192, 8), (130, 998, 4096, 8), (40, 14000, 4096, 4), (
 def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
     """k_qgemm split along K (fp32 partials per range, summed in range order by k_gemm_split_sum)
     with tiles of 16 mb rows: a 384-column slice over all rows and three full rows against the
-    oracle (the bf16-weight one, or for 16-row tiles, which compute as the GEMV does, the exact
-    one); a second call gives the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges
+    oracle (the bf16-weight one, or for the tiles that compute as the GEMV does, the exact one); a second call gives the same bits; the bf16 output is the RNE of the fp32 one; 3 ranges
     (a shorter last one) and no split agree to fp32 summation order"""
     import ctypes as C
     import torch
@@ -215,7 +214,7 @@ def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
         yf = from_torch(y1[rows])
     finally:
         q.free()
-    if mb == 1:                    # 16-row tiles compute as the GEMV does: the exact dequant
+    if gemm_exact(fmt, M):         # tiles that compute as the GEMV does: the exact dequant
         check_bf16_out(yc, orc.qmm(fmt, st, N, K, xb, N - 384, N), what=f"split-K fmt {fmt} {M}x{N}x{K} columns")
         check_bf16_out(yr, orc.qmm(fmt, st, N, K, xb[rows]), what=f"split-K fmt {fmt} {M}x{N}x{K} rows")
         check_f32_out(yf, orc.qmm(fmt, st, N, K, xb[rows]), what=f"split-K fmt {fmt} fp32 rows")
@@ -287,7 +286,7 @@ def test_argmax_at_gemm_rows(gpu, N, monkeypatch):
             lg, idx, lgv, idv = from_torch(lg), idx.cpu().numpy(), from_torch(lgv), idv.cpu().numpy()
             assert np.array_equal(idx, orc.argmax(lg)) and np.array_equal(idv, orc.argmax(lgv))
             rows = [0, M - 1]
-            bw = M > 16                # 16-row tiles compute the exact dequant, taller ones bf16 weights
+            bw = not gemm_exact(fmt, M)     # exact dequant (GEMV arithmetic) or bf16 RNE weights
             check_f32_out(lg[:, :512], orc.qmm(fmt, st, N, K, xb, 0, 512, bf16w=bw), what=f"M {M} columns")
             check_f32_out(lg[rows], orc.qmm(fmt, st, N, K, xb[rows], bf16w=bw), what=f"M {M} rows")
             top2 = np.sort(lg, axis=1)[:, -2:]

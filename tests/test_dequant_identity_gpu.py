@@ -22,7 +22,7 @@ import pytest
 
 import oracle.oracle as orc
 from opennpu_amd import synthetic as syn
-from tests.conftest import from_torch, to_torch_bf16
+from tests.conftest import from_torch, gemm_exact, to_torch_bf16
 
 pytestmark = pytest.mark.gpu
 FMTS = [orc.FMT_Q4NX, orc.FMT_Q4S, orc.FMT_G128S, orc.FMT_Q4_0]
@@ -140,8 +140,8 @@ def test_split_gemm_returns_the_bf16_weights(gpu, fmt):
     """the GEMM split along K at few rows on a 7000 x 8192 matrix (16, 24, 40 rows: GEMMs below 65
     rows with tiles of 16, 32, 64 rows; 96: 128-row tiles in 9 K ranges), rows one-hot at columns
     spread over K and across range boundaries: every range but the one holding the column adds exact
-    zeros to the partial sum, so Y is the bf16 RNE of those weight columns, or with 16-row tiles
-    (the GEMV's arithmetic) the fp32 dequantized weights themselves"""
+    zeros to the partial sum, so Y is the bf16 RNE of those weight columns, or where the tiles take
+    the GEMV's arithmetic (16 rows; 32 rows for g128s) the fp32 dequantized weights themselves"""
     import torch
     from opennpu_amd.device import QMatrix
     N, K = 7000, (8192 if fmt == orc.FMT_G128S else 8224)
@@ -157,7 +157,7 @@ def test_split_gemm_returns_the_bf16_weights(gpu, fmt):
             x = to_torch_bf16(one_hot(M, K, cols)).reshape(M, K)
             y = from_torch(q.mv(x, f32=True))
             torch.cuda.synchronize()
-            want = (W if M <= 16 else Wb)[:, cols].T
+            want = (W if gemm_exact(fmt, M) else Wb)[:, cols].T
             bad = np.argwhere(~(y == want))
             assert bad.size == 0, f"fmt {fmt} M {M}: Y[{bad[0]}] = {y[tuple(bad[0])]!r}, weight {want[tuple(bad[0])]!r}"
     finally:
