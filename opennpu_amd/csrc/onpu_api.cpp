@@ -632,21 +632,20 @@ hipError_t argmax_gemv(Mat4 * m, const uint16_t * x, int64_t M, float * logits, 
 // Up to 64 rows: the decode GEMV, whose time grows with the rows, unless the GEMM with a tile of
 // 16-64 rows split along K (about the same time from 1 to 16 rows) is faster. Crossovers measured
 // on MI355X over >= 600 MB of distinct weight copies (g128s unless named, us GEMV -> GEMM):
-// 4096 x 4096 at 64 rows 19.6 -> 17.5 (48: 15.2 / 16.2 stays); 6144 x 4096 at 24 rows 16.4 -> 14.3
-// (16: 12.0 / 13.0 stays); 4096 x 12288 at 16 rows 16.8 -> 16.6, 24576 x 4096 27.5 -> 19.7 (12: 16.6
-// / 19.5 stays), q4nx 24576 x 4096 29.3 -> 22.5; 151936 x 4096 at 12 rows 97.3 -> 74.9 (Q4_0 98.4 ->
-// 81.1; 8: 67.7 / 72.1 stays); 8192 x 28672 at 8 rows 38.6 -> 35.7 (4: 34.1 / 35.3 stays); 57344 x
-// 8192 at 4 rows 62.2 -> 58.0 (2: 48.9 / 57.7 stays); with the 16-row tile's GEMV arithmetic the g128s
-// 151936 x 4096 head at 4 / 8 rows 69.3 / 67.7 -> 61-64 / 63 (Q4_0 at 8 rows 72.1 / 75: stays).
+// 4096 x 4096 at 64 rows 19.6 -> 17.5 (48: 15.2 / 16.2 stays); 6144 x 4096 at 24 rows 16.4 -> 13.8
+// (16: 12.0 / 12.4 stays); 4096 x 12288 at 16 rows 16.6 -> 16.6, 14336 x 4096 20.5 -> 15.3, 24576 x
+// 4096 27.5 -> 22.4 (12: 16.4 / 22.0 stays), q4nx 24576 x 4096 28.3 -> 24.5; at 12 rows 151936 x 4096
+// 97.0 -> 66.7 (Q4_0 98.4 -> 81.1), 57344 x 8192 106.6 -> 64.1, 8192 x 28672 52.6 -> 37.1. At 1-8 rows
+// the two are within a few percent for the largest matrices, with the sign changing from box to
+// box (57344 x 8192 at 4 rows 49.9 / 63.8 on one, 62.2 / 58.0 on another), so the GEMV keeps them.
 // ONPU_FORCE_GEMM = 1 takes the GEMM, -1 the GEMV.
-bool rows_take_gemv(int fmt, int64_t M, int64_t N, int64_t K) {
+bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
     const int f = env_int("ONPU_FORCE_GEMM", 0);
     if (M > 64 || f == 1) return false;
     if (f == -1) return true;
     const int64_t nk = N * K;
     return !((M >= 64 && nk >= 16000000) || (M >= 24 && nk >= 24000000) || (M >= 16 && nk >= 40000000) ||
-             (M >= 12 && nk >= 200000000) || (M >= 8 && nk >= 200000000 && K >= 8192) ||
-             (M >= 4 && nk >= 400000000 && (K >= 8192 || fmt == ONPU_G128S)));
+             (M >= 12 && nk >= 200000000));
 }
 
 // mv_core's choice for M rows: the decode GEMV (path 0), k_qgemm with mb A blocks of 16 rows and ntw
@@ -654,9 +653,9 @@ bool rows_take_gemv(int fmt, int64_t M, int64_t N, int64_t K) {
 // workgroups per K range
 struct MvPlan { int path, mb, ntw; int64_t S, kbs, wgs; };
 
-MvPlan plan_mv(int fmt, int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus) {
+MvPlan plan_mv(int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus) {
     MvPlan p{0, 8, 2, 1, KB, 0};
-    if (rows_take_gemv(fmt, M, N, K)) return p;
+    if (rows_take_gemv(M, N, K)) return p;
     int cfg = 0;
     int64_t grid = 0;
     GArgs ga{};
@@ -703,7 +702,7 @@ MvPlan plan_mv(int fmt, int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M,
 hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
     if (M <= 0) return hipSuccess;
     const uint8_t * W = m->dev + e * m->dstride;
-    const MvPlan p = plan_mv(m->fmt, m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
+    const MvPlan p = plan_mv(m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
     if (p.path == 0) return gemv_core(m, e, x, M, y, yf32, s);
     if (p.path == 2) {
         int cfg = 0;
@@ -1007,7 +1006,7 @@ int onpu_has_shape(int, int, int) { return device().ok; }
 // out = mb, rt, nb, xl, tw, kw, bpw, gx, built (1 if that kernel variant exists), max waves
 void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out) {
     const Tiled g = tiled_geom(fmt, N, K);
-    const MvPlan p = plan_mv(fmt, N, K, g.NT, g.KB, M, device().cus > 0 ? device().cus : 256);
+    const MvPlan p = plan_mv(N, K, g.NT, g.KB, M, device().cus > 0 ? device().cus : 256);
     const int64_t v[6] = {p.path, p.mb, p.ntw, p.S, p.kbs, p.wgs};
     for (int i = 0; i < 6; i++) out[i] = v[i];
 }
@@ -1134,11 +1133,11 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
     // per-row counters (grown to the rows of the call; new counters zeroed by a kernel on the stream,
     // and each call leaves them zero). Outgrown buffers are kept, so graphs keep valid pointers.
     const bool fused = env_int("ONPU_ARGMAX_FUSED", 1) != 0;
-    if (rows_take_gemv(m->fmt, M, m->N, m->K) && fused) {
+    if (rows_take_gemv(M, m->N, m->K) && fused) {
         HIPR(argmax_gemv(m, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;
     }
-    const MvPlan p = plan_mv(m->fmt, m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
+    const MvPlan p = plan_mv(m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
     if (fused && p.path == 1 && p.S == 1 && p.mb <= 4 && p.ntw == 2 && M <= 16 * p.mb) {
         HIPR(argmax_gemm(m, p, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;
