@@ -370,12 +370,14 @@ def test_gemm_llama_ffn(gpu, name, N, K):
                    what=f"{name} column {n} (column tile {j})")
 
 
-def test_gemm_two_streams(gpu):
-    """split-K GEMMs on two streams at once: each stream has its own partials and slot words, so
-    both results equal the one-stream results bit for bit"""
+@pytest.mark.parametrize("M", [1024, 96])
+def test_gemm_two_streams(gpu, M):
+    """split-K GEMMs on two streams at once (1024 rows: the stream-K kernel's partial tiles and slot
+    words; 96 rows: the 128-row tiles' K-range partials): each stream has its own workspace, so both
+    results equal the one-stream results bit for bit"""
     import torch
     from opennpu_amd.device import QMatrix
-    M, N, K = 1024, 7168, 4096
+    N, K = 7168, 4096
     qa = QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 31))
     qb = QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 32))
     try:
