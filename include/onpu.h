@@ -140,8 +140,8 @@ void onpu_plan_gemv(int fmt, int64_t N, int64_t K, int M, int64_t slots, int epi
 /* what onpu_dense_mv_dev runs for M rows of an [N][K] matrix (host only; no counterpart in the
  * reference, whose NPU dispatch has no such choice): path (0 the decode GEMV, 1 the GEMM with tiles
  * of 16 mb rows, 2 the 256-row stream-K GEMM), mb, weight tiles per wave, K ranges S, K blocks per
- * range, workgroups per range */
-void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out /* [6] */);
+ * range, workgroups per range, and 1 if 16-row tiles keep the weights two blocks ahead */
+void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out /* [7] */);
 /* N, K, fmt, E, row tiles, K blocks, HBM bytes per expert, HBM base address */
 void onpu_dense_info(void * h, int64_t * out /* [8] */);
 /* dequantized weights of expert e as the GPU stores them: fp32 (bf16 = 0) or bf16 RNE bits */

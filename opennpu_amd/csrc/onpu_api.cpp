@@ -650,11 +650,11 @@ bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
 
 // mv_core's choice for M rows: the decode GEMV (path 0), k_qgemm with mb A blocks of 16 rows and ntw
 // weight tiles per wave, in S ranges of kbs K blocks (path 1), or k_qgemm_sk (path 2); wgs: k_qgemm's
-// workgroups per K range
-struct MvPlan { int path, mb, ntw; int64_t S, kbs, wgs; };
+// workgroups per K range; deep: 16-row tiles with the weights two blocks ahead
+struct MvPlan { int path, mb, ntw; int64_t S, kbs, wgs; int deep; };
 
 MvPlan plan_mv(int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus) {
-    MvPlan p{0, 8, 2, 1, KB, 0};
+    MvPlan p{0, 8, 2, 1, KB, 0, 0};
     if (rows_take_gemv(M, N, K)) return p;
     int cfg = 0;
     int64_t grid = 0;
@@ -696,6 +696,9 @@ MvPlan plan_mv(int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus)
             p.S = (KB + p.kbs - 1) / p.kbs;
         }
     }
+    // at most two workgroups per CU: one block in flight per workgroup leaves the memory idle
+    const int ed = env_int("ONPU_GEMM_DEEP", -1);
+    p.deep = p.mb == 1 && p.ntw == 2 && (ed >= 0 ? ed != 0 : p.S * p.wgs <= 2 * (int64_t) cus);
     return p;
 }
 
@@ -725,7 +728,7 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         if (e != hipSuccess) return e;
         a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
         a.x = x; a.ldx = m->K; a.ldy = m->N; a.yf32 = 1; a.y = a.ws;
-        a.splits = (int) p.S; a.kbs = p.kbs;
+        a.splits = (int) p.S; a.kbs = p.kbs; a.deep = p.deep;
         if ((e = launch_qgemm(m->fmt, a, p.ntw, p.mb, s)) != hipSuccess) return e;
         return launch_gemm_split_sum(a.ws, (int) p.S, M, m->N, y, m->N, yf32, s);
     }
@@ -735,6 +738,7 @@ hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y,
         a.W = W; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = std::min(rows_max, M - r0);
         a.x = x + r0 * m->K; a.ldx = m->K; a.ldy = m->N; a.yf32 = yf32;
         a.y = (char *) y + r0 * m->N * (yf32 ? 4 : 2);
+        a.deep = p.deep;
         const hipError_t e = launch_qgemm(m->fmt, a, p.ntw, p.mb, s);
         if (e != hipSuccess) return e;
     }
@@ -1007,8 +1011,8 @@ int onpu_has_shape(int, int, int) { return device().ok; }
 void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out) {
     const Tiled g = tiled_geom(fmt, N, K);
     const MvPlan p = plan_mv(N, K, g.NT, g.KB, M, device().cus > 0 ? device().cus : 256);
-    const int64_t v[6] = {p.path, p.mb, p.ntw, p.S, p.kbs, p.wgs};
-    for (int i = 0; i < 6; i++) out[i] = v[i];
+    const int64_t v[7] = {p.path, p.mb, p.ntw, p.S, p.kbs, p.wgs, p.deep};
+    for (int i = 0; i < 7; i++) out[i] = v[i];
 }
 
 void onpu_plan_gemv(int fmt, int64_t N, int64_t K, int M, int64_t slots, int epi, int64_t * out) {
@@ -1120,6 +1124,7 @@ static hipError_t argmax_gemm(Mat4 * m, const MvPlan & p, const uint16_t * x, in
     a.W = m->dev; a.NT = m->g.NT; a.KB = m->g.KB; a.N = m->N; a.K = m->K; a.M = M;
     a.x = x; a.ldx = m->K; a.y = logits; a.ldy = m->N; a.yf32 = 1;
     a.akeys = m->am_keys.as<uint64_t>();
+    a.deep = p.deep;
     if (const hipError_t e = launch_qgemm(m->fmt, a, p.ntw, p.mb, s); e != hipSuccess) return e;
     return launch_argmax_keys(a.akeys, gn, M, argmax, s);
 }

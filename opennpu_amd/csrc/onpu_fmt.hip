@@ -39,10 +39,12 @@ hipError_t FN(qgemm)(const GArgs & a, int ntw, int mb, hipStream_t s) {
     const int64_t gm = (a.M + 16 * mb - 1) / (16 * mb), gn = (a.NT + 4 * ntw - 1) / (4 * ntw);
     const dim3 grid((unsigned) (gm * gn * (a.splits > 1 ? a.splits : 1)));
     if (a.akeys) {                            // argmax keys: one row tile, no split (host checked)
-        if (mb == 1) k_qgemm<F, 2, 1, true><<<grid, 256, 0, s>>>(a);
+        if (mb == 1 && a.deep) k_qgemm<F, 2, 1, true, true><<<grid, 256, 0, s>>>(a);
+        else if (mb == 1) k_qgemm<F, 2, 1, true><<<grid, 256, 0, s>>>(a);
         else if (mb == 2) k_qgemm<F, 2, 2, true><<<grid, 256, 0, s>>>(a);
         else k_qgemm<F, 2, 4, true><<<grid, 256, 0, s>>>(a);
-    } else if (mb == 1 && ntw == 2) k_qgemm<F, 2, 1><<<grid, 256, 0, s>>>(a);
+    } else if (mb == 1 && ntw == 2 && a.deep) k_qgemm<F, 2, 1, false, true><<<grid, 256, 0, s>>>(a);
+    else if (mb == 1 && ntw == 2) k_qgemm<F, 2, 1><<<grid, 256, 0, s>>>(a);
     else if (mb == 2 && ntw == 2) k_qgemm<F, 2, 2><<<grid, 256, 0, s>>>(a);
     else if (mb == 4 && ntw == 2) k_qgemm<F, 2, 4><<<grid, 256, 0, s>>>(a);
     else if (mb != 8) return hipErrorInvalidValue;

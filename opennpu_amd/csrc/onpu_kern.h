@@ -1070,7 +1070,9 @@ DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int la
 
 // AK: one row tile (M <= 16 MB), no split: the epilogue also leaves the workgroup's argmax key of
 // each row over its columns in a.akeys[m][N block] (argmax_key: larger value, then lower column)
-template <int FMT, int NTW, int MB, bool AK = false>
+// DEEP (16-row tiles): weights two blocks ahead (three register sets), for grids of at most two
+// workgroups per CU, where one block in flight per workgroup leaves the memory idle
+template <int FMT, int NTW, int MB, bool AK = false, bool DEEP = false>
 __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     __shared__ u32x4 xs0[MB * 4 * 64], xs1[MB * 4 * 64];   // 2 x MB x 4 KiB
     constexpr int MT = 16 * MB;                           // rows of the workgroup tile
@@ -1142,6 +1144,53 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     // two register sets for the weights, alternating with the two LDS buffers (no copies)
     u32x4 wa[NTW], wb[NTW];
     GPar<FMT> pa[NTW], pb[NTW];
+    if constexpr (MB == 1 && DEEP) {
+        // 16-row tiles on small grids: a block's loads are small (4 KiB of X, NTW weight blocks per
+        // wave) and its compute short, so the weights stay two blocks ahead (57344 x 8192 at 4-16
+        // rows 65 -> 54 us, 8192 x 28672 38 -> 33 us; the 151936 x 4096 heads, ~4.6 workgroups per
+        // CU, measured 2-6 % slower and keep one block): three register sets in rotation,
+        // block b + 2's weights issued before block b's compute. X (from L2) stays one block ahead
+        // and is issued after each barrier: the barrier's fence waits for every LDS-DMA load issued
+        // before it, so an X load issued earlier would hold it. Each stage issues its X load, then
+        // (after a scheduling fence, so the order holds) its weight loads, and waits for all but
+        // those before the barrier. Loads past the range re-read block kb1 - 1 (in range) into a
+        // set that is not read again; the last wait drains them.
+        __shared__ u32x4 xs2[4 * 64];
+        u32x4 wc[NTW];
+        GPar<FMT> pc[NTW];
+        const int64_t bl = kb1 - 1;
+        auto issue = [&](int64_t bx, u32x4 * xsb, int64_t bw, u32x4 (&w)[NTW], GPar<FMT> (&p)[NTW]) {
+            const int64_t cx = bx < kb1 ? bx : bl, cw = bw < kb1 ? bw : bl;
+            gemm_load_x(xr, xo, cx, ktail && cx + 1 == a.KB, a.K, wave, q, xsb);
+            __builtin_amdgcn_sched_barrier(0);
+            gemm_load_w<FMT, NTW>(wrs, cw, lane, r, w, p);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        constexpr int WL = 2 * NTW;                       // weight loads of one block per wave
+        gemm_load_w<FMT, NTW>(wrs, kb0, lane, r, wa, pa);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(kb0, xs0, kb0 + 1, wb, pb);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(WL));       // X of block kb0 (and its weights) landed
+        __syncthreads();
+        // one exit and the same loads outstanding on every path into the loop head (the blocks
+        // past the range are skipped around their compute, not by leaving the loop, so the
+        // compiler's own waits stay exact)
+        for (int64_t b = kb0; b < kb1; b += 3) {
+            issue(b + 1, xs1, b + 2, wc, pc);
+            blk(xs0, wa, pa);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(WL));   // X of block b + 1 landed
+            __syncthreads();
+            issue(b + 2, xs2, b + 3, wa, pa);
+            if (b + 1 < kb1) blk(xs1, wb, pb);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(WL));
+            __syncthreads();
+            issue(b + 3, xs0, b + 4, wb, pb);
+            if (b + 2 < kb1) blk(xs2, wc, pc);
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(WL));
+            __syncthreads();
+        }
+        __builtin_amdgcn_s_waitcnt(0x0f70);               // vmcnt(0): no load still writes LDS
+    } else {
     gemm_load_x(xr, xo, kb0, ktail && kb0 + 1 == a.KB, a.K, wave, q, xs0);
     gemm_load_w<FMT, NTW>(wrs, kb0, lane, r, wa, pa);
     __builtin_amdgcn_s_waitcnt(0x0f70);                  // vmcnt(0): the DMA into xs0 is done
@@ -1165,6 +1214,7 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
         __syncthreads();
     }
     if (b < kb1) blk(xs0, wa, pa);
+    }
     // store: lane (q, r) holds rows 4 q + v of A-block mb, column r of weight tile t0 + i
 #pragma unroll
     for (int mb = 0; mb < MB; mb++)

@@ -66,6 +66,7 @@ struct GArgs {
     int64_t kbs;
     // k_qgemm, one row tile and no split: also each workgroup's argmax key per row, akeys[m][N block]
     uint64_t * akeys;
+    int deep;                 // k_qgemm 16-row tiles: weights two blocks ahead
 };
 constexpr int GSK_SYNC_STRIDE = 16;
 constexpr int GSK_CTL_TAG = 0, GSK_CTL_DONE = 16, GSK_CTL_ERR = 32, GSK_CTL_INTS = 48;

@@ -117,15 +117,16 @@ def test_mv_plans():
     beyond; K ranges that cover every K block, none empty, at least 4 blocks each unless forced, and
     fp32 partials within the 64 MiB split-K workspace; the stream-K kernel only above 128 rows"""
     L = _lib.lib()
-    o = (C.c_int64 * 6)()
+    o = (C.c_int64 * 7)()
     seen = set()
     for N in (64, 1000, 4096, 14336, 24576, 57344, 151936):
         for K in (512, 4096, 8192, 14336, 28672):
             KB = -(-K // 128)
             for M in (1, 2, 4, 8, 12, 16, 17, 24, 32, 33, 48, 64, 65, 96, 128, 129, 256, 512, 2048):
                 L.onpu_plan_mv(2, N, K, M, o)
-                path, mb, ntw, S, kbs, wgs = tuple(o)
-                seen.add((path, mb if path == 1 else 0))
+                path, mb, ntw, S, kbs, wgs, deep = tuple(o)
+                seen.add((path, mb if path == 1 else 0, deep))
+                assert deep in (0, 1) and (not deep or (path == 1 and mb == 1 and S * wgs <= 512)), (N, K, M, tuple(o))
                 assert path in (0, 1, 2) and (path != 0 or M <= 64) and (path != 2 or M > 128), (N, K, M, tuple(o))
                 if path != 1:
                     continue
@@ -135,7 +136,7 @@ def test_mv_plans():
                 if S > 1:
                     assert kbs >= 4 and S * M * N * 4 <= 256 * 256 * 1024, (N, K, M, tuple(o))
                 assert wgs == -(-M // (16 * mb)) * -(-(-(-N // 16)) // (4 * ntw)), (N, K, M, tuple(o))
-    assert {(0, 0), (1, 1), (1, 2), (1, 4), (1, 8), (2, 0)} <= seen, seen
+    assert {(0, 0, 0), (1, 1, 0), (1, 1, 1), (1, 2, 0), (1, 4, 0), (1, 8, 0), (2, 0, 0)} <= seen, seen
 
 
 @pytest.mark.parametrize("fmt", [0, 1, 2, 3])

@@ -186,7 +186,7 @@ def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
     from opennpu_amd.device import QMatrix
     if fmt != orc.FMT_G128S:
         K -= 32                                       # a K tail inside the last 128-wide block
-    o = (C.c_int64 * 6)()
+    o = (C.c_int64 * 7)()
     _lib.lib().onpu_plan_mv(fmt, N, K, M, o)
     assert o[0] == 1 and o[1] == mb and o[3] > 1, tuple(o)     # the split GEMM with these tiles
     st = syn.weights(fmt, N, K, 51 + M)
@@ -202,6 +202,13 @@ def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
         monkeypatch.setenv("ONPU_GEMM_SPLIT", "1")
         y0 = q.mv(x, f32=True)
         monkeypatch.delenv("ONPU_GEMM_SPLIT")
+        if mb == 1:                    # weights two blocks ahead (the default here) or one: same sums
+            assert o[6] == 1, tuple(o)
+            monkeypatch.setenv("ONPU_GEMM_DEEP", "0")
+            y4 = q.mv(x, f32=True)
+            monkeypatch.delenv("ONPU_GEMM_DEEP")
+            torch.cuda.synchronize()
+            assert torch.equal(y1, y4), "the deeper weight pipeline changed the result"
         torch.cuda.synchronize()
         assert torch.equal(y1, y2), "split-K GEMM is not deterministic"
         assert torch.equal(yb, y1.to(torch.bfloat16)), "bf16 output is not the RNE of the fp32 sums"
@@ -268,7 +275,7 @@ def test_argmax_at_gemm_rows(gpu, N, monkeypatch):
     from opennpu_amd import _lib
     from opennpu_amd.device import QMatrix
     fmt, K = orc.FMT_G128S, 4096
-    o = (C.c_int64 * 6)()
+    o = (C.c_int64 * 7)()
     for M in (16, 24, 48):
         _lib.lib().onpu_plan_mv(fmt, N, K, M, o)
         assert o[0] == 1 and (o[3] > 1) == (N == 20000), (N, M, tuple(o))
