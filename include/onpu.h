@@ -147,8 +147,9 @@ void onpu_dense_info(void * h, int64_t * out /* [8] */);
 /* dequantized weights of expert e as the GPU stores them: fp32 (bf16 = 0) or bf16 RNE bits */
 int onpu_dense_dequant(void * h, int64_t e, void * out_host, int bf16);
 /* y [M][N] = x [M][K] . W^T on `stream` (hipStream_t; NULL: the default stream); x bf16 in HBM,
- * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels (from 12-64 rows up, depending on
- * N K, the MFMA GEMM, which is faster there: onpu_plan_mv), larger M the MFMA GEMM. */
+ * y bf16 (y_f32 = 0) or fp32 in HBM. M <= 64 runs the GEMV kernels (for larger matrices, from 1-64
+ * rows up depending on N and K, the MFMA GEMM, which is faster there: onpu_plan_mv), larger M the
+ * MFMA GEMM. */
 int onpu_dense_mv_dev(void * h, const void * x, int64_t M, void * y, int y_f32, void * stream);
 /* Workspace of the calls above. The MFMA GEMM splits K (fp32 partials of K ranges, or the partial
  * tiles and slot words of its 256-row stream-K form above 128 rows) in a workspace of about 64 MiB (kept until the process ends): one per stream for eager

@@ -635,9 +635,11 @@ hipError_t argmax_gemv(Mat4 * m, const uint16_t * x, int64_t M, float * logits, 
 // 4096 x 4096 at 64 rows 19.6 -> 17.5 (48: 15.2 / 16.2 stays); 6144 x 4096 at 24 rows 16.4 -> 13.8
 // (16: 12.0 / 12.4 stays); 4096 x 12288 at 16 rows 16.6 -> 16.6, 14336 x 4096 20.5 -> 15.3, 24576 x
 // 4096 27.5 -> 22.4 (12: 16.4 / 22.0 stays), q4nx 24576 x 4096 28.3 -> 24.5; at 12 rows 151936 x 4096
-// 97.0 -> 66.7 (Q4_0 98.4 -> 81.1), 57344 x 8192 106.6 -> 64.1, 8192 x 28672 52.6 -> 37.1. At 1-8 rows
-// the two are within a few percent for the largest matrices, with the sign changing from box to
-// box (57344 x 8192 at 4 rows 49.9 / 63.8 on one, 62.2 / 58.0 on another), so the GEMV keeps them.
+// 97.0 -> 66.7 (Q4_0 98.4 -> 81.1), 57344 x 8192 106.6 -> 64.1, 8192 x 28672 52.6 -> 37.1. With the
+// 16-row tile's weights two blocks ahead (same process, alternating): K >= 16384 from one row
+// (4096 x 28672 31.5 -> 21.9, 5120 x 25600 28.7 -> 21.9, 8192 x 28672 34.3 -> 30.9, Q4_0 36.5 ->
+// 33.2, 16384 x 16384 34.2 -> 31.8), K = 8192 with N K >= 2e8 from 4 rows (28672 x 8192 39.3 -> 30.8,
+// 57344 x 8192 49.2 / 50.4 at 4, 61.7 -> 51.4 at 8; at 1-2 rows the GEMV: 40.9 / 50.1).
 // ONPU_FORCE_GEMM = 1 takes the GEMM, -1 the GEMV.
 bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
     const int f = env_int("ONPU_FORCE_GEMM", 0);
@@ -645,7 +647,8 @@ bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
     if (f == -1) return true;
     const int64_t nk = N * K;
     return !((M >= 64 && nk >= 16000000) || (M >= 24 && nk >= 24000000) || (M >= 16 && nk >= 40000000) ||
-             (M >= 12 && nk >= 200000000));
+             (M >= 12 && nk >= 200000000) || (M >= 4 && K >= 8192 && nk >= 200000000) ||
+             (K >= 16384 && nk >= 64000000));
 }
 
 // mv_core's choice for M rows: the decode GEMV (path 0), k_qgemm with mb A blocks of 16 rows and ntw

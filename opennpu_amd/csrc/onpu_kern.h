@@ -6,7 +6,7 @@
 //   k_qgemv      up to 64 rows: the decode GEMV family. Integer MFMA on biased codes (128 + u) in
 //                bf16, group scales applied in fp32 between MFMA steps, x column sums from an
 //                extra MFMA against ones; epilogues: store, SiLU(gate) * up, MoE slot sum
-//   k_qgemm      prefill (and 12-64 rows of larger matrices): x tile in LDS, int4 tile dequantized
+//   k_qgemm      prefill (and 1-64 rows of larger matrices): x tile in LDS, int4 tile dequantized
 //                to bf16 RNE((u-8)s) in registers and fed to v_mfma_f32_16x16x32_bf16, fp32
 //                accumulate; split along K into fp32 partials when the tiles leave CUs idle
 //   k_moe_gemm   grouped expert products (MoE prompts) over a device work list
