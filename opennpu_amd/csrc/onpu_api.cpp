@@ -656,7 +656,7 @@ bool rows_take_gemv(int64_t M, int64_t N, int64_t K) {
 // workgroups per K range; deep: 16-row tiles with the weights two blocks ahead
 struct MvPlan { int path, mb, ntw; int64_t S, kbs, wgs; int deep; };
 
-MvPlan plan_mv(int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus) {
+MvPlan plan_mv(int fmt, int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus) {
     MvPlan p{0, 8, 2, 1, KB, 0, 0};
     if (rows_take_gemv(M, N, K)) return p;
     int cfg = 0;
@@ -699,16 +699,20 @@ MvPlan plan_mv(int64_t N, int64_t K, int64_t NT, int64_t KB, int64_t M, int cus)
             p.S = (KB + p.kbs - 1) / p.kbs;
         }
     }
-    // at most two workgroups per CU: one block in flight per workgroup leaves the memory idle
+    // weights two blocks ahead with at most two workgroups per CU (one block in flight per
+    // workgroup leaves the memory idle there): 16-row tiles, and g128s 32-row tiles of larger
+    // matrices (57344 x 8192 at 17-32 rows 81-84 -> 74-80 us, 24576 x 4096 24.1-25.3 -> 22.5-24.0;
+    // the per-32 formats and matrices below 1e8 weights measured 1-7 % slower there)
     const int ed = env_int("ONPU_GEMM_DEEP", -1);
-    p.deep = p.mb == 1 && p.ntw == 2 && (ed >= 0 ? ed != 0 : p.S * p.wgs <= 2 * (int64_t) cus);
+    const bool dtile = p.mb == 1 || (p.mb == 2 && fmt == ONPU_G128S && N * K >= 100000000);
+    p.deep = p.ntw == 2 && p.mb <= 2 && (ed >= 0 ? ed != 0 : dtile && p.S * p.wgs <= 2 * (int64_t) cus);
     return p;
 }
 
 hipError_t mv_core(Mat4 * m, int64_t e, const uint16_t * x, int64_t M, void * y, int yf32, hipStream_t s) {
     if (M <= 0) return hipSuccess;
     const uint8_t * W = m->dev + e * m->dstride;
-    const MvPlan p = plan_mv(m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
+    const MvPlan p = plan_mv(m->fmt, m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
     if (p.path == 0) return gemv_core(m, e, x, M, y, yf32, s);
     if (p.path == 2) {
         int cfg = 0;
@@ -1013,7 +1017,7 @@ int onpu_has_shape(int, int, int) { return device().ok; }
 // out = mb, rt, nb, xl, tw, kw, bpw, gx, built (1 if that kernel variant exists), max waves
 void onpu_plan_mv(int fmt, int64_t N, int64_t K, int64_t M, int64_t * out) {
     const Tiled g = tiled_geom(fmt, N, K);
-    const MvPlan p = plan_mv(N, K, g.NT, g.KB, M, device().cus > 0 ? device().cus : 256);
+    const MvPlan p = plan_mv(fmt, N, K, g.NT, g.KB, M, device().cus > 0 ? device().cus : 256);
     const int64_t v[7] = {p.path, p.mb, p.ntw, p.S, p.kbs, p.wgs, p.deep};
     for (int i = 0; i < 7; i++) out[i] = v[i];
 }
@@ -1145,7 +1149,7 @@ int onpu_dense_argmax_dev(void * h, const void * x, int64_t M, float * logits, i
         HIPR(argmax_gemv(m, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;
     }
-    const MvPlan p = plan_mv(m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
+    const MvPlan p = plan_mv(m->fmt, m->N, m->K, m->g.NT, m->g.KB, M, device().cus);
     if (fused && p.path == 1 && p.S == 1 && p.mb <= 4 && p.ntw == 2 && M <= 16 * p.mb) {
         HIPR(argmax_gemm(m, p, (const uint16_t *) x, M, logits, argmax, (hipStream_t) stream));
         return 0;

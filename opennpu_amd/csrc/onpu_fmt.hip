@@ -41,9 +41,11 @@ hipError_t FN(qgemm)(const GArgs & a, int ntw, int mb, hipStream_t s) {
     if (a.akeys) {                            // argmax keys: one row tile, no split (host checked)
         if (mb == 1 && a.deep) k_qgemm<F, 2, 1, true, true><<<grid, 256, 0, s>>>(a);
         else if (mb == 1) k_qgemm<F, 2, 1, true><<<grid, 256, 0, s>>>(a);
+        else if (mb == 2 && a.deep) k_qgemm<F, 2, 2, true, true><<<grid, 256, 0, s>>>(a);
         else if (mb == 2) k_qgemm<F, 2, 2, true><<<grid, 256, 0, s>>>(a);
         else k_qgemm<F, 2, 4, true><<<grid, 256, 0, s>>>(a);
     } else if (mb == 1 && ntw == 2 && a.deep) k_qgemm<F, 2, 1, false, true><<<grid, 256, 0, s>>>(a);
+    else if (mb == 2 && ntw == 2 && a.deep) k_qgemm<F, 2, 2, false, true><<<grid, 256, 0, s>>>(a);
     else if (mb == 1 && ntw == 2) k_qgemm<F, 2, 1><<<grid, 256, 0, s>>>(a);
     else if (mb == 2 && ntw == 2) k_qgemm<F, 2, 2><<<grid, 256, 0, s>>>(a);
     else if (mb == 4 && ntw == 2) k_qgemm<F, 2, 4><<<grid, 256, 0, s>>>(a);

@@ -1070,8 +1070,8 @@ DEV void gemm_load_w(const __amdgpu_buffer_rsrc_t (&wrs)[NTW], int64_t b, int la
 
 // AK: one row tile (M <= 16 MB), no split: the epilogue also leaves the workgroup's argmax key of
 // each row over its columns in a.akeys[m][N block] (argmax_key: larger value, then lower column)
-// DEEP (16-row tiles): weights two blocks ahead (three register sets), for grids of at most two
-// workgroups per CU, where one block in flight per workgroup leaves the memory idle
+// DEEP (16- and 32-row tiles): weights two blocks ahead (three register sets), for grids of at
+// most two workgroups per CU, where one block in flight per workgroup leaves the memory idle
 template <int FMT, int NTW, int MB, bool AK = false, bool DEEP = false>
 __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     __shared__ u32x4 xs0[MB * 4 * 64], xs1[MB * 4 * 64];   // 2 x MB x 4 KiB
@@ -1144,8 +1144,8 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
     // two register sets for the weights, alternating with the two LDS buffers (no copies)
     u32x4 wa[NTW], wb[NTW];
     GPar<FMT> pa[NTW], pb[NTW];
-    if constexpr (MB == 1 && DEEP) {
-        // 16-row tiles on small grids: a block's loads are small (4 KiB of X, NTW weight blocks per
+    if constexpr (MB <= 2 && DEEP) {
+        // 16- and 32-row tiles on small grids: a block's loads are small (4 KiB of X, NTW weight blocks per
         // wave) and its compute short, so the weights stay two blocks ahead (57344 x 8192 at 4-16
         // rows 65 -> 54 us, 8192 x 28672 38 -> 33 us; the 151936 x 4096 heads, ~4.6 workgroups per
         // CU, measured 2-6 % slower and keep one block): three register sets in rotation,
@@ -1155,7 +1155,7 @@ __global__ __launch_bounds__(256, MB == 8 ? 2 : 4) void k_qgemm(GArgs a) {
         // (after a scheduling fence, so the order holds) its weight loads, and waits for all but
         // those before the barrier. Loads past the range re-read block kb1 - 1 (in range) into a
         // set that is not read again; the last wait drains them.
-        __shared__ u32x4 xs2[4 * 64];
+        __shared__ u32x4 xs2[MB * 4 * 64];
         u32x4 wc[NTW];
         GPar<FMT> pc[NTW];
         const int64_t bl = kb1 - 1;
