@@ -233,12 +233,13 @@ def test_gemm_split_k(gpu, fmt, M, N, K, mb, monkeypatch):
 
 
 def test_gemm_split_k_under_capture(gpu):
-    """split-K GEMMs recorded in a graph (their partials in the capture's own workspace) at 96 and
-    40 rows: replays interleaved with eager split-K GEMMs on the default stream each equal the eager
-    results bit for bit"""
+    """split-K GEMMs recorded in a graph (their partials in the capture's own workspace) at 96, 40
+    and 16 rows (128-, 64- and 16-row tiles, the last with the weights two blocks ahead), and the
+    long-K matrix that takes the GEMM at one row: replays interleaved with eager GEMMs on the default
+    stream each equal the eager results bit for bit"""
     import torch
     from opennpu_amd.device import QMatrix
-    shapes = [(96, 4096, 14336), (40, 14336, 4096)]
+    shapes = [(96, 4096, 14336), (40, 14336, 4096), (16, 10000, 4096), (1, 4096, 28672)]
     mats = [QMatrix(N, K, orc.FMT_G128S, syn.weights(orc.FMT_G128S, N, K, 70 + M)) for M, N, K in shapes]
     try:
         xs = [to_torch_bf16(syn.activations(M, K, 71 + M)).reshape(M, K) for M, _, K in shapes]
