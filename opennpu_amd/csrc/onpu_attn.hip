@@ -79,7 +79,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <typename KV, int LPR, int HG>
 __global__ __launch_bounds__(AT) void k_attn_part(AttnArgs a) {
     constexpr int RPW = 64 / LPR, RIT = AW * RPW * AU;          // row slots per wave; rows per pass
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const int D = a.D, C = a.C, c = blockIdx.x, g = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6, li = lane % LPR, slot = lane / LPR;
     float * P = lds, * red = P + HG * C, * wmax = red + AW * HG * D, * wsum = wmax + AW * HG, * qs = wsum + AW * HG;
@@ -409,7 +409,7 @@ struct GdnArgs {
 
 // LDS: Sl [Dk][Dv], vec [4][max(Dk, Dv)] (q, k, delta / o), part [256 / Dv][Dv], red [8]
 __global__ __launch_bounds__(256) void k_gdn_head(GdnArgs a) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x, t = threadIdx.x, Dk = a.Dk, Dv = a.Dv, rep = a.Hv / a.Hk, kh = h / rep;
     const int key_dim = a.Hk * Dk, mx = Dk > Dv ? Dk : Dv, G = 256 / Dv, j = t % Dv, g = t / Dv;
     float * Sl = lds, * qv = Sl + Dk * Dv, * kvec = qv + mx, * dv = kvec + mx, * ov = dv + mx;

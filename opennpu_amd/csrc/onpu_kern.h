@@ -718,7 +718,7 @@ constexpr int qgemv_lb(int MB, int RT, int NB, int XL) { return (MB == 1 && RT *
 //            agent-scope increments of one address queue behind each other, ~0.2 us apiece.)
 template <int FMT, int MB, int RT, int NB, int EPI, int XL>
 __global__ __launch_bounds__(qgemv_lb(MB, RT, NB, XL)) void k_qgemv(QArgs a) {
-    extern __shared__ float red[];
+    extern __shared__ __align__(16) float red[];
     // the wave index is uniform across a wave: readfirstlane lets the compiler keep tile bases,
     // block ranges and their guards in scalar registers
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
@@ -1855,7 +1855,7 @@ DEV void md_load(const uint8_t * const (&tb)[RT], int64_t b0, int nb, u32x4 (&wv
 // rounded up), both at most as built
 template <int FMT, int GB, int DB>
 __global__ __launch_bounds__(512) void k_moe_decode(MDArgs a) {
-    extern __shared__ float mds[];
+    extern __shared__ __align__(16) float mds[];
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     constexpr int GS = FMT == ONPU_G128S ? 128 : 32, GPB = 128 / GS;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 15;
@@ -2133,7 +2133,7 @@ DEV void ds_accum(const u32x4 (&wv)[GB][1], const Par<FMT> (&par)[GB][1], int nb
 // tiles.
 template <int FMT, int GB, int DQ, int NW, int SV>
 __global__ __launch_bounds__(NW * 64) void k_moe_dsplit(MSArgs a) {
-    extern __shared__ float dsl[];
+    extern __shared__ __align__(16) float dsl[];
     constexpr int BLK = 1024 + 16 * (128 / (FMT == ONPU_G128S ? 128 : 32)) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     constexpr int SB = 1024 + (FMT == ONPU_Q4NX ? 256 : 128);
     constexpr int GS = FMT == ONPU_G128S ? 128 : 32, GPB = 128 / GS;
@@ -2479,7 +2479,7 @@ __global__ __launch_bounds__((CHAIN_WAVES + CHAIN_CTRL) * 64) void k_qgemv_chain
     constexpr int BLK = 1024 + 16 * (128 / GS) * 2 * (FMT == ONPU_Q4NX ? 2 : 1);
     constexpr uint32_t CT = CHAIN_CTRL * 64;            // control threads
     static_assert(2 * (S - 1) <= 63, "ring deeper than the load counter");
-    extern __shared__ float red[];      // [2][CHAIN_WAVES][256] partial sums, x rows, column sums, ring
+    extern __shared__ __align__(16) float red[];  // [2][CHAIN_WAVES][256] partial sums, x rows, column sums, ring
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int P = (int) gridDim.x, w = (int) blockIdx.x;
     uint16_t * xs = (uint16_t *) (red + 2 * CHAIN_WAVES * 256);

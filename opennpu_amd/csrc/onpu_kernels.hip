@@ -29,7 +29,7 @@ __global__ __launch_bounds__(1024) void k_moe_permute(const int32_t * __restrict
                                                       int rows_per_item, int32_t * __restrict__ off,
                                                       int32_t * __restrict__ perm, int32_t * __restrict__ inv,
                                                       int32_t * __restrict__ items, int32_t * __restrict__ nitems) {
-    extern __shared__ int32_t sh[];
+    extern __shared__ __align__(16) int32_t sh[];
     int32_t * cnt = sh;              // [E]
     int32_t * pos = sh + E;          // [E + 1]
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
@@ -231,7 +231,7 @@ template <int CTRL> DEV float dpp_fl(float v) {
 __global__ __launch_bounds__(GI8_T) void k_gemv_i8(const int8_t * __restrict__ W, const float * __restrict__ s,
                                                    int64_t N, int64_t K, int ks, int64_t Kw,
                                                    const float * __restrict__ x, float * __restrict__ y) {
-    extern __shared__ float xs[];
+    extern __shared__ __align__(16) float xs[];
     __shared__ float wsx[GI8_T / 64];
     __shared__ float red[GI8_T / 64][4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 15, slot = lane >> 4;
