@@ -807,15 +807,16 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
 // MoE decode split along I (k_moe_dsplit + k_moe_dsum): route from logits (non-null; ids / w are then
 // written) or take ids / w. hipErrorNotSupported when the FFN has no step-major down copy, the shapes
 // are outside the kernel's, or T is above ONPU_MOE_DSPLIT_MAX_T (default 1: at Qwen3-30B-A3B shapes on
-// MI355X the split path takes 16.2 us per layer at T = 1 against 18.5 us for the two launches, but
-// 27.7 / 42.1 us at T = 2 / 4 against 22.2 / 36.1); the caller then takes the two-launch path.
+// MI355X the split path takes 12.3 us per layer at T = 1 against 15.8 us for the two launches, but
+// 19.5 / 29.9 us at T = 2 / 4 against 17.9 / 26.2); the caller then takes the two-launch path.
 hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, int64_t T, int k, int renorm, int E,
                            int32_t * ids, float * w, void * y, int yf32, hipStream_t s) {
     Mat4 * gu = f->gu, * dn = f->dn;
     // values of I per workgroup: 16 while every workgroup still gets a CU of its own (a workgroup's
     // ~100 KB of loads in flight arrive at a fixed rate per CU, so halving them halves that phase),
     // else 32. Measured at Qwen3-30B-A3B, T = 1 (I 768; k slots: 48 k workgroups of 16 values against
-    // 24 k of 32): 12.4-13.8 against 14.2-15.9 us for k = 1..5, 18.0 against 16.1 us at k = 6
+    // 24 k of 32): 12.4-13.8 against 14.2-15.9 us for k = 1..5, 18.0 against 16.1 us at k = 6 (with
+    // the dynamic LDS 16-byte aligned: 14.4 against 12.3 us at k = 8)
     const int64_t I = gu->N / 2;
     const int esv = env_int("ONPU_DS_SV", 0);
     const int sv = esv == 16 || esv == 32 ? esv : (T * k * (I / 16) <= device().cus ? 16 : 32);
@@ -824,8 +825,9 @@ hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, in
         return hipErrorNotSupported;
     // only while its workgroups (of 32 values) fit one per CU: past that each CU runs several
     // ~100-200 KB workgroups in turn and the partial sums grow with I, so the two launches win
-    // (measured at T = 1: Qwen3-235B-A22B experts 47.4 against 33.3 us, Mixtral-8x7B 101.6
-    // against 65.2 us; Qwen3-30B-A3B 16.6 against 18.6 us)
+    // (measured at T = 1: Qwen3-235B-A22B experts 30.4 against 26.5 us, Mixtral-8x7B 69.8
+    // against 48.0 us, E 32 / H 3072 / I 3072 / k 4 27.3 against 22.6 us; Qwen3-30B-A3B 12.3
+    // against 15.8 us)
     if (esv == 0 && T * k * (I / 32) > device().cus) return hipErrorNotSupported;
     hipError_t e = f->ds_part.ensure((size_t) (DS_MAX_T * DS_MAX_K) * (size_t) (S * NTq * 64) * 4);
     if (e != hipSuccess) return e;
