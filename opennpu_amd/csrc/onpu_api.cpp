@@ -807,7 +807,7 @@ hipError_t moe_decode_core(Ffn * f, const float * logits, const uint16_t * x, in
 // MoE decode split along I (k_moe_dsplit + k_moe_dsum): route from logits (non-null; ids / w are then
 // written) or take ids / w. hipErrorNotSupported when the FFN has no step-major down copy, the shapes
 // are outside the kernel's, or T is above ONPU_MOE_DSPLIT_MAX_T (default 1: at Qwen3-30B-A3B shapes on
-// MI355X the split path takes 12.3 us per layer at T = 1 against 15.8 us for the two launches, but
+// MI355X the split path takes 12.0 us per layer at T = 1 against 15.8 us for the two launches, but
 // 19.5 / 29.9 us at T = 2 / 4 against 17.9 / 26.2); the caller then takes the two-launch path.
 hipError_t moe_dsplit_core(Ffn * f, const float * logits, const uint16_t * x, int64_t T, int k, int renorm, int E,
                            int32_t * ids, float * w, void * y, int yf32, hipStream_t s) {
