@@ -632,6 +632,9 @@ hipError_t launch_zero_i32(int32_t * p, int64_t n, hipStream_t s) {
 
 // split-K GEMM epilogue: four consecutive columns of a row per thread, the planes added in order
 // (the same fp32 sum whatever the launch shape)
+// U (>= S up to 16): a thread's first U planes are loaded at once, then added in plane order (one
+// load in flight per thread left the launch at ~3.9 TB/s: too few bytes in flight for HBM)
+template <int U>
 __global__ __launch_bounds__(256) void k_gemm_split_sum(const float * __restrict__ part, int S, int64_t M, int64_t N,
                                                         void * __restrict__ y, int64_t ldy, int yf32) {
     const int64_t plane = M * N, nq = (N + 3) / 4;
@@ -639,8 +642,15 @@ __global__ __launch_bounds__(256) void k_gemm_split_sum(const float * __restrict
         const int64_t m = i / nq, n0 = 4 * (i % nq);
         const float * p = part + m * N + n0;
         if (N % 4 == 0) {                                  // planes and rows 16-byte aligned
-            f32x4 acc = *(const f32x4 *) p;
-            for (int s = 1; s < S; s++) acc += *(const f32x4 *) (p + s * plane);
+            f32x4 v[U];
+#pragma unroll
+            for (int s = 0; s < U; s++)
+                if (s < S) v[s] = *(const f32x4 *) (p + s * plane);
+            f32x4 acc = v[0];
+#pragma unroll
+            for (int s = 1; s < U; s++)
+                if (s < S) acc += v[s];
+            for (int s = U; s < S; s++) acc += *(const f32x4 *) (p + s * plane);
             for (int v = 0; v < 4; v++) store_out(y, yf32, m * ldy + n0 + v, acc[v]);
         } else {
             for (int v = 0; v < 4 && n0 + v < N; v++) {
@@ -657,7 +667,11 @@ hipError_t launch_gemm_split_sum(const float * part, int S, int64_t M, int64_t N
     if (S < 1 || M < 0 || N < 0 || ldy < N) return hipErrorInvalidValue;
     const int64_t n4 = M * ((N + 3) / 4);
     if (n4 == 0) return hipSuccess;
-    k_gemm_split_sum<<<(unsigned) std::min<int64_t>((n4 + 255) / 256, 8192), 256, 0, s>>>(part, S, M, N, y, ldy, yf32);
+    const unsigned g = (unsigned) std::min<int64_t>((n4 + 255) / 256, 8192);
+    if (S <= 2) k_gemm_split_sum<2><<<g, 256, 0, s>>>(part, S, M, N, y, ldy, yf32);
+    else if (S <= 4) k_gemm_split_sum<4><<<g, 256, 0, s>>>(part, S, M, N, y, ldy, yf32);
+    else if (S <= 8) k_gemm_split_sum<8><<<g, 256, 0, s>>>(part, S, M, N, y, ldy, yf32);
+    else k_gemm_split_sum<16><<<g, 256, 0, s>>>(part, S, M, N, y, ldy, yf32);
     CHECK_LAUNCH();
     return hipSuccess;
 }
